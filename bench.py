@@ -1,0 +1,264 @@
+"""Benchmark of the mLSTM kernel backend on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--chunk-size 64] [--algo auto]
+                    [--decode-steps 1000] [--no-cpu-baseline]
+
+Prints ONE JSON line.  Headline (`value`): chunkwise mLSTM prefill tokens/s
+at BASELINE config 2 (bf16 q/k/v/gates, float32 states, B4 NH8 S8192 DQK256
+DV512, L=64, last states returned).  One step = one `mlstm_chunkwise` call
+over the whole batch (B*S = 32768 tokens) with inputs resident in HBM; L2 and
+the 256 MB Infinity Cache are flushed (512 MB write) before every timed call,
+and each call is timed with HIP events on the stream the kernels run on.
+The decode step (config 1, B16 NH8 DQK256 DV512) is reported beside it in
+`decode`: 1000 chained steps over 6 rotating state sets (>256 MB, so the
+state really streams from HBM), captured in a HIP graph.
+
+Roofline figures use algorithmic work only:
+  prefill FLOP/call = B*NH*S*(4*DQK*DV + 2*L*(DQK+DV))      (1.6321e11 at L=64)
+  prefill bytes/call = q,k,v,h (bf16) + gates (bf16) + last states (fp32)
+  decode bytes/step  = 2|C| + 2|n| + 2|m| + |q|+|k|+|v|+|i|+|f|+|h|  (134,875,136)
+Peaks: bf16 dense MFMA 2500 TFLOP/s, HBM 8000 GB/s.
+
+The CPU baseline is the oracle (torch on the host cores, a restatement of the
+reference's torch-native code) timed on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "xlstm-metal_amd"))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def prefill_flops(B, NH, S, DQK, DV, L):
+    return B * NH * S * (4 * DQK * DV + 2 * L * (DQK + DV))
+
+
+def prefill_bytes(B, NH, S, DQK, DV, esz=2):
+    return (2 * B * NH * S * DQK * esz + 2 * B * NH * S * DV * esz + 2 * B * NH * S * esz
+            + B * NH * (DQK * DV + DQK + 1) * 4)
+
+
+def decode_bytes(B, NH, DQK, DV, esz=2, gsz=4):
+    C, n, m = B * NH * DQK * DV * 4, B * NH * DQK * 4, B * NH * 4
+    return 2 * C + 2 * n + 2 * m + 2 * B * NH * DQK * esz + 2 * B * NH * DV * esz + 2 * B * NH * gsz
+
+
+class Flusher:
+    """Writes a 512 MB buffer to evict L2 and the Infinity Cache (MALL)."""
+
+    def __init__(self, device):
+        self.buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=device)
+
+    def __call__(self):
+        self.buf.fill_(1.0)
+
+
+def bench_prefill(args, dev):
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    cfg = CFG2
+    L = args.chunk_size
+    x = chunkwise_inputs(cfg, device=dev)
+    flush = Flusher(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def call():
+        return xlstm_hip.mlstm_chunkwise(*x, return_last_states=True, chunk_size=L, algo=args.algo)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize(dev)
+    times = []
+    t_wall = 0.0
+    for _ in range(args.steps):
+        flush()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record(stream)
+        call()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        t_wall += time.perf_counter() - w0
+        times.append(e0.elapsed_time(e1))
+    ms = statistics.mean(times)
+    tokens = cfg.B * cfg.S
+    fl = prefill_flops(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, L)
+    by = prefill_bytes(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV)
+    return {
+        "ms": ms, "ms_median": statistics.median(times), "ms_min": min(times), "wall_ms": 1e3 * t_wall / args.steps,
+        "tokens": tokens, "flops": fl, "bytes": by, "L": L, "cfg": cfg,
+    }
+
+
+def bench_decode(args, dev):
+    """cfg1 decode step through the C-ABI, 6 rotating state sets, HIP-graph replay."""
+    from xlstm_hip import _lib
+    from xlstm_hip.workloads import CFG1, step_inputs
+    cfg = CFG1
+    lib = _lib.load()
+    B, NH, DQK, DV = cfg.B, cfg.NH, cfg.DQK, cfg.DV
+    q, k, v, i, f, C, n, m = step_inputs(cfg, device=dev)
+    nsets = 6
+    Cs = [C.clone() for _ in range(nsets)]  # updated in place
+    ns = [[n.clone(), torch.empty_like(n)] for _ in range(nsets)]
+    ms_ = [[m.clone(), torch.empty_like(m)] for _ in range(nsets)]
+    h = torch.empty(B, NH, DV, dtype=q.dtype, device=dev)
+    scale = DQK ** -0.5
+
+    def launch(s, parity, stream):
+        a, b = parity, 1 - parity
+        rc = lib.xl_mlstm_step_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(),
+                                   Cs[s].data_ptr(), ns[s][a].data_ptr(), ms_[s][a].data_ptr(), h.data_ptr(),
+                                   Cs[s].data_ptr(), ns[s][b].data_ptr(), ms_[s][b].data_ptr(), B, NH, DQK, DV,
+                                   scale, 1e-6, 1, 0, stream)
+        _lib.check(rc, "decode bench")
+
+    per_graph = 2 * nsets  # both ping-pong parities of every set
+    mode = "hip_graph"
+    graph = None
+    try:
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for p in (0, 1):
+                for s in range(nsets):
+                    launch(s, p, side.cuda_stream)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            st = torch.cuda.current_stream(dev).cuda_stream
+            for p in (0, 1):
+                for s in range(nsets):
+                    launch(s, p, st)
+        run = graph.replay
+    except Exception as exc:  # measurement method only; the kernel is the same
+        mode = f"eager ({type(exc).__name__})"
+        graph = None
+
+        def run():
+            st = torch.cuda.current_stream(dev).cuda_stream
+            for p in (0, 1):
+                for s in range(nsets):
+                    launch(s, p, st)
+
+    reps = max(1, args.decode_steps // per_graph)
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    steps = reps * per_graph
+    us = 1e3 * e0.elapsed_time(e1) / steps
+    by = decode_bytes(B, NH, DQK, DV)
+    return {"us_per_step": us, "steps": steps, "bytes": by, "mode": mode, "state_sets": nsets, "cfg": cfg}
+
+
+def cpu_baseline(args):
+    """Oracle (torch on the host) on a bounded sample: prefill tokens/s and decode us/step."""
+    from oracle import mlstm as om
+    from xlstm_hip.workloads import CFG1, CFG2, chunkwise_inputs, step_inputs
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    # prefill sample: batch row 0 of cfg2 (all 8 heads, full S; bf16 inputs upcast, fp32 states)
+    S = CFG2.S
+    x = tuple(t.float() for t in chunkwise_inputs(CFG2, B=1))
+    om.mlstm_chunkwise(*x, return_last_states=True, chunk_size=args.chunk_size)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or (time.perf_counter() - t0 < 10.0 and reps < 50):
+        om.mlstm_chunkwise(*x, return_last_states=True, chunk_size=args.chunk_size)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    pre_tps = S / dt
+    # decode sample: cfg1 step, 10 chained steps
+    q, k, v, i, f, C, n, m = step_inputs(CFG1)
+    om.mlstm_recurrent_step(q, k, v, i, f, C, n, m)
+    t0 = time.perf_counter()
+    nst = 10
+    for _ in range(nst):
+        _, (C, n, m) = om.mlstm_recurrent_step(q, k, v, i, f, C, n, m)
+    dec_us = 1e6 * (time.perf_counter() - t0) / nst
+    return {
+        "value": pre_tps, "unit": "tokens/s", "cores": cores, "kind": "port",
+        "sample": f"oracle.mlstm.mlstm_chunkwise (torch {torch.__version__} CPU, fp32) on cfg2 batch row 0, "
+                  f"8 heads, S={S}, L={args.chunk_size}: {reps} reps, {dt * 1e3:.1f} ms each",
+        "decode_us_per_step": dec_us,
+        "decode_sample": f"oracle.mlstm.mlstm_recurrent_step on cfg1, {nst} chained steps",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--chunk-size", type=int, default=64)
+    ap.add_argument("--algo", default="auto", choices=["auto", "fused", "two_pass"])
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on ONE GPU only (no collectives); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    import xlstm_hip
+    xlstm_hip.load_library()
+
+    pre = bench_prefill(args, dev)
+    cfg = pre["cfg"]
+    value = pre["tokens"] / (pre["ms"] * 1e-3)
+    tflops = pre["flops"] / (pre["ms"] * 1e-3) / 1e12
+    gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9
+    out = {
+        "metric": "mLSTM chunkwise prefill tokens/s (7B heads) + decode step us; % roofline",
+        "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": pre["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of BASELINE config 2)",
+        "config": {"workload": "cfg2 mlstm_chunkwise prefill", "B": cfg.B, "NH": cfg.NH, "S": cfg.S,
+                   "DQK": cfg.DQK, "DV": cfg.DV, "chunk_size": pre["L"], "states": "fp32",
+                   "return_last_states": True, "algo": args.algo},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_BF16_TFLOPS, "traffic": None,
+                     "flops_per_call": pre["flops"], "timing": "HIP events per call, caches flushed"},
+        "roofline_hbm": {"achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                         "bytes_per_call": pre["bytes"]},
+        "prefill_ms_median": pre["ms_median"], "prefill_ms_min": pre["ms_min"], "prefill_wall_ms": pre["wall_ms"],
+    }
+    if not args.no_decode:
+        dec = bench_decode(args, dev)
+        dgbs = dec["bytes"] / (dec["us_per_step"] * 1e-6) / 1e9
+        out["decode"] = {"workload": "cfg1 mlstm decode step", "us_per_step": dec["us_per_step"],
+                         "tokens_per_s": dec["cfg"].B / (dec["us_per_step"] * 1e-6), "steps": dec["steps"],
+                         "mode": dec["mode"], "state_sets": dec["state_sets"],
+                         "roofline": {"bound": "hbm", "achieved": dgbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                      "frac": dgbs / PEAK_HBM_GBS, "bytes_per_step": dec["bytes"]}}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

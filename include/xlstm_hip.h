@@ -1,0 +1,162 @@
+/*
+ * xlstm_hip.h — C-ABI of the MI355X (gfx950) mLSTM/sLSTM kernel library
+ * (libxlstm_hip.so).
+ *
+ * Drop-in boundary for the torch-native kernel backend of MLXPorts/xLSTM-metal.
+ * Each entry point replaces one reference function (paths relative to the
+ * reference root, see the comment on each).  The reference has no C ABI of its
+ * own for these functions: its native launchers are pybind11/Objective-C++
+ * (e.g. xlstm_metal/torch_native/blocks/mlstm/mlstm_chunkwise/forward/
+ * mlstm_chunkwise_recurrent_fw_C_extension.mm:62-149, soft_cap_extension.mm:
+ * 60-95).  This ABI is plain C: pointers, sizes, scalars.
+ *
+ * Conventions
+ *  - Tensors are dense, row-major, contiguous, in the reference's layouts
+ *    ([B, NH, S, D] etc.).  Device pointers.
+ *  - Every buffer is owned by the caller.  No entry point allocates device
+ *    memory; scratch comes in through `workspace` (size from the matching
+ *    *_workspace_size call).
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *    the call returns without synchronising.  Entry points are re-entrant and
+ *    keep no state between calls.
+ *  - Return 0 on success, a negative XL_ERR_* code on failure; the message is
+ *    then available from xl_last_error() on the calling thread.
+ *  - States (C, n, m) are always float32.  q/k/v/z and gates may be float32,
+ *    bfloat16 or float16 (XL_DTYPE_*); arithmetic is float32, MFMA operands
+ *    of the fused chunkwise kernel are bfloat16.
+ */
+#ifndef XLSTM_HIP_H
+#define XLSTM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XL_ABI_VERSION 1
+
+enum xl_dtype { XL_DTYPE_F32 = 0, XL_DTYPE_BF16 = 1, XL_DTYPE_F16 = 2 };
+
+enum xl_status {
+  XL_OK = 0,
+  XL_ERR_INVALID_ARG = -1,   /* bad shape, null pointer, aliasing, bad dtype */
+  XL_ERR_UNSUPPORTED = -2,   /* valid request this build does not implement */
+  XL_ERR_WORKSPACE = -3,     /* workspace missing or too small */
+  XL_ERR_LAUNCH = -4         /* the HIP runtime rejected a launch */
+};
+
+/* Chunkwise algorithm selector for xl_mlstm_chunkwise_fwd. */
+enum xl_chunkwise_algo {
+  XL_CHUNKWISE_AUTO = 0,     /* fused when supported, else two-pass */
+  XL_CHUNKWISE_TWO_PASS = 1, /* states kernel + output kernel, float32 math */
+  XL_CHUNKWISE_FUSED = 2     /* single pass, bf16 MFMA, states in registers */
+};
+
+/* ABI version of the loaded library (XL_ABI_VERSION at build time). */
+int xl_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* xl_last_error(void);
+
+/*
+ * y = cap * tanh(x / cap), elementwise over numel elements; cap <= 0 copies x.
+ * Replaces soft_cap(x, cap) (xlstm_metal/torch_native/blocks/soft_cap/
+ * softcap_metal.py:29-31 -> soft_cap_extension.mm:60-95 -> soft_cap_kernel.
+ * metal:4-15) and SoftCapCell.forward (softcap.py:25-31).  x and y have the
+ * same dtype; y may alias x.
+ */
+int xl_soft_cap_fwd(const void* x, void* y, int64_t numel, float cap, int dtype, void* stream);
+
+/*
+ * One recurrent mLSTM decode step.  Replaces mlstm_recurrent_step__native
+ * (kernel_development/xlstm/mlstm_block/mlstm_recurrent/recurrent/
+ * native_step.py:8-133).
+ *   q, k [B,NH,DQK], v [B,NH,DV] (dtype_qkv); i, f [B,NH] (dtype_gates);
+ *   c_old [B,NH,DQK,DV], n_old [B,NH,DQK], m_old [B,NH] float32;
+ *   h [B,NH,DV] (dtype_qkv); c_new, n_new, m_new float32, same shapes.
+ * c_new may equal c_old (in-place update).  n_new / m_new must not alias
+ * n_old / m_old.  The reference's dtype roundings for a bfloat16/float16 q
+ * (q*scale, k v^T, C' and n' cast to q's dtype for the h products, the
+ * products rounded to q's dtype) are reproduced.
+ */
+int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                      const float* c_old, const float* n_old, const float* m_old,
+                      void* h, float* c_new, float* n_new, float* m_new,
+                      int B, int NH, int DQK, int DV, float qk_scale, float eps,
+                      int dtype_qkv, int dtype_gates, void* stream);
+
+/*
+ * Chunkwise mLSTM forward.  Replaces mlstm_chunkwise / mlstm_chunkwise_fw
+ * (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/vendored/torch/
+ * native/fw.py:257-412) and its registry form mlstm_chunkwise__native_autograd
+ * (.../native/fwbw.py:192-229).
+ *   q, k [B,NH,S,DQK], v [B,NH,S,DV] (dtype_qkv); i, f [B,NH,S] (dtype_gates);
+ *   c0 [B,NH,DQK,DV], n0 [B,NH,DQK], m0 [B,NH] float32, all three NULL for
+ *   zero initial states (or all three non-NULL);
+ *   h [B,NH,S,DV] (dtype_qkv); c_last, n_last, m_last float32 (all NULL when
+ *   the last states are not wanted).
+ * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.
+ * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes (0 for the fused
+ * algorithm), 256-byte aligned.
+ */
+size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, int L,
+                                         int dtype_qkv, int algo);
+int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                           const float* c0, const float* n0, const float* m0,
+                           void* h, float* c_last, float* n_last, float* m_last,
+                           int B, int NH, int S, int DQK, int DV, int L, float qk_scale, float eps,
+                           int dtype_qkv, int dtype_gates, int algo,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Recurrent mLSTM over a whole sequence in one launch (the time loop runs on
+ * the GPU, states stay on chip).  Replaces mlstm_recurrent_sequence__native_fw
+ * (kernel_development/xlstm/mlstm_block/mlstm_recurrent/recurrent/
+ * native_sequence.py:18-170), used by the arbitrary-length wrapper for tails
+ * (kernel_development/xlstm/mlstm_block/mslstm_parallel/torch/
+ * kernel_wrappers.py:151-170).  Shapes as for xl_mlstm_chunkwise_fwd with any
+ * S >= 1; same dtype semantics as xl_mlstm_step_fwd.
+ */
+int xl_mlstm_sequence_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                          const float* c0, const float* n0, const float* m0,
+                          void* h, float* c_last, float* n_last, float* m_last,
+                          int B, int NH, int S, int DQK, int DV, float qk_scale, float eps,
+                          int dtype_qkv, int dtype_gates, void* stream);
+
+/*
+ * One sLSTM step.  Replaces slstm_step_pytorch (xlstm_metal/torch_native/
+ * blocks/slstm/slstm_layers/stepwise/slstm_metal_kernel.py:14-65) and
+ * sLSTMStepwiseKernelCell.forward (.../stepwise/slstm_stepwise_kernel_cell.
+ * py:47-97).
+ *   z [B,NH,H] (dtype_z); i, f, o [B,NH] (dtype_gates);
+ *   c, n [B,NH,H], m [B,NH] float32; h [B,NH,H] (dtype_h);
+ *   c_new, n_new [B,NH,H], m_new [B,NH] float32 (c_new/n_new may alias c/n,
+ *   m_new must not alias m).
+ */
+int xl_slstm_step_fwd(const void* z, const void* i, const void* f, const void* o,
+                      const float* c, const float* n, const float* m,
+                      void* h, float* c_new, float* n_new, float* m_new,
+                      int B, int NH, int H, float eps, int dtype_z, int dtype_gates, int dtype_h,
+                      void* stream);
+
+/*
+ * sLSTM over a sequence in one launch: the per-timestep loop of
+ * sLSTMNeuron.forward (xlstm_metal/torch_native/blocks/slstm/slstm_layers/
+ * slstm_neuron.py:132-143) with states in registers.
+ *   z [B,S,NH,H] (dtype_z); i, f, o [B,S,NH] (dtype_gates);
+ *   c0, n0 [B,NH,H], m0 [B,NH] float32 or all NULL (zero state);
+ *   h [B,S,NH,H] (dtype_h); c_last, n_last, m_last float32 or all NULL.
+ */
+int xl_slstm_seq_fwd(const void* z, const void* i, const void* f, const void* o,
+                     const float* c0, const float* n0, const float* m0,
+                     void* h, float* c_last, float* n_last, float* m_last,
+                     int B, int S, int NH, int H, float eps, int dtype_z, int dtype_gates, int dtype_h,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XLSTM_HIP_H */

@@ -1,0 +1,148 @@
+"""C-ABI boundary checks that need no GPU.
+
+* libxlstm_hip.so loads and exports every entry point include/xlstm_hip.h
+  declares, with the ABI version the header states;
+* argument validation fails with the documented error codes and messages
+  before any GPU call (null pointers, bad shapes, aliasing, S % L != 0,
+  unsupported chunk sizes) — the failure paths the reference raises for
+  (fw.py:303-305, native_step.py:49-67);
+* the Python ops refuse CPU tensors (there is no CPU fallback) and the
+  registry names mirror the reference's backend names.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "xlstm_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(xl_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from xlstm_hip import _lib
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    for n in ("xl_abi_version", "xl_last_error", "xl_soft_cap_fwd", "xl_mlstm_step_fwd", "xl_mlstm_chunkwise_fwd",
+              "xl_mlstm_chunkwise_workspace_size", "xl_mlstm_sequence_fwd", "xl_slstm_step_fwd", "xl_slstm_seq_fwd"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(lib._name)
+    for name in _declared():
+        assert hasattr(raw, name), f"{name} declared in include/xlstm_hip.h but not exported"
+
+
+def test_python_signatures_cover_header(lib):
+    from xlstm_hip import _lib
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_abi_version_matches_header(lib):
+    m = re.search(r"#define XL_ABI_VERSION (\d+)", open(HEADER).read())
+    assert lib.xl_abi_version() == int(m.group(1))
+
+
+def test_soft_cap_rejects_bad_args(lib):
+    assert lib.xl_soft_cap_fwd(None, None, -1, 1.0, 0, None) == -1
+    assert b"numel" in lib.xl_last_error()
+    assert lib.xl_soft_cap_fwd(None, None, 4, 1.0, 7, None) == -1
+    assert b"dtype" in lib.xl_last_error()
+    assert lib.xl_soft_cap_fwd(None, None, 4, 1.0, 0, None) == -1
+    assert b"null" in lib.xl_last_error()
+    assert lib.xl_soft_cap_fwd(None, None, 0, 1.0, 0, None) == 0  # empty input is a no-op
+
+
+def test_step_rejects_bad_args(lib):
+    f = lib.xl_mlstm_step_fwd
+    p = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    assert f(p, p, p, p, p, p, p, p, p, p, p, p, 0, 8, 256, 512, 0.0625, 1e-6, 1, 0, None) == -1
+    assert b"positive" in lib.xl_last_error()
+    assert f(p, p, p, p, p, p, p, p, p, p, p, p, 2, 8, 256, 514, 0.0625, 1e-6, 1, 0, None) == -2
+    assert f(p, p, p, p, p, p, p, p, p, p, p, p, 2, 8, 1024, 512, 0.0625, 1e-6, 1, 0, None) == -2
+    assert f(p, p, p, p, p, None, p, p, p, p, p, p, 2, 8, 256, 512, 0.0625, 1e-6, 1, 0, None) == -1
+    assert b"null" in lib.xl_last_error()
+    a, b = ctypes.c_void_p(512), ctypes.c_void_p(1024)
+    assert f(p, p, p, p, p, a, b, p, p, a, b, ctypes.c_void_p(2048), 2, 8, 256, 512, 0.0625, 1e-6, 1, 0, None) == -1
+    assert b"alias" in lib.xl_last_error()
+
+
+def test_chunkwise_rejects_bad_args(lib):
+    f = lib.xl_mlstm_chunkwise_fwd
+    p = ctypes.c_void_p(256)
+    args = lambda S, L, algo=0, c0=None: (p, p, p, p, p, c0, None, None, p, None, None, None, 1, 8, S, 256, 512, L,
+                                           0.0625, 1e-6, 1, 1, algo, None, 0, None)
+    assert f(*args(250, 64)) == -1
+    assert b"not divisible" in lib.xl_last_error()
+    assert f(*args(240, 48)) == -2
+    assert f(*args(256, 64, algo=9)) == -1
+    assert f(*args(256, 64, c0=p)) == -1
+    assert b"together" in lib.xl_last_error()
+    assert f(*args(256, 64, algo=1)) == -3  # two-pass without workspace
+    assert b"workspace" in lib.xl_last_error()
+    assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 256, 256, 512, 64, 0, 1) == (4 * 8 * (256 * 512 + 256 + 1) * 4 + 255) // 256 * 256
+    assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 250, 256, 512, 64, 0, 1) == 0
+
+
+def test_slstm_rejects_bad_args(lib):
+    p = ctypes.c_void_p(256)
+    assert lib.xl_slstm_step_fwd(p, p, p, p, p, p, p, p, p, p, p, 1, 4, 0, 1e-6, 0, 0, 0, None) == -1
+    assert lib.xl_slstm_step_fwd(p, p, p, p, p, p, p, p, p, p, p, 1, 4, 8, 1e-6, 0, 0, 0, None) == -1  # m alias
+    assert b"alias" in lib.xl_last_error()
+    assert lib.xl_slstm_seq_fwd(p, p, p, p, p, None, None, p, None, None, None, 1, 3, 4, 8, 1e-6, 0, 0, 0, None) == -1
+
+
+def test_ops_refuse_cpu_tensors():
+    import xlstm_hip
+    x = torch.randn(8)
+    with pytest.raises(RuntimeError, match="GPU"):
+        xlstm_hip.soft_cap(x, 5.0)
+    q = torch.randn(1, 2, 64, 16)
+    i = torch.randn(1, 2, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        xlstm_hip.mlstm_chunkwise(q, q, q, i, i)
+    assert xlstm_hip.soft_cap(x, 0.0) is x  # cap <= 0: identity without touching the device
+
+
+def test_registry_names():
+    import xlstm_hip
+    assert xlstm_hip.get_mlstm_kernel("chunkwise--native_autograd") is xlstm_hip.mlstm_chunkwise__native_autograd
+    assert xlstm_hip.get_mlstm_step_kernel("native") is xlstm_hip.mlstm_recurrent_step__native
+    assert xlstm_hip.get_mlstm_sequence_kernel("native_sequence__native") is \
+        xlstm_hip.mlstm_recurrent_sequence__native_fw
+    with pytest.raises(NotImplementedError):
+        xlstm_hip.get_mlstm_kernel("chunkwise--triton_xl_chunk")
+    with pytest.raises(ValueError):
+        xlstm_hip.mLSTMBackendConfig(chunkwise_kernel="parallel--native_autograd", return_last_states=True)
+
+
+def test_ops_registered_with_torch_library():
+    import xlstm_hip  # noqa: F401
+    for name in ("soft_cap", "mlstm_step", "mlstm_step_", "mlstm_chunkwise", "mlstm_sequence", "slstm_step",
+                 "slstm_sequence"):
+        assert hasattr(torch.ops.xlstm_hip, name)
+
+
+def test_fake_tensor_shapes():
+    import xlstm_hip  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        q = torch.empty(2, 4, 128, 32, dtype=torch.bfloat16, device="cuda")
+        v = torch.empty(2, 4, 128, 48, dtype=torch.bfloat16, device="cuda")
+        g = torch.empty(2, 4, 128, dtype=torch.bfloat16, device="cuda")
+        h, c, n, m = torch.ops.xlstm_hip.mlstm_chunkwise(q, q, v, g, g, None, None, None, 0.1, 64, 1e-6, True, 0)
+        assert h.shape == (2, 4, 128, 48) and h.dtype == torch.bfloat16
+        assert c.shape == (2, 4, 32, 48) and n.shape == (2, 4, 32) and m.shape == (2, 4, 1)

@@ -1,0 +1,124 @@
+"""Chunkwise mLSTM forward on the GPU vs the CPU oracle.
+
+* cfg0 at full size (float32, B1 NH8 S256 DQK256 DV512 L64): rel-err <= 1e-4
+  on h and the final C, n, m;
+* every chunk size, initial states, ragged head dims, 16-bit inputs against the
+  float32 oracle on the upcast inputs (max-abs <= 2e-2);
+* cfg2 at full size (bf16, B4 NH8 S8192, L 64 and 128): the causal prefix
+  property (tokens < S' depend only on inputs < S') lets the oracle check the
+  full-size output on a 512-token prefix of two heads; the final states are
+  checked through chunk-size invariance and against the other algorithm.
+"""
+
+import pytest
+import torch
+
+from helpers import FP32_REL, LOWP_ABS, assert_parity, dev, maxabs, relerr
+from oracle import mlstm as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, NH, S, DQK, DV, dtype, seed, with_state=False):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, NH, S, DQK, generator=g) / DQK ** 0.5).to(dtype)
+    k = torch.randn(B, NH, S, DQK, generator=g).to(dtype)
+    v = torch.randn(B, NH, S, DV, generator=g).to(dtype)
+    i = torch.randn(B, NH, S, generator=g).to(dtype)
+    f = (torch.randn(B, NH, S, generator=g) + 3).to(dtype)
+    st = (None, None, None)
+    if with_state:
+        st = (0.1 * torch.randn(B, NH, DQK, DV, generator=g), torch.randn(B, NH, DQK, generator=g).abs(),
+              torch.randn(B, NH, 1, generator=g))
+    return (q, k, v, i, f), st
+
+
+def _gpu(ts):
+    return [None if t is None else t.to(dev()) for t in ts]
+
+
+def _oracle(x, st, L):
+    return om.mlstm_chunkwise(*(t.float() for t in x), *st, return_last_states=True, chunk_size=L)
+
+
+def test_cfg0_fp32_full_size(gpu_case):
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG0, chunkwise_inputs
+    x = chunkwise_inputs(CFG0)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, chunk_size=CFG0.L)
+    hr, (Cr, nr, mr) = _oracle(x, (None, None, None), CFG0.L)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        e = relerr(got, want)
+        print(f"cfg0 {name}: rel-err {e:.3e}")
+        assert e <= FP32_REL, name
+
+
+@pytest.mark.parametrize("L", [16, 32, 64, 128])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_fp32_chunk_sizes(gpu_case, L, with_state):
+    import xlstm_hip
+    x, st = _inputs(2, 3, 256, 64, 96, torch.float32, seed=L, with_state=with_state)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=L)
+    hr, (Cr, nr, mr) = _oracle(x, st, L)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert relerr(got, want) <= FP32_REL, name
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 64, 32, 16), (2, 2, 128, 80, 72), (1, 2, 192, 256, 512)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("algo", ["auto", "two_pass"])
+def test_lowp_inputs(gpu_case, shape, dtype, algo):
+    import xlstm_hip
+    B, NH, S, DQK, DV = shape
+    x, st = _inputs(B, NH, S, DQK, DV, dtype, seed=S + DQK, with_state=True)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=64,
+                                             algo=algo)
+    hr, (Cr, nr, mr) = _oracle(x, st, 64)
+    assert h.dtype == dtype
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got, want, dtype, f"{shape} {dtype} {algo} {name}")
+
+
+def test_no_last_states_and_defaults(gpu_case):
+    import xlstm_hip
+    x, _ = _inputs(1, 2, 128, 32, 32, torch.float32, seed=3)
+    h = xlstm_hip.mlstm_chunkwise(*_gpu(x))
+    assert isinstance(h, torch.Tensor)
+    assert relerr(h, om.mlstm_chunkwise(*x)) <= FP32_REL
+    h2 = xlstm_hip.mlstm_chunkwise__native_autograd(*_gpu(x), chunk_size=32,
+                                                    autocast_kernel_dtype=torch.bfloat16)
+    assert relerr(h2, om.mlstm_chunkwise(*x, chunk_size=32)) <= FP32_REL
+
+
+def test_errors(gpu_case):
+    import xlstm_hip
+    x, _ = _inputs(1, 2, 100, 32, 32, torch.float32, seed=3)
+    with pytest.raises(AssertionError, match="not divisible"):
+        xlstm_hip.mlstm_chunkwise(*_gpu(x), chunk_size=64)
+    x, _ = _inputs(1, 2, 96, 32, 32, torch.float32, seed=3)
+    with pytest.raises(NotImplementedError):
+        xlstm_hip.mlstm_chunkwise(*_gpu(x), chunk_size=48)
+
+
+@pytest.mark.parametrize("L", [64, 128])
+def test_cfg2_full_size_prefix_and_invariance(gpu_case, L):
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    x = chunkwise_inputs(CFG2)
+    xd = _gpu(x)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*xd, return_last_states=True, chunk_size=L)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(h).all()) and bool(torch.isfinite(C).all())
+    # causal prefix: the first 512 tokens of heads (0,0) and (3,7) against the oracle
+    P = 512
+    for b, hh in ((0, 0), (3, 7)):
+        xs = tuple(t[b:b + 1, hh:hh + 1, :P] for t in x)
+        hr = om.mlstm_chunkwise(*(t.float() for t in xs), chunk_size=L)
+        e = maxabs(h[b:b + 1, hh:hh + 1, :P], hr)
+        print(f"cfg2 L={L} prefix head ({b},{hh}): max-abs {e:.3e}")
+        assert e <= LOWP_ABS
+    # final states: the two algorithms and the two chunk sizes agree
+    h2, (C2, n2, m2) = xlstm_hip.mlstm_chunkwise(*xd, return_last_states=True, chunk_size=L, algo="two_pass")
+    h3, (C3, n3, m3) = xlstm_hip.mlstm_chunkwise(*xd, return_last_states=True, chunk_size=192 - L)
+    for a, b_, c in ((h, h2, h3), (C, C2, C3), (n, n2, n3), (m, m2, m3)):
+        assert maxabs(a, b_) <= LOWP_ABS and maxabs(a, c) <= LOWP_ABS

@@ -1,0 +1,115 @@
+"""sLSTM step/sequence and the arbitrary-length backend on the GPU vs the CPU oracle.
+
+sLSTM cases reuse the shapes and seeds of the reference's
+tests/test_slstm_metal_kernel.py:110-314 (2,4,8 / zero state / gates +-10 with
+states x100 / 5 chained steps) plus cfg4's sLSTM shape (B8 NH4 H512).
+"""
+
+import pytest
+import torch
+
+from helpers import FP32_REL, assert_parity, dev, relerr
+from oracle import mlstm as om
+from oracle import slstm as osl
+
+pytestmark = pytest.mark.gpu
+
+
+def _to(ts):
+    return [None if t is None else t.to(dev()) for t in ts]
+
+
+@pytest.mark.parametrize("case", ["random", "zero", "extreme_pos", "extreme_neg"])
+def test_slstm_step_cases(gpu_case, case):
+    import xlstm_hip
+    g = torch.Generator().manual_seed(42)
+    B, NH, H = 2, 4, 8
+    z = torch.randn(B, NH, H, generator=g)
+    i, f, o = (torch.randn(B, NH, generator=g) for _ in range(3))
+    c = torch.randn(B, NH, H, generator=g)
+    n = torch.randn(B, NH, H, generator=g).abs()
+    m = torch.randn(B, NH, generator=g)
+    if case == "zero":
+        c, n, m = torch.zeros_like(c), torch.zeros_like(n), torch.zeros_like(m)
+    elif case.startswith("extreme"):
+        val = 10.0 if case.endswith("pos") else -10.0
+        i = f = o = torch.full((B, NH), val)
+        c, n = 100 * c, 100 * n
+    got = xlstm_hip.slstm_step(*_to((z, i, f, o, c, n, m)))
+    want = osl.slstm_step(z, i, f, o, c, n, m)
+    for a, b in zip(got, want):
+        assert relerr(a, b) <= FP32_REL
+
+
+def test_slstm_cell_five_steps(gpu_case):
+    import xlstm_hip
+    g = torch.Generator().manual_seed(5)
+    B, NH, H, S = 2, 4, 8, 5
+    z = torch.randn(B, S, NH, H, generator=g)
+    i, f, o = (torch.randn(B, S, NH, generator=g) for _ in range(3))
+    cell = xlstm_hip.sLSTMStepwiseKernelCell(NH, H)
+    state = None
+    hs = []
+    zd, idv, fd, od = _to((z, i, f, o))
+    for t in range(S):
+        h, state = cell(zd[:, t], idv[:, t], fd[:, t], od[:, t], state)
+        hs.append(h)
+    hr, (cr, nr, mr) = osl.slstm_sequence(z, i, f, o)
+    assert relerr(torch.stack(hs, 1), hr) <= FP32_REL
+    for a, b in zip(state, (cr, nr, mr)):
+        assert relerr(a, b) <= FP32_REL
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 7, 4, 8), (8, 256, 4, 512), (1, 33, 3, 100)])
+def test_slstm_sequence(gpu_case, dtype, shape):
+    import xlstm_hip
+    B, S, NH, H = shape
+    g = torch.Generator().manual_seed(S)
+    z = torch.randn(B, S, NH, H, generator=g).to(dtype)
+    i, f, o = ((15 * torch.tanh(torch.randn(B, S, NH, generator=g) / 15)).to(dtype) for _ in range(3))
+    st = (torch.randn(B, NH, H, generator=g), torch.randn(B, NH, H, generator=g).abs(), torch.randn(B, NH, generator=g))
+    h, (c, n, m) = xlstm_hip.slstm_sequence(*_to((z, i, f, o)), state=tuple(_to(st)))
+    hr, (cr, nr, mr) = osl.slstm_sequence(z.float(), i.float(), f.float(), o.float(), state=st)
+    for a, b, name in ((h, hr, "h"), (c, cr, "c"), (n, nr, "n"), (m, mr, "m")):
+        if dtype == torch.float32:
+            assert relerr(a, b) <= FP32_REL, name
+        else:  # h is stored in fp32 here (states are fp32), inputs were bf16
+            assert relerr(a, b) <= 1e-4, name
+
+
+@pytest.mark.parametrize("S", [1, 5, 16, 37, 100, 129, 200])
+def test_arbitrary_length_inference(gpu_case, S):
+    import xlstm_hip
+    B, NH, DQK, DV = 1, 2, 64, 64
+    g = torch.Generator().manual_seed(S)
+    q, k = (torch.randn(B, NH, S, DQK, generator=g) for _ in range(2))
+    v = torch.randn(B, NH, S, DV, generator=g)
+    i = torch.randn(B, NH, S, generator=g)
+    f = torch.randn(B, NH, S, generator=g) + 3
+    backend = xlstm_hip.mLSTMBackend(xlstm_hip.mLSTMBackendConfig(mode="inference", chunk_size=64))
+    h, (C, n, m) = backend(*_to((q, k, v, i, f)))
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, chunk_size=64)
+    for a, b, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert relerr(a, b) <= FP32_REL, f"S={S} {name}"
+
+
+def test_backend_train_modes(gpu_case):
+    import xlstm_hip
+    B, NH, S, D = 1, 2, 100, 32
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, NH, S, D, generator=g) for _ in range(3))
+    i = torch.randn(B, NH, S, generator=g)
+    f = torch.randn(B, NH, S, generator=g) + 3
+    pad = xlstm_hip.mLSTMBackend(xlstm_hip.mLSTMBackendConfig(mode="train_with_padding", return_last_states=False))
+    h = pad(*_to((q, k, v, i, f)))
+    Sp = 128
+    padded = [torch.nn.functional.pad(t, (0, 0, 0, Sp - S)) for t in (q, k, v)] + \
+             [torch.nn.functional.pad(t, (0, Sp - S)) for t in (i, f)]
+    hr = om.mlstm_chunkwise(*padded)[:, :, :S]
+    assert relerr(h, hr) <= FP32_REL
+    train = xlstm_hip.mLSTMBackend(xlstm_hip.mLSTMBackendConfig(mode="train", chunk_size=64))
+    x = [t[:, :, :64] for t in (q, k, v)] + [t[:, :, :64] for t in (i, f)]
+    h, (C, n, m) = train(*_to(x))
+    hr, (Cr, nr, mr) = om.mlstm_chunkwise(*x, return_last_states=True)
+    assert relerr(h, hr) <= FP32_REL and relerr(C, Cr) <= FP32_REL

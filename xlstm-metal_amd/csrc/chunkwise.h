@@ -1,0 +1,30 @@
+// Internal interface between the chunkwise C-ABI entry point and its kernels.
+#pragma once
+
+#include "common.h"
+
+namespace xl {
+
+struct ChunkwiseArgs {
+  const void *q, *k, *v, *i, *f;
+  const float *c0, *n0, *m0;
+  void* h;
+  float *c_last, *n_last, *m_last;
+  int B, NH, S, DQK, DV, L;
+  float qk_scale, eps;
+  int dtype_qkv, dtype_gates;
+  void* workspace;
+  size_t workspace_bytes;
+  void* stream;
+};
+
+// Two-pass algorithm (states pass + output pass), float32 arithmetic.
+size_t chunkwise_two_pass_workspace(int B, int NH, int S, int DQK, int DV, int L);
+int chunkwise_two_pass(const ChunkwiseArgs& a);
+
+// Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a
+// shape/dtype is covered (and why not, in `why`, when it is not).
+bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why);
+int chunkwise_fused(const ChunkwiseArgs& a);
+
+}  // namespace xl

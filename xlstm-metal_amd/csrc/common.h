@@ -1,0 +1,90 @@
+// Shared device helpers and host-side error plumbing for libxlstm_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "xlstm_hip.h"
+
+namespace xl {
+
+// ---------------------------------------------------------------- host errors
+// Records the message for xl_last_error() (thread local) and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// Maps a HIP launch status to XL_OK / XL_ERR_LAUNCH (recording the message).
+int check_launch(const char* what);
+
+inline bool dtype_ok(int dt) { return dt == XL_DTYPE_F32 || dt == XL_DTYPE_BF16 || dt == XL_DTYPE_F16; }
+inline int dtype_size(int dt) { return dt == XL_DTYPE_F32 ? 4 : 2; }
+
+// ------------------------------------------------------------- element types
+// Storage types: float, bf16 (raw uint16 bits) and f16 (_Float16).
+struct bf16_t { uint16_t bits; };
+typedef _Float16 f16_t;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float(((uint32_t)x.bits) << 16); }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+
+// float -> bf16 bits, round to nearest even (quiet NaN preserved).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { bf16_t r; r.bits = f32_to_bf16_bits(x); return r; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return (f16_t)x; }
+
+// Rounds a float to the precision of T (identity for float).
+template <typename T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
+
+template <typename T> struct is_f32 { static constexpr bool value = false; };
+template <> struct is_f32<float> { static constexpr bool value = true; };
+
+// ----------------------------------------------------------------- gate math
+// log(sigmoid(x)) = min(x, 0) - log1p(exp(-|x|)), accurate for all x.
+__device__ __forceinline__ float logsigmoid(float x) {
+  return fminf(x, 0.0f) - log1pf(expf(-fabsf(x)));
+}
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// tanh from its Taylor series near 0 and (1 - e)/(1 + e), e = exp(-2|x|),
+// elsewhere.  |x| < 0.3: terms through x^11 (next term < 3e-10 relative);
+// otherwise 1 - e >= 0.45 so the quotient has no cancellation.
+__device__ __forceinline__ float tanh_f32(float x) {
+  float ax = fabsf(x);
+  if (ax < 0.3f) {
+    float x2 = x * x;
+    // x - x^3/3 + 2x^5/15 - 17x^7/315 + 62x^9/2835 - 1382x^11/155925
+    float p = -1382.0f / 155925.0f;
+    p = fmaf(p, x2, 62.0f / 2835.0f);
+    p = fmaf(p, x2, -17.0f / 315.0f);
+    p = fmaf(p, x2, 2.0f / 15.0f);
+    p = fmaf(p, x2, -1.0f / 3.0f);
+    return fmaf(x * x2, p, x);
+  }
+  float e = __expf(-2.0f * ax);
+  float t = (1.0f - e) / (1.0f + e);
+  return copysignf(t, x);
+}
+
+// ------------------------------------------------------- wavefront reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace xl

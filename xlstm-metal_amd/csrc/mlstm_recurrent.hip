@@ -1,0 +1,266 @@
+// Recurrent mLSTM: one decode step (xl_mlstm_step_fwd) and a whole sequence
+// in one launch (xl_mlstm_sequence_fwd).
+//
+// Reference math (kernel_development/xlstm/mlstm_block/mlstm_recurrent/
+// recurrent/native_step.py:69-101), per (b, h) and step t:
+//   m' = max(logsig(f) + m, i);  fa = exp(logsig(f) + m - m');  ia = exp(i - m')
+//   C' = fa C + ia k v^T;        n' = fa n + ia k
+//   h  = (q s)^T C' / (max(|(q s) . n'|, exp(-m')) + eps),   s = qk_scale
+// With a 16-bit q the reference rounds q s, k v^T, and the two products
+// (q s)^T C'.to(q.dtype) and (q s) . n'.to(q.dtype) to q's dtype
+// (native_step.py:78-96); the kernel reproduces those roundings.
+//
+// Layout: one workgroup per (b*NH + h, 64-column tile of DV); 256 threads as
+// 16 column groups (4 consecutive floats each, one 16-byte access) x 16 row
+// groups.  A thread owns rows d = ty + 16 r of its 4 columns, so C' lives in
+// registers for the whole sequence and every C byte crosses HBM once per
+// launch (read at the start, written at the end).  A wave touches 4 rows x
+// 256 contiguous bytes per access.  The column partials of (q s)^T C' are
+// reduced across the 16 row groups through LDS.  n' is recomputed by every
+// tile of a head (DQK values, L2 resident) and written by tile 0 only.
+#include "common.h"
+
+namespace xl {
+
+constexpr int REC_THREADS = 256;
+constexpr int REC_COLS = 64;       // DV columns per workgroup
+constexpr int REC_MAX_DQK = 512;   // rows per thread RPT = DQK / 16 <= 32
+
+template <typename TQ, typename TG, int RPT>
+__global__ __launch_bounds__(REC_THREADS) void mlstm_recurrent_kernel(
+    const TQ* __restrict__ q, const TQ* __restrict__ k, const TQ* __restrict__ v,
+    const TG* __restrict__ ig, const TG* __restrict__ fg,
+    const float* c_old, const float* __restrict__ n_old, const float* __restrict__ m_old,
+    TQ* __restrict__ h, float* c_new, float* __restrict__ n_new, float* __restrict__ m_new,
+    int S, int DQK, int DV, int ntile, float qk_scale, float eps) {
+  constexpr bool LOWP = !is_f32<TQ>::value;
+  __shared__ float s_q[REC_MAX_DQK];
+  __shared__ float s_k[REC_MAX_DQK];
+  __shared__ float s_red[16][REC_COLS + 4];
+  __shared__ float s_wsum[REC_THREADS / 64];
+
+  const int bh = blockIdx.x / ntile;
+  const int tile = blockIdx.x - bh * ntile;
+  const int tid = threadIdx.x;
+  const int tx = tid & 15, ty = tid >> 4;
+  const int col0 = tile * REC_COLS + tx * 4;
+  const bool col_ok = col0 < DV;  // DV % 4 == 0, so a group is all in or all out
+
+  // ---- load the state: C rows of this thread, n entries of this thread, m
+  float4 C[RPT];
+  const size_t cbase = (size_t)bh * DQK * DV;
+  if (c_old) {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int d = ty + 16 * r;
+      C[r] = (col_ok && d < DQK) ? *reinterpret_cast<const float4*>(c_old + cbase + (size_t)d * DV + col0)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) C[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  constexpr int NPT = REC_MAX_DQK / REC_THREADS;  // n entries per thread (d = tid + 256 j)
+  float nst[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int d = tid + REC_THREADS * j;
+    nst[j] = (n_old && d < DQK) ? n_old[(size_t)bh * DQK + d] : 0.f;
+  }
+  float m = m_old ? m_old[bh] : 0.f;
+
+  for (int t = 0; t < S; ++t) {
+    const size_t tok = (size_t)bh * S + t;
+    // ---- gates (identical in every thread)
+    float lsf = round_to<TG>(logsigmoid(to_f32(fg[tok])));  // torch keeps logsigmoid in f's dtype
+    const float ipre = to_f32(ig[tok]);
+    const float mn = fmaxf(lsf + m, ipre);
+    const float fa = expf(lsf + m - mn);
+    const float ia = expf(ipre - mn);
+    m = mn;
+
+    // ---- stage q s and k; n' and the partial of (q s) . n'
+    const TQ* qp = q + tok * DQK;
+    const TQ* kp = k + tok * DQK;
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int d = tid + REC_THREADS * j;
+      if (d < DQK) {
+        float qs = to_f32(qp[d]) * qk_scale;
+        if (LOWP) qs = round_to<TQ>(qs);
+        const float kd = to_f32(kp[d]);
+        s_q[d] = qs;
+        s_k[d] = kd;
+        nst[j] = fa * nst[j] + ia * kd;
+        part += qs * (LOWP ? round_to<TQ>(nst[j]) : nst[j]);
+      }
+    }
+    part = wave_sum(part);
+    if ((tid & 63) == 0) s_wsum[tid >> 6] = part;
+    __syncthreads();  // s_q, s_k, s_wsum ready
+    float qn = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+    if (LOWP) qn = round_to<TQ>(qn);
+    const float den = fmaxf(fabsf(qn), expf(-mn)) + eps;
+
+    // ---- C' = fa C + ia k v^T in registers, column partials of (q s)^T C'
+    float vv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (col_ok) {
+      const TQ* vp = v + tok * DV + col0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vv[j] = to_f32(vp[j]);
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int d = ty + 16 * r;
+      if (d < DQK) {
+        const float kd = s_k[d], qd = s_q[d];
+        float kv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kv[j] = LOWP ? round_to<TQ>(kd * vv[j]) : kd * vv[j];
+        C[r].x = fa * C[r].x + ia * kv[0];
+        C[r].y = fa * C[r].y + ia * kv[1];
+        C[r].z = fa * C[r].z + ia * kv[2];
+        C[r].w = fa * C[r].w + ia * kv[3];
+        acc[0] += qd * (LOWP ? round_to<TQ>(C[r].x) : C[r].x);
+        acc[1] += qd * (LOWP ? round_to<TQ>(C[r].y) : C[r].y);
+        acc[2] += qd * (LOWP ? round_to<TQ>(C[r].z) : C[r].z);
+        acc[3] += qd * (LOWP ? round_to<TQ>(C[r].w) : C[r].w);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_red[ty][tx * 4 + j] = acc[j];
+    __syncthreads();  // s_red ready
+    if (tid < REC_COLS && tile * REC_COLS + tid < DV) {
+      float hn = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) hn += s_red[r][tid];
+      if (LOWP) hn = round_to<TQ>(hn);
+      h[tok * DV + tile * REC_COLS + tid] = from_f32<TQ>(hn / den);
+    }
+    __syncthreads();  // s_q / s_k / s_red free for the next step
+  }
+
+  // ---- write the state
+  if (c_new) {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int d = ty + 16 * r;
+      if (col_ok && d < DQK) *reinterpret_cast<float4*>(c_new + cbase + (size_t)d * DV + col0) = C[r];
+    }
+  }
+  if (tile == 0) {
+    if (n_new) {
+#pragma unroll
+      for (int j = 0; j < NPT; ++j) {
+        const int d = tid + REC_THREADS * j;
+        if (d < DQK) n_new[(size_t)bh * DQK + d] = nst[j];
+      }
+    }
+    if (m_new && tid == 0) m_new[bh] = m;
+  }
+}
+
+template <typename TQ, typename TG>
+static int launch_rec_t(const void* q, const void* k, const void* v, const void* i, const void* f,
+                        const float* c0, const float* n0, const float* m0, void* h, float* c1, float* n1,
+                        float* m1, int BNH, int S, int DQK, int DV, float qk_scale, float eps, hipStream_t s,
+                        const char* who) {
+  const int ntile = (DV + REC_COLS - 1) / REC_COLS;
+  const int rpt = (DQK + 15) / 16;
+  dim3 grid((unsigned)(BNH * ntile)), block(REC_THREADS);
+#define XL_REC_LAUNCH(R)                                                                                       \
+  hipLaunchKernelGGL((mlstm_recurrent_kernel<TQ, TG, R>), grid, block, 0, s, (const TQ*)q, (const TQ*)k,     \
+                     (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1, S, DQK, DV,      \
+                     ntile, qk_scale, eps)
+  if (rpt <= 4) XL_REC_LAUNCH(4);
+  else if (rpt <= 8) XL_REC_LAUNCH(8);
+  else if (rpt <= 16) XL_REC_LAUNCH(16);
+  else XL_REC_LAUNCH(32);
+#undef XL_REC_LAUNCH
+  return check_launch(who);
+}
+
+template <typename TQ>
+static int launch_rec_g(int dtg, const void* q, const void* k, const void* v, const void* i, const void* f,
+                        const float* c0, const float* n0, const float* m0, void* h, float* c1, float* n1,
+                        float* m1, int BNH, int S, int DQK, int DV, float qk_scale, float eps, hipStream_t s,
+                        const char* who) {
+  switch (dtg) {
+    case XL_DTYPE_F32:
+      return launch_rec_t<TQ, float>(q, k, v, i, f, c0, n0, m0, h, c1, n1, m1, BNH, S, DQK, DV, qk_scale, eps, s, who);
+    case XL_DTYPE_BF16:
+      return launch_rec_t<TQ, bf16_t>(q, k, v, i, f, c0, n0, m0, h, c1, n1, m1, BNH, S, DQK, DV, qk_scale, eps, s, who);
+    default:
+      return launch_rec_t<TQ, f16_t>(q, k, v, i, f, c0, n0, m0, h, c1, n1, m1, BNH, S, DQK, DV, qk_scale, eps, s, who);
+  }
+}
+
+static int launch_rec(int dtq, int dtg, const void* q, const void* k, const void* v, const void* i, const void* f,
+                      const float* c0, const float* n0, const float* m0, void* h, float* c1, float* n1, float* m1,
+                      int BNH, int S, int DQK, int DV, float qk_scale, float eps, hipStream_t s, const char* who) {
+  switch (dtq) {
+    case XL_DTYPE_F32:
+      return launch_rec_g<float>(dtg, q, k, v, i, f, c0, n0, m0, h, c1, n1, m1, BNH, S, DQK, DV, qk_scale, eps, s, who);
+    case XL_DTYPE_BF16:
+      return launch_rec_g<bf16_t>(dtg, q, k, v, i, f, c0, n0, m0, h, c1, n1, m1, BNH, S, DQK, DV, qk_scale, eps, s, who);
+    default:
+      return launch_rec_g<f16_t>(dtg, q, k, v, i, f, c0, n0, m0, h, c1, n1, m1, BNH, S, DQK, DV, qk_scale, eps, s, who);
+  }
+}
+
+static int check_rec_args(const char* who, int B, int NH, int S, int DQK, int DV, int dtq, int dtg) {
+  if (B <= 0 || NH <= 0 || S <= 0 || DQK <= 0 || DV <= 0)
+    return set_error(XL_ERR_INVALID_ARG, "%s: dimensions must be positive (B=%d NH=%d S=%d DQK=%d DV=%d)", who, B,
+                     NH, S, DQK, DV);
+  if ((long long)B * NH * ((DV + REC_COLS - 1) / REC_COLS) > 0x7fffffffLL)
+    return set_error(XL_ERR_INVALID_ARG, "%s: grid too large", who);
+  if (DV % 4 != 0) return set_error(XL_ERR_UNSUPPORTED, "%s: DV=%d must be a multiple of 4", who, DV);
+  if (DQK > REC_MAX_DQK) return set_error(XL_ERR_UNSUPPORTED, "%s: DQK=%d exceeds %d", who, DQK, REC_MAX_DQK);
+  if (!dtype_ok(dtq) || !dtype_ok(dtg)) return set_error(XL_ERR_INVALID_ARG, "%s: unknown dtype", who);
+  return XL_OK;
+}
+
+}  // namespace xl
+
+extern "C" int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                                 const float* c_old, const float* n_old, const float* m_old, void* h,
+                                 float* c_new, float* n_new, float* m_new, int B, int NH, int DQK, int DV,
+                                 float qk_scale, float eps, int dtype_qkv, int dtype_gates, void* stream) {
+  using namespace xl;
+  clear_error();
+  const char* who = "xl_mlstm_step_fwd";
+  int rc = check_rec_args(who, B, NH, 1, DQK, DV, dtype_qkv, dtype_gates);
+  if (rc) return rc;
+  if (!q || !k || !v || !i || !f || !c_old || !n_old || !m_old || !h || !c_new || !n_new || !m_new)
+    return set_error(XL_ERR_INVALID_ARG, "%s: null pointer", who);
+  if ((((uintptr_t)c_old) | ((uintptr_t)c_new)) & 15u)
+    return set_error(XL_ERR_INVALID_ARG, "%s: c_old / c_new must be 16-byte aligned", who);
+  if (n_new == n_old || m_new == m_old)
+    return set_error(XL_ERR_INVALID_ARG, "%s: n_new / m_new must not alias n_old / m_old", who);
+  return launch_rec(dtype_qkv, dtype_gates, q, k, v, i, f, c_old, n_old, m_old, h, c_new, n_new, m_new, B * NH, 1,
+                    DQK, DV, qk_scale, eps, (hipStream_t)stream, who);
+}
+
+extern "C" int xl_mlstm_sequence_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                                     const float* c0, const float* n0, const float* m0, void* h, float* c_last,
+                                     float* n_last, float* m_last, int B, int NH, int S, int DQK, int DV,
+                                     float qk_scale, float eps, int dtype_qkv, int dtype_gates, void* stream) {
+  using namespace xl;
+  clear_error();
+  const char* who = "xl_mlstm_sequence_fwd";
+  int rc = check_rec_args(who, B, NH, S, DQK, DV, dtype_qkv, dtype_gates);
+  if (rc) return rc;
+  if (!q || !k || !v || !i || !f || !h) return set_error(XL_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!((c0 && n0 && m0) || (!c0 && !n0 && !m0)))
+    return set_error(XL_ERR_INVALID_ARG, "%s: initial states must be given together", who);
+  if (!((c_last && n_last && m_last) || (!c_last && !n_last && !m_last)))
+    return set_error(XL_ERR_INVALID_ARG, "%s: last states must be requested together", who);
+  if ((((uintptr_t)c0) | ((uintptr_t)c_last)) & 15u)
+    return set_error(XL_ERR_INVALID_ARG, "%s: c0 / c_last must be 16-byte aligned", who);
+  if (n_last && (n_last == n0 || m_last == m0))
+    return set_error(XL_ERR_INVALID_ARG, "%s: n_last / m_last must not alias n0 / m0", who);
+  return launch_rec(dtype_qkv, dtype_gates, q, k, v, i, f, c0, n0, m0, h, c_last, n_last, m_last, B * NH, S, DQK, DV,
+                    qk_scale, eps, (hipStream_t)stream, who);
+}

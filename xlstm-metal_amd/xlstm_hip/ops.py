@@ -1,0 +1,323 @@
+"""``torch.library`` operators ``xlstm_hip::*`` backed by libxlstm_hip.so.
+
+Each op validates shapes and dtypes in Python, allocates its outputs with
+torch's caching allocator (the library itself never allocates), passes raw
+pointers and the current HIP stream through the C-ABI and returns without
+synchronising.  Fake (meta) implementations make the ops traceable.  There is
+no CPU path: CPU tensors raise.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+__all__ = [
+    "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
+    "slstm_step_op", "slstm_sequence_op", "chunkwise_workspace_bytes",
+]
+
+_EMPTY_SHAPE = (0,)
+
+
+def _prep(t: Tensor, align: int = 16) -> Tensor:
+    t = t.contiguous()
+    if t.data_ptr() % align:
+        t = t.clone()
+    return t
+
+
+def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
+    if t is None:
+        return None
+    return _prep(t if t.dtype == torch.float32 else t.to(torch.float32))
+
+
+def _check(cond: bool, what: str, msg: str) -> None:
+    if not cond:
+        raise ValueError(f"{what}: {msg}")
+
+
+# --------------------------------------------------------------------- soft_cap
+@torch.library.custom_op("xlstm_hip::soft_cap", mutates_args=())
+def soft_cap_op(x: Tensor, cap: float) -> Tensor:
+    _lib.require_gpu(x, what="soft_cap")
+    x = _prep(x)
+    y = torch.empty_like(x)
+    rc = _lib.load().xl_soft_cap_fwd(x.data_ptr(), y.data_ptr(), x.numel(), float(cap),
+                                      _lib.dtype_code(x, "soft_cap"), _lib.stream_of(x))
+    _lib.check(rc, "soft_cap")
+    return y
+
+
+@soft_cap_op.register_fake
+def _(x, cap):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+# ---------------------------------------------------------------- mLSTM step
+def _step_shapes(q, k, v, i, f, c, n, m, what):
+    _check(q.dim() == 3, what, f"q must be (B, NH, DHQK), got {tuple(q.shape)}")
+    B, NH, DQK = q.shape
+    DV = v.shape[-1]
+    _check(k.shape == q.shape, what, "q and k must have the same shape")
+    _check(v.dim() == 3 and v.shape[:2] == (B, NH), what, f"v must be (B, NH, DHV), got {tuple(v.shape)}")
+    _check(q.dtype == k.dtype == v.dtype, what, "q, k, v must share a dtype")
+    _check(c.shape == (B, NH, DQK, DV), what, f"matC_old has wrong shape, got {tuple(c.shape)}")
+    _check(n.shape == (B, NH, DQK), what, f"vecN_old has wrong shape, got {tuple(n.shape)}")
+    _check(m.numel() == B * NH, what, f"scaM_old has wrong shape, got {tuple(m.shape)}")
+    _check(i.numel() == B * NH, what, f"scaI has wrong shape, got {tuple(i.shape)}")
+    _check(f.numel() == B * NH, what, f"scaF has wrong shape, got {tuple(f.shape)}")
+    _check(i.dtype == f.dtype, what, "i and f must share a dtype")
+    return B, NH, DQK, DV
+
+
+def _launch_step(q, k, v, i, f, c, n, m, h, c_new, n_new, m_new, B, NH, DQK, DV, qk_scale, eps, what):
+    rc = _lib.load().xl_mlstm_step_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(),
+        c.data_ptr(), n.data_ptr(), m.data_ptr(), h.data_ptr(), c_new.data_ptr(), n_new.data_ptr(),
+        m_new.data_ptr(), B, NH, DQK, DV, float(qk_scale), float(eps),
+        _lib.dtype_code(q, what), _lib.dtype_code(i, what), _lib.stream_of(q))
+    _lib.check(rc, what)
+
+
+@torch.library.custom_op("xlstm_hip::mlstm_step", mutates_args=())
+def mlstm_step_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c: Tensor, n: Tensor, m: Tensor,
+                  eps: float, qk_scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    what = "mlstm_step"
+    _lib.require_gpu(q, k, v, i, f, c, n, m, what=what)
+    B, NH, DQK, DV = _step_shapes(q, k, v, i, f, c, n, m, what)
+    q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
+    c, n, m = _f32(c), _f32(n), _f32(m)
+    h = torch.empty((B, NH, DV), dtype=q.dtype, device=q.device)
+    c_new = torch.empty((B, NH, DQK, DV), dtype=torch.float32, device=q.device)
+    n_new = torch.empty((B, NH, DQK), dtype=torch.float32, device=q.device)
+    m_new = torch.empty((B, NH, 1), dtype=torch.float32, device=q.device)
+    _launch_step(q, k, v, i, f, c, n, m, h, c_new, n_new, m_new, B, NH, DQK, DV, qk_scale, eps, what)
+    return h, c_new, n_new, m_new
+
+
+@mlstm_step_op.register_fake
+def _(q, k, v, i, f, c, n, m, eps, qk_scale):
+    B, NH, DQK = q.shape
+    DV = v.shape[-1]
+    return (q.new_empty((B, NH, DV)), q.new_empty((B, NH, DQK, DV), dtype=torch.float32),
+            q.new_empty((B, NH, DQK), dtype=torch.float32), q.new_empty((B, NH, 1), dtype=torch.float32))
+
+
+@torch.library.custom_op("xlstm_hip::mlstm_step_", mutates_args=("c",))
+def mlstm_step_inplace_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c: Tensor, n: Tensor, m: Tensor,
+                          eps: float, qk_scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    """Decode step updating the float32 C state in place; returns (h, n', m')."""
+    what = "mlstm_step_"
+    _lib.require_gpu(q, k, v, i, f, c, n, m, what=what)
+    B, NH, DQK, DV = _step_shapes(q, k, v, i, f, c, n, m, what)
+    _check(c.dtype == torch.float32 and c.is_contiguous() and c.data_ptr() % 16 == 0, what,
+           "in-place C must be a contiguous, 16-byte aligned float32 tensor")
+    q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
+    n, m = _f32(n), _f32(m)
+    h = torch.empty((B, NH, DV), dtype=q.dtype, device=q.device)
+    n_new = torch.empty((B, NH, DQK), dtype=torch.float32, device=q.device)
+    m_new = torch.empty((B, NH, 1), dtype=torch.float32, device=q.device)
+    _launch_step(q, k, v, i, f, c, n, m, h, c, n_new, m_new, B, NH, DQK, DV, qk_scale, eps, what)
+    return h, n_new, m_new
+
+
+@mlstm_step_inplace_op.register_fake
+def _(q, k, v, i, f, c, n, m, eps, qk_scale):
+    B, NH, DQK = q.shape
+    DV = v.shape[-1]
+    return (q.new_empty((B, NH, DV)), q.new_empty((B, NH, DQK), dtype=torch.float32),
+            q.new_empty((B, NH, 1), dtype=torch.float32))
+
+
+# -------------------------------------------------------- chunkwise / sequence
+def _seq_shapes(q, k, v, i, f, c0, n0, m0, what):
+    _check(q.dim() == 4, what, f"q must be (B, NH, S, DHQK), got {tuple(q.shape)}")
+    B, NH, S, DQK = q.shape
+    _check(k.shape == q.shape, what, "q and k must have the same shape")
+    _check(v.dim() == 4 and v.shape[:3] == (B, NH, S), what, f"v must be (B, NH, S, DHV), got {tuple(v.shape)}")
+    DV = v.shape[-1]
+    _check(q.dtype == k.dtype == v.dtype, what, "q, k, v must share a dtype")
+    _check(i.shape == (B, NH, S) and f.shape == (B, NH, S), what, "i and f must be (B, NH, S)")
+    _check(i.dtype == f.dtype, what, "i and f must share a dtype")
+    given = [t is not None for t in (c0, n0, m0)]
+    _check(all(given) or not any(given), what, "Initial states must be provided together.")
+    if c0 is not None:
+        _check(c0.shape == (B, NH, DQK, DV), what, f"c_initial has wrong shape, got {tuple(c0.shape)}")
+        _check(n0.shape == (B, NH, DQK), what, f"n_initial has wrong shape, got {tuple(n0.shape)}")
+        _check(m0.numel() == B * NH, what, f"m_initial has wrong shape, got {tuple(m0.shape)}")
+    return B, NH, S, DQK, DV
+
+
+def chunkwise_workspace_bytes(B, NH, S, DQK, DV, L, dtype, algo="auto") -> int:
+    return int(_lib.load().xl_mlstm_chunkwise_workspace_size(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype],
+                                                             _lib.ALGO[algo]))
+
+
+def _state_outs(ret, B, NH, DQK, DV, dev):
+    if not ret:
+        e = torch.empty(_EMPTY_SHAPE, dtype=torch.float32, device=dev)
+        return e, e, e
+    return (torch.empty((B, NH, DQK, DV), dtype=torch.float32, device=dev),
+            torch.empty((B, NH, DQK), dtype=torch.float32, device=dev),
+            torch.empty((B, NH, 1), dtype=torch.float32, device=dev))
+
+
+@torch.library.custom_op("xlstm_hip::mlstm_chunkwise", mutates_args=())
+def mlstm_chunkwise_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c0: Optional[Tensor],
+                       n0: Optional[Tensor], m0: Optional[Tensor], qk_scale: float, chunk_size: int, eps: float,
+                       return_last_states: bool, algo: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    what = "mlstm_chunkwise"
+    _lib.require_gpu(q, k, v, i, f, c0, n0, m0, what=what)
+    B, NH, S, DQK, DV = _seq_shapes(q, k, v, i, f, c0, n0, m0, what)
+    if S % chunk_size != 0:
+        raise AssertionError(f"Sequence length {S} is not divisible by chunk size {chunk_size}.")
+    q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
+    c0, n0, m0 = _f32(c0), _f32(n0), _f32(m0)
+    h = torch.empty((B, NH, S, DV), dtype=q.dtype, device=q.device)
+    cl, nl, ml = _state_outs(return_last_states, B, NH, DQK, DV, q.device)
+    lib = _lib.load()
+    dq = _lib.dtype_code(q, what)
+    ws_bytes = int(lib.xl_mlstm_chunkwise_workspace_size(B, NH, S, DQK, DV, chunk_size, dq, int(algo)))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device) if ws_bytes else None
+    rc = lib.xl_mlstm_chunkwise_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(),
+        _lib.ptr(c0), _lib.ptr(n0), _lib.ptr(m0), h.data_ptr(),
+        cl.data_ptr() if return_last_states else None, nl.data_ptr() if return_last_states else None,
+        ml.data_ptr() if return_last_states else None,
+        B, NH, S, DQK, DV, int(chunk_size), float(qk_scale), float(eps), dq, _lib.dtype_code(i, what), int(algo),
+        _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+    _lib.check(rc, what)
+    return h, cl, nl, ml
+
+
+@mlstm_chunkwise_op.register_fake
+def _(q, k, v, i, f, c0, n0, m0, qk_scale, chunk_size, eps, return_last_states, algo):
+    B, NH, S, DQK = q.shape
+    DV = v.shape[-1]
+    h = q.new_empty((B, NH, S, DV))
+    if not return_last_states:
+        e = q.new_empty(_EMPTY_SHAPE, dtype=torch.float32)
+        return h, e, e, e
+    return (h, q.new_empty((B, NH, DQK, DV), dtype=torch.float32), q.new_empty((B, NH, DQK), dtype=torch.float32),
+            q.new_empty((B, NH, 1), dtype=torch.float32))
+
+
+@torch.library.custom_op("xlstm_hip::mlstm_sequence", mutates_args=())
+def mlstm_sequence_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c0: Optional[Tensor],
+                      n0: Optional[Tensor], m0: Optional[Tensor], qk_scale: float, eps: float,
+                      return_last_states: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    what = "mlstm_sequence"
+    _lib.require_gpu(q, k, v, i, f, c0, n0, m0, what=what)
+    B, NH, S, DQK, DV = _seq_shapes(q, k, v, i, f, c0, n0, m0, what)
+    q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
+    c0, n0, m0 = _f32(c0), _f32(n0), _f32(m0)
+    h = torch.empty((B, NH, S, DV), dtype=q.dtype, device=q.device)
+    cl, nl, ml = _state_outs(return_last_states, B, NH, DQK, DV, q.device)
+    rc = _lib.load().xl_mlstm_sequence_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(),
+        _lib.ptr(c0), _lib.ptr(n0), _lib.ptr(m0), h.data_ptr(),
+        cl.data_ptr() if return_last_states else None, nl.data_ptr() if return_last_states else None,
+        ml.data_ptr() if return_last_states else None,
+        B, NH, S, DQK, DV, float(qk_scale), float(eps), _lib.dtype_code(q, what), _lib.dtype_code(i, what),
+        _lib.stream_of(q))
+    _lib.check(rc, what)
+    return h, cl, nl, ml
+
+
+@mlstm_sequence_op.register_fake
+def _(q, k, v, i, f, c0, n0, m0, qk_scale, eps, return_last_states):
+    B, NH, S, DQK = q.shape
+    DV = v.shape[-1]
+    h = q.new_empty((B, NH, S, DV))
+    if not return_last_states:
+        e = q.new_empty(_EMPTY_SHAPE, dtype=torch.float32)
+        return h, e, e, e
+    return (h, q.new_empty((B, NH, DQK, DV), dtype=torch.float32), q.new_empty((B, NH, DQK), dtype=torch.float32),
+            q.new_empty((B, NH, 1), dtype=torch.float32))
+
+
+# ------------------------------------------------------------------- sLSTM
+def _slstm_out_dtype(z, i, c):
+    return torch.promote_types(torch.promote_types(z.dtype, i.dtype), c.dtype)
+
+
+@torch.library.custom_op("xlstm_hip::slstm_step", mutates_args=())
+def slstm_step_op(z: Tensor, i: Tensor, f: Tensor, o: Tensor, c: Tensor, n: Tensor, m: Tensor,
+                  eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    what = "slstm_step"
+    _lib.require_gpu(z, i, f, o, c, n, m, what=what)
+    _check(z.dim() == 3, what, f"z must be (B, NH, H), got {tuple(z.shape)}")
+    B, NH, H = z.shape
+    for name, t in (("i_preact", i), ("f_preact", f), ("o_preact", o), ("m_state", m)):
+        _check(t.shape == (B, NH), what, f"{name} must be (B, NH), got {tuple(t.shape)}")
+    _check(c.shape == (B, NH, H) and n.shape == (B, NH, H), what, "c_state and n_state must be (B, NH, H)")
+    _check(i.dtype == f.dtype == o.dtype, what, "gates must share a dtype")
+    out_dt = _slstm_out_dtype(z, i, c)
+    z, i, f, o = (_prep(t) for t in (z, i, f, o))
+    c, n, m = _f32(c), _f32(n), _f32(m)
+    h = torch.empty((B, NH, H), dtype=out_dt, device=z.device)
+    c_new = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
+    n_new = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
+    m_new = torch.empty((B, NH), dtype=torch.float32, device=z.device)
+    rc = _lib.load().xl_slstm_step_fwd(
+        z.data_ptr(), i.data_ptr(), f.data_ptr(), o.data_ptr(), c.data_ptr(), n.data_ptr(), m.data_ptr(),
+        h.data_ptr(), c_new.data_ptr(), n_new.data_ptr(), m_new.data_ptr(), B, NH, H, float(eps),
+        _lib.dtype_code(z, what), _lib.dtype_code(i, what), _lib.dtype_code(h, what), _lib.stream_of(z))
+    _lib.check(rc, what)
+    if out_dt != torch.float32:
+        return h, c_new.to(out_dt), n_new.to(out_dt), m_new.to(out_dt)
+    return h, c_new, n_new, m_new
+
+
+@slstm_step_op.register_fake
+def _(z, i, f, o, c, n, m, eps):
+    out_dt = _slstm_out_dtype(z, i, c)
+    B, NH, H = z.shape
+    return (z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((B, NH, H), dtype=out_dt),
+            z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((B, NH), dtype=out_dt))
+
+
+@torch.library.custom_op("xlstm_hip::slstm_sequence", mutates_args=())
+def slstm_sequence_op(z: Tensor, i: Tensor, f: Tensor, o: Tensor, c0: Optional[Tensor], n0: Optional[Tensor],
+                      m0: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    what = "slstm_sequence"
+    _lib.require_gpu(z, i, f, o, c0, n0, m0, what=what)
+    _check(z.dim() == 4, what, f"z must be (B, S, NH, H), got {tuple(z.shape)}")
+    B, S, NH, H = z.shape
+    for name, t in (("i_preact", i), ("f_preact", f), ("o_preact", o)):
+        _check(t.shape == (B, S, NH), what, f"{name} must be (B, S, NH), got {tuple(t.shape)}")
+    _check(i.dtype == f.dtype == o.dtype, what, "gates must share a dtype")
+    given = [t is not None for t in (c0, n0, m0)]
+    _check(all(given) or not any(given), what, "initial states must be provided together")
+    if c0 is not None:
+        _check(c0.shape == (B, NH, H) and n0.shape == (B, NH, H) and m0.shape == (B, NH), what,
+               "state must be c, n (B, NH, H) and m (B, NH)")
+    out_dt = torch.promote_types(z.dtype, i.dtype) if c0 is None else _slstm_out_dtype(z, i, c0)
+    z, i, f, o = (_prep(t) for t in (z, i, f, o))
+    c0, n0, m0 = _f32(c0), _f32(n0), _f32(m0)
+    h = torch.empty((B, S, NH, H), dtype=out_dt, device=z.device)
+    cl = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
+    nl = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
+    ml = torch.empty((B, NH), dtype=torch.float32, device=z.device)
+    rc = _lib.load().xl_slstm_seq_fwd(
+        z.data_ptr(), i.data_ptr(), f.data_ptr(), o.data_ptr(), _lib.ptr(c0), _lib.ptr(n0), _lib.ptr(m0),
+        h.data_ptr(), cl.data_ptr(), nl.data_ptr(), ml.data_ptr(), B, S, NH, H, float(eps),
+        _lib.dtype_code(z, what), _lib.dtype_code(i, what), _lib.dtype_code(h, what), _lib.stream_of(z))
+    _lib.check(rc, what)
+    if out_dt != torch.float32:
+        return h, cl.to(out_dt), nl.to(out_dt), ml.to(out_dt)
+    return h, cl, nl, ml
+
+
+@slstm_sequence_op.register_fake
+def _(z, i, f, o, c0, n0, m0, eps):
+    B, S, NH, H = z.shape
+    out_dt = torch.promote_types(z.dtype, i.dtype) if c0 is None else _slstm_out_dtype(z, i, c0)
+    return (z.new_empty((B, S, NH, H), dtype=out_dt), z.new_empty((B, NH, H), dtype=out_dt),
+            z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((B, NH), dtype=out_dt))
