@@ -7,6 +7,11 @@ import torch
 #                  the tensor (so tiny elements do not dominate);
 #  bf16/f16 inputs: max-abs error <= 2e-2 on h and on the final C, n, m,
 #                  against the float32 oracle run on the 16-bit inputs upcast.
+#                  h itself is returned in the 16-bit dtype, and rounding the
+#                  exact h to bf16 already costs up to half an ulp of |h|
+#                  (0.030 at cfg2, where |h| reaches 11.4), so for a 16-bit
+#                  output the 2e-2 applies on top of that half ulp:
+#                  |a - b| <= 2e-2 + ulp(b)/2 elementwise (lowp_excess <= 2e-2).
 FP32_REL = 1e-4
 LOWP_ABS = 2e-2
 
@@ -21,14 +26,29 @@ def maxabs(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a.detach().double().cpu() - b.detach().double().cpu()).abs().max())
 
 
+def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:
+    """Half a unit in the last place of |x| in the 16-bit `dtype` (0 for float32)."""
+    if dtype == torch.float32:
+        return torch.zeros_like(x, dtype=torch.float64)
+    mant = 7 if dtype == torch.bfloat16 else 10
+    ax = x.detach().double().cpu().abs().clamp_min(1e-30)
+    return torch.exp2(torch.floor(torch.log2(ax)) - mant - 1)
+
+
+def lowp_excess(got: torch.Tensor, want: torch.Tensor) -> float:
+    """max(|got - want| - ulp(want)/2) with ulp in got's dtype: the error beyond output rounding."""
+    d = (got.detach().double().cpu() - want.detach().double().cpu()).abs()
+    return float((d - half_ulp(want, got.dtype)).max())
+
+
 def assert_parity(got, want, dtype, what=""):
-    """fp32: relerr <= FP32_REL; 16-bit: maxabs <= LOWP_ABS."""
+    """fp32: relerr <= FP32_REL; 16-bit inputs: max-abs <= LOWP_ABS beyond the output's own rounding."""
     if dtype == torch.float32:
         e = relerr(got, want)
         assert e <= FP32_REL, f"{what}: rel-err {e:.3e} > {FP32_REL}"
     else:
-        e = maxabs(got, want)
-        assert e <= LOWP_ABS, f"{what}: max-abs {e:.3e} > {LOWP_ABS}"
+        e = lowp_excess(got, want)
+        assert e <= LOWP_ABS, f"{what}: max-abs {e:.3e} beyond output rounding > {LOWP_ABS}"
     return e
 
 

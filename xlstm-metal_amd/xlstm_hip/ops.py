@@ -160,9 +160,8 @@ def chunkwise_workspace_bytes(B, NH, S, DQK, DV, L, dtype, algo="auto") -> int:
 
 
 def _state_outs(ret, B, NH, DQK, DV, dev):
-    if not ret:
-        e = torch.empty(_EMPTY_SHAPE, dtype=torch.float32, device=dev)
-        return e, e, e
+    if not ret:  # three distinct empties: custom-op outputs may not alias each other
+        return tuple(torch.empty(_EMPTY_SHAPE, dtype=torch.float32, device=dev) for _ in range(3))
     return (torch.empty((B, NH, DQK, DV), dtype=torch.float32, device=dev),
             torch.empty((B, NH, DQK), dtype=torch.float32, device=dev),
             torch.empty((B, NH, 1), dtype=torch.float32, device=dev))
@@ -202,8 +201,7 @@ def _(q, k, v, i, f, c0, n0, m0, qk_scale, chunk_size, eps, return_last_states, 
     DV = v.shape[-1]
     h = q.new_empty((B, NH, S, DV))
     if not return_last_states:
-        e = q.new_empty(_EMPTY_SHAPE, dtype=torch.float32)
-        return h, e, e, e
+        return (h,) + tuple(q.new_empty(_EMPTY_SHAPE, dtype=torch.float32) for _ in range(3))
     return (h, q.new_empty((B, NH, DQK, DV), dtype=torch.float32), q.new_empty((B, NH, DQK), dtype=torch.float32),
             q.new_empty((B, NH, 1), dtype=torch.float32))
 
@@ -236,8 +234,7 @@ def _(q, k, v, i, f, c0, n0, m0, qk_scale, eps, return_last_states):
     DV = v.shape[-1]
     h = q.new_empty((B, NH, S, DV))
     if not return_last_states:
-        e = q.new_empty(_EMPTY_SHAPE, dtype=torch.float32)
-        return h, e, e, e
+        return (h,) + tuple(q.new_empty(_EMPTY_SHAPE, dtype=torch.float32) for _ in range(3))
     return (h, q.new_empty((B, NH, DQK, DV), dtype=torch.float32), q.new_empty((B, NH, DQK), dtype=torch.float32),
             q.new_empty((B, NH, 1), dtype=torch.float32))
 
