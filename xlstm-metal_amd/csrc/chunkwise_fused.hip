@@ -16,26 +16,29 @@
 //   h_i = H_i / (max(|den_i|, exp(-m_i)) + eps)
 //   C' = exp(g + m - m') C + sum_t exp(a_t - m') k_t v_t^T,  n' likewise
 //
+// The normaliser rides along as a fifth 16-column tile: C carries n in its
+// column 64, V carries a row of ones (for sum_j M_ij) and alpha V carries
+// alpha_t (for sum_t alpha_t k_t), so n', q.n and the row sums are produced by
+// the same MFMAs as C', q C and M V, and den_i lands in column 64 of H_i.
+//
 // Work split (4 waves, 256 threads): wave w owns rows [w*DW, (w+1)*DW) of C
-// (DW = DQK/4) and computes, for its slice of the DQK contraction, partial
-// S^T = K Q^T, partial QC, the gated partial M and M V, and its slice of the
-// state update.  The partial H's of the four waves are summed through LDS
-// once per chunk (each wave owns 16 output rows).  All dense products are
-// v_mfma_f32_16x16x32_bf16 with float32 accumulation:
-//   S^T  (j x i, over d)   A = K rows  (LDS),      B = q rows (registers)
-//   QC   (i x v, over d)   A = q rows  (registers), B = C (accumulators -> bf16)
-//   MV   (i x v, over j)   A = M hi + lo (S^T accumulators -> bf16), B = V^T (LDS)
-//   KV   (d x v, over t)   A = Kbar^T hi + lo (LDS), B = V^T (LDS)
+// (DW = DQK/4).  Per chunk each wave computes, over its slice of the DQK
+// contraction, a partial S^T = K Q^T and a partial Q [C | n]; the S partials
+// are summed through LDS so that wave w gates the exact scores of its own 16
+// output rows and multiplies them with V; the Q [C | n] partials are summed
+// through LDS the same way before the output rows are finished.  All dense
+// products are v_mfma_f32_16x16x32_bf16 with float32 accumulation:
+//   S^T  (j x i, over d)   A = K rows (LDS),        B = q rows (registers)
+//   QC   (i x v, over d)   A = q rows (registers),  B = [C | n] (accumulators -> bf16)
+//   MV   (i x v, over j)   A = M hi + lo,           B = [V | 1]^T (LDS)
+//   KV   (d x v, over t)   A = K^T (LDS),           B = (alpha [V | 1])^T hi + lo (LDS)
 // Operands coming from accumulators use a row permutation: the 16 rows of an
 // MFMA tile are mapped to physical indices so that the 4 rows a lane holds in
 // two adjacent tiles are 8 consecutive indices, i.e. exactly the 8-element
 // k-slice that lane must supply when the accumulator is reused as an operand.
-// Kbar = alpha_t k_t is split into bf16 hi + lo parts (two MFMAs) so the
-// float32 state does not inherit bf16 rounding of the gated keys.  The gated
-// scores are split the same way: each wave holds only a partial M (its slice
-// of the q.k contraction), and partials can be much larger than their sum, so
-// rounding them to bf16 alone would lose the sum.  C is rounded to bf16 only
-// as the operand of the q C product.
+// alpha_t v_t and the gated scores are split into bf16 hi + lo parts (two
+// MFMAs) so the float32 state and the outputs do not inherit bf16 rounding of
+// those products; [C | n] is rounded to bf16 only as the operand of Q [C | n].
 //
 // Grid mapping is XCD aware: the DV tiles of one head land on the same XCD so
 // the head's q/k chunks are fetched from HBM once and then hit that XCD's L2.
@@ -55,9 +58,12 @@ constexpr int L = 64;          // chunk size (= wavefront size: one lane per tok
 constexpr int NW = 4;          // waves per workgroup
 constexpr int NTHREADS = NW * 64;
 constexpr int DVT = 64;        // DV columns per workgroup
-constexpr int NVT = DVT / 16;  // 16-wide column tiles
+constexpr int NVT = DVT / 16;  // 16-wide column tiles of v
+constexpr int NVX = NVT + 1;   // ... plus the n / ones / den tile
 constexpr int PITCH = 72;      // bf16 per LDS row (144 B): 16 consecutive rows hit distinct banks
+constexpr int NST = 12;        // causal S^T tiles (jt, it) with jt/2 <= it/2
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -72,7 +78,40 @@ __device__ __forceinline__ bf16x8 pack8(f32x4 a, f32x4 b) {
   u32x4 r = {pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
   return __builtin_bit_cast(bf16x8, r);
 }
-__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
+// bf16 hi + lo split of 8 floats: hi = bf16(x), lo = bf16(x - hi)
+__device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+  const u32x4 h = {pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
+  const u32x4 l = {pack_bf16(a[0] - bf_lo(h[0]), a[1] - bf_hi(h[0])), pack_bf16(a[2] - bf_lo(h[1]), a[3] - bf_hi(h[1])),
+                   pack_bf16(b[0] - bf_lo(h[2]), b[1] - bf_hi(h[2])), pack_bf16(b[2] - bf_lo(h[3]), b[3] - bf_hi(h[3]))};
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
+__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+// log(sigmoid(x)) = min(x, 0) - log(1 + exp(-|x|)) via the hardware exp2/log2;
+// absolute error < 1e-7.
+__device__ __forceinline__ float logsig_fast(float x) {
+  return fminf(x, 0.f) - LN2 * __builtin_amdgcn_logf(1.0f + exp2_(-fabsf(x) * LOG2E));
+}
+
+// Inclusive wave64 scans with DPP (row shifts, then row broadcasts).
+template <bool MAX>
+__device__ __forceinline__ float wave_scan(float x) {
+  const float ident = MAX ? -INFINITY : 0.f;
+  const int iid = __float_as_int(ident);
+#define XL_SCAN_STEP(CTRL, ROWMASK)                                                                     \
+  {                                                                                                     \
+    const float y = __int_as_float(__builtin_amdgcn_update_dpp(iid, __float_as_int(x), CTRL, ROWMASK, 0xf, false)); \
+    x = MAX ? fmaxf(x, y) : x + y;                                                                      \
+  }
+  XL_SCAN_STEP(0x111, 0xf)  // row_shr:1
+  XL_SCAN_STEP(0x112, 0xf)  // row_shr:2
+  XL_SCAN_STEP(0x114, 0xf)  // row_shr:4
+  XL_SCAN_STEP(0x118, 0xf)  // row_shr:8
+  XL_SCAN_STEP(0x142, 0xa)  // row_bcast:15 into rows 1, 3
+  XL_SCAN_STEP(0x143, 0xc)  // row_bcast:31 into rows 2, 3
+#undef XL_SCAN_STEP
+  return x;
+}
 
 // LDS row of physical index x within a 64-row block: tiles of 16 rows, each
 // tile pair (32 indices) interleaved so that lane group g of a tile pair
@@ -82,19 +121,26 @@ __device__ __forceinline__ int lds_row(int x) {
 }
 // physical index held by accumulator element e of lane group g in tile `tile`
 __device__ __forceinline__ int phys(int tile, int g, int e) { return 32 * (tile >> 1) + 8 * g + 4 * (tile & 1) + e; }
+// slot of causal S^T tile (jt, it), jt/2 <= it/2
+__device__ __forceinline__ constexpr int st_slot(int it, int jt) { return it < 2 ? 2 * it + jt : 4 + 4 * (it - 2) + jt; }
 
 template <int DQK>
 struct Smem {
-  static constexpr int DW = DQK / NW;              // C rows per wave
-  static constexpr int KN_SLOT = NVT * (NW - 1) * 64 * 16;  // per-wave region: max(K natural, H partials)
-  static_assert(64 * PITCH * 2 <= KN_SLOT, "K tile must fit the per-wave slot");
-  static constexpr int R1 = 0;                                 // [NW][KN_SLOT]: K natural / H partials
-  static constexpr int KTH = R1 + NW * KN_SLOT;               // [NW][DW][PITCH] bf16: (alpha k)^T hi
-  static constexpr int KTL = KTH + NW * DW * PITCH * 2;        // lo
-  static constexpr int VT = KTL + NW * DW * PITCH * 2;         // [64 v][PITCH] bf16: V^T
-  static constexpr int QN = VT + DVT * PITCH * 2;              // [NW][64] float: partial q.n
-  static constexpr int RS = QN + NW * 64 * 4;                  // [NW][64] float: partial row sums of M
-  static constexpr int BYTES = RS + NW * 64 * 4;
+  static constexpr int DW = DQK / NW;                          // C rows per wave
+  static constexpr int KN_SLOT = NST * 64 * 16;                 // per wave: K natural tile, then its S^T partials
+  static_assert(64 * PITCH * 2 <= KN_SLOT, "K tile must fit its slot");
+  static constexpr int KT_SLOT = DW * PITCH * 2;                // per wave: K^T tile
+  static constexpr int VTILE = 80 * PITCH * 2;                  // [80][PITCH] bf16
+  static constexpr int HRED_BYTES = NW * 3 * NVX * 64 * 16;     // [NW][3][NVX][64] f32x4
+  static constexpr int KN = 0;                                  // [NW][KN_SLOT]
+  static constexpr int KT = KN + NW * KN_SLOT;                  // [NW][KT_SLOT]
+  static constexpr int VBH = KT + NW * KT_SLOT;                 // (alpha [V | 1])^T hi
+  static constexpr int VBL = VBH + VTILE;                       // ... lo
+  // Q [C | n] partials alias K^T and alpha V (dead once the state update is done)
+  static constexpr int HRED = KT;
+  static constexpr int VT = (VBL + VTILE > HRED + HRED_BYTES) ? VBL + VTILE : HRED + HRED_BYTES;  // [V | 1]^T
+  static constexpr int GATES = VT + VTILE;                      // [NW][5][64] float: per-wave gate rows
+  static constexpr int BYTES = GATES + NW * 5 * 64 * 4;
 };
 
 template <typename TG, int DQK>
@@ -124,170 +170,154 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const int S = NC * L;
   const int dw0 = w * DW;  // first C row of this wave
 
-  char* kn = smem + SM::R1 + w * SM::KN_SLOT;                      // this wave's K natural tile
-  __bf16* kth = (__bf16*)(smem + SM::KTH) + w * DW * PITCH;
-  __bf16* ktl = (__bf16*)(smem + SM::KTL) + w * DW * PITCH;
+  char* kn = smem + SM::KN + w * SM::KN_SLOT;  // K natural tile, then this wave's S^T partials
+  f32x4* sred = (f32x4*)(smem + SM::KN);       // [src][NST][64]
+  __bf16* kt = (__bf16*)(smem + SM::KT + w * SM::KT_SLOT);
   __bf16* vt = (__bf16*)(smem + SM::VT);
-  float* qn_red = (float*)(smem + SM::QN);
-  float* rs_red = (float*)(smem + SM::RS);
-  f32x4* h_red = (f32x4*)(smem + SM::R1);  // [src][slot][vt][lane]
+  __bf16* vbh = (__bf16*)(smem + SM::VBH);
+  __bf16* vbl = (__bf16*)(smem + SM::VBL);
+  float* gw = (float*)(smem + SM::GATES) + w * 5 * 64;  // bl, ul, qbar, mc, alpha
+  f32x4* hred = (f32x4*)(smem + SM::HRED);     // [src][slot][NVX][64]
 
-  // ---- state in registers
-  f32x4 Cacc[NDT][NVT];
-  float nv[KP][8];  // n for d_local = 32p + 8g + s (same in all r16 lanes)
+  // ---- constant rows 64..79 of the V^T tiles: ones (row 64 of [V | 1]^T) and zeros
+  for (int e = tid; e < 16 * PITCH; e += NTHREADS) {
+    const int row = 64 + e / PITCH, col = e % PITCH;
+    const __bf16 one = (__bf16)1.0f, zero = (__bf16)0.0f;
+    vt[row * PITCH + col] = (row == 64) ? one : zero;
+    vbh[row * PITCH + col] = zero;
+    vbl[row * PITCH + col] = zero;
+  }
+
+  // ---- state in registers: C tiles and the n tile (n in column 0 of tile NVT)
+  f32x4 Cacc[NDT][NVX];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int vq = 0; vq < NVT; ++vq)
+    for (int e = 0; e < 4; ++e) {
+      const int d = dw0 + phys(dt, g, e);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = dw0 + phys(dt, g, e);
+      for (int vq = 0; vq < NVT; ++vq)
         Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] : 0.f;
-      }
-#pragma unroll
-  for (int p = 0; p < KP; ++p)
-#pragma unroll
-    for (int s = 0; s < 8; ++s) nv[p][s] = n0 ? n0[(size_t)bh * DQK + dw0 + 32 * p + 8 * g + s] : 0.f;
+      Cacc[dt][NVT][e] = (n0 && r16 == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
+    }
   float m_prev = m0 ? m0[bh] : 0.f;
 
-  // ---- global prefetch registers (chunk kc and kc + 1)
+  // ---- loop-invariant global offsets (elements); per-chunk bases advance uniformly
+  const int tq = lane & 15;                    // K staging: rows 4tq..4tq+3
+  const int vtp = tid & 31, vg = tid >> 5;     // V staging: rows 2vtp, 2vtp+1, columns 8vg..8vg+7
+  uint32_t offq[4][KP], offk[KU][4], offv[2];
+#pragma unroll
+  for (int it = 0; it < 4; ++it)
+#pragma unroll
+    for (int p = 0; p < KP; ++p) offq[it][p] = (uint32_t)((16 * it + r16) * DQK + dw0 + 32 * p + 8 * g);
+#pragma unroll
+  for (int u = 0; u < KU; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) offk[u][r] = (uint32_t)((4 * tq + r) * DQK + dw0 + 8 * (g + 4 * u));
+#pragma unroll
+  for (int r = 0; r < 2; ++r) offv[r] = (uint32_t)((2 * vtp + r) * DV + v0 + 8 * vg);
   const bf16_t* qh = q + (size_t)bh * S * DQK;
   const bf16_t* kh = k + (size_t)bh * S * DQK;
   const bf16_t* vh = v + (size_t)bh * S * DV;
-  const size_t gh = (size_t)bh * S;
-  const int tq = lane & 15;        // K staging: rows 4tq..4tq+3
-  const int vtp = tid & 31, vg = tid >> 5;  // V staging: rows 2vtp, 2vtp+1, columns 8vg..8vg+7
+  const TG* fh = fg + (size_t)bh * S;
+  const TG* ih = ig + (size_t)bh * S;
+  bf16_t* hh = h + (size_t)bh * S * DV;
 
   u32x4 Qc[4][KP], Kc[KU][4], Vc[2];
   float fc, ic;
-  auto load_chunk = [&](int kc, u32x4 (&Qr)[4][KP], u32x4 (&Kr)[KU][4], u32x4 (&Vr)[2], float& fr, float& ir) {
-    const size_t row0 = (size_t)kc * L;
+  auto load_q = [&](int kc) {
+    const bf16_t* base = qh + (size_t)kc * L * DQK;
 #pragma unroll
     for (int it = 0; it < 4; ++it)
 #pragma unroll
-      for (int p = 0; p < KP; ++p)
-        Qr[it][p] = *reinterpret_cast<const u32x4*>(qh + (row0 + 16 * it + r16) * DQK + dw0 + 32 * p + 8 * g);
+      for (int p = 0; p < KP; ++p) Qc[it][p] = *reinterpret_cast<const u32x4*>(base + offq[it][p]);
+  };
+  auto load_kv = [&](int kc) {
+    const bf16_t* kb = kh + (size_t)kc * L * DQK;
+    const bf16_t* vb = vh + (size_t)kc * L * DV;
 #pragma unroll
     for (int u = 0; u < KU; ++u)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        Kr[u][r] = *reinterpret_cast<const u32x4*>(kh + (row0 + 4 * tq + r) * DQK + dw0 + 8 * (g + 4 * u));
+      for (int r = 0; r < 4; ++r) Kc[u][r] = *reinterpret_cast<const u32x4*>(kb + offk[u][r]);
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-      Vr[r] = *reinterpret_cast<const u32x4*>(vh + (row0 + 2 * vtp + r) * DV + v0 + 8 * vg);
-    fr = to_f32(fg[gh + row0 + lane]);
-    ir = to_f32(ig[gh + row0 + lane]);
+    for (int r = 0; r < 2; ++r) Vc[r] = *reinterpret_cast<const u32x4*>(vb + offv[r]);
+    fc = to_f32(fh[(size_t)kc * L + lane]);
+    ic = to_f32(ih[(size_t)kc * L + lane]);
   };
-  load_chunk(0, Qc, Kc, Vc, fc, ic);
+  load_q(0);
+  load_kv(0);
 
   for (int kc = 0; kc < NC; ++kc) {
-    // ================= gates (every wave, lane = token of the chunk)
-    const float lsf = logsigmoid(fc);
-    float b = lsf;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float y = __shfl_up(b, o, 64);
-      if (lane >= o) b += y;
-    }
-    const float gsum = __shfl(b, 63, 64);
+    // ================= gates (every wave, lane = token of the chunk) -> this wave's gate rows
+    const float b = wave_scan<false>(logsig_fast(fc));
+    const float gsum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 63));
     const float a = gsum - b + ic;
     const float m_next = fmaxf(gsum + m_prev, wave_max(a));
-    const float alpha = fast_exp(a - m_next);           // Kbar scale of token `lane`
-    const float gbar = fast_exp(gsum + m_prev - m_next);
-    const float u = ic - b;                             // i_j - b_j
-    float pm = u;                                       // prefix max of u
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float y = __shfl_up(pm, o, 64);
-      if (lane >= o) pm = fmaxf(pm, y);
-    }
+    const float alpha = exp2_((a - m_next) * LOG2E);      // exp(a_t - m')
+    const float gbar = exp2_((gsum + m_prev - m_next) * LOG2E);
+    const float u = ic - b;                              // i_j - b_j
     const float mb = b + m_prev;
-    const float mc = fmaxf(mb, b + pm);                 // combined stabiliser of row `lane`
-    const float qbar = fast_exp(mb - mc) * qk_scale;
-    const float bl = (b - mc) * LOG2E;                  // row term of the intra-chunk exponent
-    const float ul = u * LOG2E;                         // column term
+    const float mc = fmaxf(mb, b + wave_scan<true>(u));  // combined stabiliser of row `lane`
+    gw[lane] = (b - mc) * LOG2E;                         // bl: row term of the intra-chunk exponent
+    gw[64 + lane] = u * LOG2E;                           // ul: column term
+    gw[128 + lane] = exp2_((mb - mc) * LOG2E) * qk_scale;  // qbar
+    gw[192 + lane] = mc;
+    gw[256 + lane] = alpha;
 
-    // ================= stage K (natural, and alpha-scaled transposed hi/lo) and V^T into LDS
+    // ================= stage K (natural and transposed, raw) and V ([V | 1]^T and alpha-scaled hi/lo)
 #pragma unroll
     for (int uu = 0; uu < KU; ++uu) {
       const int dgl = g + 4 * uu;  // 8-column group of this wave's d-slice
-      float al[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * tq + r, 64);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         *reinterpret_cast<u32x4*>(kn + (lds_row(4 * tq + r) * PITCH + 8 * dgl) * 2) = Kc[uu][r];
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        float x[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t wd = Kc[uu][r][s >> 1];
-          x[r] = al[r] * ((s & 1) ? bf_hi(wd) : bf_lo(wd));
-        }
-        const uint32_t h01 = pack_bf16(x[0], x[1]), h23 = pack_bf16(x[2], x[3]);
-        const float l0 = x[0] - bf_lo(h01), l1 = x[1] - bf_hi(h01), l2 = x[2] - bf_lo(h23), l3 = x[3] - bf_hi(h23);
-        const int row = lds_row(8 * dgl + s);
-        u32x2 hv = {h01, h23}, lv = {pack_bf16(l0, l1), pack_bf16(l2, l3)};
-        *reinterpret_cast<u32x2*>(kth + row * PITCH + 4 * tq) = hv;
-        *reinterpret_cast<u32x2*>(ktl + row * PITCH + 4 * tq) = lv;
+        const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t p01 = __builtin_amdgcn_perm(Kc[uu][1][s >> 1], Kc[uu][0][s >> 1], sel);
+        const uint32_t p23 = __builtin_amdgcn_perm(Kc[uu][3][s >> 1], Kc[uu][2][s >> 1], sel);
+        const u32x2 pr = {p01, p23};
+        *reinterpret_cast<u32x2*>(kt + lds_row(8 * dgl + s) * PITCH + 4 * tq) = pr;
       }
     }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const uint32_t w0 = Vc[0][s >> 1], w1 = Vc[1][s >> 1];
-      const uint32_t pr = (s & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
-      *reinterpret_cast<uint32_t*>(vt + (8 * vg + s) * PITCH + 2 * vtp) = pr;
-    }
-
-    // ================= q.n with the state entering the chunk, then n' (from the staging registers)
-    float qn_part[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      float acc = 0.f;
-#pragma unroll
-      for (int p = 0; p < KP; ++p)
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const uint32_t wd = Qc[it][p][s >> 1];
-          acc += ((s & 1) ? bf_hi(wd) : bf_lo(wd)) * nv[p][s];
-        }
-      acc += __shfl_xor(acc, 16, 64);
-      acc += __shfl_xor(acc, 32, 64);
-      qn_part[it] = acc;
-    }
-#pragma unroll
-    for (int uu = 0; uu < KU; ++uu) {
-      float al[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * tq + r, 64);
+    {
+      const f32x2 al = *reinterpret_cast<const f32x2*>(gw + 256 + 2 * vtp);  // alpha of rows 2vtp, 2vtp+1
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        float x = 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t wd = Kc[uu][r][s >> 1];
-          x += al[r] * ((s & 1) ? bf_hi(wd) : bf_lo(wd));
-        }
-        // sum over the 16 lanes of a row (all 64 tokens), n' = gbar n + sum_t alpha_t k_t
-        x += __shfl_xor(x, 1, 64);
-        x += __shfl_xor(x, 2, 64);
-        x += __shfl_xor(x, 4, 64);
-        x += __shfl_xor(x, 8, 64);
-        nv[uu][s] = gbar * nv[uu][s] + x;
+        const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t pr = __builtin_amdgcn_perm(Vc[1][s >> 1], Vc[0][s >> 1], sel);
+        const int off = (8 * vg + s) * PITCH + 2 * vtp;
+        *reinterpret_cast<uint32_t*>(vt + off) = pr;
+        const float x0 = al[0] * bf_lo(pr), x1 = al[1] * bf_hi(pr);
+        const uint32_t hi = pack_bf16(x0, x1);
+        *reinterpret_cast<uint32_t*>(vbh + off) = hi;
+        *reinterpret_cast<uint32_t*>(vbl + off) = pack_bf16(x0 - bf_lo(hi), x1 - bf_hi(hi));
+      }
+      // rows 65..79 of the alpha-V tiles are zero (the previous chunk's H partials overwrote them)
+      constexpr int ZCH = 15 * PITCH / 8;  // 16-byte pieces
+      if (tid < ZCH) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(vbh + 65 * PITCH + 8 * tid) = z;
+        *reinterpret_cast<u32x4*>(vbl + 65 * PITCH + 8 * tid) = z;
+      }
+      if (tid < 32) {  // row 64 of (alpha [V | 1])^T: alpha itself
+        const uint32_t hi = pack_bf16(al[0], al[1]);
+        *reinterpret_cast<uint32_t*>(vbh + 64 * PITCH + 2 * vtp) = hi;
+        *reinterpret_cast<uint32_t*>(vbl + 64 * PITCH + 2 * vtp) = pack_bf16(al[0] - bf_lo(hi), al[1] - bf_hi(hi));
       }
     }
 
-    __syncthreads();  // B1: V^T visible to every wave, K tiles to their wave
+    __syncthreads();  // B1: V tiles visible to every wave, K tiles to their wave
+    if (kc + 1 < NC) load_kv(kc + 1);  // staging registers are free: prefetch the next chunk's k, v, gates
 
-    // ================= QC (partial over this wave's d-slice), rows scaled by qbar afterwards
-    f32x4 Hacc[4][NVT];
+    // ================= Q [C | n] (partial over this wave's d-slice)
+    f32x4 Hacc[4][NVX];
 #pragma unroll
     for (int it = 0; it < 4; ++it)
 #pragma unroll
-      for (int vq = 0; vq < NVT; ++vq) Hacc[it][vq] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int vq = 0; vq < NVX; ++vq) Hacc[it][vq] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int vq = 0; vq < NVT; ++vq) {
+    for (int vq = 0; vq < NVX; ++vq) {
       bf16x8 Cb[KP];
 #pragma unroll
       for (int p = 0; p < KP; ++p) Cb[p] = pack8(Cacc[2 * p][vq], Cacc[2 * p + 1][vq]);
@@ -300,10 +330,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // ================= S^T = K Q^T (partial over the d-slice), causal tiles only
     f32x4 Sacc[4][4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) Sacc[jt][it] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
       bf16x8 Ka[KP];
 #pragma unroll
@@ -312,137 +338,117 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         if ((jt >> 1) > (it >> 1)) continue;
+        Sacc[jt][it] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int p = 0; p < KP; ++p) Sacc[jt][it] = mfma(Ka[p], __builtin_bit_cast(bf16x8, Qc[it][p]), Sacc[jt][it]);
       }
     }
+    if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch the next chunk's
 
-    // ================= prefetch the next chunk (the current q fragments are dead now)
-    float fn = 0.f, in_ = 0.f;
-    if (kc + 1 < NC) load_chunk(kc + 1, Qc, Kc, Vc, fn, in_);
-
+    // S^T partials -> this wave's slot (its K tile is dead)
 #pragma unroll
     for (int it = 0; it < 4; ++it)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float qb = __shfl(qbar, 16 * it + 4 * g + e, 64);
-#pragma unroll
-        for (int vq = 0; vq < NVT; ++vq) Hacc[it][vq][e] *= qb;
-      }
-
-    // ================= gate S^T into M (j <= i), row sums, M V with M split into bf16 hi + lo
-    float rs_part[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int i = 16 * it + r16;
-      const float bli = __shfl(bl, i, 64);
-      float acc = 0.f;
-#pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         if ((jt >> 1) > (it >> 1)) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = phys(jt, g, e);
-          const float ulj = __shfl(ul, j, 64);
-          const float mval = (j <= i) ? Sacc[jt][it][e] * qk_scale * __builtin_amdgcn_exp2f(bli + ulj) : 0.f;
-          Sacc[jt][it][e] = mval;
-          acc += mval;
-        }
+        sred[(w * NST + st_slot(it, jt)) * 64 + lane] = Sacc[jt][it];
       }
-      acc += __shfl_xor(acc, 16, 64);
-      acc += __shfl_xor(acc, 32, 64);
-      rs_part[it] = acc;
-#pragma unroll
-      for (int pj = 0; pj < 2; ++pj) {
-        if (pj > (it >> 1)) continue;
-        const f32x4 x0 = Sacc[2 * pj][it], x1 = Sacc[2 * pj + 1][it];
-        const bf16x8 mh = pack8(x0, x1);
-        const u32x4 mw = __builtin_bit_cast(u32x4, mh);
-        const f32x4 l0 = {x0[0] - bf_lo(mw[0]), x0[1] - bf_hi(mw[0]), x0[2] - bf_lo(mw[1]), x0[3] - bf_hi(mw[1])};
-        const f32x4 l1 = {x1[0] - bf_lo(mw[2]), x1[1] - bf_hi(mw[2]), x1[2] - bf_lo(mw[3]), x1[3] - bf_hi(mw[3])};
-        const bf16x8 ml = pack8(l0, l1);
-#pragma unroll
-        for (int vq = 0; vq < NVT; ++vq) {
-          const bf16x8 vb = *reinterpret_cast<const bf16x8*>(vt + (16 * vq + r16) * PITCH + 32 * pj + 8 * g);
-          Hacc[it][vq] = mfma(mh, vb, Hacc[it][vq]);
-          Hacc[it][vq] = mfma(ml, vb, Hacc[it][vq]);
-        }
-      }
-    }
 
-    // ================= state update C' = gbar C + (Kbar hi + lo)^T V
+    // ================= state update [C | n]' = gbar [C | n] + K^T (alpha [V | 1]) (hi + lo)
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      bf16x8 Kh[2], Kl[2];
+      bf16x8 Ka[2];
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        Kh[p] = *reinterpret_cast<const bf16x8*>(kth + (16 * dt + r16) * PITCH + 32 * p + 8 * g);
-        Kl[p] = *reinterpret_cast<const bf16x8*>(ktl + (16 * dt + r16) * PITCH + 32 * p + 8 * g);
-      }
+      for (int p = 0; p < 2; ++p) Ka[p] = *reinterpret_cast<const bf16x8*>(kt + (16 * dt + r16) * PITCH + 32 * p + 8 * g);
 #pragma unroll
-      for (int vq = 0; vq < NVT; ++vq) {
+      for (int vq = 0; vq < NVX; ++vq) {
         f32x4 c = Cacc[dt][vq] * gbar;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-          const bf16x8 vb = *reinterpret_cast<const bf16x8*>(vt + (16 * vq + r16) * PITCH + 32 * p + 8 * g);
-          c = mfma(Kh[p], vb, c);
-          c = mfma(Kl[p], vb, c);
+          const int off = (16 * vq + r16) * PITCH + 32 * p + 8 * g;
+          c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbh + off), c);
+          c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbl + off), c);
         }
         Cacc[dt][vq] = c;
       }
     }
 
-    // ================= reduce H over the waves; wave w finishes rows 16w..16w+15
+    __syncthreads();  // B2: S^T partials visible
+
+    // ================= own rows i = 16w + r16: exact scores, gating, M [V | 1] with M split hi + lo
+    f32x4 Hmv[NVX];
+#pragma unroll
+    for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      const int i = 16 * w + r16;
+      const float bli = gw[i];
+      const int npj = (w >> 1) + 1;  // tile pairs with j-range starting at or before the own rows
+#pragma unroll
+      for (int pj = 0; pj < 2; ++pj) {
+        if (pj >= npj) break;
+        f32x4 Ms[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int jt = 2 * pj + hf;
+          const int slot = w < 2 ? 2 * w + jt : 4 + 4 * (w - 2) + jt;
+          f32x4 sv = sred[slot * 64 + lane];
+#pragma unroll
+          for (int src = 1; src < NW; ++src) sv += sred[(src * NST + slot) * 64 + lane];
+          const f32x4 ul = *reinterpret_cast<const f32x4*>(gw + 64 + 32 * pj + 8 * g + 4 * hf);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = 32 * pj + 8 * g + 4 * hf + e;
+            sv[e] = (j <= i) ? sv[e] * qk_scale * exp2_(bli + ul[e]) : 0.f;
+          }
+          Ms[hf] = sv;
+        }
+        bf16x8 mh, ml;
+        split8(Ms[0], Ms[1], mh, ml);
+#pragma unroll
+        for (int vq = 0; vq < NVX; ++vq) {
+          const bf16x8 vb = *reinterpret_cast<const bf16x8*>(vt + (16 * vq + r16) * PITCH + 32 * pj + 8 * g);
+          Hmv[vq] = mfma(mh, vb, Hmv[vq]);
+          Hmv[vq] = mfma(ml, vb, Hmv[vq]);
+        }
+      }
+    }
+
+    // ================= sum Q [C | n] over the waves; wave w finishes rows 16w..16w+15
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       if (it == w) continue;
       const int slot = it < w ? it : it - 1;
 #pragma unroll
-      for (int vq = 0; vq < NVT; ++vq) h_red[((w * (NW - 1) + slot) * NVT + vq) * 64 + lane] = Hacc[it][vq];
+      for (int vq = 0; vq < NVX; ++vq) hred[((w * 3 + slot) * NVX + vq) * 64 + lane] = Hacc[it][vq];
     }
-    if (g == 0) {
+    __syncthreads();  // B3: Q [C | n] partials visible (the K / S regions are dead)
+    {
+      const f32x4 qb = *reinterpret_cast<const f32x4*>(gw + 128 + 16 * w + 4 * g);  // rows 16w + 4g + e
+      const f32x4 mcr = *reinterpret_cast<const f32x4*>(gw + 192 + 16 * w + 4 * g);
+      f32x4 H[NVX];
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        qn_red[w * 64 + 16 * it + r16] = qn_part[it];
-        rs_red[w * 64 + 16 * it + r16] = rs_part[it];
+      for (int vq = 0; vq < NVX; ++vq) {
+        f32x4 acc = (w == 0) ? Hacc[0][vq] : (w == 1) ? Hacc[1][vq] : (w == 2) ? Hacc[2][vq] : Hacc[3][vq];
+#pragma unroll
+        for (int src = 0; src < NW; ++src) {
+          if (src == w) continue;
+          const int slot = w < src ? w : w - 1;
+          acc += hred[((src * 3 + slot) * NVX + vq) * 64 + lane];
+        }
+        H[vq] = qb * acc + Hmv[vq];
+      }
+      bf16_t* hb = hh + (size_t)kc * L * DV + v0 + 16 * 0 + r16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float den = __shfl(H[NVT][e], lane & 48, 64);  // column 64 lives in lane r16 == 0
+        const float inv = 1.0f / (fmaxf(fabsf(den), exp2_(-mcr[e] * LOG2E)) + eps);
+        const int i = 16 * w + 4 * g + e;
+#pragma unroll
+        for (int vq = 0; vq < NVT; ++vq) hb[(size_t)i * DV + 16 * vq] = from_f32<bf16_t>(H[vq][e] * inv);
       }
     }
-    __syncthreads();  // B2: partials visible
-    f32x4 Hown[NVT];
-#pragma unroll
-    for (int vq = 0; vq < NVT; ++vq) {
-      // runtime-indexed own tile (it == w): select without dynamic register indexing
-      f32x4 acc = (w == 0) ? Hacc[0][vq] : (w == 1) ? Hacc[1][vq] : (w == 2) ? Hacc[2][vq] : Hacc[3][vq];
-#pragma unroll
-      for (int src = 0; src < NW; ++src) {
-        if (src == w) continue;
-        const int slot = w < src ? w : w - 1;
-        acc += h_red[((src * (NW - 1) + slot) * NVT + vq) * 64 + lane];
-      }
-      Hown[vq] = acc;
-    }
-    const size_t tok0 = gh + (size_t)kc * L;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * w + 4 * g + e;
-      float qn = 0.f, rs = 0.f;
-#pragma unroll
-      for (int src = 0; src < NW; ++src) {
-        qn += qn_red[src * 64 + i];
-        rs += rs_red[src * 64 + i];
-      }
-      const float mci = __shfl(mc, i, 64);
-      const float den = __shfl(qbar, i, 64) * qn + rs;
-      const float inv = 1.0f / (fmaxf(fabsf(den), fast_exp(-mci)) + eps);
-#pragma unroll
-      for (int vq = 0; vq < NVT; ++vq)
-        h[(tok0 + i) * DV + v0 + 16 * vq + r16] = from_f32<bf16_t>(Hown[vq][e] * inv);
-    }
-    __syncthreads();  // B3: H partial slots may be overwritten by the next chunk's K tiles
-
+    __syncthreads();  // B4: H partial slots (aliasing the K regions) consumed
     m_prev = m_next;
-    fc = fn;
-    ic = in_;
   }
 
   // ---- final states
@@ -450,21 +456,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int vq = 0; vq < NVT; ++vq)
+      for (int e = 0; e < 4; ++e) {
+        const int d = dw0 + phys(dt, g, e);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = dw0 + phys(dt, g, e);
+        for (int vq = 0; vq < NVT; ++vq)
           c_last[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] = Cacc[dt][vq][e];
-        }
-    if (v0 == 0) {
-      if (r16 == 0) {
-#pragma unroll
-        for (int p = 0; p < KP; ++p)
-#pragma unroll
-          for (int s = 0; s < 8; ++s) n_last[(size_t)bh * DQK + dw0 + 32 * p + 8 * g + s] = nv[p][s];
+        if (v0 == 0 && r16 == 0) n_last[(size_t)bh * DQK + d] = Cacc[dt][NVT][e];
       }
-      if (tid == 0) m_last[bh] = m_prev;
-    }
+    if (v0 == 0 && tid == 0) m_last[bh] = m_prev;
   }
 }
 
