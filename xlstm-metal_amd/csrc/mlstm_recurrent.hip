@@ -162,6 +162,115 @@ __global__ __launch_bounds__(REC_THREADS) void mlstm_recurrent_kernel(
   }
 }
 
+// Single decode step, straight-line: every C load of the thread is issued
+// first, then each row is updated and stored as soon as it arrives, so the
+// read and write streams overlap.  n' and (q s).n' are computed one element
+// per thread (d = tid + 256 j) while the C loads are in flight.  Same thread
+// layout and reduction as mlstm_recurrent_kernel.
+typedef float nt_f4 __attribute__((ext_vector_type(4)));
+
+template <typename TQ, typename TG, int RPT>
+__global__ __launch_bounds__(REC_THREADS) void mlstm_step_kernel(
+    const TQ* __restrict__ q, const TQ* __restrict__ k, const TQ* __restrict__ v,
+    const TG* __restrict__ ig, const TG* __restrict__ fg,
+    const float* c_old, const float* __restrict__ n_old, const float* __restrict__ m_old,
+    TQ* __restrict__ h, float* c_new, float* __restrict__ n_new, float* __restrict__ m_new,
+    int DQK, int DV, int ntile, float qk_scale, float eps) {
+  constexpr bool LOWP = !is_f32<TQ>::value;
+  __shared__ float s_red[16][REC_COLS + 4];
+  __shared__ float s_wsum[REC_THREADS / 64];
+
+  const int bh = blockIdx.x / ntile;
+  const int tile = blockIdx.x - bh * ntile;
+  const int tid = threadIdx.x;
+  const int tx = tid & 15, ty = tid >> 4;
+  const int col0 = tile * REC_COLS + tx * 4;
+  const bool col_ok = col0 < DV;
+  const size_t cbase = (size_t)bh * DQK * DV;
+
+  float4 C[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int d = ty + 16 * r;
+    if (col_ok && d < DQK) {
+      const nt_f4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(c_old + cbase + (size_t)d * DV + col0));
+      C[r] = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+      C[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+
+  // gates (identical in every thread)
+  const float lsf = round_to<TG>(logsigmoid(to_f32(fg[bh])));
+  const float mo = m_old[bh];
+  const float ipre = to_f32(ig[bh]);
+  const float mn = fmaxf(lsf + mo, ipre);
+  const float fa = expf(lsf + mo - mn);
+  const float ia = expf(ipre - mn);
+
+  // n' and the partial of (q s) . n'
+  const TQ* qp = q + (size_t)bh * DQK;
+  const TQ* kp = k + (size_t)bh * DQK;
+  float part = 0.f;
+  for (int d = tid; d < DQK; d += REC_THREADS) {
+    float qs = to_f32(qp[d]) * qk_scale;
+    if (LOWP) qs = round_to<TQ>(qs);
+    const float nn = fa * n_old[(size_t)bh * DQK + d] + ia * to_f32(kp[d]);
+    if (tile == 0) n_new[(size_t)bh * DQK + d] = nn;
+    part += qs * (LOWP ? round_to<TQ>(nn) : nn);
+  }
+  part = wave_sum(part);
+  if ((tid & 63) == 0) s_wsum[tid >> 6] = part;
+
+  // C' row by row: store as soon as computed, accumulate (q s)^T C'
+  float vv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (col_ok) {
+    const TQ* vp = v + (size_t)bh * DV + col0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vv[j] = to_f32(vp[j]);
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int d = ty + 16 * r;
+    if (d < DQK) {
+      float qd = to_f32(qp[d]) * qk_scale;
+      if (LOWP) qd = round_to<TQ>(qd);
+      const float kd = to_f32(kp[d]);
+      float kv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kv[j] = LOWP ? round_to<TQ>(kd * vv[j]) : kd * vv[j];
+      float4 c = C[r];
+      c.x = fa * c.x + ia * kv[0];
+      c.y = fa * c.y + ia * kv[1];
+      c.z = fa * c.z + ia * kv[2];
+      c.w = fa * c.w + ia * kv[3];
+      if (col_ok) {
+        const nt_f4 x = {c.x, c.y, c.z, c.w};
+        __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(c_new + cbase + (size_t)d * DV + col0));
+      }
+      acc[0] += qd * (LOWP ? round_to<TQ>(c.x) : c.x);
+      acc[1] += qd * (LOWP ? round_to<TQ>(c.y) : c.y);
+      acc[2] += qd * (LOWP ? round_to<TQ>(c.z) : c.z);
+      acc[3] += qd * (LOWP ? round_to<TQ>(c.w) : c.w);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s_red[ty][tx * 4 + j] = acc[j];
+  __syncthreads();
+  if (tid < REC_COLS && tile * REC_COLS + tid < DV) {
+    float qn = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+    if (LOWP) qn = round_to<TQ>(qn);
+    const float den = fmaxf(fabsf(qn), expf(-mn)) + eps;
+    float hn = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) hn += s_red[r][tid];
+    if (LOWP) hn = round_to<TQ>(hn);
+    h[(size_t)bh * DV + tile * REC_COLS + tid] = from_f32<TQ>(hn / den);
+  }
+  if (tile == 0 && tid == 0) m_new[bh] = mn;
+}
+
 template <typename TQ, typename TG>
 static int launch_rec_t(const void* q, const void* k, const void* v, const void* i, const void* f,
                         const float* c0, const float* n0, const float* m0, void* h, float* c1, float* n1,
@@ -170,6 +279,18 @@ static int launch_rec_t(const void* q, const void* k, const void* v, const void*
   const int ntile = (DV + REC_COLS - 1) / REC_COLS;
   const int rpt = (DQK + 15) / 16;
   dim3 grid((unsigned)(BNH * ntile)), block(REC_THREADS);
+  if (S == 1 && c0 && n0 && m0 && c1 && n1 && m1) {  // decode step: straight-line kernel
+#define XL_STEP_LAUNCH(R)                                                                                      \
+  hipLaunchKernelGGL((mlstm_step_kernel<TQ, TG, R>), grid, block, 0, s, (const TQ*)q, (const TQ*)k,          \
+                     (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1, DQK, DV, ntile,  \
+                     qk_scale, eps)
+    if (rpt <= 4) XL_STEP_LAUNCH(4);
+    else if (rpt <= 8) XL_STEP_LAUNCH(8);
+    else if (rpt <= 16) XL_STEP_LAUNCH(16);
+    else XL_STEP_LAUNCH(32);
+#undef XL_STEP_LAUNCH
+    return check_launch(who);
+  }
 #define XL_REC_LAUNCH(R)                                                                                       \
   hipLaunchKernelGGL((mlstm_recurrent_kernel<TQ, TG, R>), grid, block, 0, s, (const TQ*)q, (const TQ*)k,     \
                      (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1, S, DQK, DV,      \
