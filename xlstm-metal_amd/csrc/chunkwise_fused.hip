@@ -1,12 +1,12 @@
 // Fused single-pass chunkwise mLSTM forward for bf16 q/k/v on gfx950.
 //
-// One workgroup = one (b, h) pair x one 64-column tile of DV; it marches over
-// the NC chunks of L = 64 tokens keeping its C tile (DQK x 64, float32) and
-// the normaliser n (DQK) in registers, so the only HBM traffic is q, k, v, the
-// gates, h and the final states (no per-chunk state round trip).  The math is
-// the reference's chunkwise forward (kernel_development/xlstm/mlstm_block/
-// mlstm_chunkwise/vendored/torch/native/fw.py:98-143 for the inter-chunk
-// recurrence, :193-245 for the outputs), fused per chunk:
+// One workgroup = one (b, h) pair x one 64-column tile of DV, marching over
+// the NC chunks of L = 64 tokens.  The C tile (DQK x 64, float32) and the
+// normaliser n stay on chip for the whole sequence, so the only HBM traffic is
+// q, k, v, the gates, h and the final states.  The math is the reference's
+// chunkwise forward (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/
+// vendored/torch/native/fw.py:98-143 for the inter-chunk recurrence,
+// :193-245 for the outputs), per chunk:
 //
 //   b = cumsum logsig f, g = b_L, a_t = g - b_t + i_t, m' = max(g + m, max a)
 //   m_i = max(b_i + m, max_{j<=i} (b_i - b_j + i_j))
@@ -17,28 +17,36 @@
 //   C' = exp(g + m - m') C + sum_t exp(a_t - m') k_t v_t^T,  n' likewise
 //
 // The normaliser rides along as a fifth 16-column tile: C carries n in its
-// column 64, V carries a row of ones (for sum_j M_ij) and alpha V carries
-// alpha_t (for sum_t alpha_t k_t), so n', q.n and the row sums are produced by
-// the same MFMAs as C', q C and M V, and den_i lands in column 64 of H_i.
+// column 64, V carries a row of ones and alpha V carries alpha_t, so n', q.n
+// and the row sums come out of the same MFMAs as C', q C and M V, and den_i
+// lands in column 64 of H_i.
 //
-// Work split (4 waves, 256 threads): wave w owns rows [w*DW, (w+1)*DW) of C
-// (DW = DQK/4).  Per chunk each wave computes, over its slice of the DQK
-// contraction, a partial S^T = K Q^T and a partial Q [C | n]; the S partials
-// are summed through LDS so that wave w gates the exact scores of its own 16
-// output rows and multiplies them with V; the Q [C | n] partials are summed
-// through LDS the same way before the output rows are finished.  All dense
-// products are v_mfma_f32_16x16x32_bf16 with float32 accumulation:
-//   S^T  (j x i, over d)   A = K rows (LDS),        B = q rows (registers)
-//   QC   (i x v, over d)   A = q rows (registers),  B = [C | n] (accumulators -> bf16)
-//   MV   (i x v, over j)   A = M hi + lo,           B = [V | 1]^T (LDS)
-//   KV   (d x v, over t)   A = K^T (LDS),           B = (alpha [V | 1])^T hi + lo (LDS)
-// Operands coming from accumulators use a row permutation: the 16 rows of an
-// MFMA tile are mapped to physical indices so that the 4 rows a lane holds in
-// two adjacent tiles are 8 consecutive indices, i.e. exactly the 8-element
-// k-slice that lane must supply when the accumulator is reused as an operand.
-// alpha_t v_t and the gated scores are split into bf16 hi + lo parts (two
-// MFMAs) so the float32 state and the outputs do not inherit bf16 rounding of
-// those products; [C | n] is rounded to bf16 only as the operand of Q [C | n].
+// Producer / consumer split (8 waves, two per SIMD):
+//  * state waves 0..3: wave s owns rows [s*DW, (s+1)*DW) of [C | n]
+//    (DW = DQK/4, float32 accumulators) and applies the chunk update
+//    [C | n] += K^T (alpha [V | 1]) with alpha V split into bf16 hi + lo (two
+//    MFMAs, so the state keeps float32 accuracy).  It then publishes [C | n]
+//    as bf16 hi + lo into an LDS buffer laid out as ready-made MFMA B
+//    fragments.
+//  * output waves 4..7: wave o owns output rows [16o, 16o+16) of every chunk:
+//    Q [C | n] with the state published for the previous chunk (hi and lo:
+//    two MFMAs, so q C keeps float32 accuracy), then exact S^T = K Q^T over
+//    the whole DQK, gating and M [V | 1] (M split hi + lo).  No partial sums
+//    cross waves.
+// One state buffer suffices: the output waves finish Q [C | n] before the
+// chunk's first barrier and the state waves overwrite the buffer only after
+// it, so per chunk the output waves' q C MFMAs overlap the state waves' tile
+// staging and the state waves' K^T V MFMAs overlap the output waves' S / M V.
+// All products are v_mfma_f32_16x16x32_bf16.  K^T and V operands are read
+// with ds_read_b64_tr_b16 from the natural row-major tiles (within 16 lanes,
+// output lane 4a+c receives element c of source lanes 4k+a, k = 0..3), with
+// the token order inside a k-slice chosen so that every LDS access pattern is
+// free of bank conflicts.
+//
+// The forget rescale exp(g + m - m') of C is deferred: the state is stored as
+// C e^{-G} (G = accumulated log rescale), the factor e^{-G} is folded into
+// alpha V and e^{G} into the output row scale, and C is renormalised only
+// when G drops below -30 (the eager path).
 //
 // Grid mapping is XCD aware: the DV tiles of one head land on the same XCD so
 // the head's q/k chunks are fetched from HBM once and then hit that XCD's L2.
@@ -49,21 +57,25 @@ namespace fused {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int L = 64;          // chunk size (= wavefront size: one lane per token)
-constexpr int NW = 4;          // waves per workgroup
-constexpr int NTHREADS = NW * 64;
-constexpr int DVT = 64;        // DV columns per workgroup
-constexpr int NVT = DVT / 16;  // 16-wide column tiles of v
-constexpr int NVX = NVT + 1;   // ... plus the n / ones / den tile
-constexpr int PITCH = 72;      // bf16 per LDS row (144 B): 16 consecutive rows hit distinct banks
-constexpr int NST = 12;        // causal S^T tiles (jt, it) with jt/2 <= it/2
+constexpr int L = 64;           // chunk size (= wavefront size: one lane per token)
+constexpr int NSW = 4;          // state waves
+constexpr int NOW = 4;          // output waves
+constexpr int NTHREADS = 64 * (NSW + NOW);
+constexpr int DVT = 64;         // DV columns per workgroup
+constexpr int NVT = DVT / 16;   // 16-wide column tiles of v
+constexpr int NVX = NVT + 1;    // ... plus the n / ones / den tile
+constexpr int VN_PITCH = 160;   // bytes per row of natural V (8 consecutive rows -> distinct 32 B bank groups)
+constexpr int VB_PITCH = 144;   // bytes per row of (alpha V)^T (16 consecutive rows -> distinct 16 B bank groups)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
+constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -74,10 +86,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ bf16x8 pack8(f32x4 a, f32x4 b) {
-  u32x4 r = {pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
-  return __builtin_bit_cast(bf16x8, r);
-}
 // bf16 hi + lo split of 8 floats: hi = bf16(x), lo = bf16(x - hi)
 __device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
   const u32x4 h = {pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
@@ -87,21 +95,28 @@ __device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo)
   lo = __builtin_bit_cast(bf16x8, l);
 }
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
-// log(sigmoid(x)) = min(x, 0) - log(1 + exp(-|x|)) via the hardware exp2/log2;
-// absolute error < 1e-7.
+__device__ __forceinline__ float exp_(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
+// log(sigmoid(x)) = min(x, 0) - log(1 + exp(-|x|)) via the hardware exp2/log2 (abs. error < 1e-7)
 __device__ __forceinline__ float logsig_fast(float x) {
   return fminf(x, 0.f) - LN2 * __builtin_amdgcn_logf(1.0f + exp2_(-fabsf(x) * LOG2E));
+}
+// two 64-bit transposed LDS reads -> one 8 x bf16 MFMA operand
+__device__ __forceinline__ bf16x8 tr8(const char* p0, const char* p1) {
+  const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+  const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  const u32x4 r = {ua[0], ua[1], ub[0], ub[1]};
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 // Inclusive wave64 scans with DPP (row shifts, then row broadcasts).
 template <bool MAX>
 __device__ __forceinline__ float wave_scan(float x) {
-  const float ident = MAX ? -INFINITY : 0.f;
-  const int iid = __float_as_int(ident);
-#define XL_SCAN_STEP(CTRL, ROWMASK)                                                                     \
-  {                                                                                                     \
+  const int iid = __float_as_int(MAX ? -INFINITY : 0.f);
+#define XL_SCAN_STEP(CTRL, ROWMASK)                                                                                 \
+  {                                                                                                                 \
     const float y = __int_as_float(__builtin_amdgcn_update_dpp(iid, __float_as_int(x), CTRL, ROWMASK, 0xf, false)); \
-    x = MAX ? fmaxf(x, y) : x + y;                                                                      \
+    x = MAX ? fmaxf(x, y) : x + y;                                                                                  \
   }
   XL_SCAN_STEP(0x111, 0xf)  // row_shr:1
   XL_SCAN_STEP(0x112, 0xf)  // row_shr:2
@@ -113,34 +128,24 @@ __device__ __forceinline__ float wave_scan(float x) {
   return x;
 }
 
-// LDS row of physical index x within a 64-row block: tiles of 16 rows, each
-// tile pair (32 indices) interleaved so that lane group g of a tile pair
-// covers indices 8g..8g+7 (4 in each tile).
-__device__ __forceinline__ int lds_row(int x) {
-  return 32 * (x >> 5) + 16 * ((x >> 2) & 1) + 4 * ((x >> 3) & 3) + (x & 3);
-}
-// physical index held by accumulator element e of lane group g in tile `tile`
-__device__ __forceinline__ int phys(int tile, int g, int e) { return 32 * (tile >> 1) + 8 * g + 4 * (tile & 1) + e; }
-// slot of causal S^T tile (jt, it), jt/2 <= it/2
-__device__ __forceinline__ constexpr int st_slot(int it, int jt) { return it < 2 ? 2 * it + jt : 4 + 4 * (it - 2) + jt; }
+// Column of token t in the (alpha [V | 1])^T tiles: inside each 8-token block
+// the order is (t even first), matching the transposed K operand whose k-slice
+// of lane group g is t = 32p + 8g + 2k + h (k = 0..3, h = read 0/1).
+__device__ __forceinline__ int vb_col(int t) { return (t & ~7) + 4 * (t & 1) + ((t >> 1) & 3); }
 
 template <int DQK>
 struct Smem {
-  static constexpr int DW = DQK / NW;                          // C rows per wave
-  static constexpr int KN_SLOT = NST * 64 * 16;                 // per wave: K natural tile, then its S^T partials
-  static_assert(64 * PITCH * 2 <= KN_SLOT, "K tile must fit its slot");
-  static constexpr int KT_SLOT = DW * PITCH * 2;                // per wave: K^T tile
-  static constexpr int VTILE = 80 * PITCH * 2;                  // [80][PITCH] bf16
-  static constexpr int HRED_BYTES = NW * 3 * NVX * 64 * 16;     // [NW][3][NVX][64] f32x4
-  static constexpr int KN = 0;                                  // [NW][KN_SLOT]
-  static constexpr int KT = KN + NW * KN_SLOT;                  // [NW][KT_SLOT]
-  static constexpr int VBH = KT + NW * KT_SLOT;                 // (alpha [V | 1])^T hi
-  static constexpr int VBL = VBH + VTILE;                       // ... lo
-  // Q [C | n] partials alias K^T and alpha V (dead once the state update is done)
-  static constexpr int HRED = KT;
-  static constexpr int VT = (VBL + VTILE > HRED + HRED_BYTES) ? VBL + VTILE : HRED + HRED_BYTES;  // [V | 1]^T
-  static constexpr int GATES = VT + VTILE;                      // [NW][5][64] float: per-wave gate rows
-  static constexpr int BYTES = GATES + NW * 5 * 64 * 4;
+  static constexpr int KPD = DQK / 32;                   // 32-deep k-steps over DQK
+  static constexpr int KN_PITCH = DQK * 2 + 16;          // bytes per K row: 16 consecutive rows -> distinct 16 B groups
+  static constexpr int KN = 0;                           // [64 t][KN_PITCH]: K natural
+  static constexpr int VN = KN + 64 * KN_PITCH;          // [64 t][VN_PITCH]: V natural
+  static constexpr int VBH = VN + 64 * VN_PITCH;         // [80 v][VB_PITCH]: (alpha [V | 1])^T hi
+  static constexpr int VBL = VBH + 80 * VB_PITCH;        // ... lo
+  static constexpr int CB = VBL + 80 * VB_PITCH;         // [hi, lo][KPD][NVX][64] x 16 B: [C | n] B fragments
+  static constexpr int CB_BUF = KPD * NVX * 64 * 16;
+  static constexpr int GATES = CB + 2 * CB_BUF;          // [8 waves][5][64] float
+  static constexpr int BYTES = GATES + 8 * 5 * 64 * 4;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
 template <typename TG, int DQK>
@@ -151,15 +156,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last, int NC, int DV, int BNH,
     int nvtile, float qk_scale, float eps) {
   using SM = Smem<DQK>;
-  constexpr int DW = SM::DW;    // 64 or 32
-  constexpr int KP = DW / 32;   // 32-deep k-steps of this wave's d-slice
-  constexpr int NDT = DW / 16;  // C row tiles per wave
-  constexpr int KU = DW / 32;   // K staging units per lane (4 rows x 8 d each)
+  constexpr int KPD = SM::KPD;
+  constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
+  constexpr int NDT = DW / 16;    // C row tiles per state wave
+  constexpr int NKU = DQK / 64;   // K staging: 16-byte pieces per thread (64 rows x DQK / 512 threads / 8)
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
+  const bool is_state = w < NSW;
+  const int ws = w & 3;  // index within the state or output group
 
   // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
   const int nwg = BNH * nvtile;
@@ -168,302 +175,311 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const int bh = lin / nvtile;
   const int v0 = (lin - bh * nvtile) * DVT;
   const int S = NC * L;
-  const int dw0 = w * DW;  // first C row of this wave
 
-  char* kn = smem + SM::KN + w * SM::KN_SLOT;  // K natural tile, then this wave's S^T partials
-  f32x4* sred = (f32x4*)(smem + SM::KN);       // [src][NST][64]
-  __bf16* kt = (__bf16*)(smem + SM::KT + w * SM::KT_SLOT);
-  __bf16* vt = (__bf16*)(smem + SM::VT);
-  __bf16* vbh = (__bf16*)(smem + SM::VBH);
-  __bf16* vbl = (__bf16*)(smem + SM::VBL);
-  float* gw = (float*)(smem + SM::GATES) + w * 5 * 64;  // bl, ul, qbar, mc, alpha
-  f32x4* hred = (f32x4*)(smem + SM::HRED);     // [src][slot][NVX][64]
+  char* kn = smem + SM::KN;
+  char* vn = smem + SM::VN;
+  char* vbh = smem + SM::VBH;
+  char* vbl = smem + SM::VBL;
+  u32x4* cb = (u32x4*)(smem + SM::CB);
+  float* gw = (float*)(smem + SM::GATES) + w * 5 * 64;  // this wave's rows: bl, ul, qbar, mc, alpha'
 
-  // ---- constant rows 64..79 of the V^T tiles: ones (row 64 of [V | 1]^T) and zeros
-  for (int e = tid; e < 16 * PITCH; e += NTHREADS) {
-    const int row = 64 + e / PITCH, col = e % PITCH;
-    const __bf16 one = (__bf16)1.0f, zero = (__bf16)0.0f;
-    vt[row * PITCH + col] = (row == 64) ? one : zero;
-    vbh[row * PITCH + col] = zero;
-    vbl[row * PITCH + col] = zero;
+  // constant rows 65..79 of the alpha-V tiles (zeros); row 64 is rewritten every chunk
+  for (int e = tid; e < 15 * VB_PITCH / 4; e += NTHREADS) {
+    reinterpret_cast<uint32_t*>(vbh + 65 * VB_PITCH)[e] = 0u;
+    reinterpret_cast<uint32_t*>(vbl + 65 * VB_PITCH)[e] = 0u;
   }
 
-  // ---- state in registers: C tiles and the n tile (n in column 0 of tile NVT)
-  f32x4 Cacc[NDT][NVX];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = dw0 + phys(dt, g, e);
-#pragma unroll
-      for (int vq = 0; vq < NVT; ++vq)
-        Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] : 0.f;
-      Cacc[dt][NVT][e] = (n0 && r16 == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
-    }
-  float m_prev = m0 ? m0[bh] : 0.f;
-
-  // ---- loop-invariant global offsets (elements); per-chunk bases advance uniformly
-  const int tq = lane & 15;                    // K staging: rows 4tq..4tq+3
-  const int vtp = tid & 31, vg = tid >> 5;     // V staging: rows 2vtp, 2vtp+1, columns 8vg..8vg+7
-  uint32_t offq[4][KP], offk[KU][4], offv[2];
-#pragma unroll
-  for (int it = 0; it < 4; ++it)
-#pragma unroll
-    for (int p = 0; p < KP; ++p) offq[it][p] = (uint32_t)((16 * it + r16) * DQK + dw0 + 32 * p + 8 * g);
-#pragma unroll
-  for (int u = 0; u < KU; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) offk[u][r] = (uint32_t)((4 * tq + r) * DQK + dw0 + 8 * (g + 4 * u));
-#pragma unroll
-  for (int r = 0; r < 2; ++r) offv[r] = (uint32_t)((2 * vtp + r) * DV + v0 + 8 * vg);
   const bf16_t* qh = q + (size_t)bh * S * DQK;
   const bf16_t* kh = k + (size_t)bh * S * DQK;
   const bf16_t* vh = v + (size_t)bh * S * DV;
   const TG* fh = fg + (size_t)bh * S;
   const TG* ih = ig + (size_t)bh * S;
   bf16_t* hh = h + (size_t)bh * S * DV;
+  const float m_init = m0 ? m0[bh] : 0.f;
 
-  u32x4 Qc[4][KP], Kc[KU][4], Vc[2];
-  float fc, ic;
-  auto load_q = [&](int kc) {
-    const bf16_t* base = qh + (size_t)kc * L * DQK;
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int p = 0; p < KP; ++p) Qc[it][p] = *reinterpret_cast<const u32x4*>(base + offq[it][p]);
-  };
-  auto load_kv = [&](int kc) {
+  // ---- K staging: piece u of thread tid = u*NTHREADS + tid -> row piece / (DQK/8), 16-byte column group
+  auto load_k = [&](int kc, u32x4 (&Kst)[NKU]) {
     const bf16_t* kb = kh + (size_t)kc * L * DQK;
-    const bf16_t* vb = vh + (size_t)kc * L * DV;
 #pragma unroll
-    for (int u = 0; u < KU; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Kc[u][r] = *reinterpret_cast<const u32x4*>(kb + offk[u][r]);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) Vc[r] = *reinterpret_cast<const u32x4*>(vb + offv[r]);
-    fc = to_f32(fh[(size_t)kc * L + lane]);
-    ic = to_f32(ih[(size_t)kc * L + lane]);
+    for (int u = 0; u < NKU; ++u) {
+      const int piece = u * NTHREADS + tid;
+      Kst[u] = *reinterpret_cast<const u32x4*>(kb + (size_t)(piece / (DQK / 8)) * DQK + 8 * (piece % (DQK / 8)));
+    }
   };
-  load_q(0);
-  load_kv(0);
-
-  for (int kc = 0; kc < NC; ++kc) {
-    // ================= gates (every wave, lane = token of the chunk) -> this wave's gate rows
-    const float b = wave_scan<false>(logsig_fast(fc));
+  auto store_k = [&](const u32x4 (&Kst)[NKU]) {
+#pragma unroll
+    for (int u = 0; u < NKU; ++u) {
+      const int piece = u * NTHREADS + tid;
+      *reinterpret_cast<u32x4*>(kn + (piece / (DQK / 8)) * SM::KN_PITCH + 16 * (piece % (DQK / 8))) = Kst[u];
+    }
+  };
+  auto load_gates = [&](int kc, float& fr, float& ir) {
+    fr = to_f32(fh[(size_t)kc * L + lane]);
+    ir = to_f32(ih[(size_t)kc * L + lane]);
+  };
+  // Gates of one chunk (every wave, lane = token).  Writes this wave's gate rows
+  // and returns m', the log rescale lg, and the updated deferred rescale.
+  struct Gates { float m_next, lg, G_prev, Gn; bool renorm; };
+  auto gates = [&](float fcur, float icur, float m_prev, float G) {
+    Gates r;
+    const float b = wave_scan<false>(logsig_fast(fcur));
     const float gsum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 63));
-    const float a = gsum - b + ic;
-    const float m_next = fmaxf(gsum + m_prev, wave_max(a));
-    const float alpha = exp2_((a - m_next) * LOG2E);      // exp(a_t - m')
-    const float gbar = exp2_((gsum + m_prev - m_next) * LOG2E);
-    const float u = ic - b;                              // i_j - b_j
+    const float a = gsum - b + icur;
+    r.m_next = fmaxf(gsum + m_prev, wave_max(a));
+    r.lg = gsum + m_prev - r.m_next;  // log of this chunk's rescale of the state (<= 0)
+    r.G_prev = G;
+    r.Gn = G + r.lg;
+    r.renorm = r.Gn < RENORM;         // wave-uniform, and the same in every wave
+    if (r.renorm) r.Gn = 0.f;
+    const float u = icur - b;
     const float mb = b + m_prev;
-    const float mc = fmaxf(mb, b + wave_scan<true>(u));  // combined stabiliser of row `lane`
-    gw[lane] = (b - mc) * LOG2E;                         // bl: row term of the intra-chunk exponent
-    gw[64 + lane] = u * LOG2E;                           // ul: column term
-    gw[128 + lane] = exp2_((mb - mc) * LOG2E) * qk_scale;  // qbar
+    const float mc = fmaxf(mb, b + wave_scan<true>(u));
+    gw[lane] = (b - mc) * LOG2E;                          // row term of the intra-chunk exponent
+    gw[64 + lane] = u * LOG2E;                            // column term
+    gw[128 + lane] = exp_(mb - mc + G) * qk_scale;        // output row scale (deferred state rescale folded in)
     gw[192 + lane] = mc;
-    gw[256 + lane] = alpha;
+    gw[256 + lane] = exp_(a - r.m_next - r.Gn);           // alpha' = exp(a_t - m') e^{-G}
+    return r;
+  };
 
-    // ================= stage K (natural and transposed, raw) and V ([V | 1]^T and alpha-scaled hi/lo)
-#pragma unroll
-    for (int uu = 0; uu < KU; ++uu) {
-      const int dgl = g + 4 * uu;  // 8-column group of this wave's d-slice
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<u32x4*>(kn + (lds_row(4 * tq + r) * PITCH + 8 * dgl) * 2) = Kc[uu][r];
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t p01 = __builtin_amdgcn_perm(Kc[uu][1][s >> 1], Kc[uu][0][s >> 1], sel);
-        const uint32_t p23 = __builtin_amdgcn_perm(Kc[uu][3][s >> 1], Kc[uu][2][s >> 1], sel);
-        const u32x2 pr = {p01, p23};
-        *reinterpret_cast<u32x2*>(kt + lds_row(8 * dgl + s) * PITCH + 4 * tq) = pr;
-      }
-    }
-    {
-      const f32x2 al = *reinterpret_cast<const f32x2*>(gw + 256 + 2 * vtp);  // alpha of rows 2vtp, 2vtp+1
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t pr = __builtin_amdgcn_perm(Vc[1][s >> 1], Vc[0][s >> 1], sel);
-        const int off = (8 * vg + s) * PITCH + 2 * vtp;
-        *reinterpret_cast<uint32_t*>(vt + off) = pr;
-        const float x0 = al[0] * bf_lo(pr), x1 = al[1] * bf_hi(pr);
-        const uint32_t hi = pack_bf16(x0, x1);
-        *reinterpret_cast<uint32_t*>(vbh + off) = hi;
-        *reinterpret_cast<uint32_t*>(vbl + off) = pack_bf16(x0 - bf_lo(hi), x1 - bf_hi(hi));
-      }
-      // rows 65..79 of the alpha-V tiles are zero (the previous chunk's H partials overwrote them)
-      constexpr int ZCH = 15 * PITCH / 8;  // 16-byte pieces
-      if (tid < ZCH) {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(vbh + 65 * PITCH + 8 * tid) = z;
-        *reinterpret_cast<u32x4*>(vbl + 65 * PITCH + 8 * tid) = z;
-      }
-      if (tid < 32) {  // row 64 of (alpha [V | 1])^T: alpha itself
-        const uint32_t hi = pack_bf16(al[0], al[1]);
-        *reinterpret_cast<uint32_t*>(vbh + 64 * PITCH + 2 * vtp) = hi;
-        *reinterpret_cast<uint32_t*>(vbl + 64 * PITCH + 2 * vtp) = pack_bf16(al[0] - bf_lo(hi), al[1] - bf_hi(hi));
-      }
-    }
-
-    __syncthreads();  // B1: V tiles visible to every wave, K tiles to their wave
-    if (kc + 1 < NC) load_kv(kc + 1);  // staging registers are free: prefetch the next chunk's k, v, gates
-
-    // ================= Q [C | n] (partial over this wave's d-slice)
-    f32x4 Hacc[4][NVX];
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) Hacc[it][vq] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int vq = 0; vq < NVX; ++vq) {
-      bf16x8 Cb[KP];
-#pragma unroll
-      for (int p = 0; p < KP; ++p) Cb[p] = pack8(Cacc[2 * p][vq], Cacc[2 * p + 1][vq]);
-#pragma unroll
-      for (int it = 0; it < 4; ++it)
-#pragma unroll
-        for (int p = 0; p < KP; ++p) Hacc[it][vq] = mfma(__builtin_bit_cast(bf16x8, Qc[it][p]), Cb[p], Hacc[it][vq]);
-    }
-
-    // ================= S^T = K Q^T (partial over the d-slice), causal tiles only
-    f32x4 Sacc[4][4];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      bf16x8 Ka[KP];
-#pragma unroll
-      for (int p = 0; p < KP; ++p)
-        Ka[p] = *reinterpret_cast<const bf16x8*>(kn + ((16 * jt + r16) * PITCH + 32 * p + 8 * g) * 2);
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        if ((jt >> 1) > (it >> 1)) continue;
-        Sacc[jt][it] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < KP; ++p) Sacc[jt][it] = mfma(Ka[p], __builtin_bit_cast(bf16x8, Qc[it][p]), Sacc[jt][it]);
-      }
-    }
-    if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch the next chunk's
-
-    // S^T partials -> this wave's slot (its K tile is dead)
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        if ((jt >> 1) > (it >> 1)) continue;
-        sred[(w * NST + st_slot(it, jt)) * 64 + lane] = Sacc[jt][it];
-      }
-
-    // ================= state update [C | n]' = gbar [C | n] + K^T (alpha [V | 1]) (hi + lo)
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      bf16x8 Ka[2];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) Ka[p] = *reinterpret_cast<const bf16x8*>(kt + (16 * dt + r16) * PITCH + 32 * p + 8 * g);
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) {
-        f32x4 c = Cacc[dt][vq] * gbar;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const int off = (16 * vq + r16) * PITCH + 32 * p + 8 * g;
-          c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbh + off), c);
-          c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbl + off), c);
-        }
-        Cacc[dt][vq] = c;
-      }
-    }
-
-    __syncthreads();  // B2: S^T partials visible
-
-    // ================= own rows i = 16w + r16: exact scores, gating, M [V | 1] with M split hi + lo
-    f32x4 Hmv[NVX];
-#pragma unroll
-    for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
-    {
-      const int i = 16 * w + r16;
-      const float bli = gw[i];
-      const int npj = (w >> 1) + 1;  // tile pairs with j-range starting at or before the own rows
-#pragma unroll
-      for (int pj = 0; pj < 2; ++pj) {
-        if (pj >= npj) break;
-        f32x4 Ms[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int jt = 2 * pj + hf;
-          const int slot = w < 2 ? 2 * w + jt : 4 + 4 * (w - 2) + jt;
-          f32x4 sv = sred[slot * 64 + lane];
-#pragma unroll
-          for (int src = 1; src < NW; ++src) sv += sred[(src * NST + slot) * 64 + lane];
-          const f32x4 ul = *reinterpret_cast<const f32x4*>(gw + 64 + 32 * pj + 8 * g + 4 * hf);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = 32 * pj + 8 * g + 4 * hf + e;
-            sv[e] = (j <= i) ? sv[e] * qk_scale * exp2_(bli + ul[e]) : 0.f;
-          }
-          Ms[hf] = sv;
-        }
-        bf16x8 mh, ml;
-        split8(Ms[0], Ms[1], mh, ml);
-#pragma unroll
-        for (int vq = 0; vq < NVX; ++vq) {
-          const bf16x8 vb = *reinterpret_cast<const bf16x8*>(vt + (16 * vq + r16) * PITCH + 32 * pj + 8 * g);
-          Hmv[vq] = mfma(mh, vb, Hmv[vq]);
-          Hmv[vq] = mfma(ml, vb, Hmv[vq]);
-        }
-      }
-    }
-
-    // ================= sum Q [C | n] over the waves; wave w finishes rows 16w..16w+15
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      if (it == w) continue;
-      const int slot = it < w ? it : it - 1;
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) hred[((w * 3 + slot) * NVX + vq) * 64 + lane] = Hacc[it][vq];
-    }
-    __syncthreads();  // B3: Q [C | n] partials visible (the K / S regions are dead)
-    {
-      const f32x4 qb = *reinterpret_cast<const f32x4*>(gw + 128 + 16 * w + 4 * g);  // rows 16w + 4g + e
-      const f32x4 mcr = *reinterpret_cast<const f32x4*>(gw + 192 + 16 * w + 4 * g);
-      f32x4 H[NVX];
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) {
-        f32x4 acc = (w == 0) ? Hacc[0][vq] : (w == 1) ? Hacc[1][vq] : (w == 2) ? Hacc[2][vq] : Hacc[3][vq];
-#pragma unroll
-        for (int src = 0; src < NW; ++src) {
-          if (src == w) continue;
-          const int slot = w < src ? w : w - 1;
-          acc += hred[((src * 3 + slot) * NVX + vq) * 64 + lane];
-        }
-        H[vq] = qb * acc + Hmv[vq];
-      }
-      bf16_t* hb = hh + (size_t)kc * L * DV + v0 + 16 * 0 + r16;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float den = __shfl(H[NVT][e], lane & 48, 64);  // column 64 lives in lane r16 == 0
-        const float inv = 1.0f / (fmaxf(fabsf(den), exp2_(-mcr[e] * LOG2E)) + eps);
-        const int i = 16 * w + 4 * g + e;
-#pragma unroll
-        for (int vq = 0; vq < NVT; ++vq) hb[(size_t)i * DV + 16 * vq] = from_f32<bf16_t>(H[vq][e] * inv);
-      }
-    }
-    __syncthreads();  // B4: H partial slots (aliasing the K regions) consumed
-    m_prev = m_next;
-  }
-
-  // ---- final states
-  if (c_last) {
+  if (w < NSW) {
+    // =====================================================================
+    // state waves: rows [dw0, dw0 + DW) of [C | n], stored as C e^{-G}
+    // =====================================================================
+    const int dw0 = ws * DW;
+    f32x4 Cacc[NDT][NVX];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int d = dw0 + phys(dt, g, e);
+        const int d = dw0 + 16 * dt + 4 * g + e;  // accumulator row 4g+e of tile dt
 #pragma unroll
         for (int vq = 0; vq < NVT; ++vq)
-          c_last[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] = Cacc[dt][vq][e];
-        if (v0 == 0 && r16 == 0) n_last[(size_t)bh * DQK + d] = Cacc[dt][NVT][e];
+          Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] : 0.f;
+        Cacc[dt][NVT][e] = (n0 && r16 == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
       }
-    if (v0 == 0 && tid == 0) m_last[bh] = m_prev;
+    // publish [C | n] as bf16 hi + lo B fragments (k-slice p of this wave's rows)
+    auto publish = [&]() {
+#pragma unroll
+      for (int p = 0; p < DW / 32; ++p)
+#pragma unroll
+        for (int vq = 0; vq < NVX; ++vq) {
+          bf16x8 hi, lo;
+          split8(Cacc[2 * p][vq], Cacc[2 * p + 1][vq], hi, lo);
+          const int x = (((DW / 32) * ws + p) * NVX + vq) * 64 + lane;
+          cb[x] = __builtin_bit_cast(u32x4, hi);
+          cb[KPD * NVX * 64 + x] = __builtin_bit_cast(u32x4, lo);
+        }
+    };
+    publish();        // the initial state, read by chunk 0's outputs
+    __syncthreads();  // B0
+
+    // V staging (state threads): rows t0 = 4*(tid>>4) + ((tid>>3)&1) and t0 + 2, columns 8*(tid&7)
+    const int vrow = 4 * (tid >> 4) + ((tid >> 3) & 1), vcol = 8 * (tid & 7);
+    u32x4 Kst[NKU], Vst[2];
+    float fcur, icur;
+    auto load_v = [&](int kc) {
+      const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
+      Vst[0] = *reinterpret_cast<const u32x4*>(vb + (size_t)vrow * DV);
+      Vst[1] = *reinterpret_cast<const u32x4*>(vb + (size_t)(vrow + 2) * DV);
+    };
+    load_k(0, Kst);
+    load_v(0);
+    load_gates(0, fcur, icur);
+    float m_prev = m_init, G = 0.f;
+    for (int kc = 0; kc < NC; ++kc) {
+      const Gates gt = gates(fcur, icur, m_prev, G);
+      store_k(Kst);
+      // V natural and (alpha' V)^T hi / lo
+      *reinterpret_cast<u32x4*>(vn + vrow * VN_PITCH + 2 * vcol) = Vst[0];
+      *reinterpret_cast<u32x4*>(vn + (vrow + 2) * VN_PITCH + 2 * vcol) = Vst[1];
+      {
+        const float al0 = gw[256 + vrow], al1 = gw[256 + vrow + 2];
+        const int col = vb_col(vrow);  // vb_col(vrow + 2) == col + 1
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) {
+          const uint32_t sel = (s2 & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t pr = __builtin_amdgcn_perm(Vst[1][s2 >> 1], Vst[0][s2 >> 1], sel);  // (v[t0][c], v[t0+2][c])
+          const float x0 = al0 * bf_lo(pr), x1 = al1 * bf_hi(pr);
+          const uint32_t hv = pack_bf16(x0, x1);
+          const int off = (vcol + s2) * VB_PITCH + 2 * col;
+          *reinterpret_cast<uint32_t*>(vbh + off) = hv;
+          *reinterpret_cast<uint32_t*>(vbl + off) = pack_bf16(x0 - bf_lo(hv), x1 - bf_hi(hv));
+        }
+      }
+      __syncthreads();  // B1: the chunk's tiles are visible
+      if (kc + 1 < NC) {  // staging registers are free: prefetch
+        load_k(kc + 1, Kst);
+        load_v(kc + 1);
+        load_gates(kc + 1, fcur, icur);
+      }
+      if (gt.renorm) {
+        const float sc = exp_(gt.G_prev + gt.lg);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int vq = 0; vq < NVX; ++vq) Cacc[dt][vq] *= sc;
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        bf16x8 Ka[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          // source lane 4k+a of group g: token 32p + 8g + 2k (+1), columns dw0 + 16dt + 4a .. +3
+          const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * (dw0 + 16 * dt + 4 * (r16 & 3));
+          Ka[p] = tr8(base, base + SM::KN_PITCH);
+        }
+#pragma unroll
+        for (int vq = 0; vq < NVX; ++vq) {
+          f32x4 c = Cacc[dt][vq];
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const int off = (16 * vq + r16) * VB_PITCH + 2 * (32 * p + 8 * g);
+            c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbh + off), c);
+            c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbl + off), c);
+          }
+          Cacc[dt][vq] = c;
+        }
+      }
+      // every output wave has read the previous state (before B1): publish the new one
+      publish();
+      __syncthreads();  // B2: published state complete; the chunk's tiles may be overwritten
+      m_prev = gt.m_next;
+      G = gt.Gn;
+    }
+    // ---- final states (undo the deferred rescale)
+    if (c_last) {
+      const float sc = exp_(G);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = dw0 + 16 * dt + 4 * g + e;
+#pragma unroll
+          for (int vq = 0; vq < NVT; ++vq)
+            c_last[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] = Cacc[dt][vq][e] * sc;
+          if (v0 == 0 && r16 == 0) n_last[(size_t)bh * DQK + d] = Cacc[dt][NVT][e] * sc;
+        }
+      if (v0 == 0 && tid == 0) m_last[bh] = m_prev;
+    }
+  } else {
+    // =====================================================================
+    // output waves: rows [16o, 16o + 16) of every chunk
+    // =====================================================================
+    const int o = ws;
+    u32x4 Kst[NKU], Qf[KPD];
+    float fcur, icur;
+    // q fragments of rows 16o + r16: k-slices 32p + 4g + {0..3} and 32p + 16 + 4g + {0..3}
+    auto load_q = [&](int kc) {
+      const bf16_t* qb = qh + ((size_t)kc * L + 16 * o + r16) * DQK + 4 * g;
+#pragma unroll
+      for (int p = 0; p < KPD; ++p) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(qb + 32 * p);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(qb + 32 * p + 16);
+        Qf[p] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+    };
+    load_k(0, Kst);
+    load_q(0);
+    load_gates(0, fcur, icur);
+    __syncthreads();  // B0: the initial state is published
+    float m_prev = m_init, G = 0.f;
+    for (int kc = 0; kc < NC; ++kc) {
+      // Q [C | n] with the state published for the previous chunk (hi + lo)
+      f32x4 Hqc[NVX];
+#pragma unroll
+      for (int vq = 0; vq < NVX; ++vq) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < KPD; ++p) {
+          const int x = (p * NVX + vq) * 64 + lane;
+          acc = mfma(__builtin_bit_cast(bf16x8, Qf[p]), __builtin_bit_cast(bf16x8, cb[x]), acc);
+          acc = mfma(__builtin_bit_cast(bf16x8, Qf[p]), __builtin_bit_cast(bf16x8, cb[KPD * NVX * 64 + x]), acc);
+        }
+        Hqc[vq] = acc;
+      }
+      const Gates gt = gates(fcur, icur, m_prev, G);
+      store_k(Kst);
+      if (o == 0) {  // row 64 of (alpha' [V | 1])^T: alpha' itself
+        const float al = gw[256 + lane];
+        const uint32_t hv = pack_bf16(al, 0.f);
+        reinterpret_cast<uint16_t*>(vbh + 64 * VB_PITCH)[vb_col(lane)] = (uint16_t)hv;
+        reinterpret_cast<uint16_t*>(vbl + 64 * VB_PITCH)[vb_col(lane)] = (uint16_t)pack_bf16(al - bf_lo(hv), 0.f);
+      }
+      __syncthreads();  // B1
+      if (kc + 1 < NC) {
+        load_k(kc + 1, Kst);
+        load_gates(kc + 1, fcur, icur);
+      }
+      // S^T tiles (j-tile jt <= o) over the whole DQK: A = K rows 16jt + r16, B = q rows
+      f32x4 Sacc[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (jt > o) continue;
+        const char* krow = kn + (16 * jt + r16) * SM::KN_PITCH + 8 * g;
+#pragma unroll
+        for (int p = 0; p < KPD; ++p) {
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(krow + 64 * p);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(krow + 64 * p + 32);
+          const u32x4 ka = {lo[0], lo[1], hi[0], hi[1]};
+          Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, ka), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
+        }
+      }
+      if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch
+      // gate the scores of row i = 16o + r16, then M [V | 1] with M split hi + lo
+      const int i = 16 * o + r16;
+      const float bli = gw[i];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        if (jt > o) continue;
+        const f32x4 ul = *reinterpret_cast<const f32x4*>(gw + 64 + 16 * jt + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 16 * jt + 4 * g + e;
+          Sacc[jt][e] = (j <= i) ? Sacc[jt][e] * qk_scale * exp2_(bli + ul[e]) : 0.f;
+        }
+      }
+      f32x4 Hmv[NVX];
+#pragma unroll
+      for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int pj = 0; pj < 2; ++pj) {
+        if (2 * pj > o) continue;
+        bf16x8 mh, ml;
+        split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
+#pragma unroll
+        for (int vq = 0; vq < NVX; ++vq) {
+          bf16x8 vb;
+          if (vq < NVT) {
+            // source lane 4k+a of group g: token 32pj + 4g + k (+16), columns 16vq + 4a .. +3
+            const char* base = vn + (32 * pj + 4 * g + (r16 >> 2)) * VN_PITCH + 2 * (16 * vq + 4 * (r16 & 3));
+            vb = tr8(base, base + 16 * VN_PITCH);
+          } else {  // [.. | 1]: column 64 is all ones
+            const uint32_t one = (r16 == 0) ? 0x3f803f80u : 0u;
+            vb = __builtin_bit_cast(bf16x8, u32x4{one, one, one, one});
+          }
+          Hmv[vq] = mfma(mh, vb, Hmv[vq]);
+          Hmv[vq] = mfma(ml, vb, Hmv[vq]);
+        }
+      }
+      // finish rows 16o + 4g + e
+      const f32x4 qb = *reinterpret_cast<const f32x4*>(gw + 128 + 16 * o + 4 * g);
+      const f32x4 mcr = *reinterpret_cast<const f32x4*>(gw + 192 + 16 * o + 4 * g);
+      bf16_t* hb = hh + (size_t)kc * L * DV + v0 + r16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float den = __shfl(qb[e] * Hqc[NVT][e] + Hmv[NVT][e], lane & 48, 64);  // column 64 is in lane r16 == 0
+        const float inv = 1.0f / (fmaxf(fabsf(den), exp_(-mcr[e])) + eps);
+        const size_t row = (size_t)(16 * o + 4 * g + e) * DV;
+#pragma unroll
+        for (int vq = 0; vq < NVT; ++vq)
+          hb[row + 16 * vq] = from_f32<bf16_t>((qb[e] * Hqc[vq][e] + Hmv[vq][e]) * inv);
+      }
+      __syncthreads();  // B2
+      m_prev = gt.m_next;
+      G = gt.Gn;
+    }
   }
 }
 
