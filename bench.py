@@ -1,17 +1,30 @@
 """Benchmark of the mLSTM kernel backend on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--chunk-size 64] [--algo auto]
-                    [--decode-steps 1000] [--no-cpu-baseline]
+                    [--decode-steps 1000] [--no-cpu-baseline] [--no-decode] [--no-soft-cap]
+    python bench.py --summarize-pmc FETCH_DIR WRITE_DIR      (no GPU: reads rocprofv3 CSVs)
 
 Prints ONE JSON line.  Headline (`value`): chunkwise mLSTM prefill tokens/s
 at BASELINE config 2 (bf16 q/k/v/gates, float32 states, B4 NH8 S8192 DQK256
 DV512, L=64, last states returned).  One step = one `mlstm_chunkwise` call
 over the whole batch (B*S = 32768 tokens) with inputs resident in HBM; L2 and
 the 256 MB Infinity Cache are flushed (512 MB write) before every timed call,
-and each call is timed with HIP events on the stream the kernels run on.
+and each call is timed with HIP events on the stream the kernels run on (the
+flush is queued without a host sync, so the events bracket the kernel and not
+the host-side launch latency).
 The decode step (config 1, B16 NH8 DQK256 DV512) is reported beside it in
 `decode`: 1000 chained steps over 6 rotating state sets (>256 MB, so the
-state really streams from HBM), captured in a HIP graph.
+state really streams from HBM), captured in a HIP graph.  `soft_cap` reports
+the logit soft-cap (cap 30) over config 3's prefill logits [1, 2048, 50304]
+bf16, a pure HBM stream; the same kernel serves as the known-size streaming
+kernel that calibrates the rocprofv3 FETCH_SIZE / WRITE_SIZE counters.
+
+HBM traffic (`roofline.traffic`) cannot be measured from inside the process:
+it comes from two rocprofv3 --pmc passes over this script (FETCH_SIZE, then
+WRITE_SIZE), each scaled by what the same counter reads for the soft-cap
+stream of known size.  `--summarize-pmc` turns those CSVs into
+profiles/hbm_traffic.json, which the timed run reports when its kernel and
+workload match.
 
 Roofline figures use algorithmic work only:
   prefill FLOP/call = B*NH*S*(4*DQK*DV + 2*L*(DQK+DV))      (1.6321e11 at L=64)
@@ -40,6 +53,10 @@ import torch  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+PREFILL_KERNEL = "chunkwise_fused_kernel"
+SOFT_CAP_KERNEL = "soft_cap_kernel"
+SOFT_CAP_SHAPE = (1, 2048, 50304)  # config 3 prefill logits
 
 
 def prefill_flops(B, NH, S, DQK, DV, L):
@@ -84,10 +101,10 @@ def bench_prefill(args, dev):
     times = []
     t_wall = 0.0
     for _ in range(args.steps):
-        flush()
         torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         w0 = time.perf_counter()
+        flush()  # ~0.1 ms on the GPU: hides the host-side launch latency of the call behind it
         e0.record(stream)
         call()
         e1.record(stream)
@@ -173,6 +190,94 @@ def bench_decode(args, dev):
     return {"us_per_step": us, "steps": steps, "bytes": by, "mode": mode, "state_sets": nsets, "cfg": cfg}
 
 
+def bench_soft_cap(args, dev):
+    """Logit soft-cap (cap 30) over config 3's prefill logits, bf16, through the C-ABI."""
+    from xlstm_hip import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = (40 * torch.randn(SOFT_CAP_SHAPE, generator=g, device=dev)).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    flush = Flusher(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def call():
+        _lib.check(lib.xl_soft_cap_fwd(x.data_ptr(), y.data_ptr(), x.numel(), 30.0, 1, stream.cuda_stream), "soft_cap")
+
+    for _ in range(3):
+        call()
+    times = []
+    for _ in range(max(5, args.steps)):
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        flush()
+        e0.record(stream)
+        call()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1))
+    us = 1e3 * statistics.mean(times)
+    by = 2 * x.numel() * x.element_size()
+    return {"workload": "cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16", "us_per_call": us,
+            "roofline": {"bound": "hbm", "achieved": by / (us * 1e-6) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": by / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, "bytes_per_call": by,
+                         "traffic": load_traffic(SOFT_CAP_KERNEL, "cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16")}}
+
+
+def load_traffic(kernel, workload):
+    """Calibrated HBM bytes per launch of `kernel` on `workload` from profiles/hbm_traffic.json, else None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            rec = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    ent = rec.get("kernels", {}).get(kernel)
+    if not ent or ent.get("workload") != workload:
+        return None
+    return ent.get("hbm_bytes_per_launch")
+
+
+def summarize_pmc(fetch_dir, write_dir):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of every kernel, scaled by the soft-cap stream's reading."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        acc = {}
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(fn) as fh:
+                for row in csv.DictReader(fh):
+                    if row["Counter_Name"] != counter:
+                        continue
+                    name = row["Kernel_Name"]
+                    key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel") if k in name), None)
+                    if key is None:
+                        continue
+                    acc.setdefault(key, {}).setdefault(row["Dispatch_Id"], 0.0)
+                    acc[key][row["Dispatch_Id"]] += float(row["Counter_Value"])  # summed over TCC instances
+        return {k: statistics.median(v.values()) * 1024 for k, v in acc.items()}  # KiB -> bytes
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    if SOFT_CAP_KERNEL not in fetch or SOFT_CAP_KERNEL not in write:
+        raise SystemExit("summarize-pmc: the soft-cap calibration stream is missing from the CSVs")
+    sc_bytes = 2 * SOFT_CAP_SHAPE[0] * SOFT_CAP_SHAPE[1] * SOFT_CAP_SHAPE[2]  # read once, written once
+    f_scale, w_scale = sc_bytes / fetch[SOFT_CAP_KERNEL], sc_bytes / write[SOFT_CAP_KERNEL]
+    from xlstm_hip.workloads import CFG1, CFG2
+    work = {PREFILL_KERNEL: ("cfg2 mlstm_chunkwise prefill",
+                             prefill_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV)),
+            SOFT_CAP_KERNEL: ("cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16", 2 * sc_bytes),
+            "mlstm_step_kernel": ("cfg1 mlstm decode step", decode_bytes(CFG1.B, CFG1.NH, CFG1.DQK, CFG1.DV))}
+    out = {"calibration": {"kernel": SOFT_CAP_KERNEL, "bytes_read": sc_bytes, "bytes_written": sc_bytes,
+                           "fetch_scale": f_scale, "write_scale": w_scale},
+           "kernels": {}}
+    for k in sorted(set(fetch) & set(write)):
+        rd, wr = fetch[k] * f_scale, write[k] * w_scale
+        out["kernels"][k] = {"workload": work[k][0], "fetch_bytes": rd, "write_bytes": wr,
+                             "hbm_bytes_per_launch": rd + wr, "algorithmic_bytes": work[k][1],
+                             "ratio_to_algorithmic": (rd + wr) / work[k][1],
+                             "raw_fetch_kib": fetch[k] / 1024, "raw_write_kib": write[k] / 1024}
+    print(json.dumps(out, indent=1))
+
+
 def cpu_baseline(args):
     """Oracle (torch on the host) on a bounded sample: prefill tokens/s and decode us/step."""
     from oracle import mlstm as om
@@ -216,7 +321,12 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-soft-cap", action="store_true")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on ONE GPU only (no collectives); use --gpus 1", file=sys.stderr)
         sys.exit(2)
@@ -241,7 +351,9 @@ def main():
                    "DQK": cfg.DQK, "DV": cfg.DV, "chunk_size": pre["L"], "states": "fp32",
                    "return_last_states": True, "algo": args.algo},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / PEAK_BF16_TFLOPS, "traffic": None,
+                     "frac": tflops / PEAK_BF16_TFLOPS,
+                     "traffic": load_traffic(PREFILL_KERNEL, "cfg2 mlstm_chunkwise prefill")
+                     if (pre["L"] == 64 and args.algo in ("auto", "fused")) else None,
                      "flops_per_call": pre["flops"], "timing": "HIP events per call, caches flushed"},
         "roofline_hbm": {"achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
                          "bytes_per_call": pre["bytes"]},
@@ -254,7 +366,10 @@ def main():
                          "tokens_per_s": dec["cfg"].B / (dec["us_per_step"] * 1e-6), "steps": dec["steps"],
                          "mode": dec["mode"], "state_sets": dec["state_sets"],
                          "roofline": {"bound": "hbm", "achieved": dgbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                      "frac": dgbs / PEAK_HBM_GBS, "bytes_per_step": dec["bytes"]}}
+                                      "frac": dgbs / PEAK_HBM_GBS, "bytes_per_step": dec["bytes"],
+                                      "traffic": load_traffic("mlstm_step_kernel", "cfg1 mlstm decode step")}}
+    if not args.no_soft_cap:
+        out["soft_cap"] = bench_soft_cap(args, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(out), flush=True)

@@ -23,20 +23,18 @@
 //
 // Producer / consumer split (8 waves, two per SIMD):
 //  * state waves 0..3: wave s owns rows [s*DW, (s+1)*DW) of [C | n]
-//    (DW = DQK/4, float32 accumulators) and applies the chunk update
-//    [C | n] += K^T (alpha [V | 1]) with alpha V split into bf16 hi + lo (two
-//    MFMAs, so the state keeps float32 accuracy).  It then publishes [C | n]
-//    as bf16 hi + lo into an LDS buffer laid out as ready-made MFMA B
-//    fragments.
+//    (DW = DQK/4, float32 accumulators).  Per chunk it first forms the
+//    partial product Q[:, rows] [C | n][rows, :] for all 64 tokens, with the
+//    B operand built straight from its accumulators as bf16 hi + lo (two
+//    MFMAs, so q C keeps float32 accuracy), and leaves it in LDS.  It then
+//    applies the chunk update [C | n] += K^T (alpha [V | 1]) with alpha V
+//    split into bf16 hi + lo, so the state keeps float32 accuracy too.
 //  * output waves 4..7: wave o owns output rows [16o, 16o+16) of every chunk:
-//    Q [C | n] with the state published for the previous chunk (hi and lo:
-//    two MFMAs, so q C keeps float32 accuracy), then exact S^T = K Q^T over
-//    the whole DQK, gating and M [V | 1] (M split hi + lo).  No partial sums
-//    cross waves.
-// One state buffer suffices: the output waves finish Q [C | n] before the
-// chunk's first barrier and the state waves overwrite the buffer only after
-// it, so per chunk the output waves' q C MFMAs overlap the state waves' tile
-// staging and the state waves' K^T V MFMAs overlap the output waves' S / M V.
+//    exact S^T = K Q^T over the whole DQK, gating and M [V | 1] (M split
+//    hi + lo); after the chunk's second barrier it adds the four partial
+//    Q [C | n] rows and writes h.
+// The state never leaves the state waves' registers; the only cross-wave
+// traffic besides the staged q/k/v tiles is the 16-byte-per-lane partials.
 // All products are v_mfma_f32_16x16x32_bf16.  K^T and V operands are read
 // with ds_read_b64_tr_b16 from the natural row-major tiles (within 16 lanes,
 // output lane 4a+c receives element c of source lanes 4k+a, k = 0..3), with
@@ -128,6 +126,14 @@ __device__ __forceinline__ float wave_scan(float x) {
   return x;
 }
 
+__device__ __forceinline__ float lane63(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+// x of lane 16r in every lane of row r (DPP row_newbcast:0)
+__device__ __forceinline__ float row_bcast0(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150, 0xf, 0xf, false));
+}
+
 // Column of token t in the (alpha [V | 1])^T tiles: inside each 8-token block
 // the order is (t even first), matching the transposed K operand whose k-slice
 // of lane group g is t = 32p + 8g + 2k + h (k = 0..3, h = read 0/1).
@@ -141,9 +147,8 @@ struct Smem {
   static constexpr int VN = KN + 64 * KN_PITCH;          // [64 t][VN_PITCH]: V natural
   static constexpr int VBH = VN + 64 * VN_PITCH;         // [80 v][VB_PITCH]: (alpha [V | 1])^T hi
   static constexpr int VBL = VBH + 80 * VB_PITCH;        // ... lo
-  static constexpr int CB = VBL + 80 * VB_PITCH;         // [hi, lo][KPD][NVX][64] x 16 B: [C | n] B fragments
-  static constexpr int CB_BUF = KPD * NVX * 64 * 16;
-  static constexpr int GATES = CB + 2 * CB_BUF;          // [8 waves][5][64] float
+  static constexpr int HP = VBL + 80 * VB_PITCH;         // [4 state waves][4 row tiles][NVX][64] f32x4: partial Q [C | n]
+  static constexpr int GATES = HP + 4 * 4 * NVX * 64 * 16;  // [8 waves][5][64] float
   static constexpr int BYTES = GATES + 8 * 5 * 64 * 4;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
@@ -160,6 +165,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
   constexpr int NDT = DW / 16;    // C row tiles per state wave
   constexpr int NKU = DQK / 64;   // K staging: 16-byte pieces per thread (64 rows x DQK / 512 threads / 8)
+  constexpr int KS = DW / 32;     // 32-deep k-steps over a state wave's rows
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x;
@@ -180,7 +186,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   char* vn = smem + SM::VN;
   char* vbh = smem + SM::VBH;
   char* vbl = smem + SM::VBL;
-  u32x4* cb = (u32x4*)(smem + SM::CB);
+  f32x4* hp = (f32x4*)(smem + SM::HP);
   float* gw = (float*)(smem + SM::GATES) + w * 5 * 64;  // this wave's rows: bl, ul, qbar, mc, alpha'
 
   // constant rows 65..79 of the alpha-V tiles (zeros); row 64 is rewritten every chunk
@@ -213,9 +219,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       *reinterpret_cast<u32x4*>(kn + (piece / (DQK / 8)) * SM::KN_PITCH + 16 * (piece % (DQK / 8))) = Kst[u];
     }
   };
-  auto load_gates = [&](int kc, float& fr, float& ir) {
-    fr = to_f32(fh[(size_t)kc * L + lane]);
-    ir = to_f32(ih[(size_t)kc * L + lane]);
+  // gates stay in their storage type until the chunk that uses them, so the
+  // prefetch never waits for the load to land
+  auto load_gates = [&](int kc, TG& fr, TG& ir) {
+    fr = fh[(size_t)kc * L + lane];
+    ir = ih[(size_t)kc * L + lane];
   };
   // Gates of one chunk (every wave, lane = token).  Writes this wave's gate rows
   // and returns m', the log rescale lg, and the updated deferred rescale.
@@ -223,9 +231,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   auto gates = [&](float fcur, float icur, float m_prev, float G) {
     Gates r;
     const float b = wave_scan<false>(logsig_fast(fcur));
-    const float gsum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 63));
+    const float gsum = lane63(b);
     const float a = gsum - b + icur;
-    r.m_next = fmaxf(gsum + m_prev, wave_max(a));
+    r.m_next = fmaxf(gsum + m_prev, lane63(wave_scan<true>(a)));
     r.lg = gsum + m_prev - r.m_next;  // log of this chunk's rescale of the state (<= 0)
     r.G_prev = G;
     r.Gn = G + r.lg;
@@ -258,37 +266,37 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] : 0.f;
         Cacc[dt][NVT][e] = (n0 && r16 == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
       }
-    // publish [C | n] as bf16 hi + lo B fragments (k-slice p of this wave's rows)
-    auto publish = [&]() {
-#pragma unroll
-      for (int p = 0; p < DW / 32; ++p)
-#pragma unroll
-        for (int vq = 0; vq < NVX; ++vq) {
-          bf16x8 hi, lo;
-          split8(Cacc[2 * p][vq], Cacc[2 * p + 1][vq], hi, lo);
-          const int x = (((DW / 32) * ws + p) * NVX + vq) * 64 + lane;
-          cb[x] = __builtin_bit_cast(u32x4, hi);
-          cb[KPD * NVX * 64 + x] = __builtin_bit_cast(u32x4, lo);
-        }
-    };
-    publish();        // the initial state, read by chunk 0's outputs
-    __syncthreads();  // B0
 
     // V staging (state threads): rows t0 = 4*(tid>>4) + ((tid>>3)&1) and t0 + 2, columns 8*(tid&7)
     const int vrow = 4 * (tid >> 4) + ((tid >> 3) & 1), vcol = 8 * (tid & 7);
     u32x4 Kst[NKU], Vst[2];
-    float fcur, icur;
+    // q fragments of this wave's k range for every row: rows 16rt + r16, columns
+    // dw0 + 32p + 4g + {0..3} and dw0 + 32p + 16 + 4g + {0..3} -- the k order of
+    // the B fragments that split8(Cacc[2p], Cacc[2p+1]) yields
+    u32x2 Qs[4][KS][2];
+    TG fraw, iraw;
     auto load_v = [&](int kc) {
       const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
       Vst[0] = *reinterpret_cast<const u32x4*>(vb + (size_t)vrow * DV);
       Vst[1] = *reinterpret_cast<const u32x4*>(vb + (size_t)(vrow + 2) * DV);
     };
+    auto load_qs = [&](int kc) {
+      const bf16_t* qb = qh + ((size_t)kc * L + r16) * DQK + dw0 + 4 * g;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int p = 0; p < KS; ++p) {
+          Qs[rt][p][0] = *reinterpret_cast<const u32x2*>(qb + (size_t)16 * rt * DQK + 32 * p);
+          Qs[rt][p][1] = *reinterpret_cast<const u32x2*>(qb + (size_t)16 * rt * DQK + 32 * p + 16);
+        }
+    };
     load_k(0, Kst);
     load_v(0);
-    load_gates(0, fcur, icur);
+    load_qs(0);
+    load_gates(0, fraw, iraw);
     float m_prev = m_init, G = 0.f;
     for (int kc = 0; kc < NC; ++kc) {
-      const Gates gt = gates(fcur, icur, m_prev, G);
+      const Gates gt = gates(to_f32(fraw), to_f32(iraw), m_prev, G);
       store_k(Kst);
       // V natural and (alpha' V)^T hi / lo
       *reinterpret_cast<u32x4*>(vn + vrow * VN_PITCH + 2 * vcol) = Vst[0];
@@ -307,11 +315,33 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           *reinterpret_cast<uint32_t*>(vbl + off) = pack_bf16(x0 - bf_lo(hv), x1 - bf_hi(hv));
         }
       }
-      __syncthreads();  // B1: the chunk's tiles are visible
+      __syncthreads();  // B1: the chunk's tiles are visible; the previous chunk's partials have been read
+      // partial Q [C | n] over this wave's rows, with the state before this chunk
+      // (bf16 hi + lo of the float32 accumulators, so q C keeps float32 accuracy)
+#pragma unroll
+      for (int vq = 0; vq < NVX; ++vq) {
+        f32x4 Hp[4];
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) Hp[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < KS; ++p) {
+          bf16x8 bh, bl;
+          split8(Cacc[2 * p][vq], Cacc[2 * p + 1][vq], bh, bl);
+#pragma unroll
+          for (int rt = 0; rt < 4; ++rt) {
+            const u32x4 qa = {Qs[rt][p][0][0], Qs[rt][p][0][1], Qs[rt][p][1][0], Qs[rt][p][1][1]};
+            Hp[rt] = mfma(__builtin_bit_cast(bf16x8, qa), bh, Hp[rt]);
+            Hp[rt] = mfma(__builtin_bit_cast(bf16x8, qa), bl, Hp[rt]);
+          }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + vq) * 64 + lane] = Hp[rt];
+      }
       if (kc + 1 < NC) {  // staging registers are free: prefetch
         load_k(kc + 1, Kst);
         load_v(kc + 1);
-        load_gates(kc + 1, fcur, icur);
+        load_qs(kc + 1);
+        load_gates(kc + 1, fraw, iraw);
       }
       if (gt.renorm) {
         const float sc = exp_(gt.G_prev + gt.lg);
@@ -320,30 +350,31 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
           for (int vq = 0; vq < NVX; ++vq) Cacc[dt][vq] *= sc;
       }
+      // K^T fragments of all this wave's row tiles stay in registers, so every
+      // (alpha [V | 1])^T fragment is read from LDS once per wave
+      bf16x8 Ka[NDT][2];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        bf16x8 Ka[2];
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           // source lane 4k+a of group g: token 32p + 8g + 2k (+1), columns dw0 + 16dt + 4a .. +3
           const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * (dw0 + 16 * dt + 4 * (r16 & 3));
-          Ka[p] = tr8(base, base + SM::KN_PITCH);
+          Ka[dt][p] = tr8(base, base + SM::KN_PITCH);
         }
 #pragma unroll
-        for (int vq = 0; vq < NVX; ++vq) {
-          f32x4 c = Cacc[dt][vq];
+      for (int vq = 0; vq < NVX; ++vq)
 #pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            const int off = (16 * vq + r16) * VB_PITCH + 2 * (32 * p + 8 * g);
-            c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbh + off), c);
-            c = mfma(Ka[p], *reinterpret_cast<const bf16x8*>(vbl + off), c);
+        for (int p = 0; p < 2; ++p) {
+          const int off = (16 * vq + r16) * VB_PITCH + 2 * (32 * p + 8 * g);
+          const bf16x8 bh = *reinterpret_cast<const bf16x8*>(vbh + off);
+          const bf16x8 bl = *reinterpret_cast<const bf16x8*>(vbl + off);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            Cacc[dt][vq] = mfma(Ka[dt][p], bh, Cacc[dt][vq]);
+            Cacc[dt][vq] = mfma(Ka[dt][p], bl, Cacc[dt][vq]);
           }
-          Cacc[dt][vq] = c;
         }
-      }
-      // every output wave has read the previous state (before B1): publish the new one
-      publish();
-      __syncthreads();  // B2: published state complete; the chunk's tiles may be overwritten
+      __syncthreads();  // B2: partials complete; the chunk's tiles may be overwritten
       m_prev = gt.m_next;
       G = gt.Gn;
     }
@@ -368,7 +399,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // =====================================================================
     const int o = ws;
     u32x4 Kst[NKU], Qf[KPD];
-    float fcur, icur;
+    TG fraw, iraw;
     // q fragments of rows 16o + r16: k-slices 32p + 4g + {0..3} and 32p + 16 + 4g + {0..3}
     auto load_q = [&](int kc) {
       const bf16_t* qb = qh + ((size_t)kc * L + 16 * o + r16) * DQK + 4 * g;
@@ -381,24 +412,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     };
     load_k(0, Kst);
     load_q(0);
-    load_gates(0, fcur, icur);
-    __syncthreads();  // B0: the initial state is published
+    load_gates(0, fraw, iraw);
     float m_prev = m_init, G = 0.f;
     for (int kc = 0; kc < NC; ++kc) {
-      // Q [C | n] with the state published for the previous chunk (hi + lo)
-      f32x4 Hqc[NVX];
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < KPD; ++p) {
-          const int x = (p * NVX + vq) * 64 + lane;
-          acc = mfma(__builtin_bit_cast(bf16x8, Qf[p]), __builtin_bit_cast(bf16x8, cb[x]), acc);
-          acc = mfma(__builtin_bit_cast(bf16x8, Qf[p]), __builtin_bit_cast(bf16x8, cb[KPD * NVX * 64 + x]), acc);
-        }
-        Hqc[vq] = acc;
-      }
-      const Gates gt = gates(fcur, icur, m_prev, G);
+      const Gates gt = gates(to_f32(fraw), to_f32(iraw), m_prev, G);
       store_k(Kst);
       if (o == 0) {  // row 64 of (alpha' [V | 1])^T: alpha' itself
         const float al = gw[256 + lane];
@@ -409,22 +426,33 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       __syncthreads();  // B1
       if (kc + 1 < NC) {
         load_k(kc + 1, Kst);
-        load_gates(kc + 1, fcur, icur);
+        load_gates(kc + 1, fraw, iraw);
       }
-      // S^T tiles (j-tile jt <= o) over the whole DQK: A = K rows 16jt + r16, B = q rows
+      // S^T tiles of all four j-tiles over the whole DQK: A = K rows 16jt + r16,
+      // B = q rows.  Every output wave computes all four (tiles above the
+      // diagonal are masked in the gating), so the code is branch-free and the
+      // K fragments of step p+1 load while step p multiplies; the busiest SIMD
+      // (the wave of the last row tile) does the same work as before.
       f32x4 Sacc[4];
+      u32x4 kf[2][4];
+      auto load_kf = [&](int p, u32x4 (&dst)[4]) {
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (jt > o) continue;
-        const char* krow = kn + (16 * jt + r16) * SM::KN_PITCH + 8 * g;
-#pragma unroll
-        for (int p = 0; p < KPD; ++p) {
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(krow + 64 * p);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(krow + 64 * p + 32);
-          const u32x4 ka = {lo[0], lo[1], hi[0], hi[1]};
-          Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, ka), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
+        for (int jt = 0; jt < 4; ++jt) {
+          const char* krow = kn + (16 * jt + r16) * SM::KN_PITCH + 8 * g + 64 * p;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(krow);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(krow + 32);
+          dst[jt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
+      };
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      load_kf(0, kf[0]);
+#pragma unroll
+      for (int p = 0; p < KPD; ++p) {
+        if (p + 1 < KPD) load_kf(p + 1, kf[(p + 1) & 1]);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+          Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p & 1][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
       }
       if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch
       // gate the scores of row i = 16o + r16, then M [V | 1] with M split hi + lo
@@ -432,7 +460,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       const float bli = gw[i];
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        if (jt > o) continue;
         const f32x4 ul = *reinterpret_cast<const f32x4*>(gw + 64 + 16 * jt + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -445,7 +472,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int pj = 0; pj < 2; ++pj) {
-        if (2 * pj > o) continue;
         bf16x8 mh, ml;
         split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
 #pragma unroll
@@ -463,20 +489,28 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           Hmv[vq] = mfma(ml, vb, Hmv[vq]);
         }
       }
+      __syncthreads();  // B2: the state waves' partial Q [C | n] of this chunk are complete
+      // Q [C | n] of rows 16o + 4g + e: sum of the four state waves' partials
+      f32x4 Hqc[NVX];
+#pragma unroll
+      for (int vq = 0; vq < NVX; ++vq) {
+        Hqc[vq] = hp[((0 * 4 + o) * NVX + vq) * 64 + lane];
+#pragma unroll
+        for (int sw = 1; sw < NSW; ++sw) Hqc[vq] += hp[((sw * 4 + o) * NVX + vq) * 64 + lane];
+      }
       // finish rows 16o + 4g + e
       const f32x4 qb = *reinterpret_cast<const f32x4*>(gw + 128 + 16 * o + 4 * g);
       const f32x4 mcr = *reinterpret_cast<const f32x4*>(gw + 192 + 16 * o + 4 * g);
       bf16_t* hb = hh + (size_t)kc * L * DV + v0 + r16;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float den = __shfl(qb[e] * Hqc[NVT][e] + Hmv[NVT][e], lane & 48, 64);  // column 64 is in lane r16 == 0
-        const float inv = 1.0f / (fmaxf(fabsf(den), exp_(-mcr[e])) + eps);
+        const float den = row_bcast0(qb[e] * Hqc[NVT][e] + Hmv[NVT][e]);  // column 64 is in lane r16 == 0
+        const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr[e])) + eps);
         const size_t row = (size_t)(16 * o + 4 * g + e) * DV;
 #pragma unroll
         for (int vq = 0; vq < NVT; ++vq)
           hb[row + 16 * vq] = from_f32<bf16_t>((qb[e] * Hqc[vq][e] + Hmv[vq][e]) * inv);
       }
-      __syncthreads();  // B2
       m_prev = gt.m_next;
       G = gt.Gn;
     }
