@@ -129,10 +129,14 @@ __device__ __forceinline__ float wave_scan(float x) {
 __device__ __forceinline__ float lane63(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
-// x of lane 16r in every lane of row r (DPP row_newbcast:0)
-__device__ __forceinline__ float row_bcast0(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150, 0xf, 0xf, false));
-}
+
+// Column of the 64-wide DV tile held by column n of 16-wide tile vq (vq < 4):
+// runs of 4 consecutive columns, and the tile pair (2h, 2h+1) covers columns
+// 32h .. 32h+31 so that a lane of the transposed output holds 8 consecutive
+// columns (one 16-byte store).
+__device__ __forceinline__ int vcol_of(int vq, int n) { return 32 * (vq >> 1) + 8 * (n >> 2) + 4 * (vq & 1) + (n & 3); }
+// Row of the (alpha [V | 1])^T tiles that holds DV-tile column c (inverse of vcol_of)
+__device__ __forceinline__ int vrow_of(int c) { return 16 * (2 * (c >> 5) + ((c >> 2) & 1)) + 4 * ((c >> 3) & 3) + (c & 3); }
 
 // Column of token t in the (alpha [V | 1])^T tiles: inside each 8-token block
 // the order is (t even first), matching the transposed K operand whose k-slice
@@ -254,26 +258,33 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // =====================================================================
     // state waves: rows [dw0, dw0 + DW) of [C | n], stored as C e^{-G}
     // =====================================================================
+    // Row 4a + c of accumulator tile dt holds state row d = dw0 + 32 (dt >> 1) +
+    // 8a + 4 (dt & 1) + c: each tile's rows come in runs of 4 consecutive d (what
+    // a transposed K read delivers), and the tile pair (2p, 2p+1) covers the 32
+    // consecutive d = dw0 + 32p .. +31 in k order, so q fragments are one
+    // 16-byte load.
     const int dw0 = ws * DW;
+    auto crow = [&](int dt, int a, int c) { return dw0 + 32 * (dt >> 1) + 8 * a + 4 * (dt & 1) + c; };
     f32x4 Cacc[NDT][NVX];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int d = dw0 + 16 * dt + 4 * g + e;  // accumulator row 4g+e of tile dt
+        const int d = crow(dt, g, e);  // accumulator row 4g+e of tile dt
 #pragma unroll
         for (int vq = 0; vq < NVT; ++vq)
-          Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] : 0.f;
-        Cacc[dt][NVT][e] = (n0 && r16 == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
+          Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + vcol_of(vq, r16)] : 0.f;
+        // n is replicated in columns 0, 4, 8, 12 of the fifth tile
+        Cacc[dt][NVT][e] = (n0 && (r16 & 3) == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
       }
 
     // V staging (state threads): rows t0 = 4*(tid>>4) + ((tid>>3)&1) and t0 + 2, columns 8*(tid&7)
     const int vrow = 4 * (tid >> 4) + ((tid >> 3) & 1), vcol = 8 * (tid & 7);
     u32x4 Kst[NKU], Vst[2];
     // q fragments of this wave's k range for every row: rows 16rt + r16, columns
-    // dw0 + 32p + 4g + {0..3} and dw0 + 32p + 16 + 4g + {0..3} -- the k order of
-    // the B fragments that split8(Cacc[2p], Cacc[2p+1]) yields
-    u32x2 Qs[4][KS][2];
+    // dw0 + 32p + 8g .. +7 -- the k order of the B fragments that
+    // split8(Cacc[2p], Cacc[2p+1]) yields
+    u32x4 Qs[4][KS];
     TG fraw, iraw;
     auto load_v = [&](int kc) {
       const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
@@ -281,14 +292,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       Vst[1] = *reinterpret_cast<const u32x4*>(vb + (size_t)(vrow + 2) * DV);
     };
     auto load_qs = [&](int kc) {
-      const bf16_t* qb = qh + ((size_t)kc * L + r16) * DQK + dw0 + 4 * g;
+      const bf16_t* qb = qh + ((size_t)kc * L + r16) * DQK + dw0 + 8 * g;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int p = 0; p < KS; ++p) {
-          Qs[rt][p][0] = *reinterpret_cast<const u32x2*>(qb + (size_t)16 * rt * DQK + 32 * p);
-          Qs[rt][p][1] = *reinterpret_cast<const u32x2*>(qb + (size_t)16 * rt * DQK + 32 * p + 16);
-        }
+        for (int p = 0; p < KS; ++p) Qs[rt][p] = *reinterpret_cast<const u32x4*>(qb + (size_t)16 * rt * DQK + 32 * p);
     };
     load_k(0, Kst);
     load_v(0);
@@ -310,39 +318,61 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           const uint32_t pr = __builtin_amdgcn_perm(Vst[1][s2 >> 1], Vst[0][s2 >> 1], sel);  // (v[t0][c], v[t0+2][c])
           const float x0 = al0 * bf_lo(pr), x1 = al1 * bf_hi(pr);
           const uint32_t hv = pack_bf16(x0, x1);
-          const int off = (vcol + s2) * VB_PITCH + 2 * col;
+          const int off = vrow_of(vcol + s2) * VB_PITCH + 2 * col;
           *reinterpret_cast<uint32_t*>(vbh + off) = hv;
           *reinterpret_cast<uint32_t*>(vbl + off) = pack_bf16(x0 - bf_lo(hv), x1 - bf_hi(hv));
         }
       }
       __syncthreads();  // B1: the chunk's tiles are visible; the previous chunk's partials have been read
-      // partial Q [C | n] over this wave's rows, with the state before this chunk
-      // (bf16 hi + lo of the float32 accumulators, so q C keeps float32 accuracy)
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) {
-        f32x4 Hp[4];
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) Hp[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < KS; ++p) {
-          bf16x8 bh, bl;
-          split8(Cacc[2 * p][vq], Cacc[2 * p + 1][vq], bh, bl);
-#pragma unroll
-          for (int rt = 0; rt < 4; ++rt) {
-            const u32x4 qa = {Qs[rt][p][0][0], Qs[rt][p][0][1], Qs[rt][p][1][0], Qs[rt][p][1][1]};
-            Hp[rt] = mfma(__builtin_bit_cast(bf16x8, qa), bh, Hp[rt]);
-            Hp[rt] = mfma(__builtin_bit_cast(bf16x8, qa), bl, Hp[rt]);
-          }
-        }
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + vq) * 64 + lane] = Hp[rt];
-      }
-      if (kc + 1 < NC) {  // staging registers are free: prefetch
+      if (kc + 1 < NC) {  // staging registers are free: prefetch (q after its last use below)
         load_k(kc + 1, Kst);
         load_v(kc + 1);
-        load_qs(kc + 1);
         load_gates(kc + 1, fraw, iraw);
       }
+      // partial Q [C | n] over this wave's rows, with the state before this chunk
+      // (bf16 hi + lo of the float32 accumulators, so q C keeps float32 accuracy).
+      // Transposed product [C | n]^T Q^T: lane (g, r16) gets columns 4g+e of
+      // token 16rt + r16.  Software pipelined: the split of tile vq+1 (VALU) is
+      // interleaved with the MFMAs of tile vq, and tile vq's partials are stored
+      // one tile later, when its MFMAs have retired.
+      {
+        bf16x8 bsp[2][KS][2];
+        f32x4 Hp[2][4];
+#pragma unroll
+        for (int p = 0; p < KS; ++p) split8(Cacc[2 * p][0], Cacc[2 * p + 1][0], bsp[0][p][0], bsp[0][p][1]);
+#pragma unroll
+        for (int vq = 0; vq < NVX; ++vq) {
+          const int cur = vq & 1;
+          if (vq + 1 < NVX) {
+#pragma unroll
+            for (int p = 0; p < KS; ++p)
+              split8(Cacc[2 * p][vq + 1], Cacc[2 * p + 1][vq + 1], bsp[cur ^ 1][p][0], bsp[cur ^ 1][p][1]);
+          }
+#pragma unroll
+          for (int rt = 0; rt < 4; ++rt) Hp[cur][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int p = 0; p < KS; ++p)
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+              Hp[cur][rt] = mfma(bsp[cur][p][0], __builtin_bit_cast(bf16x8, Qs[rt][p]), Hp[cur][rt]);
+              Hp[cur][rt] = mfma(bsp[cur][p][1], __builtin_bit_cast(bf16x8, Qs[rt][p]), Hp[cur][rt]);
+            }
+          if (vq > 0) {
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + vq - 1) * 64 + lane] = Hp[cur ^ 1][rt];
+          }
+          // ask the scheduler for 1 MFMA : 3 VALU, then the stores
+#pragma unroll
+          for (int u = 0; u < 8 * KS; ++u) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + NVX - 1) * 64 + lane] = Hp[(NVX - 1) & 1][rt];
+      }
+      if (kc + 1 < NC) load_qs(kc + 1);
       if (gt.renorm) {
         const float sc = exp_(gt.G_prev + gt.lg);
 #pragma unroll
@@ -357,8 +387,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-          // source lane 4k+a of group g: token 32p + 8g + 2k (+1), columns dw0 + 16dt + 4a .. +3
-          const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * (dw0 + 16 * dt + 4 * (r16 & 3));
+          // source lane 4k+a of group g: token 32p + 8g + 2k (+1), state rows crow(dt, a, 0 .. 3)
+          const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * crow(dt, r16 & 3, 0);
           Ka[dt][p] = tr8(base, base + SM::KN_PITCH);
         }
 #pragma unroll
@@ -385,10 +415,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int d = dw0 + 16 * dt + 4 * g + e;
+          const int d = crow(dt, g, e);
 #pragma unroll
           for (int vq = 0; vq < NVT; ++vq)
-            c_last[((size_t)bh * DQK + d) * DV + v0 + 16 * vq + r16] = Cacc[dt][vq][e] * sc;
+            c_last[((size_t)bh * DQK + d) * DV + v0 + vcol_of(vq, r16)] = Cacc[dt][vq][e] * sc;
           if (v0 == 0 && r16 == 0) n_last[(size_t)bh * DQK + d] = Cacc[dt][NVT][e] * sc;
         }
       if (v0 == 0 && tid == 0) m_last[bh] = m_prev;
@@ -400,15 +430,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     const int o = ws;
     u32x4 Kst[NKU], Qf[KPD];
     TG fraw, iraw;
-    // q fragments of rows 16o + r16: k-slices 32p + 4g + {0..3} and 32p + 16 + 4g + {0..3}
+    // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
+    // 16-byte load; the K operand below uses the same contiguous k order)
     auto load_q = [&](int kc) {
-      const bf16_t* qb = qh + ((size_t)kc * L + 16 * o + r16) * DQK + 4 * g;
+      const bf16_t* qb = qh + ((size_t)kc * L + 16 * o + r16) * DQK + 8 * g;
 #pragma unroll
-      for (int p = 0; p < KPD; ++p) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(qb + 32 * p);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(qb + 32 * p + 16);
-        Qf[p] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
+      for (int p = 0; p < KPD; ++p) Qf[p] = *reinterpret_cast<const u32x4*>(qb + 32 * p);
     };
     load_k(0, Kst);
     load_q(0);
@@ -417,11 +444,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     for (int kc = 0; kc < NC; ++kc) {
       const Gates gt = gates(to_f32(fraw), to_f32(iraw), m_prev, G);
       store_k(Kst);
-      if (o == 0) {  // row 64 of (alpha' [V | 1])^T: alpha' itself
+      if (o == 0) {  // rows 64, 68, 72, 76 of (alpha' [V | 1])^T: alpha' itself (n replicated 4x)
         const float al = gw[256 + lane];
         const uint32_t hv = pack_bf16(al, 0.f);
-        reinterpret_cast<uint16_t*>(vbh + 64 * VB_PITCH)[vb_col(lane)] = (uint16_t)hv;
-        reinterpret_cast<uint16_t*>(vbl + 64 * VB_PITCH)[vb_col(lane)] = (uint16_t)pack_bf16(al - bf_lo(hv), 0.f);
+        const uint16_t lo = (uint16_t)pack_bf16(al - bf_lo(hv), 0.f);
+#pragma unroll
+        for (int rr = 64; rr < 80; rr += 4) {
+          reinterpret_cast<uint16_t*>(vbh + rr * VB_PITCH)[vb_col(lane)] = (uint16_t)hv;
+          reinterpret_cast<uint16_t*>(vbl + rr * VB_PITCH)[vb_col(lane)] = lo;
+        }
       }
       __syncthreads();  // B1
       if (kc + 1 < NC) {
@@ -437,12 +468,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       u32x4 kf[2][4];
       auto load_kf = [&](int p, u32x4 (&dst)[4]) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          const char* krow = kn + (16 * jt + r16) * SM::KN_PITCH + 8 * g + 64 * p;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(krow);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(krow + 32);
-          dst[jt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
+        for (int jt = 0; jt < 4; ++jt)
+          dst[jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
       };
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -478,15 +505,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int vq = 0; vq < NVX; ++vq) {
           bf16x8 vb;
           if (vq < NVT) {
-            // source lane 4k+a of group g: token 32pj + 4g + k (+16), columns 16vq + 4a .. +3
-            const char* base = vn + (32 * pj + 4 * g + (r16 >> 2)) * VN_PITCH + 2 * (16 * vq + 4 * (r16 & 3));
+            // source lane 4k+a of group g: token 32pj + 4g + k (+16), columns vcol_of(vq, 4a) .. +3
+            const char* base = vn + (32 * pj + 4 * g + (r16 >> 2)) * VN_PITCH + 2 * vcol_of(vq, 4 * (r16 & 3));
             vb = tr8(base, base + 16 * VN_PITCH);
-          } else {  // [.. | 1]: column 64 is all ones
-            const uint32_t one = (r16 == 0) ? 0x3f803f80u : 0u;
+          } else {  // [.. | 1]: rows 0, 4, 8, 12 of the fifth tile are all ones
+            const uint32_t one = ((r16 & 3) == 0) ? 0x3f803f80u : 0u;
             vb = __builtin_bit_cast(bf16x8, u32x4{one, one, one, one});
           }
-          Hmv[vq] = mfma(mh, vb, Hmv[vq]);
-          Hmv[vq] = mfma(ml, vb, Hmv[vq]);
+          // transposed product [V | 1]^T M^T: lane (g, r16) gets columns 4g+e of row r16
+          Hmv[vq] = mfma(vb, mh, Hmv[vq]);
+          Hmv[vq] = mfma(vb, ml, Hmv[vq]);
         }
       }
       __syncthreads();  // B2: the state waves' partial Q [C | n] of this chunk are complete
@@ -498,18 +526,24 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
         for (int sw = 1; sw < NSW; ++sw) Hqc[vq] += hp[((sw * 4 + o) * NVX + vq) * 64 + lane];
       }
-      // finish rows 16o + 4g + e
-      const f32x4 qb = *reinterpret_cast<const f32x4*>(gw + 128 + 16 * o + 4 * g);
-      const f32x4 mcr = *reinterpret_cast<const f32x4*>(gw + 192 + 16 * o + 4 * g);
-      bf16_t* hb = hh + (size_t)kc * L * DV + v0 + r16;
+      // finish row 16o + r16: this lane holds columns vcol_of(vq, 4g + e), i.e. the
+      // 8 consecutive columns 32h + 8g .. +7 of tiles (2h, 2h+1); the denominator
+      // (n / ones replicated in rows 0, 4, 8, 12 of the fifth tile) is element 0
+      const float qb = gw[128 + 16 * o + r16];
+      const float mcr = gw[192 + 16 * o + r16];
+      const float den = qb * Hqc[NVT][0] + Hmv[NVT][0];
+      const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr)) + eps);
+      bf16_t* hb = hh + ((size_t)kc * L + 16 * o + r16) * DV + v0 + 8 * g;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float den = row_bcast0(qb[e] * Hqc[NVT][e] + Hmv[NVT][e]);  // column 64 is in lane r16 == 0
-        const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr[e])) + eps);
-        const size_t row = (size_t)(16 * o + 4 * g + e) * DV;
+      for (int h2 = 0; h2 < NVT / 2; ++h2) {
+        u32x4 out;
 #pragma unroll
-        for (int vq = 0; vq < NVT; ++vq)
-          hb[row + 16 * vq] = from_f32<bf16_t>((qb[e] * Hqc[vq][e] + Hmv[vq][e]) * inv);
+        for (int b = 0; b < 2; ++b) {
+          const int vq = 2 * h2 + b;
+          out[2 * b] = pack_bf16((qb * Hqc[vq][0] + Hmv[vq][0]) * inv, (qb * Hqc[vq][1] + Hmv[vq][1]) * inv);
+          out[2 * b + 1] = pack_bf16((qb * Hqc[vq][2] + Hmv[vq][2]) * inv, (qb * Hqc[vq][3] + Hmv[vq][3]) * inv);
+        }
+        *reinterpret_cast<u32x4*>(hb + 32 * h2) = out;
       }
       m_prev = gt.m_next;
       G = gt.Gn;
