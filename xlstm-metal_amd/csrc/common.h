@@ -43,6 +43,26 @@ template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return (
 // Rounds a float to the precision of T (identity for float).
 template <typename T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
 
+// Rounds a pair of floats to T in place with one packed hardware conversion
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: round to nearest even, NaN kept).
+typedef __bf16 xl_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 xl_f16x2 __attribute__((ext_vector_type(2)));
+typedef float xl_f32x2 __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ void round2_to(float& a, float& b);
+template <> __device__ __forceinline__ void round2_to<float>(float&, float&) {}
+template <> __device__ __forceinline__ void round2_to<bf16_t>(float& a, float& b) {
+  const xl_f32x2 v = {a, b};
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, xl_bf16x2));
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void round2_to<f16_t>(float& a, float& b) {
+  const xl_f32x2 v = {a, b};
+  const xl_f16x2 h = __builtin_convertvector(v, xl_f16x2);
+  a = (float)h[0];
+  b = (float)h[1];
+}
+
 template <typename T> struct is_f32 { static constexpr bool value = false; };
 template <> struct is_f32<float> { static constexpr bool value = true; };
 
@@ -79,6 +99,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// Sum over the 64 lanes with DPP row shifts and row broadcasts (no LDS
+// round trips); the total lands in lane 63.
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+#define XL_DPP_ADD(CTRL, ROWMASK) \
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWMASK, 0xf, false));
+  XL_DPP_ADD(0x111, 0xf)  // row_shr:1
+  XL_DPP_ADD(0x112, 0xf)  // row_shr:2
+  XL_DPP_ADD(0x114, 0xf)  // row_shr:4
+  XL_DPP_ADD(0x118, 0xf)  // row_shr:8
+  XL_DPP_ADD(0x142, 0xa)  // row_bcast:15 into rows 1, 3
+  XL_DPP_ADD(0x143, 0xc)  // row_bcast:31 into rows 2, 3
+#undef XL_DPP_ADD
+  return x;
 }
 
 __device__ __forceinline__ float wave_max(float v) {

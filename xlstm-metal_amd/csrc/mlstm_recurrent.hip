@@ -25,6 +25,9 @@ namespace xl {
 constexpr int REC_THREADS = 256;
 constexpr int REC_COLS = 64;       // DV columns per workgroup
 constexpr int REC_MAX_DQK = 512;   // rows per thread RPT = DQK / 16 <= 32
+// decode step: 1024 threads = 16 column groups x 64 row groups, RPT = DQK / 64 <= 8 rows per thread
+constexpr int STEP_THREADS = 1024;
+constexpr int STEP_RG = STEP_THREADS / 16;
 
 template <typename TQ, typename TG, int RPT>
 __global__ __launch_bounds__(REC_THREADS) void mlstm_recurrent_kernel(
@@ -162,23 +165,32 @@ __global__ __launch_bounds__(REC_THREADS) void mlstm_recurrent_kernel(
   }
 }
 
-// Single decode step, straight-line: every C load of the thread is issued
-// first, then each row is updated and stored as soon as it arrives, so the
-// read and write streams overlap.  n' and (q s).n' are computed one element
-// per thread (d = tid + 256 j) while the C loads are in flight.  Same thread
-// layout and reduction as mlstm_recurrent_kernel.
+// Single decode step, straight-line.  Every small operand (gates, m, q, k, n,
+// v) is requested first and the whole C tile of the thread right behind it;
+// the thread then waits for all of it before the first store, so each wave
+// reads its C rows and then writes them (measured on MI355X at cfg1: per-wave
+// read-then-write phases beat storing each row as it lands by ~2 us of 27).
+// q s and k go to LDS once (one element per thread), so the row loop reads
+// them as LDS broadcasts.  Workgroups of 1024 threads (16 column groups x 64
+// row groups, 4 rows per thread at DQK = 256): at cfg1 this runs as fast as a
+// plain copy with the same access pattern, where 256 threads x 16 rows left a
+// VALU phase exposed.  Column partials are reduced through LDS as in
+// mlstm_recurrent_kernel.
 typedef float nt_f4 __attribute__((ext_vector_type(4)));
 
 template <typename TQ, typename TG, int RPT>
-__global__ __launch_bounds__(REC_THREADS) void mlstm_step_kernel(
+__global__ __launch_bounds__(STEP_THREADS) void mlstm_step_kernel(
     const TQ* __restrict__ q, const TQ* __restrict__ k, const TQ* __restrict__ v,
     const TG* __restrict__ ig, const TG* __restrict__ fg,
     const float* c_old, const float* __restrict__ n_old, const float* __restrict__ m_old,
     TQ* __restrict__ h, float* c_new, float* __restrict__ n_new, float* __restrict__ m_new,
     int DQK, int DV, int ntile, float qk_scale, float eps) {
   constexpr bool LOWP = !is_f32<TQ>::value;
-  __shared__ float s_red[16][REC_COLS + 4];
-  __shared__ float s_wsum[REC_THREADS / 64];
+  constexpr int NPT = (RPT * STEP_RG + STEP_THREADS - 1) / STEP_THREADS;  // n entries per thread (d = tid + 1024 j)
+  __shared__ float s_q[RPT * STEP_RG];
+  __shared__ float s_k[RPT * STEP_RG];
+  __shared__ float s_red[STEP_RG][REC_COLS + 4];
+  __shared__ float s_wsum[STEP_THREADS / 64];
 
   const int bh = blockIdx.x / ntile;
   const int tile = blockIdx.x - bh * ntile;
@@ -186,89 +198,125 @@ __global__ __launch_bounds__(REC_THREADS) void mlstm_step_kernel(
   const int tx = tid & 15, ty = tid >> 4;
   const int col0 = tile * REC_COLS + tx * 4;
   const bool col_ok = col0 < DV;
+  const int colc = col_ok ? col0 : 0;  // clamped: every load below is unconditional and in bounds
   const size_t cbase = (size_t)bh * DQK * DV;
 
+  // ---- small operands first (no branches, so the wait counts stay exact)
+  const TG fraw = fg[bh], iraw = ig[bh];
+  const float mo = m_old[bh];
+  const TQ* qp = q + (size_t)bh * DQK;
+  const TQ* kp = k + (size_t)bh * DQK;
+  TQ qr[NPT], kr[NPT];
+  float nr[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int d = tid + STEP_THREADS * j;
+    const int dc = d < DQK ? d : 0;
+    qr[j] = qp[dc];
+    kr[j] = kp[dc];
+    nr[j] = n_old[(size_t)bh * DQK + dc];
+  }
+  TQ vr[4];
+  {
+    const TQ* vp = v + (size_t)bh * DV + colc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vr[j] = vp[j];
+  }
+  asm volatile("" ::: "memory");  // keep the small loads ahead of the C stream
+  // ---- then the C stream (rows past DQK re-read row 0 and are never stored)
   float4 C[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
-    const int d = ty + 16 * r;
-    if (col_ok && d < DQK) {
-      const nt_f4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(c_old + cbase + (size_t)d * DV + col0));
-      C[r] = make_float4(x[0], x[1], x[2], x[3]);
-    } else {
-      C[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    const int d = ty + STEP_RG * r;
+    const int dc = d < DQK ? d : 0;
+    const nt_f4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(c_old + cbase + (size_t)dc * DV + colc));
+    C[r] = make_float4(x[0], x[1], x[2], x[3]);
   }
 
   // gates (identical in every thread)
-  const float lsf = round_to<TG>(logsigmoid(to_f32(fg[bh])));
-  const float mo = m_old[bh];
-  const float ipre = to_f32(ig[bh]);
+  const float lsf = round_to<TG>(logsigmoid(to_f32(fraw)));
+  const float ipre = to_f32(iraw);
   const float mn = fmaxf(lsf + mo, ipre);
   const float fa = expf(lsf + mo - mn);
   const float ia = expf(ipre - mn);
 
-  // n' and the partial of (q s) . n'
-  const TQ* qp = q + (size_t)bh * DQK;
-  const TQ* kp = k + (size_t)bh * DQK;
-  float part = 0.f;
-  for (int d = tid; d < DQK; d += REC_THREADS) {
-    float qs = to_f32(qp[d]) * qk_scale;
+  // n', q s and k to LDS, and the partial of (q s) . n'
+  float part = 0.f, nn[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int d = tid + STEP_THREADS * j;
+    float qs = to_f32(qr[j]) * qk_scale;
     if (LOWP) qs = round_to<TQ>(qs);
-    const float nn = fa * n_old[(size_t)bh * DQK + d] + ia * to_f32(kp[d]);
-    if (tile == 0) n_new[(size_t)bh * DQK + d] = nn;
-    part += qs * (LOWP ? round_to<TQ>(nn) : nn);
+    const float kd = to_f32(kr[j]);
+    nn[j] = fa * nr[j] + ia * kd;
+    const bool ok = d < DQK;
+    part += ok ? qs * (LOWP ? round_to<TQ>(nn[j]) : nn[j]) : 0.f;
+    if (d < RPT * STEP_RG) {
+      s_q[d] = ok ? qs : 0.f;
+      s_k[d] = ok ? kd : 0.f;
+    }
   }
-  part = wave_sum(part);
-  if ((tid & 63) == 0) s_wsum[tid >> 6] = part;
+  part = wave_sum_dpp(part);
+  if ((tid & 63) == 63) s_wsum[tid >> 6] = part;
+  float vv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) vv[j] = to_f32(vr[j]);
+  // the gate and n work above only waited for the small loads; the read
+  // phase of the C stream ends here (see the header)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // s_q, s_k, s_wsum ready
 
   // C' row by row: store as soon as computed, accumulate (q s)^T C'
-  float vv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (col_ok) {
-    const TQ* vp = v + (size_t)bh * DV + col0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vv[j] = to_f32(vp[j]);
-  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
-    const int d = ty + 16 * r;
-    if (d < DQK) {
-      float qd = to_f32(qp[d]) * qk_scale;
-      if (LOWP) qd = round_to<TQ>(qd);
-      const float kd = to_f32(kp[d]);
-      float kv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kv[j] = LOWP ? round_to<TQ>(kd * vv[j]) : kd * vv[j];
-      float4 c = C[r];
-      c.x = fa * c.x + ia * kv[0];
-      c.y = fa * c.y + ia * kv[1];
-      c.z = fa * c.z + ia * kv[2];
-      c.w = fa * c.w + ia * kv[3];
-      if (col_ok) {
-        const nt_f4 x = {c.x, c.y, c.z, c.w};
-        __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(c_new + cbase + (size_t)d * DV + col0));
-      }
-      acc[0] += qd * (LOWP ? round_to<TQ>(c.x) : c.x);
-      acc[1] += qd * (LOWP ? round_to<TQ>(c.y) : c.y);
-      acc[2] += qd * (LOWP ? round_to<TQ>(c.z) : c.z);
-      acc[3] += qd * (LOWP ? round_to<TQ>(c.w) : c.w);
+    const int d = ty + STEP_RG * r;
+    const float qd = s_q[d], kd = s_k[d];  // 0 past DQK: the row adds nothing
+    float kv[4] = {kd * vv[0], kd * vv[1], kd * vv[2], kd * vv[3]};
+    if (LOWP) {
+      round2_to<TQ>(kv[0], kv[1]);
+      round2_to<TQ>(kv[2], kv[3]);
     }
+    float4 c = C[r];
+    c.x = fa * c.x + ia * kv[0];
+    c.y = fa * c.y + ia * kv[1];
+    c.z = fa * c.z + ia * kv[2];
+    c.w = fa * c.w + ia * kv[3];
+    if (col_ok && d < DQK) {
+      const nt_f4 x = {c.x, c.y, c.z, c.w};
+      __builtin_nontemporal_store(x, reinterpret_cast<nt_f4*>(c_new + cbase + (size_t)d * DV + col0));
+    }
+    float cr[4] = {c.x, c.y, c.z, c.w};
+    if (LOWP) {
+      round2_to<TQ>(cr[0], cr[1]);
+      round2_to<TQ>(cr[2], cr[3]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += qd * cr[j];
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) s_red[ty][tx * 4 + j] = acc[j];
   __syncthreads();
   if (tid < REC_COLS && tile * REC_COLS + tid < DV) {
-    float qn = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+    float qn = 0.f;
+#pragma unroll
+    for (int w = 0; w < STEP_THREADS / 64; ++w) qn += s_wsum[w];
     if (LOWP) qn = round_to<TQ>(qn);
     const float den = fmaxf(fabsf(qn), expf(-mn)) + eps;
     float hn = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) hn += s_red[r][tid];
+    for (int r = 0; r < STEP_RG; ++r) hn += s_red[r][tid];
     if (LOWP) hn = round_to<TQ>(hn);
     h[(size_t)bh * DV + tile * REC_COLS + tid] = from_f32<TQ>(hn / den);
   }
-  if (tile == 0 && tid == 0) m_new[bh] = mn;
+  if (tile == 0) {  // n' and m' once per head, after the C stream
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int d = tid + STEP_THREADS * j;
+      if (d < DQK) n_new[(size_t)bh * DQK + d] = nn[j];
+    }
+    if (tid == 0) m_new[bh] = mn;
+  }
 }
 
 template <typename TQ, typename TG>
@@ -280,14 +328,15 @@ static int launch_rec_t(const void* q, const void* k, const void* v, const void*
   const int rpt = (DQK + 15) / 16;
   dim3 grid((unsigned)(BNH * ntile)), block(REC_THREADS);
   if (S == 1 && c0 && n0 && m0 && c1 && n1 && m1) {  // decode step: straight-line kernel
+    const int rps = (DQK + STEP_RG - 1) / STEP_RG;
 #define XL_STEP_LAUNCH(R)                                                                                      \
-  hipLaunchKernelGGL((mlstm_step_kernel<TQ, TG, R>), grid, block, 0, s, (const TQ*)q, (const TQ*)k,          \
-                     (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1, DQK, DV, ntile,  \
-                     qk_scale, eps)
-    if (rpt <= 4) XL_STEP_LAUNCH(4);
-    else if (rpt <= 8) XL_STEP_LAUNCH(8);
-    else if (rpt <= 16) XL_STEP_LAUNCH(16);
-    else XL_STEP_LAUNCH(32);
+  hipLaunchKernelGGL((mlstm_step_kernel<TQ, TG, R>), grid, dim3(STEP_THREADS), 0, s, (const TQ*)q,           \
+                     (const TQ*)k, (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1,    \
+                     DQK, DV, ntile, qk_scale, eps)
+    if (rps <= 1) XL_STEP_LAUNCH(1);
+    else if (rps <= 2) XL_STEP_LAUNCH(2);
+    else if (rps <= 4) XL_STEP_LAUNCH(4);
+    else XL_STEP_LAUNCH(8);
 #undef XL_STEP_LAUNCH
     return check_launch(who);
   }
