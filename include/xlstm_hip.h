@@ -98,8 +98,9 @@ int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i
  *   h [B,NH,S,DV] (dtype_qkv); c_last, n_last, m_last float32 (all NULL when
  *   the last states are not wanted).
  * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.
- * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes (0 for the fused
- * algorithm), 256-byte aligned.
+ * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned
+ * (fused algorithm: the per-chunk gate prep, 1280 bytes per 64 tokens of
+ * every head; two-pass algorithm: the chunk-entry states).
  */
 size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, int L,
                                          int dtype_qkv, int algo);

@@ -25,6 +25,7 @@ int chunkwise_two_pass(const ChunkwiseArgs& a);
 // Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a
 // shape/dtype is covered (and why not, in `why`, when it is not).
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why);
+size_t chunkwise_fused_workspace(int B, int NH, int S);  // gate prep: 1280 bytes per 64-token chunk
 int chunkwise_fused(const ChunkwiseArgs& a);
 
 }  // namespace xl

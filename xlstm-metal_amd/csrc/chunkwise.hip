@@ -51,7 +51,8 @@ extern "C" size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQ
   a.dtype_qkv = dtype_qkv; a.dtype_gates = dtype_qkv;
   int chosen = XL_CHUNKWISE_TWO_PASS;
   if (pick(a, algo, &chosen) != XL_OK) return 0;
-  return chosen == XL_CHUNKWISE_FUSED ? 0 : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
+  return chosen == XL_CHUNKWISE_FUSED ? chunkwise_fused_workspace(B, NH, S)
+                                     : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
 }
 
 extern "C" int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
@@ -68,12 +69,12 @@ extern "C" int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* 
   int chosen = XL_CHUNKWISE_TWO_PASS;
   rc = pick(a, algo, &chosen);
   if (rc) return rc;
-  if (chosen == XL_CHUNKWISE_FUSED) return chunkwise_fused(a);
-  const size_t need = chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
+  const bool fused = chosen == XL_CHUNKWISE_FUSED;
+  const size_t need = fused ? chunkwise_fused_workspace(B, NH, S) : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
   if (!workspace || workspace_bytes < need)
-    return set_error(XL_ERR_WORKSPACE, "xl_mlstm_chunkwise_fwd: two-pass workspace needs %zu bytes, got %zu", need,
-                     workspace ? workspace_bytes : (size_t)0);
+    return set_error(XL_ERR_WORKSPACE, "xl_mlstm_chunkwise_fwd: %s workspace needs %zu bytes, got %zu",
+                     fused ? "fused" : "two-pass", need, workspace ? workspace_bytes : (size_t)0);
   if (((uintptr_t)workspace) & 255u)
     return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_fwd: workspace must be 256-byte aligned");
-  return chunkwise_two_pass(a);
+  return fused ? chunkwise_fused(a) : chunkwise_two_pass(a);
 }

@@ -74,6 +74,8 @@ constexpr int VB_PITCH = 144;   // bytes per row of (alpha V)^T (16 consecutive 
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
+constexpr int PREP_STRIDE = 320;  // floats per chunk of gate prep: b, a, cummax(i - b), (i - b) log2e, [g, max a]
+constexpr int GROWS = 6;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G]
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -130,6 +132,36 @@ __device__ __forceinline__ float lane63(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
+// Chunk-local gate prep, one wave per (head, chunk), lane = token t
+// (fw.py:308-316 and :98, :204-213 before the running stabiliser enters):
+//   b_t = sum_{s<=t} logsig f_s,  g = b_63,  a_t = g - b_t + i_t,  max_t a_t,
+//   u_t = i_t - b_t (stored times log2 e),  cummax_{s<=t} u_s.
+// These are the scans of the chunk; the main kernel folds in the running m
+// and the deferred state rescale with a handful of scalar operations.
+template <typename TG>
+__global__ __launch_bounds__(256) void gate_prep_kernel(const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                        float* __restrict__ prep, int total_chunks) {
+  const int lane = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);  // bh * NC + chunk: the tokens of chunk c are 64c .. 64c + 63
+  if (c >= total_chunks) return;
+  const float f = to_f32(fg[(size_t)c * L + lane]), i = to_f32(ig[(size_t)c * L + lane]);
+  const float b = wave_scan<false>(logsig_fast(f));
+  const float g = lane63(b);
+  const float a = g - b + i;
+  const float amax = lane63(wave_scan<true>(a));
+  const float u = i - b;
+  const float cmu = wave_scan<true>(u);
+  float* p = prep + (size_t)c * PREP_STRIDE;
+  p[lane] = b;
+  p[64 + lane] = a;
+  p[128 + lane] = cmu;
+  p[192 + lane] = u * LOG2E;
+  if (lane == 0) {
+    p[256] = g;
+    p[257] = amax;
+  }
+}
+
 // Column of the 64-wide DV tile held by column n of 16-wide tile vq (vq < 4):
 // runs of 4 consecutive columns, and the tile pair (2h, 2h+1) covers columns
 // 32h .. 32h+31 so that a lane of the transposed output holds 8 consecutive
@@ -152,18 +184,18 @@ struct Smem {
   static constexpr int VBH = VN + 64 * VN_PITCH;         // [80 v][VB_PITCH]: (alpha [V | 1])^T hi
   static constexpr int VBL = VBH + 80 * VB_PITCH;        // ... lo
   static constexpr int HP = VBL + 80 * VB_PITCH;         // [4 state waves][4 row tiles][NVX][64] f32x4: partial Q [C | n]
-  static constexpr int GATES = HP + 4 * 4 * NVX * 64 * 16;  // [8 waves][5][64] float
-  static constexpr int BYTES = GATES + 8 * 5 * 64 * 4;
+  static constexpr int GATES = HP + 4 * 4 * NVX * 64 * 16;  // [2 chunks][GROWS][64] float: gate rows + scalars
+  static constexpr int BYTES = GATES + 2 * GROWS * 64 * 4;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <typename TG, int DQK>
+template <int DQK>
 __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const TG* __restrict__ ig, const TG* __restrict__ fg, const float* __restrict__ c0,
+    const float* __restrict__ c0,
     const float* __restrict__ n0, const float* __restrict__ m0, bf16_t* __restrict__ h,
-    float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last, int NC, int DV, int BNH,
-    int nvtile, float qk_scale, float eps) {
+    float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last,
+    const float* __restrict__ prep, int NC, int DV, int BNH, int nvtile, float qk_scale, float eps) {
   using SM = Smem<DQK>;
   constexpr int KPD = SM::KPD;
   constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
@@ -175,7 +207,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const int tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
-  const bool is_state = w < NSW;
   const int ws = w & 3;  // index within the state or output group
 
   // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
@@ -191,7 +222,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   char* vbh = smem + SM::VBH;
   char* vbl = smem + SM::VBL;
   f32x4* hp = (f32x4*)(smem + SM::HP);
-  float* gw = (float*)(smem + SM::GATES) + w * 5 * 64;  // this wave's rows: bl, ul, qbar, mc, alpha'
+  float* gbuf = (float*)(smem + SM::GATES);  // [2][GROWS][64]: rows of chunk kc live in buffer kc & 1
 
   // constant rows 65..79 of the alpha-V tiles (zeros); row 64 is rewritten every chunk
   for (int e = tid; e < 15 * VB_PITCH / 4; e += NTHREADS) {
@@ -202,8 +233,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const bf16_t* qh = q + (size_t)bh * S * DQK;
   const bf16_t* kh = k + (size_t)bh * S * DQK;
   const bf16_t* vh = v + (size_t)bh * S * DV;
-  const TG* fh = fg + (size_t)bh * S;
-  const TG* ih = ig + (size_t)bh * S;
   bf16_t* hh = h + (size_t)bh * S * DV;
   const float m_init = m0 ? m0[bh] : 0.f;
 
@@ -223,36 +252,55 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       *reinterpret_cast<u32x4*>(kn + (piece / (DQK / 8)) * SM::KN_PITCH + 16 * (piece % (DQK / 8))) = Kst[u];
     }
   };
-  // gates stay in their storage type until the chunk that uses them, so the
-  // prefetch never waits for the load to land
-  auto load_gates = [&](int kc, TG& fr, TG& ir) {
-    fr = fh[(size_t)kc * L + lane];
-    ir = ih[(size_t)kc * L + lane];
+  // ---- gate rows (computed by the gate wave, output wave 0, one chunk ahead)
+  // Row terms of the intra-chunk exponent, column terms, output row scales,
+  // the combined stabiliser mc and alpha' = exp(a_t - m') e^{-G} of chunk c go
+  // to buffer c & 1 together with the chunk's renormalisation factor of the
+  // stored state, m', the deferred log rescale G and the renormalise flag.
+  const float* preph = prep + (size_t)bh * NC * PREP_STRIDE;
+  float gm = m_init, gG = 0.f;  // running m and G (gate wave only)
+  // pv[4] holds g (lane 0) and max a (lane 1): a per-lane load, so it is
+  // counted with the vector loads and never stalls the LDS waits
+  auto prep_load = [&](int c, float (&pv)[5]) {
+    const float* pc = preph + (size_t)c * PREP_STRIDE;
+    pv[0] = pc[lane];
+    pv[1] = pc[64 + lane];
+    pv[2] = pc[128 + lane];
+    pv[3] = pc[192 + lane];
+    pv[4] = pc[256 + (lane & 1)];
   };
-  // Gates of one chunk (every wave, lane = token).  Writes this wave's gate rows
-  // and returns m', the log rescale lg, and the updated deferred rescale.
-  struct Gates { float m_next, lg, G_prev, Gn; bool renorm; };
-  auto gates = [&](float fcur, float icur, float m_prev, float G) {
-    Gates r;
-    const float b = wave_scan<false>(logsig_fast(fcur));
-    const float gsum = lane63(b);
-    const float a = gsum - b + icur;
-    r.m_next = fmaxf(gsum + m_prev, lane63(wave_scan<true>(a)));
-    r.lg = gsum + m_prev - r.m_next;  // log of this chunk's rescale of the state (<= 0)
-    r.G_prev = G;
-    r.Gn = G + r.lg;
-    r.renorm = r.Gn < RENORM;         // wave-uniform, and the same in every wave
-    if (r.renorm) r.Gn = 0.f;
-    const float u = icur - b;
-    const float mb = b + m_prev;
-    const float mc = fmaxf(mb, b + wave_scan<true>(u));
-    gw[lane] = (b - mc) * LOG2E;                          // row term of the intra-chunk exponent
-    gw[64 + lane] = u * LOG2E;                            // column term
-    gw[128 + lane] = exp_(mb - mc + G) * qk_scale;        // output row scale (deferred state rescale folded in)
-    gw[192 + lane] = mc;
-    gw[256 + lane] = exp_(a - r.m_next - r.Gn);           // alpha' = exp(a_t - m') e^{-G}
-    return r;
+  auto gate_rows = [&](int c, const float (&pv)[5]) {
+    float* gb = gbuf + (c & 1) * GROWS * 64;
+    const float pg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[4]), 0));
+    const float pamax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[4]), 1));
+    const float b = pv[0], a = pv[1], cmu = pv[2];
+    const float m_next = fmaxf(pg + gm, pamax);
+    const float lg = pg + gm - m_next;  // log of this chunk's rescale of the state (<= 0)
+    float Gn = gG + lg;
+    const bool renorm = Gn < RENORM;   // wave-uniform
+    if (renorm) Gn = 0.f;
+    const float mb = b + gm;
+    const float mc = fmaxf(mb, b + cmu);
+    gb[lane] = (b - mc) * LOG2E;                       // row term of the intra-chunk exponent
+    gb[64 + lane] = pv[3];                             // column term
+    gb[128 + lane] = exp_(mb - mc + gG) * qk_scale;    // output row scale (deferred state rescale folded in)
+    gb[192 + lane] = mc;
+    gb[256 + lane] = exp_(a - m_next - Gn);            // alpha' = exp(a_t - m') e^{-G}
+    if (lane == 0) {
+      gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
+      gb[321] = m_next;
+      gb[322] = Gn;
+      gb[323] = renorm ? 1.f : 0.f;
+    }
+    gm = m_next;
+    gG = Gn;
   };
+  if (w == NSW) {
+    float pv[5];
+    prep_load(0, pv);
+    gate_rows(0, pv);
+  }
+  __syncthreads();  // B0: gate rows of chunk 0
 
   if (w < NSW) {
     // =====================================================================
@@ -285,7 +333,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // dw0 + 32p + 8g .. +7 -- the k order of the B fragments that
     // split8(Cacc[2p], Cacc[2p+1]) yields
     u32x4 Qs[4][KS];
-    TG fraw, iraw;
     auto load_v = [&](int kc) {
       const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
       Vst[0] = *reinterpret_cast<const u32x4*>(vb + (size_t)vrow * DV);
@@ -301,16 +348,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     load_k(0, Kst);
     load_v(0);
     load_qs(0);
-    load_gates(0, fraw, iraw);
-    float m_prev = m_init, G = 0.f;
     for (int kc = 0; kc < NC; ++kc) {
-      const Gates gt = gates(to_f32(fraw), to_f32(iraw), m_prev, G);
+      const float* gb = gbuf + (kc & 1) * GROWS * 64;
       store_k(Kst);
       // V natural and (alpha' V)^T hi / lo
       *reinterpret_cast<u32x4*>(vn + vrow * VN_PITCH + 2 * vcol) = Vst[0];
       *reinterpret_cast<u32x4*>(vn + (vrow + 2) * VN_PITCH + 2 * vcol) = Vst[1];
       {
-        const float al0 = gw[256 + vrow], al1 = gw[256 + vrow + 2];
+        const float al0 = gb[256 + vrow], al1 = gb[256 + vrow + 2];
         const int col = vb_col(vrow);  // vb_col(vrow + 2) == col + 1
 #pragma unroll
         for (int s2 = 0; s2 < 8; ++s2) {
@@ -327,7 +372,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       if (kc + 1 < NC) {  // staging registers are free: prefetch (q after its last use below)
         load_k(kc + 1, Kst);
         load_v(kc + 1);
-        load_gates(kc + 1, fraw, iraw);
       }
       // partial Q [C | n] over this wave's rows, with the state before this chunk
       // (bf16 hi + lo of the float32 accumulators, so q C keeps float32 accuracy).
@@ -373,8 +417,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + NVX - 1) * 64 + lane] = Hp[(NVX - 1) & 1][rt];
       }
       if (kc + 1 < NC) load_qs(kc + 1);
-      if (gt.renorm) {
-        const float sc = exp_(gt.G_prev + gt.lg);
+      if (gb[323] != 0.f) {  // renormalise the stored state (wave-uniform)
+        const float sc = gb[320];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -405,12 +449,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           }
         }
       __syncthreads();  // B2: partials complete; the chunk's tiles may be overwritten
-      m_prev = gt.m_next;
-      G = gt.Gn;
     }
     // ---- final states (undo the deferred rescale)
     if (c_last) {
-      const float sc = exp_(G);
+      const float* gl = gbuf + ((NC - 1) & 1) * GROWS * 64;
+      const float sc = exp_(gl[322]);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -421,7 +464,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
             c_last[((size_t)bh * DQK + d) * DV + v0 + vcol_of(vq, r16)] = Cacc[dt][vq][e] * sc;
           if (v0 == 0 && r16 == 0) n_last[(size_t)bh * DQK + d] = Cacc[dt][NVT][e] * sc;
         }
-      if (v0 == 0 && tid == 0) m_last[bh] = m_prev;
+      if (v0 == 0 && tid == 0) m_last[bh] = gl[321];
     }
   } else {
     // =====================================================================
@@ -429,7 +472,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // =====================================================================
     const int o = ws;
     u32x4 Kst[NKU], Qf[KPD];
-    TG fraw, iraw;
+    float pv[5];  // gate prep of the next chunk (gate wave)
     // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
     // 16-byte load; the K operand below uses the same contiguous k order)
     auto load_q = [&](int kc) {
@@ -439,13 +482,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     };
     load_k(0, Kst);
     load_q(0);
-    load_gates(0, fraw, iraw);
-    float m_prev = m_init, G = 0.f;
     for (int kc = 0; kc < NC; ++kc) {
-      const Gates gt = gates(to_f32(fraw), to_f32(iraw), m_prev, G);
+      const float* gb = gbuf + (kc & 1) * GROWS * 64;
       store_k(Kst);
       if (o == 0) {  // rows 64, 68, 72, 76 of (alpha' [V | 1])^T: alpha' itself (n replicated 4x)
-        const float al = gw[256 + lane];
+        const float al = gb[256 + lane];
         const uint32_t hv = pack_bf16(al, 0.f);
         const uint16_t lo = (uint16_t)pack_bf16(al - bf_lo(hv), 0.f);
 #pragma unroll
@@ -457,37 +498,43 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       __syncthreads();  // B1
       if (kc + 1 < NC) {
         load_k(kc + 1, Kst);
-        load_gates(kc + 1, fraw, iraw);
+        if (o == 0) prep_load(kc + 1, pv);
       }
+
       // S^T tiles of all four j-tiles over the whole DQK: A = K rows 16jt + r16,
       // B = q rows.  Every output wave computes all four (tiles above the
-      // diagonal are masked in the gating), so the code is branch-free and the
-      // K fragments of step p+1 load while step p multiplies; the busiest SIMD
-      // (the wave of the last row tile) does the same work as before.
+      // diagonal are masked in the gating), so the code is branch-free; the
+      // busiest SIMD (the wave of the last row tile) does the same work as
+      // before.  All K fragments are requested up front: LDS latency is many
+      // times the four MFMAs of one k-step.
       f32x4 Sacc[4];
-      u32x4 kf[2][4];
-      auto load_kf = [&](int p, u32x4 (&dst)[4]) {
+      constexpr int KD = 2;
+      u32x4 kf[KD][4];
+#pragma unroll
+      for (int p = 0; p < KD - 1; ++p)
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
-          dst[jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
-      };
+          kf[p][jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      load_kf(0, kf[0]);
 #pragma unroll
       for (int p = 0; p < KPD; ++p) {
-        if (p + 1 < KPD) load_kf(p + 1, kf[(p + 1) & 1]);
+        if (p + KD - 1 < KPD) {
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            kf[(p + KD - 1) % KD][jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * (p + KD - 1));
+        }
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
-          Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p & 1][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
+          Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
       }
       if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch
       // gate the scores of row i = 16o + r16, then M [V | 1] with M split hi + lo
       const int i = 16 * o + r16;
-      const float bli = gw[i];
+      const float bli = gb[i];
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        const f32x4 ul = *reinterpret_cast<const f32x4*>(gw + 64 + 16 * jt + 4 * g);
+        const f32x4 ul = *reinterpret_cast<const f32x4*>(gb + 64 + 16 * jt + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = 16 * jt + 4 * g + e;
@@ -505,7 +552,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int vq = 0; vq < NVX; ++vq) {
           bf16x8 vb;
           if (vq < NVT) {
-            // source lane 4k+a of group g: token 32pj + 4g + k (+16), columns vcol_of(vq, 4a) .. +3
             const char* base = vn + (32 * pj + 4 * g + (r16 >> 2)) * VN_PITCH + 2 * vcol_of(vq, 4 * (r16 & 3));
             vb = tr8(base, base + 16 * VN_PITCH);
           } else {  // [.. | 1]: rows 0, 4, 8, 12 of the fifth tile are all ones
@@ -517,6 +563,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           Hmv[vq] = mfma(vb, ml, Hmv[vq]);
         }
       }
+      // the gate wave forms the gate rows of chunk kc + 1 (buffer (kc + 1) & 1,
+      // last read before B1 of this chunk)
+      if (o == 0 && kc + 1 < NC) gate_rows(kc + 1, pv);
       __syncthreads();  // B2: the state waves' partial Q [C | n] of this chunk are complete
       // Q [C | n] of rows 16o + 4g + e: sum of the four state waves' partials
       f32x4 Hqc[NVX];
@@ -529,8 +578,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       // finish row 16o + r16: this lane holds columns vcol_of(vq, 4g + e), i.e. the
       // 8 consecutive columns 32h + 8g .. +7 of tiles (2h, 2h+1); the denominator
       // (n / ones replicated in rows 0, 4, 8, 12 of the fifth tile) is element 0
-      const float qb = gw[128 + 16 * o + r16];
-      const float mcr = gw[192 + 16 * o + r16];
+      const float qb = gb[128 + 16 * o + r16];
+      const float mcr = gb[192 + 16 * o + r16];
       const float den = qb * Hqc[NVT][0] + Hmv[NVT][0];
       const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr)) + eps);
       bf16_t* hb = hh + ((size_t)kc * L + 16 * o + r16) * DV + v0 + 8 * g;
@@ -545,8 +594,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         }
         *reinterpret_cast<u32x4*>(hb + 32 * h2) = out;
       }
-      m_prev = gt.m_next;
-      G = gt.Gn;
     }
   }
 }
@@ -556,15 +603,18 @@ static int launch(const ChunkwiseArgs& A) {
   const int BNH = A.B * A.NH;
   const int nvtile = A.DV / DVT;
   const int NC = A.S / L;
-  auto kern = chunkwise_fused_kernel<TG, DQK>;
+  float* prep = (float*)A.workspace;
+  const int total = BNH * NC;
+  hipLaunchKernelGGL(gate_prep_kernel<TG>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, (hipStream_t)A.stream,
+                     (const TG*)A.i, (const TG*)A.f, prep, total);
+  auto kern = chunkwise_fused_kernel<DQK>;
   const size_t smem = Smem<DQK>::BYTES;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess)
     return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
   hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvtile)), dim3(NTHREADS), smem, (hipStream_t)A.stream,
-                     (const bf16_t*)A.q, (const bf16_t*)A.k, (const bf16_t*)A.v, (const TG*)A.i, (const TG*)A.f,
-                     A.c0, A.n0, A.m0, (bf16_t*)A.h, A.c_last, A.n_last, A.m_last, NC, A.DV, BNH, nvtile,
-                     A.qk_scale, A.eps);
+                     (const bf16_t*)A.q, (const bf16_t*)A.k, (const bf16_t*)A.v, A.c0, A.n0, A.m0, (bf16_t*)A.h,
+                     A.c_last, A.n_last, A.m_last, prep, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps);
   return check_launch("xl_mlstm_chunkwise_fwd(fused)");
 }
 
@@ -574,6 +624,10 @@ static int launch_d(const ChunkwiseArgs& A) {
 }
 
 }  // namespace fused
+
+size_t chunkwise_fused_workspace(int B, int NH, int S) {
+  return ((size_t)B * NH * (S / fused::L) * fused::PREP_STRIDE * sizeof(float) + 255) / 256 * 256;
+}
 
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why) {
   const char* r = nullptr;
