@@ -70,7 +70,7 @@ constexpr int DVT = 64;         // DV columns per workgroup
 constexpr int NVT = DVT / 16;   // 16-wide column tiles of v
 constexpr int NVX = NVT + 1;    // ... plus the n / ones / den tile
 constexpr int VN_PITCH = 160;   // bytes per row of natural V (8 consecutive rows -> distinct 32 B bank groups)
-constexpr int VB_PITCH = 144;   // bytes per row of (alpha V)^T (16 consecutive rows -> distinct 16 B bank groups)
+constexpr int AV_PITCH = 160;   // bytes per row of natural alpha' [V | n] (80 columns; 2-row steps hit distinct banks)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
@@ -167,13 +167,10 @@ __global__ __launch_bounds__(256) void gate_prep_kernel(const TG* __restrict__ i
 // 32h .. 32h+31 so that a lane of the transposed output holds 8 consecutive
 // columns (one 16-byte store).
 __device__ __forceinline__ int vcol_of(int vq, int n) { return 32 * (vq >> 1) + 8 * (n >> 2) + 4 * (vq & 1) + (n & 3); }
-// Row of the (alpha [V | 1])^T tiles that holds DV-tile column c (inverse of vcol_of)
-__device__ __forceinline__ int vrow_of(int c) { return 16 * (2 * (c >> 5) + ((c >> 2) & 1)) + 4 * ((c >> 3) & 3) + (c & 3); }
-
-// Column of token t in the (alpha [V | 1])^T tiles: inside each 8-token block
-// the order is (t even first), matching the transposed K operand whose k-slice
-// of lane group g is t = 32p + 8g + 2k + h (k = 0..3, h = read 0/1).
-__device__ __forceinline__ int vb_col(int t) { return (t & ~7) + 4 * (t & 1) + ((t >> 1) & 3); }
+// First of the 4 consecutive natural columns of alpha' [V | n] that source
+// lane 4k + a of a transposed read of column tile vq fetches: the V columns of
+// tile vq (vq < 4), or the n tile's columns 64 + 4a .. 64 + 4a + 3.
+__device__ __forceinline__ int avcol(int vq, int a) { return vq < NVT ? vcol_of(vq, 4 * a) : 64 + 4 * a; }
 
 template <int DQK>
 struct Smem {
@@ -181,9 +178,9 @@ struct Smem {
   static constexpr int KN_PITCH = DQK * 2 + 16;          // bytes per K row: 16 consecutive rows -> distinct 16 B groups
   static constexpr int KN = 0;                           // [64 t][KN_PITCH]: K natural
   static constexpr int VN = KN + 64 * KN_PITCH;          // [64 t][VN_PITCH]: V natural
-  static constexpr int VBH = VN + 64 * VN_PITCH;         // [80 v][VB_PITCH]: (alpha [V | 1])^T hi
-  static constexpr int VBL = VBH + 80 * VB_PITCH;        // ... lo
-  static constexpr int HP = VBL + 80 * VB_PITCH;         // [4 state waves][4 row tiles][NVX][64] f32x4: partial Q [C | n]
+  static constexpr int AVH = VN + 64 * VN_PITCH;         // [64 t][AV_PITCH]: alpha' [V | n] hi, natural
+  static constexpr int AVL = AVH + 64 * AV_PITCH;        // ... lo
+  static constexpr int HP = AVL + 64 * AV_PITCH;         // [4 state waves][4 row tiles][NVX][64] f32x4: partial Q [C | n]
   static constexpr int GATES = HP + 4 * 4 * NVX * 64 * 16;  // [2 chunks][GROWS][64] float: gate rows + scalars
   static constexpr int BYTES = GATES + 2 * GROWS * 64 * 4;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
@@ -219,15 +216,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 
   char* kn = smem + SM::KN;
   char* vn = smem + SM::VN;
-  char* vbh = smem + SM::VBH;
-  char* vbl = smem + SM::VBL;
+  char* avh = smem + SM::AVH;
+  char* avl = smem + SM::AVL;
   f32x4* hp = (f32x4*)(smem + SM::HP);
   float* gbuf = (float*)(smem + SM::GATES);  // [2][GROWS][64]: rows of chunk kc live in buffer kc & 1
 
-  // constant rows 65..79 of the alpha-V tiles (zeros); row 64 is rewritten every chunk
-  for (int e = tid; e < 15 * VB_PITCH / 4; e += NTHREADS) {
-    reinterpret_cast<uint32_t*>(vbh + 65 * VB_PITCH)[e] = 0u;
-    reinterpret_cast<uint32_t*>(vbl + 65 * VB_PITCH)[e] = 0u;
+  // n-tile columns 64..79 of alpha' [V | n]: zeros, except columns 64, 68, 72,
+  // 76, which carry alpha' itself and are rewritten every chunk
+  for (int e = tid; e < 64 * 8; e += NTHREADS) {
+    reinterpret_cast<uint32_t*>(avh + (e >> 3) * AV_PITCH + 128)[e & 7] = 0u;
+    reinterpret_cast<uint32_t*>(avl + (e >> 3) * AV_PITCH + 128)[e & 7] = 0u;
   }
 
   const bf16_t* qh = q + (size_t)bh * S * DQK;
@@ -351,22 +349,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     for (int kc = 0; kc < NC; ++kc) {
       const float* gb = gbuf + (kc & 1) * GROWS * 64;
       store_k(Kst);
-      // V natural and (alpha' V)^T hi / lo
+      // V natural and alpha' V hi / lo (natural layout, 16-byte rows)
       *reinterpret_cast<u32x4*>(vn + vrow * VN_PITCH + 2 * vcol) = Vst[0];
       *reinterpret_cast<u32x4*>(vn + (vrow + 2) * VN_PITCH + 2 * vcol) = Vst[1];
-      {
-        const float al0 = gb[256 + vrow], al1 = gb[256 + vrow + 2];
-        const int col = vb_col(vrow);  // vb_col(vrow + 2) == col + 1
 #pragma unroll
-        for (int s2 = 0; s2 < 8; ++s2) {
-          const uint32_t sel = (s2 & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t pr = __builtin_amdgcn_perm(Vst[1][s2 >> 1], Vst[0][s2 >> 1], sel);  // (v[t0][c], v[t0+2][c])
-          const float x0 = al0 * bf_lo(pr), x1 = al1 * bf_hi(pr);
-          const uint32_t hv = pack_bf16(x0, x1);
-          const int off = vrow_of(vcol + s2) * VB_PITCH + 2 * col;
-          *reinterpret_cast<uint32_t*>(vbh + off) = hv;
-          *reinterpret_cast<uint32_t*>(vbl + off) = pack_bf16(x0 - bf_lo(hv), x1 - bf_hi(hv));
+      for (int r = 0; r < 2; ++r) {
+        const float al = gb[256 + vrow + 2 * r];
+        u32x4 hv, lv;
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) {
+          const float x0 = al * bf_lo(Vst[r][c2]), x1 = al * bf_hi(Vst[r][c2]);
+          hv[c2] = pack_bf16(x0, x1);
+          lv[c2] = pack_bf16(x0 - bf_lo(hv[c2]), x1 - bf_hi(hv[c2]));
         }
+        *reinterpret_cast<u32x4*>(avh + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = hv;
+        *reinterpret_cast<u32x4*>(avl + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = lv;
       }
       __syncthreads();  // B1: the chunk's tiles are visible; the previous chunk's partials have been read
       if (kc + 1 < NC) {  // staging registers are free: prefetch (q after its last use below)
@@ -425,7 +422,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           for (int vq = 0; vq < NVX; ++vq) Cacc[dt][vq] *= sc;
       }
       // K^T fragments of all this wave's row tiles stay in registers, so every
-      // (alpha [V | 1])^T fragment is read from LDS once per wave
+      // alpha' [V | n] fragment is read from LDS once per wave
       bf16x8 Ka[NDT][2];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
@@ -439,9 +436,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int vq = 0; vq < NVX; ++vq)
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-          const int off = (16 * vq + r16) * VB_PITCH + 2 * (32 * p + 8 * g);
-          const bf16x8 bh = *reinterpret_cast<const bf16x8*>(vbh + off);
-          const bf16x8 bl = *reinterpret_cast<const bf16x8*>(vbl + off);
+          // source lane 4k+a of group g: token 32p + 8g + 2k (+1) -- the token order
+          // of the K^T operand -- and 4 consecutive columns from avcol(vq, a)
+          const int off = (32 * p + 8 * g + 2 * (r16 >> 2)) * AV_PITCH + 2 * avcol(vq, r16 & 3);
+          const bf16x8 bh = tr8(avh + off, avh + off + AV_PITCH);
+          const bf16x8 bl = tr8(avl + off, avl + off + AV_PITCH);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
             Cacc[dt][vq] = mfma(Ka[dt][p], bh, Cacc[dt][vq]);
@@ -485,14 +484,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     for (int kc = 0; kc < NC; ++kc) {
       const float* gb = gbuf + (kc & 1) * GROWS * 64;
       store_k(Kst);
-      if (o == 0) {  // rows 64, 68, 72, 76 of (alpha' [V | 1])^T: alpha' itself (n replicated 4x)
+      if (o == 0) {  // columns 64, 68, 72, 76 of alpha' [V | n], token `lane`: alpha' itself (n replicated 4x)
         const float al = gb[256 + lane];
         const uint32_t hv = pack_bf16(al, 0.f);
         const uint16_t lo = (uint16_t)pack_bf16(al - bf_lo(hv), 0.f);
 #pragma unroll
-        for (int rr = 64; rr < 80; rr += 4) {
-          reinterpret_cast<uint16_t*>(vbh + rr * VB_PITCH)[vb_col(lane)] = (uint16_t)hv;
-          reinterpret_cast<uint16_t*>(vbl + rr * VB_PITCH)[vb_col(lane)] = lo;
+        for (int c = 64; c < 80; c += 4) {
+          reinterpret_cast<uint16_t*>(avh + lane * AV_PITCH)[c] = (uint16_t)hv;
+          reinterpret_cast<uint16_t*>(avl + lane * AV_PITCH)[c] = lo;
         }
       }
       __syncthreads();  // B1
