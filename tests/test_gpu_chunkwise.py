@@ -4,10 +4,13 @@
   on h and the final C, n, m;
 * every chunk size, initial states, ragged head dims, 16-bit inputs against the
   float32 oracle on the upcast inputs (max-abs <= 2e-2);
-* cfg2 at full size (bf16, B4 NH8 S8192, L 64 and 128): the causal prefix
-  property (tokens < S' depend only on inputs < S') lets the oracle check the
-  full-size output on a 512-token prefix of two heads; the final states are
-  checked through chunk-size invariance and against the other algorithm.
+* cfg2 at full size (bf16, B4 NH8 S8192, L 64 and 128) against the oracle on
+  the whole batch, plus the causal prefix property (tokens < S' depend only
+  on inputs < S'), chunk-size invariance and agreement with the other
+  algorithm;
+* the fused kernel works on 64-token chunks for every chunk_size (the forward
+  is chunk-size invariant): chunk sizes 16, 32, 128 against the oracle at that
+  chunk size.
 """
 
 import pytest
@@ -164,15 +167,32 @@ def test_fused_strong_forget_gates(gpu_case):
         assert e <= LOWP_ABS, name
 
 
-def test_cfg2_full_size_vs_oracle(gpu_case):
-    """cfg2 at full size, fused path, against the oracle on the whole batch (h and final states)."""
+@pytest.mark.parametrize("L", [64, 128])
+def test_cfg2_full_size_vs_oracle(gpu_case, L):
+    """cfg2 at full size, fused path, against the oracle at the same chunk size on the whole batch
+    (h and final states).  chunk_size=128 runs on the fused kernel's 64-token chunks: the forward is
+    chunk-size invariant, so only rounding separates it from the oracle's 128-token chunks."""
     import xlstm_hip
     from xlstm_hip.workloads import CFG2, chunkwise_inputs
     x = chunkwise_inputs(CFG2)
-    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, chunk_size=64)
-    hr, (Cr, nr, mr) = _oracle(x, (None, None, None), 64)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, chunk_size=L, algo="fused")
+    hr, (Cr, nr, mr) = _oracle(x, (None, None, None), L)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         e = lowp_excess(got, want)
-        print(f"cfg2 full {name}: max-abs {maxabs(got, want):.3e}, beyond output rounding {e:.3e}, "
+        print(f"cfg2 full L={L} {name}: max-abs {maxabs(got, want):.3e}, beyond output rounding {e:.3e}, "
               f"rel {relerr(got, want):.3e}")
         assert e <= LOWP_ABS, name
+
+
+@pytest.mark.parametrize("L", [16, 32, 128])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_fused_other_chunk_sizes(gpu_case, L, with_state):
+    """chunk_size 16, 32 and 128 on the fused kernel (S a multiple of 64) against the oracle at that chunk size."""
+    import xlstm_hip
+    B, NH, S, DQK, DV = 1, 2, 256, 256, 128
+    x, st = _inputs(B, NH, S, DQK, DV, torch.bfloat16, seed=L + with_state, with_state=with_state)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=L,
+                                             algo="fused")
+    hr, (Cr, nr, mr) = _oracle(x, st, L)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got, want, torch.bfloat16, f"fused L={L} state={with_state} {name}")

@@ -631,7 +631,7 @@ size_t chunkwise_fused_workspace(int B, int NH, int S) {
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why) {
   const char* r = nullptr;
   if (a.dtype_qkv != XL_DTYPE_BF16) r = "q/k/v must be bfloat16";
-  else if (a.L != fused::L) r = "chunk size must be 64";
+  else if (a.S % fused::L != 0) r = "sequence length must be a multiple of 64";
   else if (a.DQK != 128 && a.DQK != 256) r = "DQK must be 128 or 256";
   else if (a.DV % fused::DVT != 0) r = "DV must be a multiple of 64";
   if (why) *why = r;
