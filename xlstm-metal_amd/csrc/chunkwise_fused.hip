@@ -16,30 +16,30 @@
 //   h_i = H_i / (max(|den_i|, exp(-m_i)) + eps)
 //   C' = exp(g + m - m') C + sum_t exp(a_t - m') k_t v_t^T,  n' likewise
 //
-// The normaliser rides along as a fifth 16-column tile: C carries n in its
-// column 64, V carries a row of ones and alpha V carries alpha_t, so n', q.n
-// and the row sums come out of the same MFMAs as C', q C and M V, and den_i
-// lands in column 64 of H_i.
-//
 // Producer / consumer split (8 waves, two per SIMD):
-//  * state waves 0..3: wave s owns rows [s*DW, (s+1)*DW) of [C | n]
-//    (DW = DQK/4, float32 accumulators).  Per chunk it first forms the
-//    partial product Q[:, rows] [C | n][rows, :] for all 64 tokens, with the
-//    B operand built straight from its accumulators as bf16 hi + lo (two
+//  * state waves 0..3: wave s owns rows [s*DW, (s+1)*DW) of C (DW = DQK/4,
+//    float32 accumulators of v_mfma_f32_32x32x16_bf16).  Per chunk it first
+//    forms the partial product Q[:, rows] C[rows, :] for all 64 tokens, with
+//    the A operand built straight from its accumulators as bf16 hi + lo (two
 //    MFMAs, so q C keeps float32 accuracy), and leaves it in LDS.  It then
-//    applies the chunk update [C | n] += K^T (alpha [V | 1]) with alpha V
-//    split into bf16 hi + lo, so the state keeps float32 accuracy too.
+//    applies the chunk update C += K^T (alpha V) with alpha V split into bf16
+//    hi + lo, so the state keeps float32 accuracy too.
 //  * output waves 4..7: wave o owns output rows [16o, 16o+16) of every chunk:
 //    exact S^T = K Q^T over the whole DQK, gating and M [V | 1] (M split
 //    hi + lo); after the chunk's second barrier it adds the four partial
-//    Q [C | n] rows and writes h.
+//    Q C rows and writes h.  Wave o also carries rows [o*DQK/4, (o+1)*DQK/4)
+//    of the normaliser n (16 x 16 accumulators, alpha' hi and lo in
+//    alternate columns) and applies n += K^T alpha'; q.n comes out of a fifth
+//    A tile of the S product that holds n as four bf16 rows (hi and lo of
+//    both column sums), staged in LDS once per chunk.
 // The state never leaves the state waves' registers; the only cross-wave
 // traffic besides the staged q/k/v tiles is the 16-byte-per-lane partials.
-// All products are v_mfma_f32_16x16x32_bf16.  K^T and V operands are read
-// with ds_read_b64_tr_b16 from the natural row-major tiles (within 16 lanes,
-// output lane 4a+c receives element c of source lanes 4k+a, k = 0..3), with
-// the token order inside a k-slice chosen so that every LDS access pattern is
-// free of bank conflicts.
+// K^T, V and alpha V operands are read with ds_read_b64_tr_b16 from the
+// natural row-major tiles (within 16 lanes, output lane 4a+c receives element
+// c of source lanes 4k+a, k = 0..3).  Row pitches follow measured LDS rates
+// on gfx950: 16-byte reads of 16 consecutive rows at one column (the S
+// operand, the n rows) run at full rate when the pitch is 32 mod 64 bytes,
+// and the transposed reads of 4 consecutive rows stay conflict free there.
 //
 // The forget rescale exp(g + m - m') of C is deferred: the state is stored as
 // C e^{-G} (G = accumulated log rescale), the factor e^{-G} is folded into
@@ -58,6 +58,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -68,17 +69,23 @@ constexpr int NOW = 4;          // output waves
 constexpr int NTHREADS = 64 * (NSW + NOW);
 constexpr int DVT = 64;         // DV columns per workgroup
 constexpr int NVT = DVT / 16;   // 16-wide column tiles of v
-constexpr int NVX = NVT + 1;    // ... plus the n / ones / den tile
+constexpr int NVX = NVT + 1;    // ... plus the ones tile (row sums of M)
 constexpr int VN_PITCH = 160;   // bytes per row of natural V (8 consecutive rows -> distinct 32 B bank groups)
-constexpr int AV_PITCH = 160;   // bytes per row of natural alpha' [V | n] (80 columns; 2-row steps hit distinct banks)
+constexpr int AV_PITCH = 304;   // bytes per row of natural alpha' V: hi (64 bf16) | lo (64 bf16) | pad
+constexpr int HP_PITCH = 68;    // floats per token row of the partial Q C tiles
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
 constexpr int PREP_STRIDE = 320;  // floats per chunk of gate prep: b, a, cummax(i - b), (i - b) log2e, [g, max a]
-constexpr int GROWS = 6;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G]
+constexpr int GROWS = 7;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G], alpha' bf16 hi | lo
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// 32 x 32 x 16: lane l holds A row l % 32 / B column l % 32 at k = 8 (l / 32) .. +7;
+// D column l % 32, rows 8i + 4 (l / 32) + j in element 4i + j
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   f32x2 v = {lo, hi};
@@ -162,26 +169,23 @@ __global__ __launch_bounds__(256) void gate_prep_kernel(const TG* __restrict__ i
   }
 }
 
-// Column of the 64-wide DV tile held by column n of 16-wide tile vq (vq < 4):
-// runs of 4 consecutive columns, and the tile pair (2h, 2h+1) covers columns
-// 32h .. 32h+31 so that a lane of the transposed output holds 8 consecutive
-// columns (one 16-byte store).
+// Column of the 64-wide DV tile held by column n of 16-wide tile vq of the
+// output waves: runs of 4 consecutive columns, and the tile pair (2h, 2h+1)
+// covers columns 32h .. 32h+31 so that a lane of the transposed output holds 8
+// consecutive columns (one 16-byte store).
 __device__ __forceinline__ int vcol_of(int vq, int n) { return 32 * (vq >> 1) + 8 * (n >> 2) + 4 * (vq & 1) + (n & 3); }
-// First of the 4 consecutive natural columns of alpha' [V | n] that source
-// lane 4k + a of a transposed read of column tile vq fetches: the V columns of
-// tile vq (vq < 4), or the n tile's columns 64 + 4a .. 64 + 4a + 3.
-__device__ __forceinline__ int avcol(int vq, int a) { return vq < NVT ? vcol_of(vq, 4 * a) : 64 + 4 * a; }
 
 template <int DQK>
 struct Smem {
   static constexpr int KPD = DQK / 32;                   // 32-deep k-steps over DQK
-  static constexpr int KN_PITCH = DQK * 2 + 16;          // bytes per K row: 16 consecutive rows -> distinct 16 B groups
+  static constexpr int KN_PITCH = DQK * 2 + 32;          // bytes per K row (= 32 mod 64, see the header)
   static constexpr int KN = 0;                           // [64 t][KN_PITCH]: K natural
   static constexpr int VN = KN + 64 * KN_PITCH;          // [64 t][VN_PITCH]: V natural
-  static constexpr int AVH = VN + 64 * VN_PITCH;         // [64 t][AV_PITCH]: alpha' [V | n] hi, natural
-  static constexpr int AVL = AVH + 64 * AV_PITCH;        // ... lo
-  static constexpr int HP = AVL + 64 * AV_PITCH;         // [4 state waves][4 row tiles][NVX][64] f32x4: partial Q [C | n]
-  static constexpr int GATES = HP + 4 * 4 * NVX * 64 * 16;  // [2 chunks][GROWS][64] float: gate rows + scalars
+  static constexpr int AV = VN + 64 * VN_PITCH;          // [64 t][AV_PITCH]: alpha' V hi (64 bf16) | lo (64 bf16)
+  static constexpr int HP = AV + 64 * AV_PITCH;          // [4 state waves][64 t][HP_PITCH] float: partial Q C
+  static constexpr int NB = HP + NSW * 64 * HP_PITCH * 4;  // [2 chunks][4 parts][NB_PITCH] bf16: n (hi, lo of both halves)
+  static constexpr int NB_PITCH = DQK + 16;              // bf16 per n part row (= 32 mod 64 bytes)
+  static constexpr int GATES = NB + 2 * 4 * NB_PITCH * 2;     // [2 chunks][GROWS][64] float: gate rows + scalars
   static constexpr int BYTES = GATES + 2 * GROWS * 64 * 4;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
@@ -196,9 +200,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   using SM = Smem<DQK>;
   constexpr int KPD = SM::KPD;
   constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
-  constexpr int NDT = DW / 16;    // C row tiles per state wave
   constexpr int NKU = DQK / 64;   // K staging: 16-byte pieces per thread (64 rows x DQK / 512 threads / 8)
-  constexpr int KS = DW / 32;     // 32-deep k-steps over a state wave's rows
+  constexpr int ND = DQK / NOW;   // n rows per output wave
+  constexpr int NTO = ND / 16;    // 16-row n tiles per output wave
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x;
@@ -216,17 +220,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 
   char* kn = smem + SM::KN;
   char* vn = smem + SM::VN;
-  char* avh = smem + SM::AVH;
-  char* avl = smem + SM::AVL;
-  f32x4* hp = (f32x4*)(smem + SM::HP);
+  char* av = smem + SM::AV;
+  float* hp = (float*)(smem + SM::HP);
+  bf16_t* nbuf = (bf16_t*)(smem + SM::NB);   // [2][4][NB_PITCH]: n parts of chunk kc live in buffer kc & 1
   float* gbuf = (float*)(smem + SM::GATES);  // [2][GROWS][64]: rows of chunk kc live in buffer kc & 1
-
-  // n-tile columns 64..79 of alpha' [V | n]: zeros, except columns 64, 68, 72,
-  // 76, which carry alpha' itself and are rewritten every chunk
-  for (int e = tid; e < 64 * 8; e += NTHREADS) {
-    reinterpret_cast<uint32_t*>(avh + (e >> 3) * AV_PITCH + 128)[e & 7] = 0u;
-    reinterpret_cast<uint32_t*>(avl + (e >> 3) * AV_PITCH + 128)[e & 7] = 0u;
-  }
 
   const bf16_t* qh = q + (size_t)bh * S * DQK;
   const bf16_t* kh = k + (size_t)bh * S * DQK;
@@ -254,7 +251,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   // Row terms of the intra-chunk exponent, column terms, output row scales,
   // the combined stabiliser mc and alpha' = exp(a_t - m') e^{-G} of chunk c go
   // to buffer c & 1 together with the chunk's renormalisation factor of the
-  // stored state, m', the deferred log rescale G and the renormalise flag.
+  // stored state, m', the deferred log rescale G, the renormalise flag and
+  // alpha' as bf16 hi / lo (the B operand of the n update).
   const float* preph = prep + (size_t)bh * NC * PREP_STRIDE;
   float gm = m_init, gG = 0.f;  // running m and G (gate wave only)
   // pv[4] holds g (lane 0) and max a (lane 1): a per-lane load, so it is
@@ -283,7 +281,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     gb[64 + lane] = pv[3];                             // column term
     gb[128 + lane] = exp_(mb - mc + gG) * qk_scale;    // output row scale (deferred state rescale folded in)
     gb[192 + lane] = mc;
-    gb[256 + lane] = exp_(a - m_next - Gn);            // alpha' = exp(a_t - m') e^{-G}
+    const float al = exp_(a - m_next - Gn);            // alpha' = exp(a_t - m') e^{-G}
+    gb[256 + lane] = al;
+    // alpha' hi / lo as bf16; token t of each 8-token group at 4 (t & 1) + (t & 7) / 2, the k
+    // order of the transposed K reads of the n update
+    const uint32_t ahi = pack_bf16(al, 0.f);
+    uint16_t* ar = reinterpret_cast<uint16_t*>(gb + 384);
+    const int pos = (lane & ~7) + 4 * (lane & 1) + ((lane & 7) >> 1);
+    ar[pos] = (uint16_t)ahi;
+    ar[64 + pos] = (uint16_t)pack_bf16(al - bf_lo(ahi), 0.f);
     if (lane == 0) {
       gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
       gb[321] = m_next;
@@ -293,55 +299,88 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     gm = m_next;
     gG = Gn;
   };
+
+  // ---- n (output waves): wave o holds rows [o*ND, (o+1)*ND) as NTO 16 x 16 MFMA
+  // accumulator tiles; lane (g, r16) holds rows 16 dt + 4g + e of column r16.
+  // Even columns accumulate K^T alpha'_hi, odd columns K^T alpha'_lo, so
+  // n = (even column) + (odd column) keeps float32 accuracy with one MFMA per
+  // k-step.  Before every chunk the four parts (hi, lo of both halves) go to
+  // LDS as bf16 rows, the A operand of q.n in the output waves' S product.
+  const int nd0 = ND * ws;
+  f32x4 nacc[NTO];
+  auto store_nparts = [&](int buf) {
+    if (r16 < 2) {  // lane 0: even column (parts 0, 1), lane 1: odd column (parts 2, 3)
+      bf16_t* nb = nbuf + buf * 4 * SM::NB_PITCH + nd0 + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < NTO; ++dt) {
+        const f32x4 x = nacc[dt];
+        const u32x2 hi = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
+        const u32x2 lo = {pack_bf16(x[0] - bf_lo(hi[0]), x[1] - bf_hi(hi[0])),
+                          pack_bf16(x[2] - bf_lo(hi[1]), x[3] - bf_hi(hi[1]))};
+        *reinterpret_cast<u32x2*>(nb + (2 * r16) * SM::NB_PITCH + 16 * dt) = hi;
+        *reinterpret_cast<u32x2*>(nb + (2 * r16 + 1) * SM::NB_PITCH + 16 * dt) = lo;
+      }
+    }
+  };
+  if (w >= NSW) {
+#pragma unroll
+    for (int dt = 0; dt < NTO; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        nacc[dt][e] = (n0 && (r16 & 1) == 0) ? n0[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] : 0.f;
+    store_nparts(0);
+  }
   if (w == NSW) {
     float pv[5];
     prep_load(0, pv);
     gate_rows(0, pv);
   }
-  __syncthreads();  // B0: gate rows of chunk 0
+  __syncthreads();  // B0: gate rows and n parts of chunk 0
 
   if (w < NSW) {
     // =====================================================================
-    // state waves: rows [dw0, dw0 + DW) of [C | n], stored as C e^{-G}
+    // state waves: rows [dw0, dw0 + DW) of C, stored as C e^{-G}
     // =====================================================================
-    // Row 4a + c of accumulator tile dt holds state row d = dw0 + 32 (dt >> 1) +
-    // 8a + 4 (dt & 1) + c: each tile's rows come in runs of 4 consecutive d (what
-    // a transposed K read delivers), and the tile pair (2p, 2p+1) covers the 32
-    // consecutive d = dw0 + 32p .. +31 in k order, so q fragments are one
-    // 16-byte load.
+    // 32 x 32 accumulator tiles acc[dt][vt]: lane (hh, l32) holds column
+    // 32 vt + l32 and, in element e = 4i + j, state row
+    //   dw0 + 32 dt + 16 (i >> 1) + 8 hh + 4 (i & 1) + j,
+    // so the 8 elements 8s' .. 8s'+7 of a lane are the 8 consecutive rows
+    // 16 s' + 8 hh .. +7 of the tile: a q C k-step of 16 rows is one split of
+    // 8 accumulator values per lane and one 16-byte q load.
+    constexpr int NDT = DW / 32;   // 32-row tiles per state wave (1 or 2)
+    constexpr int QKS = DW / 16;   // 16-deep k-steps of q C over the wave's rows
     const int dw0 = ws * DW;
-    auto crow = [&](int dt, int a, int c) { return dw0 + 32 * (dt >> 1) + 8 * a + 4 * (dt & 1) + c; };
-    f32x4 Cacc[NDT][NVX];
+    const int l32 = lane & 31, hh = lane >> 5;
+    auto srow = [&](int dt, int e) {
+      const int i = e >> 2;
+      return dw0 + 32 * dt + 16 * (i >> 1) + 8 * hh + 4 * (i & 1) + (e & 3);
+    };
+    f32x16 acc[NDT][2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = crow(dt, g, e);  // accumulator row 4g+e of tile dt
+      for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-        for (int vq = 0; vq < NVT; ++vq)
-          Cacc[dt][vq][e] = c0 ? c0[((size_t)bh * DQK + d) * DV + v0 + vcol_of(vq, r16)] : 0.f;
-        // n is replicated in columns 0, 4, 8, 12 of the fifth tile
-        Cacc[dt][NVT][e] = (n0 && (r16 & 3) == 0) ? n0[(size_t)bh * DQK + d] : 0.f;
-      }
+        for (int e = 0; e < 16; ++e)
+          acc[dt][vt][e] = c0 ? c0[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] : 0.f;
 
     // V staging (state threads): rows t0 = 4*(tid>>4) + ((tid>>3)&1) and t0 + 2, columns 8*(tid&7)
     const int vrow = 4 * (tid >> 4) + ((tid >> 3) & 1), vcol = 8 * (tid & 7);
     u32x4 Kst[NKU], Vst[2];
-    // q fragments of this wave's k range for every row: rows 16rt + r16, columns
-    // dw0 + 32p + 8g .. +7 -- the k order of the B fragments that
-    // split8(Cacc[2p], Cacc[2p+1]) yields
-    u32x4 Qs[4][KS];
+    // q fragments (B operand of the transposed product C^T Q^T): token 32 tt + l32,
+    // rows dw0 + 16 s + 8 hh .. +7
+    u32x4 Qs[2][QKS];
     auto load_v = [&](int kc) {
       const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
       Vst[0] = *reinterpret_cast<const u32x4*>(vb + (size_t)vrow * DV);
       Vst[1] = *reinterpret_cast<const u32x4*>(vb + (size_t)(vrow + 2) * DV);
     };
     auto load_qs = [&](int kc) {
-      const bf16_t* qb = qh + ((size_t)kc * L + r16) * DQK + dw0 + 8 * g;
+      const bf16_t* qb = qh + ((size_t)kc * L + l32) * DQK + dw0 + 8 * hh;
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int p = 0; p < KS; ++p) Qs[rt][p] = *reinterpret_cast<const u32x4*>(qb + (size_t)16 * rt * DQK + 32 * p);
+        for (int s = 0; s < QKS; ++s) Qs[tt][s] = *reinterpret_cast<const u32x4*>(qb + (size_t)32 * tt * DQK + 16 * s);
     };
     load_k(0, Kst);
     load_v(0);
@@ -352,66 +391,73 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       // V natural and alpha' V hi / lo (natural layout, 16-byte rows)
       *reinterpret_cast<u32x4*>(vn + vrow * VN_PITCH + 2 * vcol) = Vst[0];
       *reinterpret_cast<u32x4*>(vn + (vrow + 2) * VN_PITCH + 2 * vcol) = Vst[1];
+      const float al2[2] = {gb[256 + vrow], gb[256 + vrow + 2]};
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const float al = gb[256 + vrow + 2 * r];
         u32x4 hv, lv;
 #pragma unroll
         for (int c2 = 0; c2 < 4; ++c2) {
-          const float x0 = al * bf_lo(Vst[r][c2]), x1 = al * bf_hi(Vst[r][c2]);
+          const float x0 = al2[r] * bf_lo(Vst[r][c2]), x1 = al2[r] * bf_hi(Vst[r][c2]);
           hv[c2] = pack_bf16(x0, x1);
           lv[c2] = pack_bf16(x0 - bf_lo(hv[c2]), x1 - bf_hi(hv[c2]));
         }
-        *reinterpret_cast<u32x4*>(avh + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = hv;
-        *reinterpret_cast<u32x4*>(avl + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = lv;
+        *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = hv;
+        *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 128 + 2 * vcol) = lv;
       }
       __syncthreads();  // B1: the chunk's tiles are visible; the previous chunk's partials have been read
       if (kc + 1 < NC) {  // staging registers are free: prefetch (q after its last use below)
         load_k(kc + 1, Kst);
         load_v(kc + 1);
       }
-      // partial Q [C | n] over this wave's rows, with the state before this chunk
-      // (bf16 hi + lo of the float32 accumulators, so q C keeps float32 accuracy).
-      // Transposed product [C | n]^T Q^T: lane (g, r16) gets columns 4g+e of
-      // token 16rt + r16.  Software pipelined: the split of tile vq+1 (VALU) is
-      // interleaved with the MFMAs of tile vq, and tile vq's partials are stored
-      // one tile later, when its MFMAs have retired.
+      // partial Q C over this wave's rows, with the state before this chunk
+      // (bf16 hi + lo of the float32 accumulators, so q C keeps float32
+      // accuracy).  Transposed product C^T Q^T per 32-column tile vt: lane
+      // (hh, l32) gets columns 32 vt + 8i + 4hh + j of token 32 tt + l32.
+      // Software pipelined: the split of k-step q+1 (VALU) is interleaved with
+      // the four MFMAs of k-step q, and the partials of column tile 0 are
+      // stored one k-step into tile 1, when their MFMAs have retired.
       {
-        bf16x8 bsp[2][KS][2];
-        f32x4 Hp[2][4];
+        constexpr int NQ = 2 * QKS;
+        bf16x8 bsp[2][2];
+        f32x16 P[2][2];
+        auto split_q = [&](int qi, bf16x8 (&o)[2]) {
+          const int vt = qi / QKS, s = qi % QKS;
+          const f32x16& a = acc[s >> 1][vt];
+          const int e0 = 8 * (s & 1);
+          split8(f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]}, f32x4{a[e0 + 4], a[e0 + 5], a[e0 + 6], a[e0 + 7]},
+                 o[0], o[1]);
+        };
+        auto store_p = [&](int vt) {
 #pragma unroll
-        for (int p = 0; p < KS; ++p) split8(Cacc[2 * p][0], Cacc[2 * p + 1][0], bsp[0][p][0], bsp[0][p][1]);
+          for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int vq = 0; vq < NVX; ++vq) {
-          const int cur = vq & 1;
-          if (vq + 1 < NVX) {
+            for (int i = 0; i < 4; ++i)
+              *reinterpret_cast<f32x4*>(hp + (ws * 64 + 32 * tt + l32) * HP_PITCH + 32 * vt + 8 * i + 4 * hh) =
+                  f32x4{P[vt][tt][4 * i], P[vt][tt][4 * i + 1], P[vt][tt][4 * i + 2], P[vt][tt][4 * i + 3]};
+        };
+        split_q(0, bsp[0]);
 #pragma unroll
-            for (int p = 0; p < KS; ++p)
-              split8(Cacc[2 * p][vq + 1], Cacc[2 * p + 1][vq + 1], bsp[cur ^ 1][p][0], bsp[cur ^ 1][p][1]);
+        for (int qi = 0; qi < NQ; ++qi) {
+          const int cur = qi & 1, vt = qi / QKS, s = qi % QKS;
+          if (qi + 1 < NQ) split_q(qi + 1, bsp[cur ^ 1]);
+          if (s == 0) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) P[vt][tt] = f32x16{};
           }
 #pragma unroll
-          for (int rt = 0; rt < 4; ++rt) Hp[cur][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int hl = 0; hl < 2; ++hl)
 #pragma unroll
-          for (int p = 0; p < KS; ++p)
+            for (int tt = 0; tt < 2; ++tt)
+              P[vt][tt] = mfma32(bsp[cur][hl], __builtin_bit_cast(bf16x8, Qs[tt][s]), P[vt][tt]);
+          if (vt == 1 && s == 1) store_p(0);
+          // ask the scheduler for 1 MFMA : 6 VALU
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-              Hp[cur][rt] = mfma(bsp[cur][p][0], __builtin_bit_cast(bf16x8, Qs[rt][p]), Hp[cur][rt]);
-              Hp[cur][rt] = mfma(bsp[cur][p][1], __builtin_bit_cast(bf16x8, Qs[rt][p]), Hp[cur][rt]);
-            }
-          if (vq > 0) {
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + vq - 1) * 64 + lane] = Hp[cur ^ 1][rt];
-          }
-          // ask the scheduler for 1 MFMA : 3 VALU, then the stores
-#pragma unroll
-          for (int u = 0; u < 8 * KS; ++u) {
+          for (int u = 0; u < 4; ++u) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
           }
-          __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
         }
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) hp[((ws * 4 + rt) * NVX + NVX - 1) * 64 + lane] = Hp[(NVX - 1) & 1][rt];
+        store_p(1);
       }
       if (kc + 1 < NC) load_qs(kc + 1);
       if (gb[323] != 0.f) {  // renormalise the stored state (wave-uniform)
@@ -419,34 +465,38 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-          for (int vq = 0; vq < NVX; ++vq) Cacc[dt][vq] *= sc;
+          for (int vt = 0; vt < 2; ++vt) acc[dt][vt] *= sc;
       }
-      // K^T fragments of all this wave's row tiles stay in registers, so every
-      // alpha' [V | n] fragment is read from LDS once per wave
-      bf16x8 Ka[NDT][2];
+      // update C += K^T (alpha' V): A = K^T (row l32 of tile dt is state row
+      // srow(dt, .) of that accumulator row), B = alpha' V (column 32 vt + l32),
+      // 16-token k-steps, tokens 16 ks + 8 hh + jj in both.  Transposed reads:
+      // within 16 lanes, source lane 4kk + a reads token 16 ks + 8 hh + kk (+4
+      // for the second read) at 4 consecutive columns.
+      {
+        const int kk = r16 >> 2, ka = r16 & 3;
+        bf16x8 Kt[NDT][4];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          // source lane 4k+a of group g: token 32p + 8g + 2k (+1), state rows crow(dt, a, 0 .. 3)
-          const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * crow(dt, r16 & 3, 0);
-          Ka[dt][p] = tr8(base, base + SM::KN_PITCH);
-        }
-#pragma unroll
-      for (int vq = 0; vq < NVX; ++vq)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          // source lane 4k+a of group g: token 32p + 8g + 2k (+1) -- the token order
-          // of the K^T operand -- and 4 consecutive columns from avcol(vq, a)
-          const int off = (32 * p + 8 * g + 2 * (r16 >> 2)) * AV_PITCH + 2 * avcol(vq, r16 & 3);
-          const bf16x8 bh = tr8(avh + off, avh + off + AV_PITCH);
-          const bf16x8 bl = tr8(avl + off, avl + off + AV_PITCH);
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            Cacc[dt][vq] = mfma(Ka[dt][p], bh, Cacc[dt][vq]);
-            Cacc[dt][vq] = mfma(Ka[dt][p], bl, Cacc[dt][vq]);
+          for (int ks = 0; ks < 4; ++ks) {
+            const char* base = kn + (16 * ks + 8 * hh + kk) * SM::KN_PITCH +
+                               2 * (dw0 + 32 * dt + 16 * (g & 1) + 8 * (ka & 1) + 4 * (ka >> 1));
+            Kt[dt][ks] = tr8(base, base + 4 * SM::KN_PITCH);
           }
-        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int vt = 0; vt < 2; ++vt) {
+            const char* base = av + (16 * ks + 8 * hh + kk) * AV_PITCH + 2 * (32 * vt + 16 * (g & 1) + 4 * ka);
+            const bf16x8 bh = tr8(base, base + 4 * AV_PITCH);
+            const bf16x8 bl = tr8(base + 128, base + 128 + 4 * AV_PITCH);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+              acc[dt][vt] = mfma32(Kt[dt][ks], bh, acc[dt][vt]);
+              acc[dt][vt] = mfma32(Kt[dt][ks], bl, acc[dt][vt]);
+            }
+          }
+      }
       __syncthreads();  // B2: partials complete; the chunk's tiles may be overwritten
     }
     // ---- final states (undo the deferred rescale)
@@ -456,19 +506,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = crow(dt, g, e);
+        for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-          for (int vq = 0; vq < NVT; ++vq)
-            c_last[((size_t)bh * DQK + d) * DV + v0 + vcol_of(vq, r16)] = Cacc[dt][vq][e] * sc;
-          if (v0 == 0 && r16 == 0) n_last[(size_t)bh * DQK + d] = Cacc[dt][NVT][e] * sc;
-        }
+          for (int e = 0; e < 16; ++e)
+            c_last[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] = acc[dt][vt][e] * sc;
       if (v0 == 0 && tid == 0) m_last[bh] = gl[321];
     }
   } else {
     // =====================================================================
-    // output waves: rows [16o, 16o + 16) of every chunk
+    // output waves: rows [16o, 16o + 16) of every chunk, and n rows [nd0, nd0 + ND)
     // =====================================================================
+    // the output waves are the longer dependency chain of a chunk: let their
+    // MFMAs and loads win the SIMD's issue arbitration over the state waves'
+    __builtin_amdgcn_s_setprio(2);
     const int o = ws;
     u32x4 Kst[NKU], Qf[KPD];
     float pv[5];  // gate prep of the next chunk (gate wave)
@@ -483,17 +533,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     load_q(0);
     for (int kc = 0; kc < NC; ++kc) {
       const float* gb = gbuf + (kc & 1) * GROWS * 64;
+      const bf16_t* nbk = nbuf + (kc & 1) * 4 * SM::NB_PITCH;
       store_k(Kst);
-      if (o == 0) {  // columns 64, 68, 72, 76 of alpha' [V | n], token `lane`: alpha' itself (n replicated 4x)
-        const float al = gb[256 + lane];
-        const uint32_t hv = pack_bf16(al, 0.f);
-        const uint16_t lo = (uint16_t)pack_bf16(al - bf_lo(hv), 0.f);
-#pragma unroll
-        for (int c = 64; c < 80; c += 4) {
-          reinterpret_cast<uint16_t*>(avh + lane * AV_PITCH)[c] = (uint16_t)hv;
-          reinterpret_cast<uint16_t*>(avl + lane * AV_PITCH)[c] = lo;
-        }
-      }
       __syncthreads();  // B1
       if (kc + 1 < NC) {
         load_k(kc + 1, Kst);
@@ -504,30 +545,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       // B = q rows.  Every output wave computes all four (tiles above the
       // diagonal are masked in the gating), so the code is branch-free; the
       // busiest SIMD (the wave of the last row tile) does the same work as
-      // before.  All K fragments are requested up front: LDS latency is many
-      // times the four MFMAs of one k-step.
-      f32x4 Sacc[4];
+      // before.  A fifth A tile holds the four parts of n (row r16 = part
+      // r16 & 3), so the same MFMAs give q.n in every lane.
+      f32x4 Sacc[5];
       constexpr int KD = 2;
-      u32x4 kf[KD][4];
-#pragma unroll
-      for (int p = 0; p < KD - 1; ++p)
+      u32x4 kf[KD][5];
+      auto load_kf = [&](int p, u32x4 (&dst)[5]) {
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
-          kf[p][jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
+          dst[jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
+        dst[4] = *reinterpret_cast<const u32x4*>(nbk + (r16 & 3) * SM::NB_PITCH + 32 * p + 8 * g);
+      };
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < KD - 1; ++p) load_kf(p, kf[p]);
+#pragma unroll
+      for (int jt = 0; jt < 5; ++jt) Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < KPD; ++p) {
-        if (p + KD - 1 < KPD) {
+        if (p + KD - 1 < KPD) load_kf(p + KD - 1, kf[(p + KD - 1) % KD]);
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt)
-            kf[(p + KD - 1) % KD][jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * (p + KD - 1));
-        }
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+        for (int jt = 0; jt < 5; ++jt)
           Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
       }
       if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch
+      const float qn = (Sacc[4][0] + Sacc[4][1]) + (Sacc[4][2] + Sacc[4][3]);  // q . n (stored state)
       // gate the scores of row i = 16o + r16, then M [V | 1] with M split hi + lo
       const int i = 16 * o + r16;
       const float bli = gb[i];
@@ -562,24 +603,49 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           Hmv[vq] = mfma(vb, ml, Hmv[vq]);
         }
       }
-      // the gate wave forms the gate rows of chunk kc + 1 (buffer (kc + 1) & 1,
-      // last read before B1 of this chunk)
-      if (o == 0 && kc + 1 < NC) gate_rows(kc + 1, pv);
-      __syncthreads();  // B2: the state waves' partial Q [C | n] of this chunk are complete
-      // Q [C | n] of rows 16o + 4g + e: sum of the four state waves' partials
-      f32x4 Hqc[NVX];
+      // n update: n += K^T alpha' over rows [nd0, nd0 + ND) (renormalised first
+      // when the chunk asks for it).  A = K^T (transposed reads: source lane 4kk + a
+      // of group g reads token 32p + 8g + 2kk (+1) at rows nd0 + 16dt + 4a ..),
+      // B = alpha' hi (even columns) / lo (odd columns) in the same token order.
+      {
+        if (gb[323] != 0.f) {
+          const float sc = gb[320];
 #pragma unroll
-      for (int vq = 0; vq < NVX; ++vq) {
-        Hqc[vq] = hp[((0 * 4 + o) * NVX + vq) * 64 + lane];
+          for (int dt = 0; dt < NTO; ++dt) nacc[dt] *= sc;
+        }
+        const uint16_t* ar = reinterpret_cast<const uint16_t*>(gb + 384) + 64 * (r16 & 1);
 #pragma unroll
-        for (int sw = 1; sw < NSW; ++sw) Hqc[vq] += hp[((sw * 4 + o) * NVX + vq) * 64 + lane];
+        for (int p = 0; p < 2; ++p) {
+          const bf16x8 ab = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ar + 32 * p + 8 * g));
+#pragma unroll
+          for (int dt = 0; dt < NTO; ++dt) {
+            const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * (nd0 + 16 * dt + 4 * (r16 & 3));
+            nacc[dt] = mfma(tr8(base, base + SM::KN_PITCH), ab, nacc[dt]);
+          }
+        }
+        store_nparts((kc + 1) & 1);
       }
+      // the gate wave forms the gate rows of chunk kc + 1 (buffer (kc + 1) & 1,
+      // last read before B2 of the previous chunk)
+      if (o == 0 && kc + 1 < NC) gate_rows(kc + 1, pv);
+      __syncthreads();  // B2: the state waves' partial Q C of this chunk are complete
+      // Q C of row 16o + r16, columns vcol_of(vq, 4g + e): sum of the four state
+      // waves' partials (two 16-byte runs of 4 columns per tile pair)
+      f32x4 Hqc[NVT];
+      const float* pr = hp + (16 * o + r16) * HP_PITCH + 8 * g;
+#pragma unroll
+      for (int vq = 0; vq < NVT; ++vq) Hqc[vq] = *reinterpret_cast<const f32x4*>(pr + 32 * (vq >> 1) + 4 * (vq & 1));
+#pragma unroll
+      for (int sw = 1; sw < NSW; ++sw)
+#pragma unroll
+        for (int vq = 0; vq < NVT; ++vq)
+          Hqc[vq] += *reinterpret_cast<const f32x4*>(pr + sw * 64 * HP_PITCH + 32 * (vq >> 1) + 4 * (vq & 1));
       // finish row 16o + r16: this lane holds columns vcol_of(vq, 4g + e), i.e. the
-      // 8 consecutive columns 32h + 8g .. +7 of tiles (2h, 2h+1); the denominator
-      // (n / ones replicated in rows 0, 4, 8, 12 of the fifth tile) is element 0
+      // 8 consecutive columns 32h + 8g .. +7 of tiles (2h, 2h+1); the row sum of M
+      // (ones in rows 0, 4, 8, 12 of the fifth tile) is element 0
       const float qb = gb[128 + 16 * o + r16];
       const float mcr = gb[192 + 16 * o + r16];
-      const float den = qb * Hqc[NVT][0] + Hmv[NVT][0];
+      const float den = qb * qn + Hmv[NVT][0];
       const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr)) + eps);
       bf16_t* hb = hh + ((size_t)kc * L + 16 * o + r16) * DV + v0 + 8 * g;
 #pragma unroll
@@ -593,6 +659,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         }
         *reinterpret_cast<u32x4*>(hb + 32 * h2) = out;
       }
+    }
+    // ---- final n (undo the deferred rescale): even + odd column, lanes r16 = 0, 1
+    if (c_last && v0 == 0) {
+      const float* gl = gbuf + ((NC - 1) & 1) * GROWS * 64;
+      const float sc = exp_(gl[322]);
+#pragma unroll
+      for (int dt = 0; dt < NTO; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float na = nacc[dt][e];
+          // quad_perm [1, 0, 3, 2]: lane 4q gets lane 4q + 1
+          const float nb = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, na), 0xB1, 0xf, 0xf, false));
+          if (r16 == 0) n_last[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] = (na + nb) * sc;
+        }
     }
   }
 }
