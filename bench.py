@@ -1,7 +1,7 @@
 """Benchmark of the mLSTM kernel backend on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--chunk-size 64] [--algo auto]
-                    [--decode-steps 1000] [--no-cpu-baseline] [--no-decode] [--no-soft-cap]
+                    [--decode-steps 1000] [--no-cpu-baseline] [--no-decode] [--no-soft-cap] [--no-extra]
     python bench.py --summarize-pmc FETCH_DIR WRITE_DIR      (no GPU: reads rocprofv3 CSVs)
 
 Prints ONE JSON line.  Headline (`value`): chunkwise mLSTM prefill tokens/s
@@ -19,6 +19,11 @@ state really streams from HBM), captured in a HIP graph.  `soft_cap` reports
 the logit soft-cap (cap 30) over config 3's prefill logits [1, 2048, 50304]
 bf16, a pure HBM stream; the same kernel serves as the known-size streaming
 kernel that calibrates the rocprofv3 FETCH_SIZE / WRITE_SIZE counters.
+`slstm_sequence` (config 4's sLSTM layer, one time-loop launch),
+`mlstm_sequence` (the recurrent mLSTM time loop over 64 tokens of config 2's
+heads) and `arbitrary_length` (the any-S wrapper on config 2 with S = 8255)
+measure the remaining rows of the path; each is timed like the headline
+(cache flush, HIP graph replay, HIP events) and reported against HBM.
 
 HBM traffic (`roofline.traffic`) cannot be measured from inside the process:
 it comes from two rocprofv3 --pmc passes over this script (FETCH_SIZE, then
@@ -244,6 +249,109 @@ def bench_soft_cap(args, dev):
                          "traffic": load_traffic(SOFT_CAP_KERNEL, "cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16")}}
 
 
+def _timed(call, dev, steps, warmup=3):
+    """Mean / median / min HIP-event ms of `call` over `steps` runs, each after a cache flush.
+    The call is replayed from a HIP graph when it can be captured (host dispatch stays out of
+    the timed region), else run eagerly."""
+    flush = Flusher(dev)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize(dev)
+    mode = "hip_graph"
+    try:
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            call()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            call()
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        run = graph.replay
+    except Exception as exc:  # measurement method only; the kernels are the same
+        mode, run = f"eager ({type(exc).__name__})", call
+    times = []
+    for _ in range(steps):
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        flush()
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1))
+    return {"ms": statistics.mean(times), "ms_median": statistics.median(times), "ms_min": min(times), "mode": mode}
+
+
+def _hbm(by, ms):
+    gbs = by / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+            "bytes_per_call": by}
+
+
+def bench_slstm_sequence(args, dev):
+    """sLSTM time loop over config 4's sLSTM layer (B8 S4096 NH4 H512, bf16 z / gates / h,
+    float32 states from zero, last states returned): one xl_slstm_seq_fwd launch.
+    Bytes: z and h (bf16) + the three gates (bf16) + last c, n, m (float32)."""
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG4_SLSTM as c, slstm_inputs
+    z, i, f, o = slstm_inputs(c, device=dev)
+    t = _timed(lambda: xlstm_hip.slstm_sequence(z, i, f, o), dev, max(5, args.steps))
+    by = 2 * c.B * c.S * c.NH * c.H * 2 + 3 * c.B * c.S * c.NH * 2 + c.B * c.NH * (2 * c.H + 1) * 4
+    return {"workload": f"cfg4 sLSTM layer sequence B{c.B} S{c.S} NH{c.NH} H{c.H} bf16", "us_per_call": 1e3 * t["ms"],
+            "us_min": 1e3 * t["ms_min"], "tokens_per_s": c.B * c.S / (t["ms"] * 1e-3), "mode": t["mode"],
+            "roofline": _hbm(by, t["ms"])}
+
+
+def bench_mlstm_sequence(args, dev):
+    """Recurrent mLSTM time loop (xl_mlstm_sequence_fwd) over 64 tokens of config 2's heads
+    (B4 NH8 DQK256 DV512, bf16 q/k/v/gates) from config-1-style float32 initial states, last
+    states returned.  Bytes: C, n, m read and written once + q, k, v, h, gates of the 64 tokens."""
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    cfg, S = CFG2, 64
+    q, k, v, i, f = chunkwise_inputs(cfg, device=dev, S=S)
+    g = torch.Generator("cpu").manual_seed(5)
+    C = (0.1 * torch.randn(cfg.B, cfg.NH, cfg.DQK, cfg.DV, generator=g)).to(dev)
+    n = torch.randn(cfg.B, cfg.NH, cfg.DQK, generator=g).abs().to(dev)
+    m = torch.randn(cfg.B, cfg.NH, 1, generator=g).to(dev)
+    t = _timed(lambda: xlstm_hip.mlstm_recurrent_sequence__native_fw(q, k, v, i, f, C, n, m, return_last_states=True),
+               dev, max(5, args.steps))
+    BH = cfg.B * cfg.NH
+    by = 2 * BH * (cfg.DQK * cfg.DV + cfg.DQK + 1) * 4 + BH * S * (2 * cfg.DQK + 2 * cfg.DV + 2) * 2
+    return {"workload": f"mlstm recurrent sequence, cfg2 heads B{cfg.B} NH{cfg.NH} DQK{cfg.DQK} DV{cfg.DV}, S={S}",
+            "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "us_per_token": 1e3 * t["ms"] / S,
+            "mode": t["mode"], "roofline": _hbm(by, t["ms"])}
+
+
+def bench_arbitrary_length(args, dev):
+    """Any-S inference wrapper (wrap_chunkwise__arbitrary_sequence_length) on config 2 with
+    S = 8192 + 63: chunk sizes 64 (8192 tokens), 32, 16 and a 15-token recurrent tail, states
+    carried between the pieces.  Compared with the S = 8192 headline call."""
+    from xlstm_hip import backend
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    cfg, S = CFG2, 8192 + 63
+    q, k, v, i, f = chunkwise_inputs(cfg, device=dev, S=S)
+
+    def call():
+        return backend.wrap_chunkwise__arbitrary_sequence_length(
+            backend.get_mlstm_kernel("chunkwise--native_autograd"),
+            backend.get_mlstm_sequence_kernel("native_sequence__native"), backend.get_mlstm_step_kernel("native"),
+            q=q, k=k, v=v, f=f, i=i, return_last_states=True, chunk_size=64)
+
+    t = _timed(call, dev, max(5, args.steps // 2))
+    fl = prefill_flops(cfg.B, cfg.NH, S, cfg.DQK, cfg.DV, 64)
+    by = prefill_bytes(cfg.B, cfg.NH, S, cfg.DQK, cfg.DV)
+    return {"workload": f"cfg2 arbitrary-length wrapper, S={S} (64 x 128 + 32 + 16 + 15-token tail)",
+            "ms_per_call": t["ms"], "ms_min": t["ms_min"], "tokens_per_s": cfg.B * S / (t["ms"] * 1e-3),
+            "mode": t["mode"], "tflops_64_token_algorithm": fl / (t["ms"] * 1e-3) / 1e12,
+            "roofline_hbm": _hbm(by, t["ms"])}
+
+
 def load_traffic(kernel, workload):
     """Calibrated HBM bytes per launch of `kernel` on `workload` from profiles/hbm_traffic.json, else None."""
     try:
@@ -346,6 +454,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-soft-cap", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the sLSTM, recurrent-sequence and any-S entries")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
     if args.summarize_pmc:
@@ -404,6 +513,10 @@ def main():
                                       "traffic": load_traffic("mlstm_step_kernel", "cfg1 mlstm decode step")}}
     if not args.no_soft_cap:
         out["soft_cap"] = bench_soft_cap(args, dev)
+    if not args.no_extra:
+        out["slstm_sequence"] = bench_slstm_sequence(args, dev)
+        out["mlstm_sequence"] = bench_mlstm_sequence(args, dev)
+        out["arbitrary_length"] = bench_arbitrary_length(args, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(out), flush=True)

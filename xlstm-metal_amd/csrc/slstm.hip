@@ -6,9 +6,10 @@
 //   c' = fg c + ig tanh(z);      n' = fg n + ig;    h = sigmoid(o) c' / (|n'| + eps)
 // Gates are per (b, h) and there is no recurrent matrix, so the recurrence is
 // elementwise: one thread per (b, h, d), coalesced along d.  The sequence
-// kernel keeps c, n, m in registers across all S steps and prefetches the
-// next step's z and gates while the current one is computed.
+// kernel splits the time axis over the waves of a workgroup (see below).
 #include "common.h"
+
+#include <type_traits>
 
 namespace xl {
 
@@ -45,49 +46,235 @@ __global__ __launch_bounds__(256) void slstm_step_kernel(const TZ* __restrict__ 
   if (idx - bh * H == 0) m_new[bh] = g.mn;
 }
 
-template <typename TZ, typename TG, typename TH>
-__global__ __launch_bounds__(256) void slstm_seq_kernel(const TZ* __restrict__ z, const TG* __restrict__ ip,
-                                                        const TG* __restrict__ fp, const TG* __restrict__ op,
-                                                        const float* __restrict__ c0, const float* __restrict__ n0,
-                                                        const float* __restrict__ m0, TH* __restrict__ h,
-                                                        float* __restrict__ c_last, float* __restrict__ n_last,
-                                                        float* __restrict__ m_last, int S, int NH, int H,
-                                                        int64_t total, float eps) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over B*NH*H
-  if (idx >= total) return;
-  const int64_t bh = idx / H;
-  const int d = (int)(idx - bh * H);
-  const int64_t b = bh / NH;
-  const int hh = (int)(bh - b * NH);
-  float c = c0 ? c0[idx] : 0.f;
-  float n = n0 ? n0[idx] : 0.f;
-  float m = m0 ? m0[bh] : 0.f;
-  // z[b, t, hh, d] and gates[b, t, hh]
-  const int64_t zstride = (int64_t)NH * H, gstride = NH;
-  const TZ* zp = z + b * S * zstride + (int64_t)hh * H + d;
-  TH* hp = h + b * S * zstride + (int64_t)hh * H + d;
-  const int64_t g0 = b * S * gstride + hh;
-  float zn = to_f32(zp[0]);
-  float in = to_f32(ip[g0]), fn = to_f32(fp[g0]), on = to_f32(op[g0]);
-  for (int t = 0; t < S; ++t) {
-    const float zc = zn, ic = in, fc = fn, oc = on;
-    if (t + 1 < S) {  // prefetch step t+1
-      zn = to_f32(zp[(int64_t)(t + 1) * zstride]);
-      const int64_t gi = g0 + (int64_t)(t + 1) * gstride;
-      in = to_f32(ip[gi]);
-      fn = to_f32(fp[gi]);
-      on = to_f32(op[gi]);
-    }
-    const SGate g = slstm_gates(ic, fc, oc, m);
-    c = g.fg * c + g.ig * tanh_f32(zc);
-    n = g.fg * n + g.ig;
-    m = g.mn;
-    hp[(int64_t)t * zstride] = from_f32<TH>(g.og * c / (fabsf(n) + eps));
+// ---------------------------------------------------------------- sequence
+// The per-element recurrence is linear in (c, n) once the gates are known,
+// and the stabiliser m depends on the gates of its head only.  So the time
+// axis is split: one workgroup per (b, h, 64 consecutive d) with SEQ_WAVES
+// waves, wave w owning the time segment [w*SL, (w+1)*SL) (SL = ceil(S/16)).
+//  * Gates, 64 steps at a time with lane = step: m_t = max(m_{t-1} + logsig f_t, i_t)
+//    is the scan of the max-plus maps m -> max(m + a, b), a = logsig f_t,
+//    b = i_t, composed as (a, b) o (a', b') = (a + a', max(b + a', b')).  The
+//    map of a span carries the sums of logsig f over sub-spans only, so m has
+//    the rounding of the step-by-step recurrence (exact where i_t resets it).
+//  * Pass 0: each wave composes the map of its segment; the incoming m of
+//    segment w is m0 pushed through the maps of segments 0 .. w-1 (LDS).
+//  * Pass 1: each wave runs its segment from c = 0 (per lane) and the scans
+//    give the segment's F = prod fg and n from 0 (uniform), to LDS.
+//  * Pass 2: each wave composes its start state c = F c + c_seg over the
+//    earlier segments and reruns its segment from it, writing h; the wave of
+//    the last step writes the final states.
+// z is read twice (the second read mostly hits the Infinity Cache); every
+// step of both passes keeps z loads SEQ_PF steps ahead.
+constexpr int SEQ_WAVES = 16;
+constexpr int SEQ_PF = 16;
+constexpr float SEQ_LOG2E = 1.4426950408889634f;
+
+// inclusive scan over the lanes (lane order = time) of the maps m -> max(m + a, b)
+__device__ __forceinline__ void maxplus_scan(float& a, float& b) {
+  const int ida = __float_as_int(0.f), idb = __float_as_int(-INFINITY);
+#define XL_MP_STEP(CTRL, ROWMASK)                                                                                 \
+  {                                                                                                               \
+    const float ae = __int_as_float(__builtin_amdgcn_update_dpp(ida, __float_as_int(a), CTRL, ROWMASK, 0xf, false)); \
+    const float be = __int_as_float(__builtin_amdgcn_update_dpp(idb, __float_as_int(b), CTRL, ROWMASK, 0xf, false)); \
+    b = fmaxf(be + a, b);                                                                                         \
+    a = ae + a;                                                                                                   \
   }
-  if (c_last) {
-    c_last[idx] = c;
-    n_last[idx] = n;
-    if (d == 0) m_last[bh] = m;
+  XL_MP_STEP(0x111, 0xf)  // row_shr:1
+  XL_MP_STEP(0x112, 0xf)  // row_shr:2
+  XL_MP_STEP(0x114, 0xf)  // row_shr:4
+  XL_MP_STEP(0x118, 0xf)  // row_shr:8
+  XL_MP_STEP(0x142, 0xa)  // row_bcast:15 into rows 1, 3
+  XL_MP_STEP(0x143, 0xc)  // row_bcast:31 into rows 2, 3
+#undef XL_MP_STEP
+}
+
+// inclusive scan of the affine maps x -> F x + N (n from 0 and prod fg)
+__device__ __forceinline__ void affine_scan(float& F, float& N) {
+  const int idf = __float_as_int(1.f), idn = __float_as_int(0.f);
+#define XL_AF_STEP(CTRL, ROWMASK)                                                                                 \
+  {                                                                                                               \
+    const float fe = __int_as_float(__builtin_amdgcn_update_dpp(idf, __float_as_int(F), CTRL, ROWMASK, 0xf, false)); \
+    const float ne = __int_as_float(__builtin_amdgcn_update_dpp(idn, __float_as_int(N), CTRL, ROWMASK, 0xf, false)); \
+    N = fmaf(ne, F, N);                                                                                           \
+    F = fe * F;                                                                                                   \
+  }
+  XL_AF_STEP(0x111, 0xf)
+  XL_AF_STEP(0x112, 0xf)
+  XL_AF_STEP(0x114, 0xf)
+  XL_AF_STEP(0x118, 0xf)
+  XL_AF_STEP(0x142, 0xa)
+  XL_AF_STEP(0x143, 0xc)
+#undef XL_AF_STEP
+}
+
+// float -> T with one v_cvt_pk (round to nearest even, NaN kept) for the 16-bit types
+template <typename T> __device__ __forceinline__ T from_f32_fast(float x) { return from_f32<T>(x); }
+template <> __device__ __forceinline__ bf16_t from_f32_fast<bf16_t>(float x) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const b2 r = __builtin_convertvector(f2{x, 0.f}, b2);
+  return __builtin_bit_cast(bf16_t, r[0]);
+}
+
+__device__ __forceinline__ float lane_of(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * SEQ_LOG2E); }
+__device__ __forceinline__ float logsig_f(float x) {
+  return fminf(x, 0.f) - 0.6931471805599453f * __builtin_amdgcn_logf(1.0f + exp_f(-fabsf(x)));
+}
+// tanh(x) = sign(x) (1 - 2 / (1 + e^{2|x|})): absolute error ~1e-7, no branch
+__device__ __forceinline__ float tanh_seq(float x) {
+  const float e = __builtin_amdgcn_exp2f(fabsf(x) * (2.0f * SEQ_LOG2E));
+  return copysignf(fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f), x);
+}
+
+// Gates of the 64 steps c0 + lane (< t1) given m at step c0 - 1; returns the
+// per-lane fg, ig, og, the max-plus map of the chunk in lane 63 and m at its
+// last valid step.
+template <typename TG>
+__device__ __forceinline__ void seq_gates(const TG* __restrict__ ip, const TG* __restrict__ fp,
+                                          const TG* __restrict__ op, int64_t gbase, int gstride, int c0, int t1,
+                                          int lane, float mprev, float& fg, float& ig, float& og, float& ma,
+                                          float& mb, float& mlast) {
+  const int t = c0 + lane;
+  const bool ok = t < t1;
+  const int64_t gi = gbase + (int64_t)(ok ? t : c0) * gstride;
+  const float iv = to_f32(ip[gi]), fv = to_f32(fp[gi]), ov = to_f32(op[gi]);
+  const float lsf = ok ? logsig_f(fv) : 0.f;
+  float a = lsf, b = ok ? iv : -INFINITY;
+  maxplus_scan(a, b);
+  const float mt = fmaxf(mprev + a, b);                    // m_t
+  float mp = __shfl_up(mt, 1, 64);                         // m_{t-1}
+  if (lane == 0) mp = mprev;
+  fg = exp_f(mp + lsf - mt);
+  ig = exp_f(iv - mt);
+  og = __builtin_amdgcn_rcpf(1.0f + exp_f(-ov));
+  ma = a;
+  mb = b;
+  mlast = lane_of(mt, 63);  // invalid lanes repeat the last valid m
+}
+
+template <typename TZ, typename TG, typename TH>
+__global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
+    const TZ* __restrict__ z, const TG* __restrict__ ip, const TG* __restrict__ fp, const TG* __restrict__ op,
+    const float* __restrict__ c0, const float* __restrict__ n0, const float* __restrict__ m0, TH* __restrict__ h,
+    float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last, int S, int NH, int H,
+    int ndb, float eps) {
+  __shared__ float s_map[SEQ_WAVES][2];        // max-plus map of each segment
+  __shared__ float s_aff[SEQ_WAVES][2];        // F, n-from-0 of each segment
+  __shared__ float s_cseg[SEQ_WAVES][64];      // c from 0 at each segment's end, per lane
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;  // w: wave-uniform
+  const int bh = blockIdx.x / ndb, db = blockIdx.x - bh * ndb;
+  const int b = bh / NH, hh = bh - b * NH;
+  const int d = 64 * db + lane;
+  const bool dok = d < H;
+  const int dc = dok ? d : 0;
+  const int SL = (S + SEQ_WAVES - 1) / SEQ_WAVES;
+  const int t0 = min(S, w * SL), t1 = min(S, t0 + SL);
+  const int64_t gbase = (int64_t)b * S * NH + hh;  // gates[b, t, hh] = gbase + t * NH
+  const int64_t zrow = (int64_t)NH * H;            // z[b, t, hh, d] = zbase + t * zrow
+  const int64_t zbase = (int64_t)b * S * zrow + (int64_t)hh * H + dc;
+  const float m_init = m0 ? m0[bh] : 0.f;
+
+  // ---- pass 0: the max-plus map of this segment
+  float sa = 0.f, sb = -INFINITY;
+  for (int c = t0; c < t1; c += 64) {
+    float fg, ig, og, ma, mb, ml;
+    seq_gates(ip, fp, op, gbase, NH, c, t1, lane, 0.f, fg, ig, og, ma, mb, ml);
+    const float ca = lane_of(ma, 63), cb = lane_of(mb, 63);
+    sb = fmaxf(sb + ca, cb);
+    sa += ca;
+  }
+  if (lane == 0) {
+    s_map[w][0] = sa;
+    s_map[w][1] = sb;
+  }
+  __syncthreads();
+  float m_in = m_init;  // m at step t0 - 1
+  for (int q = 0; q < w; ++q) m_in = fmaxf(m_in + s_map[q][0], s_map[q][1]);
+
+  // one segment from (c, n) with the gates of its steps; PASS 1: c from 0,
+  // segment F and n from the scans; PASS 2: writes h.  Step indices are
+  // wave-uniform, so addresses are one scalar multiply and one vector add.
+  const bool dfull = 64 * (db + 1) <= H;  // uniform: every lane of the block is a real d
+  auto run = [&](auto pass_tag, float& c, float& n) {
+    constexpr int PASS = decltype(pass_tag)::value;
+    float mprev = m_in, Fs = 1.f, Ns = 0.f;
+    TZ zq[SEQ_PF];  // raw prefetched z (converted when used, so the load is not waited for early)
+    const TZ* zl = z + zbase;
+    TH* hl = h + zbase + (int64_t)t0 * zrow;
+    const int tlast = max(t1 - 1, 0);
+    // every prefetch is its own load at step min(t + SEQ_PF, tlast) (wave-uniform index)
+#pragma unroll
+    for (int j = 0; j < SEQ_PF; ++j) zq[j] = zl[(int64_t)min(t0 + j, tlast) * zrow];
+    auto step = [&](float zt, float fgj, float igj, float ogj, auto store_tag) {
+      c = fmaf(fgj, c, igj * tanh_seq(zt));
+      if (PASS == 2) {
+        n = fmaf(fgj, n, igj);
+        const float hv = ogj * c * __builtin_amdgcn_rcpf(fabsf(n) + eps);
+        if (decltype(store_tag)::value || dok) *hl = from_f32_fast<TH>(hv);
+        hl += zrow;
+      }
+    };
+    for (int cst = t0; cst < t1; cst += 64) {
+      float fg, ig, og, ma, mb, ml;
+      seq_gates(ip, fp, op, gbase, NH, cst, t1, lane, mprev, fg, ig, og, ma, mb, ml);
+      mprev = ml;
+      if (PASS == 1) {
+        float F = (cst + lane < t1) ? fg : 1.f, N = (cst + lane < t1) ? ig : 0.f;
+        affine_scan(F, N);
+        const float cF = lane_of(F, 63), cN = lane_of(N, 63);
+        Ns = fmaf(Ns, cF, cN);
+        Fs *= cF;
+      }
+      if (cst + 64 <= t1) {
+        auto chunk = [&](auto store_tag) {
+#pragma unroll
+          for (int j = 0; j < 64; ++j) {
+            const float zt = to_f32(zq[j % SEQ_PF]);
+            zq[j % SEQ_PF] = zl[(int64_t)min(cst + j + SEQ_PF, tlast) * zrow];
+            step(zt, lane_of(fg, j), lane_of(ig, j), PASS == 2 ? lane_of(og, j) : 0.f, store_tag);
+          }
+        };
+        if (dfull) chunk(std::true_type{});
+        else chunk(std::false_type{});
+      } else {  // partial chunk at the segment end: no prefetch
+        const TZ* zt_p = zl + (int64_t)cst * zrow;
+        for (int j = 0; j < t1 - cst; ++j) {
+          step(to_f32(*zt_p), lane_of(fg, j), lane_of(ig, j), PASS == 2 ? lane_of(og, j) : 0.f, std::false_type{});
+          zt_p += zrow;
+        }
+      }
+    }
+    if (PASS == 1) {
+      n = Ns;
+      if (lane == 0) {
+        s_aff[w][0] = Fs;
+        s_aff[w][1] = Ns;
+      }
+    }
+    return mprev;
+  };
+
+  // ---- pass 1: this segment from c = 0
+  float c = 0.f, n = 0.f;
+  run(std::integral_constant<int, 1>{}, c, n);
+  s_cseg[w][lane] = c;
+  __syncthreads();
+  // ---- start state of this segment, then pass 2
+  c = (c0 && dok) ? c0[(int64_t)bh * H + d] : 0.f;
+  n = (n0 && dok) ? n0[(int64_t)bh * H + d] : 0.f;
+  for (int q = 0; q < w; ++q) {
+    const float F = s_aff[q][0];
+    c = fmaf(F, c, s_cseg[q][lane]);
+    n = fmaf(F, n, s_aff[q][1]);
+  }
+  const float m_end = run(std::integral_constant<int, 2>{}, c, n);
+  if (c_last && t0 < t1 && t1 == S && dok) {  // the wave of the last step
+    c_last[(int64_t)bh * H + d] = c;
+    n_last[(int64_t)bh * H + d] = n;
+    if (d == 0) m_last[bh] = m_end;
   }
 }
 
@@ -105,9 +292,11 @@ template <typename TZ, typename TG, typename TH>
 static int launch_seq3(const void* z, const void* i, const void* f, const void* o, const float* c, const float* n,
                        const float* m, void* h, float* c1, float* n1, float* m1, int S, int NH, int H,
                        int64_t total, float eps, hipStream_t s) {
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  hipLaunchKernelGGL((slstm_seq_kernel<TZ, TG, TH>), dim3(blocks), dim3(256), 0, s, (const TZ*)z, (const TG*)i,
-                     (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H, total, eps);
+  const int ndb = (H + 63) / 64;  // 64-element d blocks per head
+  const int64_t blocks = total / H * ndb;
+  hipLaunchKernelGGL((slstm_seq_kernel<TZ, TG, TH>), dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), 0, s,
+                     (const TZ*)z, (const TG*)i, (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H,
+                     ndb, eps);
   return check_launch("xl_slstm_seq_fwd");
 }
 

@@ -2,7 +2,8 @@
 
 Shapes and distributions are BASELINE's configs; draws use
 ``torch.Generator('cpu').manual_seed(seed)`` in the order q, k, v, i, f (then
-C, n, m), in float32, then cast.  Seeds: cfg0 -> 0, cfg1 -> 1, cfg2 -> 2.
+C, n, m), in float32, then cast.  Seeds: cfg0 -> 0, cfg1 -> 1, cfg2 -> 2,
+cfg4 (the sLSTM layer) -> 4.
 """
 
 from __future__ import annotations
@@ -11,8 +12,8 @@ from dataclasses import dataclass
 
 import torch
 
-__all__ = ["ChunkwiseConfig", "StepConfig", "CFG0", "CFG1", "CFG2", "chunkwise_inputs", "step_inputs",
-           "soft_cap15"]
+__all__ = ["ChunkwiseConfig", "StepConfig", "SLSTMConfig", "CFG0", "CFG1", "CFG2", "CFG4_SLSTM",
+           "chunkwise_inputs", "step_inputs", "slstm_inputs", "soft_cap15"]
 
 
 @dataclass(frozen=True)
@@ -39,9 +40,22 @@ class StepConfig:
     seed: int
 
 
+@dataclass(frozen=True)
+class SLSTMConfig:
+    name: str
+    B: int
+    S: int
+    NH: int
+    H: int
+    dtype: torch.dtype
+    seed: int
+
+
 CFG0 = ChunkwiseConfig("cfg0_chunkwise_fp32", 1, 8, 256, 256, 512, 64, torch.float32, 0)
 CFG1 = StepConfig("cfg1_decode_step_bf16", 16, 8, 256, 512, torch.bfloat16, 1)
 CFG2 = ChunkwiseConfig("cfg2_chunkwise_prefill_bf16", 4, 8, 8192, 256, 512, 64, torch.bfloat16, 2)
+# config 4's sLSTM layer: NH = 4 heads of H = 512 (d = 2048), B = 8, S = 4096 prefill
+CFG4_SLSTM = SLSTMConfig("cfg4_slstm_layer_bf16", 8, 4096, 4, 512, torch.bfloat16, 4)
 
 
 def soft_cap15(x: torch.Tensor) -> torch.Tensor:
@@ -79,3 +93,14 @@ def step_inputs(cfg: StepConfig, device="cpu", gate_dtype=torch.float32):
     qkv = tuple(t.to(cfg.dtype).to(device) for t in (q, k, v))
     gates = tuple(t.to(gate_dtype).to(device) for t in (i, f))
     return qkv + gates + (C.to(device), n.to(device), m.to(device))
+
+
+def slstm_inputs(cfg: SLSTMConfig, device="cpu"):
+    """z [B,S,NH,H] ~ N(0,1); i ~ N(0,1), f ~ N(3,1), o ~ N(0,1) [B,S,NH]; drawn in that order, cast to
+    cfg.dtype (the sequence starts from the zero state)."""
+    g = torch.Generator("cpu").manual_seed(cfg.seed)
+    z = torch.randn(cfg.B, cfg.S, cfg.NH, cfg.H, generator=g)
+    i = torch.randn(cfg.B, cfg.S, cfg.NH, generator=g)
+    f = torch.randn(cfg.B, cfg.S, cfg.NH, generator=g) + 3.0
+    o = torch.randn(cfg.B, cfg.S, cfg.NH, generator=g)
+    return tuple(t.to(cfg.dtype).to(device) for t in (z, i, f, o))
