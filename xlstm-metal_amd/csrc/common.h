@@ -122,4 +122,33 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ------------------------------------------------- stabiliser scans over time
+// The stabiliser recurrence m_t = max(m_{t-1} + a_t, b_t) (a = logsig f, b = i)
+// is the composition of the max-plus maps m -> max(m + a, b):
+// (a, b) o (a', b') = (a + a', max(b + a', b')).  A span's map carries sums
+// of a over sub-spans only, so m has the rounding of the step-by-step
+// recurrence (exact wherever b_t resets it).
+// inclusive scan over the lanes (lane order = time) of the maps m -> max(m + a, b)
+__device__ __forceinline__ void maxplus_scan(float& a, float& b) {
+  const int ida = __float_as_int(0.f), idb = __float_as_int(-INFINITY);
+#define XL_MP_STEP(CTRL, ROWMASK)                                                                                 \
+  {                                                                                                               \
+    const float ae = __int_as_float(__builtin_amdgcn_update_dpp(ida, __float_as_int(a), CTRL, ROWMASK, 0xf, false)); \
+    const float be = __int_as_float(__builtin_amdgcn_update_dpp(idb, __float_as_int(b), CTRL, ROWMASK, 0xf, false)); \
+    b = fmaxf(be + a, b);                                                                                         \
+    a = ae + a;                                                                                                   \
+  }
+  XL_MP_STEP(0x111, 0xf)  // row_shr:1
+  XL_MP_STEP(0x112, 0xf)  // row_shr:2
+  XL_MP_STEP(0x114, 0xf)  // row_shr:4
+  XL_MP_STEP(0x118, 0xf)  // row_shr:8
+  XL_MP_STEP(0x142, 0xa)  // row_bcast:15 into rows 1, 3
+  XL_MP_STEP(0x143, 0xc)  // row_bcast:31 into rows 2, 3
+#undef XL_MP_STEP
+}
+
+__device__ __forceinline__ float lane_of(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
 }  // namespace xl

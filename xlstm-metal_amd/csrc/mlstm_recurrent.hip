@@ -10,146 +10,192 @@
 // (q s)^T C'.to(q.dtype) and (q s) . n'.to(q.dtype) to q's dtype
 // (native_step.py:78-96); the kernel reproduces those roundings.
 //
-// Layout: one workgroup per (b*NH + h, 64-column tile of DV); 256 threads as
-// 16 column groups (4 consecutive floats each, one 16-byte access) x 16 row
-// groups.  A thread owns rows d = ty + 16 r of its 4 columns, so C' lives in
-// registers for the whole sequence and every C byte crosses HBM once per
-// launch (read at the start, written at the end).  A wave touches 4 rows x
-// 256 contiguous bytes per access.  The column partials of (q s)^T C' are
-// reduced across the 16 row groups through LDS.  n' is recomputed by every
-// tile of a head (DQK values, L2 resident) and written by tile 0 only.
+// Layout (both kernels): one workgroup per (b*NH + h, 64-column tile of DV),
+// 1024 threads as 16 column groups (4 consecutive floats each, one 16-byte
+// access) x 64 row groups; a thread owns rows d = ty + 64 r of its 4 columns.
+// The column partials of (q s)^T C' are reduced across the 64 row groups
+// through LDS.  n' is recomputed by every tile of a head (DQK values, L2
+// resident) and written by tile 0 only.  In the sequence kernel C' lives in
+// registers for the whole sequence (every C byte crosses HBM once per launch),
+// the gates of 64 steps come from one max-plus scan (lane = step), the next
+// step's q, k and v are loaded while the current step runs, and the LDS
+// buffers alternate with the step's parity, so a step costs two workgroup
+// barriers.
 #include "common.h"
 
 namespace xl {
 
-constexpr int REC_THREADS = 256;
 constexpr int REC_COLS = 64;       // DV columns per workgroup
-constexpr int REC_MAX_DQK = 512;   // rows per thread RPT = DQK / 16 <= 32
-// decode step: 1024 threads = 16 column groups x 64 row groups, RPT = DQK / 64 <= 8 rows per thread
+constexpr int REC_MAX_DQK = 512;   // rows per thread RPT = DQK / 64 <= 8
+// 1024 threads = 16 column groups x 64 row groups
 constexpr int STEP_THREADS = 1024;
 constexpr int STEP_RG = STEP_THREADS / 16;
 
 template <typename TQ, typename TG, int RPT>
-__global__ __launch_bounds__(REC_THREADS) void mlstm_recurrent_kernel(
+__global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
     const TQ* __restrict__ q, const TQ* __restrict__ k, const TQ* __restrict__ v,
     const TG* __restrict__ ig, const TG* __restrict__ fg,
     const float* c_old, const float* __restrict__ n_old, const float* __restrict__ m_old,
     TQ* __restrict__ h, float* c_new, float* __restrict__ n_new, float* __restrict__ m_new,
     int S, int DQK, int DV, int ntile, float qk_scale, float eps) {
   constexpr bool LOWP = !is_f32<TQ>::value;
-  __shared__ float s_q[REC_MAX_DQK];
-  __shared__ float s_k[REC_MAX_DQK];
-  __shared__ float s_red[16][REC_COLS + 4];
-  __shared__ float s_wsum[REC_THREADS / 64];
+  constexpr int NR = RPT * STEP_RG;                                  // rows covered (>= DQK)
+  constexpr int NPT = (NR + STEP_THREADS - 1) / STEP_THREADS;        // n entries per thread (d = tid + 1024 j)
+  // double-buffered by step parity: two barriers per step
+  __shared__ float s_q[2][NR];
+  __shared__ float s_k[2][NR];
+  __shared__ float s_red[2][STEP_RG][REC_COLS + 4];
+  __shared__ float s_wsum[2][STEP_THREADS / 64];
 
   const int bh = blockIdx.x / ntile;
   const int tile = blockIdx.x - bh * ntile;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int tx = tid & 15, ty = tid >> 4;
   const int col0 = tile * REC_COLS + tx * 4;
   const bool col_ok = col0 < DV;  // DV % 4 == 0, so a group is all in or all out
-
-  // ---- load the state: C rows of this thread, n entries of this thread, m
-  float4 C[RPT];
+  const int colc = col_ok ? col0 : 0;
   const size_t cbase = (size_t)bh * DQK * DV;
-  if (c_old) {
+
+  // ---- the state: C rows d = ty + 64 r of this thread's 4 columns, n entries, m
+  float4 C[RPT];
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-      const int d = ty + 16 * r;
-      C[r] = (col_ok && d < DQK) ? *reinterpret_cast<const float4*>(c_old + cbase + (size_t)d * DV + col0)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) C[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < RPT; ++r) {
+    const int d = ty + STEP_RG * r;
+    C[r] = (c_old && col_ok && d < DQK) ? *reinterpret_cast<const float4*>(c_old + cbase + (size_t)d * DV + col0)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  constexpr int NPT = REC_MAX_DQK / REC_THREADS;  // n entries per thread (d = tid + 256 j)
   float nst[NPT];
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
-    const int d = tid + REC_THREADS * j;
+    const int d = tid + STEP_THREADS * j;
     nst[j] = (n_old && d < DQK) ? n_old[(size_t)bh * DQK + d] : 0.f;
   }
   float m = m_old ? m_old[bh] : 0.f;
 
-  for (int t = 0; t < S; ++t) {
+  // ---- operands of one step, raw (converted when used, one step after the load)
+  TQ qr[NPT], kr[NPT], vr[4];
+  auto fetch = [&](int t) {
     const size_t tok = (size_t)bh * S + t;
-    // ---- gates (identical in every thread)
-    float lsf = round_to<TG>(logsigmoid(to_f32(fg[tok])));  // torch keeps logsigmoid in f's dtype
-    const float ipre = to_f32(ig[tok]);
-    const float mn = fmaxf(lsf + m, ipre);
-    const float fa = expf(lsf + m - mn);
-    const float ia = expf(ipre - mn);
-    m = mn;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int d = tid + STEP_THREADS * j;
+      const int dc = d < DQK ? d : 0;
+      qr[j] = q[tok * DQK + dc];
+      kr[j] = k[tok * DQK + dc];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vr[j] = v[tok * DV + colc + j];
+  };
+  fetch(0);
 
-    // ---- stage q s and k; n' and the partial of (q s) . n'
-    const TQ* qp = q + tok * DQK;
-    const TQ* kp = k + tok * DQK;
+  // ---- gates, 64 steps at a time with lane = step: the stabiliser by the
+  // max-plus scan (common.h), then fa, ia and exp(-m') of every step, read
+  // back per step with v_readlane
+  float gfa = 0.f, gia = 0.f, gem = 0.f;
+  for (int t = 0; t < S; ++t) {
+    const int jg = t & 63;
+    if (jg == 0) {  // uniform
+      const int tg = t + lane;
+      const bool ok = tg < S;
+      const size_t gtok = (size_t)bh * S + (ok ? tg : t);
+      const float lsf = ok ? round_to<TG>(logsigmoid(to_f32(fg[gtok]))) : 0.f;  // torch keeps logsigmoid in f's dtype
+      const float ipre = to_f32(ig[gtok]);
+      float a = lsf, b = ok ? ipre : -INFINITY;
+      maxplus_scan(a, b);
+      const float mt = fmaxf(m + a, b);
+      float mp = __shfl_up(mt, 1, 64);
+      if (lane == 0) mp = m;
+      gfa = expf(lsf + mp - mt);
+      gia = expf(ipre - mt);
+      gem = expf(-mt);
+      m = lane_of(mt, 63);  // invalid lanes repeat the last valid m
+    }
+    const int buf = t & 1;
+    const size_t tok = (size_t)bh * S + t;
+    float qv[NPT], kv_[NPT], vv[4];
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      qv[j] = to_f32(qr[j]);
+      kv_[j] = to_f32(kr[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vv[j] = to_f32(vr[j]);
+    fetch(t + 1 < S ? t + 1 : t);  // the next step's operands, in flight during this step
+    const float fa = lane_of(gfa, jg), ia = lane_of(gia, jg), emn = lane_of(gem, jg);
+
+    // ---- n', q s and k to LDS, and the partial of (q s) . n'
     float part = 0.f;
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
-      const int d = tid + REC_THREADS * j;
-      if (d < DQK) {
-        float qs = to_f32(qp[d]) * qk_scale;
-        if (LOWP) qs = round_to<TQ>(qs);
-        const float kd = to_f32(kp[d]);
-        s_q[d] = qs;
-        s_k[d] = kd;
-        nst[j] = fa * nst[j] + ia * kd;
-        part += qs * (LOWP ? round_to<TQ>(nst[j]) : nst[j]);
+      const int d = tid + STEP_THREADS * j;
+      float qs = qv[j] * qk_scale;
+      if (LOWP) qs = round_to<TQ>(qs);
+      const float kd = kv_[j];
+      const bool ok = d < DQK;
+      nst[j] = fa * nst[j] + ia * kd;
+      part += ok ? qs * (LOWP ? round_to<TQ>(nst[j]) : nst[j]) : 0.f;
+      if (d < NR) {
+        s_q[buf][d] = ok ? qs : 0.f;
+        s_k[buf][d] = ok ? kd : 0.f;
       }
     }
-    part = wave_sum(part);
-    if ((tid & 63) == 0) s_wsum[tid >> 6] = part;
-    __syncthreads();  // s_q, s_k, s_wsum ready
-    float qn = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
-    if (LOWP) qn = round_to<TQ>(qn);
-    const float den = fmaxf(fabsf(qn), expf(-mn)) + eps;
+    part = wave_sum_dpp(part);
+    if (lane == 63) s_wsum[buf][tid >> 6] = part;
+    __syncthreads();  // s_q, s_k, s_wsum of this step ready
 
     // ---- C' = fa C + ia k v^T in registers, column partials of (q s)^T C'
-    float vv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (col_ok) {
-      const TQ* vp = v + tok * DV + col0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vv[j] = to_f32(vp[j]);
-    }
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-      const int d = ty + 16 * r;
-      if (d < DQK) {
-        const float kd = s_k[d], qd = s_q[d];
-        float kv[4];
+      const int d = ty + STEP_RG * r;
+      const float qd = s_q[buf][d], kd = s_k[buf][d];  // 0 past DQK: the row adds nothing
+      float kv[4] = {kd * vv[0], kd * vv[1], kd * vv[2], kd * vv[3]};
+      if (LOWP) {
+        round2_to<TQ>(kv[0], kv[1]);
+        round2_to<TQ>(kv[2], kv[3]);
+      }
+      C[r].x = fa * C[r].x + ia * kv[0];
+      C[r].y = fa * C[r].y + ia * kv[1];
+      C[r].z = fa * C[r].z + ia * kv[2];
+      C[r].w = fa * C[r].w + ia * kv[3];
+      float cr[4] = {C[r].x, C[r].y, C[r].z, C[r].w};
+      if (LOWP) {
+        round2_to<TQ>(cr[0], cr[1]);
+        round2_to<TQ>(cr[2], cr[3]);
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kv[j] = LOWP ? round_to<TQ>(kd * vv[j]) : kd * vv[j];
-        C[r].x = fa * C[r].x + ia * kv[0];
-        C[r].y = fa * C[r].y + ia * kv[1];
-        C[r].z = fa * C[r].z + ia * kv[2];
-        C[r].w = fa * C[r].w + ia * kv[3];
-        acc[0] += qd * (LOWP ? round_to<TQ>(C[r].x) : C[r].x);
-        acc[1] += qd * (LOWP ? round_to<TQ>(C[r].y) : C[r].y);
-        acc[2] += qd * (LOWP ? round_to<TQ>(C[r].z) : C[r].z);
-        acc[3] += qd * (LOWP ? round_to<TQ>(C[r].w) : C[r].w);
+      for (int j = 0; j < 4; ++j) acc[j] += qd * cr[j];
+    }
+    *reinterpret_cast<float4*>(&s_red[buf][ty][tx * 4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();  // s_red of this step ready
+
+    // ---- column c = tid / 16: 16 lanes add 4 row groups each, then a 16-lane DPP sum
+    {
+      const int c = tid >> 4, pr = tid & 15;
+      float hs = (s_red[buf][pr][c] + s_red[buf][pr + 16][c]) + (s_red[buf][pr + 32][c] + s_red[buf][pr + 48][c]);
+#define XL_ROW_ADD(CTRL) hs += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(hs), CTRL, 0xf, 0xf, false));
+      XL_ROW_ADD(0x111)  // row_shr:1
+      XL_ROW_ADD(0x112)  // row_shr:2
+      XL_ROW_ADD(0x114)  // row_shr:4
+      XL_ROW_ADD(0x118)  // row_shr:8
+#undef XL_ROW_ADD
+      if (pr == 15 && tile * REC_COLS + c < DV) {
+        float qn = 0.f;
+#pragma unroll
+        for (int w = 0; w < STEP_THREADS / 64; ++w) qn += s_wsum[buf][w];
+        if (LOWP) qn = round_to<TQ>(qn);
+        const float den = fmaxf(fabsf(qn), emn) + eps;
+        if (LOWP) hs = round_to<TQ>(hs);
+        h[tok * DV + tile * REC_COLS + c] = from_f32<TQ>(hs / den);
       }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_red[ty][tx * 4 + j] = acc[j];
-    __syncthreads();  // s_red ready
-    if (tid < REC_COLS && tile * REC_COLS + tid < DV) {
-      float hn = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) hn += s_red[r][tid];
-      if (LOWP) hn = round_to<TQ>(hn);
-      h[tok * DV + tile * REC_COLS + tid] = from_f32<TQ>(hn / den);
-    }
-    __syncthreads();  // s_q / s_k / s_red free for the next step
   }
 
   // ---- write the state
   if (c_new) {
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-      const int d = ty + 16 * r;
+      const int d = ty + STEP_RG * r;
       if (col_ok && d < DQK) *reinterpret_cast<float4*>(c_new + cbase + (size_t)d * DV + col0) = C[r];
     }
   }
@@ -157,7 +203,7 @@ __global__ __launch_bounds__(REC_THREADS) void mlstm_recurrent_kernel(
     if (n_new) {
 #pragma unroll
       for (int j = 0; j < NPT; ++j) {
-        const int d = tid + REC_THREADS * j;
+        const int d = tid + STEP_THREADS * j;
         if (d < DQK) n_new[(size_t)bh * DQK + d] = nst[j];
       }
     }
@@ -325,8 +371,7 @@ static int launch_rec_t(const void* q, const void* k, const void* v, const void*
                         float* m1, int BNH, int S, int DQK, int DV, float qk_scale, float eps, hipStream_t s,
                         const char* who) {
   const int ntile = (DV + REC_COLS - 1) / REC_COLS;
-  const int rpt = (DQK + 15) / 16;
-  dim3 grid((unsigned)(BNH * ntile)), block(REC_THREADS);
+  dim3 grid((unsigned)(BNH * ntile));
   if (S == 1 && c0 && n0 && m0 && c1 && n1 && m1) {  // decode step: straight-line kernel
     const int rps = (DQK + STEP_RG - 1) / STEP_RG;
 #define XL_STEP_LAUNCH(R)                                                                                      \
@@ -340,14 +385,15 @@ static int launch_rec_t(const void* q, const void* k, const void* v, const void*
 #undef XL_STEP_LAUNCH
     return check_launch(who);
   }
+  const int rps = (DQK + STEP_RG - 1) / STEP_RG;
 #define XL_REC_LAUNCH(R)                                                                                       \
-  hipLaunchKernelGGL((mlstm_recurrent_kernel<TQ, TG, R>), grid, block, 0, s, (const TQ*)q, (const TQ*)k,     \
-                     (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1, S, DQK, DV,      \
-                     ntile, qk_scale, eps)
-  if (rpt <= 4) XL_REC_LAUNCH(4);
-  else if (rpt <= 8) XL_REC_LAUNCH(8);
-  else if (rpt <= 16) XL_REC_LAUNCH(16);
-  else XL_REC_LAUNCH(32);
+  hipLaunchKernelGGL((mlstm_recurrent_kernel<TQ, TG, R>), grid, dim3(STEP_THREADS), 0, s, (const TQ*)q,      \
+                     (const TQ*)k, (const TQ*)v, (const TG*)i, (const TG*)f, c0, n0, m0, (TQ*)h, c1, n1, m1,    \
+                     S, DQK, DV, ntile, qk_scale, eps)
+  if (rps <= 1) XL_REC_LAUNCH(1);
+  else if (rps <= 2) XL_REC_LAUNCH(2);
+  else if (rps <= 4) XL_REC_LAUNCH(4);
+  else XL_REC_LAUNCH(8);
 #undef XL_REC_LAUNCH
   return check_launch(who);
 }

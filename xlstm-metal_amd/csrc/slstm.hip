@@ -69,25 +69,6 @@ constexpr int SEQ_WAVES = 16;
 constexpr int SEQ_PF = 16;
 constexpr float SEQ_LOG2E = 1.4426950408889634f;
 
-// inclusive scan over the lanes (lane order = time) of the maps m -> max(m + a, b)
-__device__ __forceinline__ void maxplus_scan(float& a, float& b) {
-  const int ida = __float_as_int(0.f), idb = __float_as_int(-INFINITY);
-#define XL_MP_STEP(CTRL, ROWMASK)                                                                                 \
-  {                                                                                                               \
-    const float ae = __int_as_float(__builtin_amdgcn_update_dpp(ida, __float_as_int(a), CTRL, ROWMASK, 0xf, false)); \
-    const float be = __int_as_float(__builtin_amdgcn_update_dpp(idb, __float_as_int(b), CTRL, ROWMASK, 0xf, false)); \
-    b = fmaxf(be + a, b);                                                                                         \
-    a = ae + a;                                                                                                   \
-  }
-  XL_MP_STEP(0x111, 0xf)  // row_shr:1
-  XL_MP_STEP(0x112, 0xf)  // row_shr:2
-  XL_MP_STEP(0x114, 0xf)  // row_shr:4
-  XL_MP_STEP(0x118, 0xf)  // row_shr:8
-  XL_MP_STEP(0x142, 0xa)  // row_bcast:15 into rows 1, 3
-  XL_MP_STEP(0x143, 0xc)  // row_bcast:31 into rows 2, 3
-#undef XL_MP_STEP
-}
-
 // inclusive scan of the affine maps x -> F x + N (n from 0 and prod fg)
 __device__ __forceinline__ void affine_scan(float& F, float& N) {
   const int idf = __float_as_int(1.f), idn = __float_as_int(0.f);
@@ -116,9 +97,6 @@ template <> __device__ __forceinline__ bf16_t from_f32_fast<bf16_t>(float x) {
   return __builtin_bit_cast(bf16_t, r[0]);
 }
 
-__device__ __forceinline__ float lane_of(float x, int l) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
-}
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * SEQ_LOG2E); }
 __device__ __forceinline__ float logsig_f(float x) {
   return fminf(x, 0.f) - 0.6931471805599453f * __builtin_amdgcn_logf(1.0f + exp_f(-fabsf(x)));
