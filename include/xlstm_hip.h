@@ -97,7 +97,11 @@ int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i
  *   zero initial states (or all three non-NULL);
  *   h [B,NH,S,DV] (dtype_qkv); c_last, n_last, m_last float32 (all NULL when
  *   the last states are not wanted).
- * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.
+ * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.  With algo =
+ * XL_CHUNKWISE_FUSED (bf16 q/k/v, DQK 128 or 256, DV % 64 == 0) any S >= 1 is
+ * accepted: the fused kernel runs 64-token chunks and a ragged last chunk
+ * (the forward is chunk-size invariant, so L only names the reference's
+ * chunking there).
  * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned
  * (fused algorithm: the per-chunk gate prep, 1280 bytes per 64 tokens of
  * every head; two-pass algorithm: the chunk-entry states).

@@ -10,7 +10,9 @@
   algorithm;
 * the fused kernel works on 64-token chunks for every chunk_size (the forward
   is chunk-size invariant): chunk sizes 16, 32, 128 against the oracle at that
-  chunk size.
+  chunk size;
+* algo="fused" with any S (ragged last chunk) and the any-S backend's one-call
+  bf16 path against the oracle's any-S driver.
 """
 
 import pytest
@@ -196,3 +198,42 @@ def test_fused_other_chunk_sizes(gpu_case, L, with_state):
     hr, (Cr, nr, mr) = _oracle(x, st, L)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got, want, torch.bfloat16, f"fused L={L} state={with_state} {name}")
+
+
+@pytest.mark.parametrize("S", [1, 5, 63, 65, 100, 200, 1000])
+@pytest.mark.parametrize("DQK,DV", [(256, 64), (128, 128)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_fused_ragged_length(gpu_case, S, DQK, DV, with_state):
+    """algo="fused" takes any S (64-token chunks, ragged last chunk), against the oracle's any-S
+    driver (chunkwise pieces of 64/32/16 tokens, then the recurrent tail) on the same inputs."""
+    import xlstm_hip
+    x, st = _inputs(1, 2, S, DQK, DV, torch.bfloat16, seed=S + DQK, with_state=with_state)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=64,
+                                             algo="fused")
+    q, k, v, i, f = (t.float() for t in x)
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got, want, torch.bfloat16, f"fused ragged S={S} DQK={DQK} DV={DV} state={with_state} {name}")
+    # auto and two_pass keep the reference's contract
+    if S % 64:
+        with pytest.raises(AssertionError, match="not divisible"):
+            xlstm_hip.mlstm_chunkwise(*_gpu(x), chunk_size=64)
+
+
+@pytest.mark.parametrize("S", [37, 100, 8255])
+def test_backend_any_length_bf16(gpu_case, S):
+    """mLSTMBackend inference on bf16 inputs: one fused call for any S (the any-S wrapper's fast
+    path), against the oracle's any-S driver; S = 8255 is config 2's heads of one batch row with
+    the worst tail (32 + 16 + 15 tokens after 8192)."""
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    if S == 8255:
+        x = chunkwise_inputs(CFG2, S=S, B=1)
+    else:
+        x, _ = _inputs(1, 2, S, 256, 128, torch.bfloat16, seed=S)
+    backend = xlstm_hip.mLSTMBackend(xlstm_hip.mLSTMBackendConfig(mode="inference", chunk_size=64))
+    h, (C, n, m) = backend(*_gpu(x))
+    q, k, v, i, f = (t.float() for t in x)
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, chunk_size=64)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got, want, torch.bfloat16, f"backend any-S bf16 S={S} {name}")

@@ -12,7 +12,9 @@ static int check_args(const ChunkwiseArgs& a, int algo) {
     return set_error(XL_ERR_INVALID_ARG, "%s: dimensions must be positive (B=%d NH=%d S=%d DQK=%d DV=%d)", who, a.B,
                      a.NH, a.S, a.DQK, a.DV);
   if (!valid_L(a.L)) return set_error(XL_ERR_UNSUPPORTED, "%s: chunk_size=%d not in {16,32,64,128}", who, a.L);
-  if (a.S % a.L != 0)
+  // the reference's contract; the fused algorithm, asked for explicitly, runs 64-token
+  // chunks with a ragged last chunk and accepts any S
+  if (a.S % a.L != 0 && algo != XL_CHUNKWISE_FUSED)
     return set_error(XL_ERR_INVALID_ARG, "%s: Sequence length %d is not divisible by chunk size %d.", who, a.S, a.L);
   if (!dtype_ok(a.dtype_qkv) || !dtype_ok(a.dtype_gates)) return set_error(XL_ERR_INVALID_ARG, "%s: unknown dtype", who);
   if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_FUSED)
@@ -25,7 +27,8 @@ static int check_args(const ChunkwiseArgs& a, int algo) {
   if (a.c_last && (a.c_last == a.c0 || a.n_last == a.n0 || a.m_last == a.m0))
     return set_error(XL_ERR_INVALID_ARG, "%s: last states must not alias the initial states", who);
   const long long BNH = (long long)a.B * a.NH;
-  if (BNH * (a.S / a.L) * ((a.DV + 63) / 64) > 0x7fffffffLL) return set_error(XL_ERR_INVALID_ARG, "%s: too large", who);
+  if (BNH * ((a.S + a.L - 1) / a.L) * ((a.DV + 63) / 64) > 0x7fffffffLL)
+    return set_error(XL_ERR_INVALID_ARG, "%s: too large", who);
   return XL_OK;
 }
 
@@ -45,7 +48,8 @@ static int pick(const ChunkwiseArgs& a, int algo, int* chosen) {
 extern "C" size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, int L, int dtype_qkv,
                                                     int algo) {
   using namespace xl;
-  if (B <= 0 || NH <= 0 || S <= 0 || DQK <= 0 || DV <= 0 || !valid_L(L) || S % L) return 0;
+  if (B <= 0 || NH <= 0 || S <= 0 || DQK <= 0 || DV <= 0 || !valid_L(L)) return 0;
+  if (S % L && algo != XL_CHUNKWISE_FUSED) return 0;
   ChunkwiseArgs a = {};
   a.B = B; a.NH = NH; a.S = S; a.DQK = DQK; a.DV = DV; a.L = L;
   a.dtype_qkv = dtype_qkv; a.dtype_gates = dtype_qkv;

@@ -1,7 +1,8 @@
 // Fused single-pass chunkwise mLSTM forward for bf16 q/k/v on gfx950.
 //
 // One workgroup = one (b, h) pair x one 64-column tile of DV, marching over
-// the NC chunks of L = 64 tokens.  The C tile (DQK x 64, float32) and the
+// the NC = ceil(S / 64) chunks of L = 64 tokens (a ragged last chunk is
+// zero-filled and its tokens past S are given no weight).  The C tile (DQK x 64, float32) and the
 // normaliser n stay on chip for the whole sequence, so the only HBM traffic is
 // q, k, v, the gates, h and the final states.  The math is the reference's
 // chunkwise forward (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/
@@ -144,15 +145,20 @@ __device__ __forceinline__ float lane63(float x) {
 //   b_t = sum_{s<=t} logsig f_s,  g = b_63,  a_t = g - b_t + i_t,  max_t a_t,
 //   u_t = i_t - b_t (stored times log2 e),  cummax_{s<=t} u_s.
 // These are the scans of the chunk; the main kernel folds in the running m
-// and the deferred state rescale with a handful of scalar operations.
+// and the deferred state rescale with a handful of scalar operations.  Tokens
+// past S (a ragged last chunk) enter as logsig f = 0 and i = -inf: they leave
+// b unchanged and contribute nothing to the state, n or max a.
 template <typename TG>
 __global__ __launch_bounds__(256) void gate_prep_kernel(const TG* __restrict__ ig, const TG* __restrict__ fg,
-                                                        float* __restrict__ prep, int total_chunks) {
+                                                        float* __restrict__ prep, int total_chunks, int NC, int S) {
   const int lane = threadIdx.x & 63;
-  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);  // bh * NC + chunk: the tokens of chunk c are 64c .. 64c + 63
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);  // bh * NC + chunk
   if (c >= total_chunks) return;
-  const float f = to_f32(fg[(size_t)c * L + lane]), i = to_f32(ig[(size_t)c * L + lane]);
-  const float b = wave_scan<false>(logsig_fast(f));
+  const int bh = c / NC, t = (c - bh * NC) * L + lane;  // token t of head bh
+  const bool ok = t < S;
+  const size_t gi = (size_t)bh * S + (ok ? t : S - 1);
+  const float f = to_f32(fg[gi]), i = ok ? to_f32(ig[gi]) : -INFINITY;
+  const float b = wave_scan<false>(ok ? logsig_fast(f) : 0.f);
   const float g = lane63(b);
   const float a = g - b + i;
   const float amax = lane63(wave_scan<true>(a));
@@ -196,7 +202,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     const float* __restrict__ c0,
     const float* __restrict__ n0, const float* __restrict__ m0, bf16_t* __restrict__ h,
     float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last,
-    const float* __restrict__ prep, int NC, int DV, int BNH, int nvtile, float qk_scale, float eps) {
+    const float* __restrict__ prep, int S, int NC, int DV, int BNH, int nvtile, float qk_scale, float eps) {
   using SM = Smem<DQK>;
   constexpr int KPD = SM::KPD;
   constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
@@ -216,7 +222,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   if ((nwg & 7) == 0) lin = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
   const int bh = lin / nvtile;
   const int v0 = (lin - bh * nvtile) * DVT;
-  const int S = NC * L;
 
   char* kn = smem + SM::KN;
   char* vn = smem + SM::VN;
@@ -232,12 +237,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const float m_init = m0 ? m0[bh] : 0.f;
 
   // ---- K staging: piece u of thread tid = u*NTHREADS + tid -> row piece / (DQK/8), 16-byte column group
+  // rows past S (ragged last chunk) load row 0 of the chunk and are zeroed
   auto load_k = [&](int kc, u32x4 (&Kst)[NKU]) {
     const bf16_t* kb = kh + (size_t)kc * L * DQK;
 #pragma unroll
     for (int u = 0; u < NKU; ++u) {
       const int piece = u * NTHREADS + tid;
-      Kst[u] = *reinterpret_cast<const u32x4*>(kb + (size_t)(piece / (DQK / 8)) * DQK + 8 * (piece % (DQK / 8)));
+      const int row = piece / (DQK / 8);
+      const bool ok = kc * L + row < S;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(kb + (size_t)(ok ? row : 0) * DQK + 8 * (piece % (DQK / 8)));
+      Kst[u] = ok ? x : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto store_k = [&](const u32x4 (&Kst)[NKU]) {
@@ -372,15 +381,24 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     u32x4 Qs[2][QKS];
     auto load_v = [&](int kc) {
       const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
-      Vst[0] = *reinterpret_cast<const u32x4*>(vb + (size_t)vrow * DV);
-      Vst[1] = *reinterpret_cast<const u32x4*>(vb + (size_t)(vrow + 2) * DV);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const bool ok = kc * L + vrow + 2 * r < S;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(vb + (size_t)(ok ? vrow + 2 * r : 0) * DV);
+        Vst[r] = ok ? x : u32x4{0u, 0u, 0u, 0u};
+      }
     };
     auto load_qs = [&](int kc) {
-      const bf16_t* qb = qh + ((size_t)kc * L + l32) * DQK + dw0 + 8 * hh;
+      const bf16_t* qb = qh + (size_t)kc * L * DQK + dw0 + 8 * hh;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < 2; ++tt) {
+        const bool ok = kc * L + 32 * tt + l32 < S;
 #pragma unroll
-        for (int s = 0; s < QKS; ++s) Qs[tt][s] = *reinterpret_cast<const u32x4*>(qb + (size_t)32 * tt * DQK + 16 * s);
+        for (int s = 0; s < QKS; ++s) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(qb + (size_t)(ok ? 32 * tt + l32 : 0) * DQK + 16 * s);
+          Qs[tt][s] = ok ? x : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
     };
     load_k(0, Kst);
     load_v(0);
@@ -525,9 +543,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
     // 16-byte load; the K operand below uses the same contiguous k order)
     auto load_q = [&](int kc) {
-      const bf16_t* qb = qh + ((size_t)kc * L + 16 * o + r16) * DQK + 8 * g;
+      const bool ok = kc * L + 16 * o + r16 < S;
+      const bf16_t* qb = qh + ((size_t)kc * L + (ok ? 16 * o + r16 : 0)) * DQK + 8 * g;
 #pragma unroll
-      for (int p = 0; p < KPD; ++p) Qf[p] = *reinterpret_cast<const u32x4*>(qb + 32 * p);
+      for (int p = 0; p < KPD; ++p) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(qb + 32 * p);
+        Qf[p] = ok ? x : u32x4{0u, 0u, 0u, 0u};
+      }
     };
     load_k(0, Kst);
     load_q(0);
@@ -648,6 +670,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       const float den = qb * qn + Hmv[NVT][0];
       const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr)) + eps);
       bf16_t* hb = hh + ((size_t)kc * L + 16 * o + r16) * DV + v0 + 8 * g;
+      const bool hok = kc * L + 16 * o + r16 < S;  // rows past S (ragged last chunk) are not stored
 #pragma unroll
       for (int h2 = 0; h2 < NVT / 2; ++h2) {
         u32x4 out;
@@ -657,7 +680,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           out[2 * b] = pack_bf16((qb * Hqc[vq][0] + Hmv[vq][0]) * inv, (qb * Hqc[vq][1] + Hmv[vq][1]) * inv);
           out[2 * b + 1] = pack_bf16((qb * Hqc[vq][2] + Hmv[vq][2]) * inv, (qb * Hqc[vq][3] + Hmv[vq][3]) * inv);
         }
-        *reinterpret_cast<u32x4*>(hb + 32 * h2) = out;
+        if (hok) *reinterpret_cast<u32x4*>(hb + 32 * h2) = out;
       }
     }
     // ---- final n (undo the deferred rescale): even + odd column, lanes r16 = 0, 1
@@ -681,11 +704,11 @@ template <typename TG, int DQK>
 static int launch(const ChunkwiseArgs& A) {
   const int BNH = A.B * A.NH;
   const int nvtile = A.DV / DVT;
-  const int NC = A.S / L;
+  const int NC = (A.S + L - 1) / L;  // the last chunk may be ragged
   float* prep = (float*)A.workspace;
   const int total = BNH * NC;
   hipLaunchKernelGGL(gate_prep_kernel<TG>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, (hipStream_t)A.stream,
-                     (const TG*)A.i, (const TG*)A.f, prep, total);
+                     (const TG*)A.i, (const TG*)A.f, prep, total, NC, A.S);
   auto kern = chunkwise_fused_kernel<DQK>;
   const size_t smem = Smem<DQK>::BYTES;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -693,7 +716,7 @@ static int launch(const ChunkwiseArgs& A) {
     return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
   hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvtile)), dim3(NTHREADS), smem, (hipStream_t)A.stream,
                      (const bf16_t*)A.q, (const bf16_t*)A.k, (const bf16_t*)A.v, A.c0, A.n0, A.m0, (bf16_t*)A.h,
-                     A.c_last, A.n_last, A.m_last, prep, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps);
+                     A.c_last, A.n_last, A.m_last, prep, A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps);
   return check_launch("xl_mlstm_chunkwise_fwd(fused)");
 }
 
@@ -705,13 +728,12 @@ static int launch_d(const ChunkwiseArgs& A) {
 }  // namespace fused
 
 size_t chunkwise_fused_workspace(int B, int NH, int S) {
-  return ((size_t)B * NH * (S / fused::L) * fused::PREP_STRIDE * sizeof(float) + 255) / 256 * 256;
+  return ((size_t)B * NH * ((S + fused::L - 1) / fused::L) * fused::PREP_STRIDE * sizeof(float) + 255) / 256 * 256;
 }
 
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why) {
   const char* r = nullptr;
   if (a.dtype_qkv != XL_DTYPE_BF16) r = "q/k/v must be bfloat16";
-  else if (a.S % fused::L != 0) r = "sequence length must be a multiple of 64";
   else if (a.DQK != 128 && a.DQK != 256) r = "DQK must be 128 or 256";
   else if (a.DV % fused::DVT != 0) r = "DV must be a multiple of 64";
   if (why) *why = r;

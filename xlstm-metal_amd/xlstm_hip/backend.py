@@ -20,6 +20,7 @@ import torch
 from torch import nn
 
 from .chunkwise import mlstm_chunkwise__native_autograd
+from .ops import chunkwise_workspace_bytes
 from .recurrent import mlstm_recurrent_sequence__native_fw, mlstm_recurrent_step__native
 
 __all__ = [
@@ -71,6 +72,15 @@ def available_kernels() -> dict:
     return {"chunkwise": sorted(_CHUNKWISE), "sequence": sorted(_SEQUENCE), "step": sorted(_STEP)}
 
 
+def _fused_takes_any_length(q, k, v) -> bool:
+    """True when this library's fused chunkwise kernel runs the whole sequence in one call
+    (bf16 q/k/v and a head shape it supports; it runs 64-token chunks with a ragged last chunk)."""
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        return False
+    B, NH, S, DQK = q.shape
+    return chunkwise_workspace_bytes(B, NH, S, DQK, v.shape[-1], 64, q.dtype, algo="fused") > 0
+
+
 def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequence_kernel, mlstm_step_kernel, q,
                                               k, v, f, i, c_initial=None, n_initial=None, m_initial=None,
                                               return_last_states=True, eps=1e-6,
@@ -78,7 +88,10 @@ def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequ
                                               enable_logging=False):
     """Any-S inference (kernel_wrappers.py:12-202): chunk sizes chunk_size, /2, ... >= 16
     on the largest whole number of chunks each, carrying (C, n, m); the sequence kernel
-    for a tail < 16; the step kernel when S == 1.  Zero states are float32 (:84-98)."""
+    for a tail < 16; the step kernel when S == 1.  Zero states are float32 (:84-98).
+    With this library's chunkwise kernel and inputs its fused kernel takes, the whole
+    sequence is one fused call instead: the forward is chunk-size invariant, so the split
+    above changes rounding only, and the slicing copies and the concatenation go away."""
     B, NH, S, DHQK = k.shape
     DHHV = v.shape[-1]
     sizes = []
@@ -90,7 +103,11 @@ def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequ
     c_state = c_initial if c_initial is not None else torch.zeros(B, NH, DHQK, DHHV, device=dev, dtype=torch.float32)
     n_state = n_initial if n_initial is not None else torch.zeros(B, NH, DHQK, device=dev, dtype=torch.float32)
     m_state = m_initial if m_initial is not None else torch.zeros(B, NH, 1, device=dev, dtype=torch.float32)
-    if S > 1:
+    if S > 1 and mlstm_chunkwise_kernel is mlstm_chunkwise__native_autograd and _fused_takes_any_length(q, k, v):
+        h_out, (c_state, n_state, m_state) = mlstm_chunkwise_kernel(
+            q=q, k=k, v=v, f=f, i=i, c_initial=c_state, n_initial=n_state, m_initial=m_state, chunk_size=chunk_size,
+            return_last_states=True, eps=eps, algo="fused")
+    elif S > 1:
         h_outs = []
         start = 0
         for cs in sizes:

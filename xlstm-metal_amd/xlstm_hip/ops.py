@@ -174,7 +174,7 @@ def mlstm_chunkwise_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c0
     what = "mlstm_chunkwise"
     _lib.require_gpu(q, k, v, i, f, c0, n0, m0, what=what)
     B, NH, S, DQK, DV = _seq_shapes(q, k, v, i, f, c0, n0, m0, what)
-    if S % chunk_size != 0:
+    if S % chunk_size != 0 and algo != _lib.ALGO["fused"]:  # the fused kernel also takes a ragged last chunk
         raise AssertionError(f"Sequence length {S} is not divisible by chunk size {chunk_size}.")
     q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
     c0, n0, m0 = _f32(c0), _f32(n0), _f32(m0)
