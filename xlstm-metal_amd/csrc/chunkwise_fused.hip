@@ -1,8 +1,8 @@
 // Fused single-pass chunkwise mLSTM forward for bf16 q/k/v on gfx950.
 //
 // One workgroup = one (b, h) pair x one 64-column tile of DV, marching over
-// the NC = ceil(S / 64) chunks of L = 64 tokens (a ragged last chunk is
-// zero-filled and its tokens past S are given no weight).  The C tile (DQK x 64, float32) and the
+// the NC = ceil(S / 64) chunks of L = 64 tokens (in a ragged last chunk the
+// tokens past S are given no weight and their outputs are not stored).  The C tile (DQK x 64, float32) and the
 // normaliser n stay on chip for the whole sequence, so the only HBM traffic is
 // q, k, v, the gates, h and the final states.  The math is the reference's
 // chunkwise forward (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/
@@ -237,16 +237,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const float m_init = m0 ? m0[bh] : 0.f;
 
   // ---- K staging: piece u of thread tid = u*NTHREADS + tid -> row piece / (DQK/8), 16-byte column group
-  // rows past S (ragged last chunk) load row 0 of the chunk and are zeroed
+  // Rows past S (a ragged last chunk) read row 0 of the chunk instead: any
+  // finite values do, since those tokens carry alpha' = 0 and gate weight
+  // exp(-inf) = 0, their S columns are causally masked for real rows, and their
+  // own rows of h are not stored.
   auto load_k = [&](int kc, u32x4 (&Kst)[NKU]) {
     const bf16_t* kb = kh + (size_t)kc * L * DQK;
 #pragma unroll
     for (int u = 0; u < NKU; ++u) {
       const int piece = u * NTHREADS + tid;
       const int row = piece / (DQK / 8);
-      const bool ok = kc * L + row < S;
-      const u32x4 x = *reinterpret_cast<const u32x4*>(kb + (size_t)(ok ? row : 0) * DQK + 8 * (piece % (DQK / 8)));
-      Kst[u] = ok ? x : u32x4{0u, 0u, 0u, 0u};
+      Kst[u] = *reinterpret_cast<const u32x4*>(kb + (size_t)(kc * L + row < S ? row : 0) * DQK + 8 * (piece % (DQK / 8)));
     }
   };
   auto store_k = [&](const u32x4 (&Kst)[NKU]) {
@@ -382,22 +383,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     auto load_v = [&](int kc) {
       const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const bool ok = kc * L + vrow + 2 * r < S;
-        const u32x4 x = *reinterpret_cast<const u32x4*>(vb + (size_t)(ok ? vrow + 2 * r : 0) * DV);
-        Vst[r] = ok ? x : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int r = 0; r < 2; ++r)
+        Vst[r] = *reinterpret_cast<const u32x4*>(vb + (size_t)(kc * L + vrow + 2 * r < S ? vrow + 2 * r : 0) * DV);
     };
     auto load_qs = [&](int kc) {
       const bf16_t* qb = qh + (size_t)kc * L * DQK + dw0 + 8 * hh;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const bool ok = kc * L + 32 * tt + l32 < S;
+        const int row = kc * L + 32 * tt + l32 < S ? 32 * tt + l32 : 0;
 #pragma unroll
-        for (int s = 0; s < QKS; ++s) {
-          const u32x4 x = *reinterpret_cast<const u32x4*>(qb + (size_t)(ok ? 32 * tt + l32 : 0) * DQK + 16 * s);
-          Qs[tt][s] = ok ? x : u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int s = 0; s < QKS; ++s) Qs[tt][s] = *reinterpret_cast<const u32x4*>(qb + (size_t)row * DQK + 16 * s);
       }
     };
     load_k(0, Kst);
@@ -543,13 +538,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
     // 16-byte load; the K operand below uses the same contiguous k order)
     auto load_q = [&](int kc) {
-      const bool ok = kc * L + 16 * o + r16 < S;
-      const bf16_t* qb = qh + ((size_t)kc * L + (ok ? 16 * o + r16 : 0)) * DQK + 8 * g;
+      const bf16_t* qb = qh + ((size_t)kc * L + (kc * L + 16 * o + r16 < S ? 16 * o + r16 : 0)) * DQK + 8 * g;
 #pragma unroll
-      for (int p = 0; p < KPD; ++p) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(qb + 32 * p);
-        Qf[p] = ok ? x : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int p = 0; p < KPD; ++p) Qf[p] = *reinterpret_cast<const u32x4*>(qb + 32 * p);
     };
     load_k(0, Kst);
     load_q(0);
