@@ -63,6 +63,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 PREFILL_KERNEL = "chunkwise_fused_kernel"
 SOFT_CAP_KERNEL = "soft_cap_kernel"
 SOFT_CAP_SHAPE = (1, 2048, 50304)  # config 3 prefill logits
+SLSTM_KERNEL = "slstm_seq_kernel"
+SEQ_KERNEL = "mlstm_recurrent_kernel"
+SEQ_TOKENS = 64  # recurrent-sequence bench: tokens per call on config 2's heads
 
 
 def prefill_flops(B, NH, S, DQK, DV, L):
@@ -293,6 +296,25 @@ def _hbm(by, ms):
             "bytes_per_call": by}
 
 
+def slstm_bytes():
+    """cfg4 sLSTM layer: z and h (bf16) + the three gates (bf16) + last c, n, m (float32)."""
+    from xlstm_hip.workloads import CFG4_SLSTM as c
+    return 2 * c.B * c.S * c.NH * c.H * 2 + 3 * c.B * c.S * c.NH * 2 + c.B * c.NH * (2 * c.H + 1) * 4
+
+
+def mlstm_sequence_bytes():
+    """Recurrent sequence on cfg2's heads: C, n, m read and written once + q, k, v, h, gates of the tokens."""
+    from xlstm_hip.workloads import CFG2 as c
+    BH = c.B * c.NH
+    return 2 * BH * (c.DQK * c.DV + c.DQK + 1) * 4 + BH * SEQ_TOKENS * (2 * c.DQK + 2 * c.DV + 2) * 2
+
+
+def _workloads():
+    from xlstm_hip.workloads import CFG2, CFG4_SLSTM as c
+    return (f"cfg4 sLSTM layer sequence B{c.B} S{c.S} NH{c.NH} H{c.H} bf16",
+            f"mlstm recurrent sequence, cfg2 heads B{CFG2.B} NH{CFG2.NH} DQK{CFG2.DQK} DV{CFG2.DV}, S={SEQ_TOKENS}")
+
+
 def bench_slstm_sequence(args, dev):
     """sLSTM time loop over config 4's sLSTM layer (B8 S4096 NH4 H512, bf16 z / gates / h,
     float32 states from zero, last states returned): one xl_slstm_seq_fwd launch.
@@ -301,10 +323,10 @@ def bench_slstm_sequence(args, dev):
     from xlstm_hip.workloads import CFG4_SLSTM as c, slstm_inputs
     z, i, f, o = slstm_inputs(c, device=dev)
     t = _timed(lambda: xlstm_hip.slstm_sequence(z, i, f, o), dev, max(5, args.steps))
-    by = 2 * c.B * c.S * c.NH * c.H * 2 + 3 * c.B * c.S * c.NH * 2 + c.B * c.NH * (2 * c.H + 1) * 4
-    return {"workload": f"cfg4 sLSTM layer sequence B{c.B} S{c.S} NH{c.NH} H{c.H} bf16", "us_per_call": 1e3 * t["ms"],
-            "us_min": 1e3 * t["ms_min"], "tokens_per_s": c.B * c.S / (t["ms"] * 1e-3), "mode": t["mode"],
-            "roofline": _hbm(by, t["ms"])}
+    wl = _workloads()[0]
+    return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"],
+            "tokens_per_s": c.B * c.S / (t["ms"] * 1e-3), "mode": t["mode"],
+            "roofline": dict(_hbm(slstm_bytes(), t["ms"]), traffic=load_traffic(SLSTM_KERNEL, wl))}
 
 
 def bench_mlstm_sequence(args, dev):
@@ -313,7 +335,7 @@ def bench_mlstm_sequence(args, dev):
     states returned.  Bytes: C, n, m read and written once + q, k, v, h, gates of the 64 tokens."""
     import xlstm_hip
     from xlstm_hip.workloads import CFG2, chunkwise_inputs
-    cfg, S = CFG2, 64
+    cfg, S = CFG2, SEQ_TOKENS
     q, k, v, i, f = chunkwise_inputs(cfg, device=dev, S=S)
     g = torch.Generator("cpu").manual_seed(5)
     C = (0.1 * torch.randn(cfg.B, cfg.NH, cfg.DQK, cfg.DV, generator=g)).to(dev)
@@ -321,11 +343,10 @@ def bench_mlstm_sequence(args, dev):
     m = torch.randn(cfg.B, cfg.NH, 1, generator=g).to(dev)
     t = _timed(lambda: xlstm_hip.mlstm_recurrent_sequence__native_fw(q, k, v, i, f, C, n, m, return_last_states=True),
                dev, max(5, args.steps))
-    BH = cfg.B * cfg.NH
-    by = 2 * BH * (cfg.DQK * cfg.DV + cfg.DQK + 1) * 4 + BH * S * (2 * cfg.DQK + 2 * cfg.DV + 2) * 2
-    return {"workload": f"mlstm recurrent sequence, cfg2 heads B{cfg.B} NH{cfg.NH} DQK{cfg.DQK} DV{cfg.DV}, S={S}",
-            "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "us_per_token": 1e3 * t["ms"] / S,
-            "mode": t["mode"], "roofline": _hbm(by, t["ms"])}
+    wl = _workloads()[1]
+    return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "us_per_token": 1e3 * t["ms"] / S,
+            "mode": t["mode"],
+            "roofline": dict(_hbm(mlstm_sequence_bytes(), t["ms"]), traffic=load_traffic(SEQ_KERNEL, wl))}
 
 
 def bench_arbitrary_length(args, dev):
@@ -367,19 +388,23 @@ def load_traffic(kernel, workload):
 
 
 def summarize_pmc(fetch_dir, write_dir):
-    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of every kernel, scaled by the soft-cap stream's reading."""
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of every kernel, scaled by the soft-cap stream's reading.
+    Each argument may list several rocprofv3 output directories, comma-separated."""
     import csv
     import glob
 
-    def per_kernel(d, counter):
+    def per_kernel(dirs, counter):
         acc = {}
-        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        files = [fn for d in dirs.split(",") for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"),
+                                                                  recursive=True)]
+        for fn in files:
             with open(fn) as fh:
                 for row in csv.DictReader(fh):
                     if row["Counter_Name"] != counter:
                         continue
                     name = row["Kernel_Name"]
-                    key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel") if k in name), None)
+                    key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel",
+                                            SLSTM_KERNEL, SEQ_KERNEL) if k in name), None)
                     if key is None:
                         continue
                     acc.setdefault(key, {}).setdefault(row["Dispatch_Id"], 0.0)
@@ -392,7 +417,9 @@ def summarize_pmc(fetch_dir, write_dir):
     sc_bytes = 2 * SOFT_CAP_SHAPE[0] * SOFT_CAP_SHAPE[1] * SOFT_CAP_SHAPE[2]  # read once, written once
     f_scale, w_scale = sc_bytes / fetch[SOFT_CAP_KERNEL], sc_bytes / write[SOFT_CAP_KERNEL]
     from xlstm_hip.workloads import CFG1, CFG2
-    work = {PREFILL_KERNEL: ("cfg2 mlstm_chunkwise prefill",
+    wl_slstm, wl_seq = _workloads()
+    work = {SLSTM_KERNEL: (wl_slstm, slstm_bytes()), SEQ_KERNEL: (wl_seq, mlstm_sequence_bytes()),
+            PREFILL_KERNEL: ("cfg2 mlstm_chunkwise prefill",
                              prefill_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV)),
             SOFT_CAP_KERNEL: ("cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16", 2 * sc_bytes),
             "mlstm_step_kernel": ("cfg1 mlstm decode step", decode_bytes(CFG1.B, CFG1.NH, CFG1.DQK, CFG1.DV)),
