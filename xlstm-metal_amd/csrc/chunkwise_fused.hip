@@ -51,6 +51,8 @@
 // the head's q/k chunks are fetched from HBM once and then hit that XCD's L2.
 #include "chunkwise.h"
 
+#include <type_traits>
+
 namespace xl {
 namespace fused {
 
@@ -532,7 +534,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // the output waves are the longer dependency chain of a chunk: let their
     // MFMAs and loads win the SIMD's issue arbitration over the state waves'
     __builtin_amdgcn_s_setprio(2);
-    const int o = ws;
+    // one specialisation per output row tile O: the causal bounds of the S and
+    // M V products are compile-time constants
+    auto out_wave = [&](auto otag) {
+    constexpr int o = decltype(otag)::value;
     u32x4 Kst[NKU], Qf[KPD];
     float pv[5];  // gate prep of the next chunk (gate wave)
     // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
@@ -554,18 +559,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         if (o == 0) prep_load(kc + 1, pv);
       }
 
-      // S^T tiles of all four j-tiles over the whole DQK: A = K rows 16jt + r16,
-      // B = q rows.  Every output wave computes all four (tiles above the
-      // diagonal are masked in the gating), so the code is branch-free; the
-      // busiest SIMD (the wave of the last row tile) does the same work as
-      // before.  A fifth A tile holds the four parts of n (row r16 = part
-      // r16 & 3), so the same MFMAs give q.n in every lane.
+      // S^T tiles over the whole DQK: A = K rows 16jt + r16, B = q rows; only the
+      // causal j-tiles jt <= o (the rest are masked), the bound a compile-time
+      // constant of this specialisation.  A fifth A tile holds the four parts of
+      // n (row r16 = part r16 & 3), so the same MFMAs give q.n in every lane.
       f32x4 Sacc[5];
       constexpr int KD = 2;
       u32x4 kf[KD][5];
       auto load_kf = [&](int p, u32x4 (&dst)[5]) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+        for (int jt = 0; jt <= o; ++jt)
           dst[jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
         dst[4] = *reinterpret_cast<const u32x4*>(nbk + (r16 & 3) * SM::NB_PITCH + 32 * p + 8 * g);
       };
@@ -578,7 +581,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         if (p + KD - 1 < KPD) load_kf(p + KD - 1, kf[(p + KD - 1) % KD]);
 #pragma unroll
         for (int jt = 0; jt < 5; ++jt)
-          Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
+          if (jt == 4 || jt <= o)  // j-tiles above the diagonal are all masked (compile-time)
+            Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
       }
       if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch
       const float qn = (Sacc[4][0] + Sacc[4][1]) + (Sacc[4][2] + Sacc[4][3]);  // q . n (stored state)
@@ -599,6 +603,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int pj = 0; pj < 2; ++pj) {
+        if (32 * pj > 16 * o + 15) continue;  // all of M is masked for these tokens (compile-time)
         bf16x8 mh, ml;
         split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
 #pragma unroll
@@ -687,6 +692,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           const float nb = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, na), 0xB1, 0xf, 0xf, false));
           if (r16 == 0) n_last[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] = (na + nb) * sc;
         }
+    }
+    };
+    switch (__builtin_amdgcn_readfirstlane(ws)) {
+      case 0: out_wave(std::integral_constant<int, 0>{}); break;
+      case 1: out_wave(std::integral_constant<int, 1>{}); break;
+      case 2: out_wave(std::integral_constant<int, 2>{}); break;
+      default: out_wave(std::integral_constant<int, 3>{}); break;
     }
   }
 }
