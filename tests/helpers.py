@@ -35,19 +35,21 @@ def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(ax)) - mant - 1)
 
 
-def lowp_excess(got: torch.Tensor, want: torch.Tensor) -> float:
-    """max(|got - want| - ulp(want)/2) with ulp in got's dtype: the error beyond output rounding."""
+def lowp_excess(got: torch.Tensor, want: torch.Tensor, roundings: int = 1) -> float:
+    """max(|got - want| - roundings * ulp(want)/2) with ulp in got's dtype: the error beyond
+    `roundings` 16-bit roundings of the output (1: the output's own)."""
     d = (got.detach().double().cpu() - want.detach().double().cpu()).abs()
-    return float((d - half_ulp(want, got.dtype)).max())
+    return float((d - roundings * half_ulp(want, got.dtype)).max())
 
 
-def assert_parity(got, want, dtype, what=""):
-    """fp32: relerr <= FP32_REL; 16-bit inputs: max-abs <= LOWP_ABS beyond the output's own rounding."""
+def assert_parity(got, want, dtype, what="", roundings=1):
+    """fp32: relerr <= FP32_REL; 16-bit inputs: max-abs <= LOWP_ABS beyond the output's own rounding
+    (and, with roundings=2, one more 16-bit rounding the reference applies on the way to it)."""
     if dtype == torch.float32:
         e = relerr(got, want)
         assert e <= FP32_REL, f"{what}: rel-err {e:.3e} > {FP32_REL}"
     else:
-        e = lowp_excess(got, want)
+        e = lowp_excess(got, want, roundings)
         assert e <= LOWP_ABS, f"{what}: max-abs {e:.3e} beyond output rounding > {LOWP_ABS}"
     return e
 

@@ -107,7 +107,7 @@ def test_chained_steps_match_sequence_oracle(gpu_case):
         assert relerr(got, want) <= FP32_REL
 
 
-@pytest.mark.parametrize("S", [1, 5, 15, 64])
+@pytest.mark.parametrize("S", [1, 5, 15, 64, 65, 130, 200])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_sequence_kernel(gpu_case, S, dtype):
     import xlstm_hip
@@ -123,10 +123,15 @@ def test_sequence_kernel(gpu_case, S, dtype):
     h, (C, n, m) = xlstm_hip.mlstm_recurrent_sequence__native_fw(*_to((q, k, v, i, f, C0, n0, m0)),
                                                                 return_last_states=True)
     hr, (Cr, nr, mr) = om.mlstm_recurrent_sequence(q, k, v, i, f, C0, n0, m0, return_last_states=True)
+    # With a 16-bit q the reference rounds q . n' to q's dtype before dividing by it
+    # (native_step.py:86-96), so a 1-ulp difference of the float32 gate exponentials (GPU
+    # and CPU exp) can flip that rounding and move h by one bf16 ulp of its own: over long
+    # sequences h is held to 2e-2 beyond two bf16 roundings (its own and the denominator's).
+    rnd = 2 if S > 64 else 1
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
-        assert_parity(got, want, dtype, f"S={S} {dtype} {name}")
+        assert_parity(got, want, dtype, f"S={S} {dtype} {name}", roundings=rnd if name == "h" else 1)
     h0 = xlstm_hip.mlstm_recurrent_sequence__native_fw(*_to((q, k, v, i, f)))
-    assert_parity(h0, om.mlstm_recurrent_sequence(q, k, v, i, f), dtype, "zero state")
+    assert_parity(h0, om.mlstm_recurrent_sequence(q, k, v, i, f), dtype, "zero state", roundings=rnd)
 
 
 def test_step_alias_rejected(gpu_case):
@@ -139,3 +144,25 @@ def test_step_alias_rejected(gpu_case):
                                n.data_ptr(), m.data_ptr(), h.data_ptr(), C.data_ptr(), n.data_ptr(),
                                torch.empty_like(m).data_ptr(), 1, 2, 64, 64, 0.125, 1e-6, 0, 0, None)
     assert rc == -1 and b"alias" in lib.xl_last_error()
+
+
+@pytest.mark.parametrize("DQK,DV", [(64, 64), (128, 256), (512, 128)])
+@pytest.mark.parametrize("S", [63, 150])
+def test_sequence_kernel_heads_and_strong_gates(gpu_case, DQK, DV, S):
+    """Head sizes of every row-per-thread variant (DQK 64 .. 512) and gates spanning +-15, so the
+    stabiliser resets to i_t often and the 64-step gate chunks carry m across their boundary."""
+    import xlstm_hip
+    B, NH = 1, 2
+    g = torch.Generator().manual_seed(DQK + S)
+    q, k = (torch.randn(B, NH, S, DQK, generator=g) for _ in range(2))
+    v = torch.randn(B, NH, S, DV, generator=g)
+    i = 15 * torch.tanh(4 * torch.randn(B, NH, S, generator=g) / 15)
+    f = 15 * torch.tanh(6 * torch.randn(B, NH, S, generator=g) / 15)
+    C0 = 0.1 * torch.randn(B, NH, DQK, DV, generator=g)
+    n0 = torch.randn(B, NH, DQK, generator=g).abs()
+    m0 = torch.randn(B, NH, 1, generator=g)
+    h, (C, n, m) = xlstm_hip.mlstm_recurrent_sequence__native_fw(*_to((q, k, v, i, f, C0, n0, m0)),
+                                                                return_last_states=True)
+    hr, (Cr, nr, mr) = om.mlstm_recurrent_sequence(q, k, v, i, f, C0, n0, m0, return_last_states=True)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got, want, torch.float32, f"DQK={DQK} DV={DV} S={S} {name}")

@@ -61,7 +61,8 @@ def test_slstm_cell_five_steps(gpu_case):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(2, 7, 4, 8), (8, 256, 4, 512), (1, 33, 3, 100)])
+@pytest.mark.parametrize("shape", [(2, 7, 4, 8), (8, 256, 4, 512), (1, 33, 3, 100), (2, 1100, 2, 64),
+                                   (1, 4096, 2, 128), (1, 2000, 1, 200)])
 def test_slstm_sequence(gpu_case, dtype, shape):
     import xlstm_hip
     B, S, NH, H = shape

@@ -17,7 +17,7 @@
 // through LDS.  n' is recomputed by every tile of a head (DQK values, L2
 // resident) and written by tile 0 only.  In the sequence kernel C' lives in
 // registers for the whole sequence (every C byte crosses HBM once per launch),
-// the gates of 64 steps come from one max-plus scan (lane = step), the next
+// the gates of 64 steps are formed together (lane = step), the next
 // step's q, k and v are loaded while the current step runs, and the LDS
 // buffers alternate with the step's parity, so a step costs two workgroup
 // barriers.
@@ -88,9 +88,12 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
   };
   fetch(0);
 
-  // ---- gates, 64 steps at a time with lane = step: the stabiliser by the
-  // max-plus scan (common.h), then fa, ia and exp(-m') of every step, read
-  // back per step with v_readlane
+  // ---- gates, 64 steps at a time with lane = step: logsig f and i per lane,
+  // the stabiliser m' = max(logsig f + m, i) step by step exactly as the
+  // reference forms it (two dependent operations per step, so m is bit-equal
+  // to the step recurrence: with 16-bit q the reference rounds q.n' and
+  // (q s)^T C' to bf16, and a 1-ulp change of m can flip those roundings),
+  // then fa, ia and exp(-m') of every step, read back per step with v_readlane
   float gfa = 0.f, gia = 0.f, gem = 0.f;
   for (int t = 0; t < S; ++t) {
     const int jg = t & 63;
@@ -100,15 +103,18 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
       const size_t gtok = (size_t)bh * S + (ok ? tg : t);
       const float lsf = ok ? round_to<TG>(logsigmoid(to_f32(fg[gtok]))) : 0.f;  // torch keeps logsigmoid in f's dtype
       const float ipre = to_f32(ig[gtok]);
-      float a = lsf, b = ok ? ipre : -INFINITY;
-      maxplus_scan(a, b);
-      const float mt = fmaxf(m + a, b);
+      const int cnt = S - t < 64 ? S - t : 64;
+      float mt = 0.f, mc = m;
+      for (int j = 0; j < cnt; ++j) {
+        mc = fmaxf(lane_of(lsf, j) + mc, lane_of(ipre, j));
+        mt = lane == j ? mc : mt;
+      }
       float mp = __shfl_up(mt, 1, 64);
       if (lane == 0) mp = m;
       gfa = expf(lsf + mp - mt);
       gia = expf(ipre - mt);
       gem = expf(-mt);
-      m = lane_of(mt, 63);  // invalid lanes repeat the last valid m
+      m = mc;
     }
     const int buf = t & 1;
     const size_t tok = (size_t)bh * S + t;
