@@ -58,15 +58,18 @@ __global__ __launch_bounds__(256) void slstm_step_kernel(const TZ* __restrict__ 
 //    the rounding of the step-by-step recurrence (exact where i_t resets it).
 //  * Pass 0: each wave composes the map of its segment; the incoming m of
 //    segment w is m0 pushed through the maps of segments 0 .. w-1 (LDS).
-//  * Pass 1: each wave runs its segment from c = 0 (per lane) and the scans
-//    give the segment's F = prod fg and n from 0 (uniform), to LDS.
+//  * Pass 1: each wave forms c at its segment's end from c = 0 (per lane) as
+//    a weighted sum of tanh z_t (one multiply-add per element and step), and
+//    the scans give the segment's F = prod fg and n from 0 (uniform), to LDS.
 //  * Pass 2: each wave composes its start state c = F c + c_seg over the
 //    earlier segments and reruns its segment from it, writing h; the wave of
-//    the last step writes the final states.
+//    the last step writes the final states.  Without an initial n, n is the
+//    same for every d of a head and h = c * og / (|n| + eps) takes one
+//    multiply per element (the scale is formed per step in the gate phase).
 // z is read twice (the second read mostly hits the Infinity Cache); every
 // step of both passes keeps z loads SEQ_PF steps ahead.
 constexpr int SEQ_WAVES = 16;
-constexpr int SEQ_PF = 16;
+constexpr int SEQ_PF = 32;
 constexpr float SEQ_LOG2E = 1.4426950408889634f;
 
 // inclusive scan of the affine maps x -> F x + N (n from 0 and prod fg)
@@ -133,7 +136,43 @@ __device__ __forceinline__ void seq_gates(const TG* __restrict__ ip, const TG* _
   mlast = lane_of(mt, 63);  // invalid lanes repeat the last valid m
 }
 
-template <typename TZ, typename TG, typename TH>
+// Raw buffer access: wave-uniform resource and scalar byte offset, per-lane
+// byte offset (the step address costs no vector instruction).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+template <typename T> __device__ __forceinline__ T buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff);
+template <> __device__ __forceinline__ float buf_ld<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+template <> __device__ __forceinline__ bf16_t buf_ld<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  bf16_t x;
+  x.bits = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+  return x;
+}
+template <> __device__ __forceinline__ f16_t buf_ld<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  return __builtin_bit_cast(f16_t, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_st(float x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, voff, soff, 0);
+}
+__device__ __forceinline__ void buf_st(bf16_t x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b16(x.bits, r, voff, soff, 0);
+}
+__device__ __forceinline__ void buf_st(f16_t x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, x), r, voff, soff, 0);
+}
+
+// Per-wave gate rows of the current 64-step chunk in LDS, read with one
+// broadcast load per step (no v_readlane): {fg, ig, og or the h scale, w}.
+struct SeqGateRow {
+  float fg, ig, hs, w;
+};
+
+// UN (uniform n): no initial n, so n_t = fg_t n_{t-1} + ig_t is the same for
+// every d of a head; it is formed per step in the gate phase (lane = step)
+// together with the h scale og_t / (|n_t| + eps), and h = c * scale.
+template <typename TZ, typename TG, typename TH, bool UN>
 __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
     const TZ* __restrict__ z, const TG* __restrict__ ip, const TG* __restrict__ fp, const TG* __restrict__ op,
     const float* __restrict__ c0, const float* __restrict__ n0, const float* __restrict__ m0, TH* __restrict__ h,
@@ -142,18 +181,22 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
   __shared__ float s_map[SEQ_WAVES][2];        // max-plus map of each segment
   __shared__ float s_aff[SEQ_WAVES][2];        // F, n-from-0 of each segment
   __shared__ float s_cseg[SEQ_WAVES][64];      // c from 0 at each segment's end, per lane
+  __shared__ SeqGateRow s_gate[SEQ_WAVES][64]; // gate rows of the wave's current chunk
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;  // w: wave-uniform
   const int bh = blockIdx.x / ndb, db = blockIdx.x - bh * ndb;
   const int b = bh / NH, hh = bh - b * NH;
   const int d = 64 * db + lane;
   const bool dok = d < H;
-  const int dc = dok ? d : 0;
+  // lane byte offsets within the d block (lanes past H read lane 0's element)
+  const uint32_t zlb = (dok ? lane : 0) * (uint32_t)sizeof(TZ), hlb = lane * (uint32_t)sizeof(TH);
   const int SL = (S + SEQ_WAVES - 1) / SEQ_WAVES;
   const int t0 = min(S, w * SL), t1 = min(S, t0 + SL);
   const int64_t gbase = (int64_t)b * S * NH + hh;  // gates[b, t, hh] = gbase + t * NH
-  const int64_t zrow = (int64_t)NH * H;            // z[b, t, hh, d] = zbase + t * zrow
-  const int64_t zbase = (int64_t)b * S * zrow + (int64_t)hh * H + dc;
+  const int64_t zrow = (int64_t)NH * H;            // z[b, t, hh, d] = z + zblk + t * zrow + lane
+  const int64_t zblk = (int64_t)b * S * zrow + (int64_t)hh * H + 64 * db;  // wave-uniform
+  const int zrowb = (int)zrow * (int)sizeof(TZ), hrowb = (int)zrow * (int)sizeof(TH);  // bytes per step
   const float m_init = m0 ? m0[bh] : 0.f;
+  SeqGateRow* gr = s_gate[w];
 
   // ---- pass 0: the max-plus map of this segment
   float sa = 0.f, sb = -INFINITY;
@@ -172,58 +215,95 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
   float m_in = m_init;  // m at step t0 - 1
   for (int q = 0; q < w; ++q) m_in = fmaxf(m_in + s_map[q][0], s_map[q][1]);
 
-  // one segment from (c, n) with the gates of its steps; PASS 1: c from 0,
-  // segment F and n from the scans; PASS 2: writes h.  Step indices are
-  // wave-uniform, so addresses are one scalar multiply and one vector add.
+  // One segment with the gates of its steps.  PASS 1: c at the segment end
+  // from c = 0, as the weighted sum sum_t w_t tanh z_t per chunk (w_t = ig_t
+  // prod_{s>t} fg_s, formed in the gate phase), and the segment's affine map of
+  // n.  PASS 2: the recurrence from the true start state, writing h.  Step
+  // indices are wave-uniform, so a step's z and h addresses are a scalar
+  // base plus the lane offset.
   const bool dfull = 64 * (db + 1) <= H;  // uniform: every lane of the block is a real d
   auto run = [&](auto pass_tag, float& c, float& n) {
     constexpr int PASS = decltype(pass_tag)::value;
     float mprev = m_in, Fs = 1.f, Ns = 0.f;
+    float nu = n;  // UN, pass 2: the uniform n
     TZ zq[SEQ_PF];  // raw prefetched z (converted when used, so the load is not waited for early)
-    const TZ* zl = z + zbase;
-    TH* hl = h + zbase + (int64_t)t0 * zrow;
     const int tlast = max(t1 - 1, 0);
-    // every prefetch is its own load at step min(t + SEQ_PF, tlast) (wave-uniform index)
+    // z of step t relative to the chunk starting at step cb (byte offsets < 2^31: checked at launch)
+    auto zat = [&](__amdgpu_buffer_rsrc_t r, int cb, int t) { return buf_ld<TZ>(r, zlb, (t - cb) * zrowb); };
+    {
+      const auto zr = seq_rsrc(z + zblk + (int64_t)t0 * zrow);
 #pragma unroll
-    for (int j = 0; j < SEQ_PF; ++j) zq[j] = zl[(int64_t)min(t0 + j, tlast) * zrow];
-    auto step = [&](float zt, float fgj, float igj, float ogj, auto store_tag) {
-      c = fmaf(fgj, c, igj * tanh_seq(zt));
-      if (PASS == 2) {
-        n = fmaf(fgj, n, igj);
-        const float hv = ogj * c * __builtin_amdgcn_rcpf(fabsf(n) + eps);
-        if (decltype(store_tag)::value || dok) *hl = from_f32_fast<TH>(hv);
-        hl += zrow;
-      }
-    };
+      for (int j = 0; j < SEQ_PF; ++j) zq[j] = zat(zr, t0, min(t0 + j, tlast));
+    }
     for (int cst = t0; cst < t1; cst += 64) {
       float fg, ig, og, ma, mb, ml;
       seq_gates(ip, fp, op, gbase, NH, cst, t1, lane, mprev, fg, ig, og, ma, mb, ml);
       mprev = ml;
+      const bool ok = cst + lane < t1;
+      const float fgv = ok ? fg : 1.f, igv = ok ? ig : 0.f;
+      float Fc = 1.f;  // PASS 1: prod fg over the chunk
       if (PASS == 1) {
-        float F = (cst + lane < t1) ? fg : 1.f, N = (cst + lane < t1) ? ig : 0.f;
+        // suffix products prod_{s>=t} fg_s: inclusive scan of the lane-reversed fg
+        float y = __shfl(fgv, 63 - lane, 64), yn = 0.f;
+        affine_scan(y, yn);
+        Fc = lane_of(y, 63);
+        const float pin = __shfl(y, 63 - lane, 64);
+        float pex = __shfl_down(pin, 1, 64);
+        if (lane == 63) pex = 1.f;
+        gr[lane].w = igv * pex;
+        float F = fgv, N = igv;
         affine_scan(F, N);
         const float cF = lane_of(F, 63), cN = lane_of(N, 63);
         Ns = fmaf(Ns, cF, cN);
         Fs *= cF;
+      } else {
+        float hs = og;
+        if (UN) {
+          float F = fgv, N = igv;
+          affine_scan(F, N);
+          const float nt = fmaf(F, nu, N);  // n at step cst + lane
+          hs = og * __builtin_amdgcn_rcpf(fabsf(nt) + eps);
+          nu = lane_of(nt, 63);  // invalid lanes keep the last valid n
+        }
+        gr[lane] = SeqGateRow{fg, ig, hs, 0.f};
       }
+      __builtin_amdgcn_wave_barrier();
+      const auto zr = seq_rsrc(z + zblk + (int64_t)cst * zrow);
+      const auto hr = seq_rsrc(h + zblk + (int64_t)cst * zrow);
+      float acc = 0.f;  // PASS 1: sum_t w_t tanh z_t over the chunk
+      auto step = [&](int j, float zt, auto store_tag) {
+        const float tz = tanh_seq(zt);
+        if (PASS == 1) {
+          acc = fmaf(gr[j].w, tz, acc);
+        } else {
+          const SeqGateRow gj = gr[j];
+          c = fmaf(gj.fg, c, gj.ig * tz);
+          float hv;
+          if (UN) {
+            hv = c * gj.hs;
+          } else {
+            n = fmaf(gj.fg, n, gj.ig);
+            hv = gj.hs * c * __builtin_amdgcn_rcpf(fabsf(n) + eps);
+          }
+          if (decltype(store_tag)::value || dok) buf_st(from_f32_fast<TH>(hv), hr, hlb, j * hrowb);
+        }
+      };
       if (cst + 64 <= t1) {
         auto chunk = [&](auto store_tag) {
 #pragma unroll
           for (int j = 0; j < 64; ++j) {
             const float zt = to_f32(zq[j % SEQ_PF]);
-            zq[j % SEQ_PF] = zl[(int64_t)min(cst + j + SEQ_PF, tlast) * zrow];
-            step(zt, lane_of(fg, j), lane_of(ig, j), PASS == 2 ? lane_of(og, j) : 0.f, store_tag);
+            zq[j % SEQ_PF] = zat(zr, cst, min(cst + j + SEQ_PF, tlast));
+            step(j, zt, store_tag);
           }
         };
         if (dfull) chunk(std::true_type{});
         else chunk(std::false_type{});
       } else {  // partial chunk at the segment end: no prefetch
-        const TZ* zt_p = zl + (int64_t)cst * zrow;
-        for (int j = 0; j < t1 - cst; ++j) {
-          step(to_f32(*zt_p), lane_of(fg, j), lane_of(ig, j), PASS == 2 ? lane_of(og, j) : 0.f, std::false_type{});
-          zt_p += zrow;
-        }
+        for (int j = 0; j < t1 - cst; ++j) step(j, to_f32(zat(zr, cst, cst + j)), std::false_type{});
       }
+      if (PASS == 1) c = fmaf(Fc, c, acc);
+      __builtin_amdgcn_wave_barrier();
     }
     if (PASS == 1) {
       n = Ns;
@@ -232,6 +312,7 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
         s_aff[w][1] = Ns;
       }
     }
+    if (PASS == 2 && UN) n = nu;
     return mprev;
   };
 
@@ -272,9 +353,9 @@ static int launch_seq3(const void* z, const void* i, const void* f, const void* 
                        int64_t total, float eps, hipStream_t s) {
   const int ndb = (H + 63) / 64;  // 64-element d blocks per head
   const int64_t blocks = total / H * ndb;
-  hipLaunchKernelGGL((slstm_seq_kernel<TZ, TG, TH>), dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), 0, s,
-                     (const TZ*)z, (const TG*)i, (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H,
-                     ndb, eps);
+  auto kern = n ? slstm_seq_kernel<TZ, TG, TH, false> : slstm_seq_kernel<TZ, TG, TH, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), 0, s, (const TZ*)z, (const TG*)i,
+                     (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H, ndb, eps);
   return check_launch("xl_slstm_seq_fwd");
 }
 
@@ -354,6 +435,9 @@ extern "C" int xl_slstm_seq_fwd(const void* z, const void* i, const void* f, con
   if (m_last && m_last == m0) return set_error(XL_ERR_INVALID_ARG, "%s: m_last must not alias m0", who);
   const int64_t total = (int64_t)B * NH * H;
   if ((total + 255) / 256 > 0x7fffffffLL) return set_error(XL_ERR_INVALID_ARG, "%s: too large", who);
+  // the kernel addresses z and h within a 64-step chunk (plus its prefetch) with 32-bit offsets
+  if ((int64_t)(64 + SEQ_PF) * NH * H * 4 > 0x7fffffffLL)
+    return set_error(XL_ERR_INVALID_ARG, "%s: NH * H = %lld too large", who, (long long)NH * H);
   return dispatch3<SeqFn>(dtype_z, dtype_gates, dtype_h, z, i, f, o, c0, n0, m0, h, c_last, n_last, m_last, S, NH,
                           H, total, eps, (hipStream_t)stream);
 }
