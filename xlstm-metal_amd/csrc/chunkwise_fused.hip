@@ -96,11 +96,29 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// The low part x - hi of a pair packed as hi = {bf16(x0), bf16(x1)}, one
+// v_dot2c_f32_bf16 per element: x_e + hi . (-1 in element e) is exact, since
+// x - bf16(x) is representable.  The {-1, 0} operand (bf16 bits 0x0000bf80) is
+// kept in an SGPR: the inline-constant form the compiler picks for it reads
+// as {0, -1} on gfx950.
+struct LoOps {
+  bf16x2 m0, m1;
+};
+__device__ __forceinline__ LoOps lo_ops() {
+  uint32_t k0 = 0x0000bf80u;
+  asm volatile("" : "+s"(k0));
+  return LoOps{__builtin_bit_cast(bf16x2, k0), __builtin_bit_cast(bf16x2, 0xbf800000u)};
+}
+__device__ __forceinline__ uint32_t pack_lo(const LoOps& lo, uint32_t hi, float x0, float x1) {
+  const bf16x2 h = __builtin_bit_cast(bf16x2, hi);
+  return pack_bf16(__builtin_amdgcn_fdot2_f32_bf16(h, lo.m0, x0, false),
+                   __builtin_amdgcn_fdot2_f32_bf16(h, lo.m1, x1, false));
+}
 // bf16 hi + lo split of 8 floats: hi = bf16(x), lo = bf16(x - hi)
-__device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+__device__ __forceinline__ void split8(const LoOps& lk, f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
   const u32x4 h = {pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
-  const u32x4 l = {pack_bf16(a[0] - bf_lo(h[0]), a[1] - bf_hi(h[0])), pack_bf16(a[2] - bf_lo(h[1]), a[3] - bf_hi(h[1])),
-                   pack_bf16(b[0] - bf_lo(h[2]), b[1] - bf_hi(h[2])), pack_bf16(b[2] - bf_lo(h[3]), b[3] - bf_hi(h[3]))};
+  const u32x4 l = {pack_lo(lk, h[0], a[0], a[1]), pack_lo(lk, h[1], a[2], a[3]), pack_lo(lk, h[2], b[0], b[1]),
+                   pack_lo(lk, h[3], b[2], b[3])};
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);
 }
@@ -217,6 +235,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const int w = tid >> 6, lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
   const int ws = w & 3;  // index within the state or output group
+  const LoOps lk = lo_ops();
 
   // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
   const int nwg = BNH * nvtile;
@@ -327,8 +346,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int dt = 0; dt < NTO; ++dt) {
         const f32x4 x = nacc[dt];
         const u32x2 hi = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
-        const u32x2 lo = {pack_bf16(x[0] - bf_lo(hi[0]), x[1] - bf_hi(hi[0])),
-                          pack_bf16(x[2] - bf_lo(hi[1]), x[3] - bf_hi(hi[1]))};
+        const u32x2 lo = {pack_lo(lk, hi[0], x[0], x[1]), pack_lo(lk, hi[1], x[2], x[3])};
         *reinterpret_cast<u32x2*>(nb + (2 * r16) * SM::NB_PITCH + 16 * dt) = hi;
         *reinterpret_cast<u32x2*>(nb + (2 * r16 + 1) * SM::NB_PITCH + 16 * dt) = lo;
       }
@@ -414,7 +432,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int c2 = 0; c2 < 4; ++c2) {
           const float x0 = al2[r] * bf_lo(Vst[r][c2]), x1 = al2[r] * bf_hi(Vst[r][c2]);
           hv[c2] = pack_bf16(x0, x1);
-          lv[c2] = pack_bf16(x0 - bf_lo(hv[c2]), x1 - bf_hi(hv[c2]));
+          lv[c2] = pack_lo(lk, hv[c2], x0, x1);
         }
         *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = hv;
         *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 128 + 2 * vcol) = lv;
@@ -439,7 +457,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           const int vt = qi / QKS, s = qi % QKS;
           const f32x16& a = acc[s >> 1][vt];
           const int e0 = 8 * (s & 1);
-          split8(f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]}, f32x4{a[e0 + 4], a[e0 + 5], a[e0 + 6], a[e0 + 7]},
+          split8(lk, f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]}, f32x4{a[e0 + 4], a[e0 + 5], a[e0 + 6], a[e0 + 7]},
                  o[0], o[1]);
         };
         auto store_p = [&](int vt) {
@@ -605,7 +623,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int pj = 0; pj < 2; ++pj) {
         if (32 * pj > 16 * o + 15) continue;  // all of M is masked for these tokens (compile-time)
         bf16x8 mh, ml;
-        split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
+        split8(lk, Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
 #pragma unroll
         for (int vq = 0; vq < NVX; ++vq) {
           bf16x8 vb;
