@@ -141,26 +141,23 @@ __device__ __forceinline__ void seq_gates(const TG* __restrict__ ip, const TG* _
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
-template <typename T> __device__ __forceinline__ T buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff);
-template <> __device__ __forceinline__ float buf_ld<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+// CP: cache policy bits of the access.  z keeps the default policy (the
+// second pass re-reads it, often from the Infinity Cache; nontemporal z loads
+// measured slower whenever z is cached), h is stored nontemporal (written once).
+constexpr int SEQ_NT = 2;
+template <typename T, int CP> __device__ __forceinline__ T buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CP));
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, CP));
+  }
 }
-template <> __device__ __forceinline__ bf16_t buf_ld<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  bf16_t x;
-  x.bits = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
-  return x;
-}
-template <> __device__ __forceinline__ f16_t buf_ld<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  return __builtin_bit_cast(f16_t, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
-}
-__device__ __forceinline__ void buf_st(float x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, voff, soff, 0);
-}
-__device__ __forceinline__ void buf_st(bf16_t x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  __builtin_amdgcn_raw_buffer_store_b16(x.bits, r, voff, soff, 0);
-}
-__device__ __forceinline__ void buf_st(f16_t x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, x), r, voff, soff, 0);
+template <int CP, typename T> __device__ __forceinline__ void buf_st(T x, __amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, voff, soff, CP);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, x), r, voff, soff, CP);
+  }
 }
 
 // Per-wave gate rows of the current 64-step chunk in LDS, read with one
@@ -229,7 +226,7 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
     TZ zq[SEQ_PF];  // raw prefetched z (converted when used, so the load is not waited for early)
     const int tlast = max(t1 - 1, 0);
     // z of step t relative to the chunk starting at step cb (byte offsets < 2^31: checked at launch)
-    auto zat = [&](__amdgpu_buffer_rsrc_t r, int cb, int t) { return buf_ld<TZ>(r, zlb, (t - cb) * zrowb); };
+    auto zat = [&](__amdgpu_buffer_rsrc_t r, int cb, int t) { return buf_ld<TZ, 0>(r, zlb, (t - cb) * zrowb); };
     {
       const auto zr = seq_rsrc(z + zblk + (int64_t)t0 * zrow);
 #pragma unroll
@@ -285,7 +282,7 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
             n = fmaf(gj.fg, n, gj.ig);
             hv = gj.hs * c * __builtin_amdgcn_rcpf(fabsf(n) + eps);
           }
-          if (decltype(store_tag)::value || dok) buf_st(from_f32_fast<TH>(hv), hr, hlb, j * hrowb);
+          if (decltype(store_tag)::value || dok) buf_st<SEQ_NT>(from_f32_fast<TH>(hv), hr, hlb, j * hrowb);
         }
       };
       if (cst + 64 <= t1) {
