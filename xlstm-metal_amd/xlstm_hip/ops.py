@@ -246,7 +246,9 @@ def _slstm_out_dtype(z, i, c):
 
 @torch.library.custom_op("xlstm_hip::slstm_step", mutates_args=())
 def slstm_step_op(z: Tensor, i: Tensor, f: Tensor, o: Tensor, c: Tensor, n: Tensor, m: Tensor,
-                  eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+                  eps: float) -> tuple[Tensor, Tensor]:
+    """Returns h and the new states packed as one flat tensor [c | n | m] (``state_views``
+    splits it): one allocation and, for 16-bit outputs, one conversion kernel."""
     what = "slstm_step"
     _lib.require_gpu(z, i, f, o, c, n, m, what=what)
     _check(z.dim() == 3, what, f"z must be (B, NH, H), got {tuple(z.shape)}")
@@ -259,30 +261,33 @@ def slstm_step_op(z: Tensor, i: Tensor, f: Tensor, o: Tensor, c: Tensor, n: Tens
     z, i, f, o = (_prep(t) for t in (z, i, f, o))
     c, n, m = _f32(c), _f32(n), _f32(m)
     h = torch.empty((B, NH, H), dtype=out_dt, device=z.device)
-    c_new = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
-    n_new = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
-    m_new = torch.empty((B, NH), dtype=torch.float32, device=z.device)
+    st = torch.empty(2 * B * NH * H + B * NH, dtype=torch.float32, device=z.device)
+    c_new, n_new, m_new = state_views(st, B, NH, H)
     rc = _lib.load().xl_slstm_step_fwd(
         z.data_ptr(), i.data_ptr(), f.data_ptr(), o.data_ptr(), c.data_ptr(), n.data_ptr(), m.data_ptr(),
         h.data_ptr(), c_new.data_ptr(), n_new.data_ptr(), m_new.data_ptr(), B, NH, H, float(eps),
         _lib.dtype_code(z, what), _lib.dtype_code(i, what), _lib.dtype_code(h, what), _lib.stream_of(z))
     _lib.check(rc, what)
-    if out_dt != torch.float32:
-        return h, c_new.to(out_dt), n_new.to(out_dt), m_new.to(out_dt)
-    return h, c_new, n_new, m_new
+    return h, (st.to(out_dt) if out_dt != torch.float32 else st)
 
 
 @slstm_step_op.register_fake
 def _(z, i, f, o, c, n, m, eps):
     out_dt = _slstm_out_dtype(z, i, c)
     B, NH, H = z.shape
-    return (z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((B, NH, H), dtype=out_dt),
-            z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((B, NH), dtype=out_dt))
+    return z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((2 * B * NH * H + B * NH,), dtype=out_dt)
+
+
+def state_views(st: Tensor, B: int, NH: int, H: int) -> tuple[Tensor, Tensor, Tensor]:
+    """c [B,NH,H], n [B,NH,H], m [B,NH]: the consecutive pieces of a flat sLSTM state tensor."""
+    k = B * NH * H
+    return st[:k].view(B, NH, H), st[k:2 * k].view(B, NH, H), st[2 * k:].view(B, NH)
 
 
 @torch.library.custom_op("xlstm_hip::slstm_sequence", mutates_args=())
 def slstm_sequence_op(z: Tensor, i: Tensor, f: Tensor, o: Tensor, c0: Optional[Tensor], n0: Optional[Tensor],
-                      m0: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+                      m0: Optional[Tensor], eps: float) -> tuple[Tensor, Tensor]:
+    """Returns h and the last states packed as one flat tensor [c | n | m] (``state_views``)."""
     what = "slstm_sequence"
     _lib.require_gpu(z, i, f, o, c0, n0, m0, what=what)
     _check(z.dim() == 4, what, f"z must be (B, S, NH, H), got {tuple(z.shape)}")
@@ -299,22 +304,18 @@ def slstm_sequence_op(z: Tensor, i: Tensor, f: Tensor, o: Tensor, c0: Optional[T
     z, i, f, o = (_prep(t) for t in (z, i, f, o))
     c0, n0, m0 = _f32(c0), _f32(n0), _f32(m0)
     h = torch.empty((B, S, NH, H), dtype=out_dt, device=z.device)
-    cl = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
-    nl = torch.empty((B, NH, H), dtype=torch.float32, device=z.device)
-    ml = torch.empty((B, NH), dtype=torch.float32, device=z.device)
+    st = torch.empty(2 * B * NH * H + B * NH, dtype=torch.float32, device=z.device)
+    cl, nl, ml = state_views(st, B, NH, H)
     rc = _lib.load().xl_slstm_seq_fwd(
         z.data_ptr(), i.data_ptr(), f.data_ptr(), o.data_ptr(), _lib.ptr(c0), _lib.ptr(n0), _lib.ptr(m0),
         h.data_ptr(), cl.data_ptr(), nl.data_ptr(), ml.data_ptr(), B, S, NH, H, float(eps),
         _lib.dtype_code(z, what), _lib.dtype_code(i, what), _lib.dtype_code(h, what), _lib.stream_of(z))
     _lib.check(rc, what)
-    if out_dt != torch.float32:
-        return h, cl.to(out_dt), nl.to(out_dt), ml.to(out_dt)
-    return h, cl, nl, ml
+    return h, (st.to(out_dt) if out_dt != torch.float32 else st)
 
 
 @slstm_sequence_op.register_fake
 def _(z, i, f, o, c0, n0, m0, eps):
     B, S, NH, H = z.shape
     out_dt = torch.promote_types(z.dtype, i.dtype) if c0 is None else _slstm_out_dtype(z, i, c0)
-    return (z.new_empty((B, S, NH, H), dtype=out_dt), z.new_empty((B, NH, H), dtype=out_dt),
-            z.new_empty((B, NH, H), dtype=out_dt), z.new_empty((B, NH), dtype=out_dt))
+    return z.new_empty((B, S, NH, H), dtype=out_dt), z.new_empty((2 * B * NH * H + B * NH,), dtype=out_dt)

@@ -13,14 +13,15 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from .ops import slstm_sequence_op, slstm_step_op
+from .ops import slstm_sequence_op, slstm_step_op, state_views
 
 __all__ = ["slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell"]
 
 
 def slstm_step(z, i_preact, f_preact, o_preact, c_state, n_state, m_state, eps: float = 1e-6):
     """Returns (h [B,NH,H], c [B,NH,H], n [B,NH,H], m [B,NH])."""
-    return slstm_step_op(z, i_preact, f_preact, o_preact, c_state, n_state, m_state, float(eps))
+    h, st = slstm_step_op(z, i_preact, f_preact, o_preact, c_state, n_state, m_state, float(eps))
+    return (h, *state_views(st, *z.shape))
 
 
 slstm_step_pytorch = slstm_step
@@ -29,8 +30,9 @@ slstm_step_pytorch = slstm_step
 def slstm_sequence(z, i_preact, f_preact, o_preact, state=None, eps: float = 1e-6):
     """z [B,S,NH,H], gates [B,S,NH] -> (h [B,S,NH,H], (c, n, m)); one launch for all S."""
     c0, n0, m0 = state if state is not None else (None, None, None)
-    h, c, n, m = slstm_sequence_op(z, i_preact, f_preact, o_preact, c0, n0, m0, float(eps))
-    return h, (c, n, m)
+    h, st = slstm_sequence_op(z, i_preact, f_preact, o_preact, c0, n0, m0, float(eps))
+    B, _, NH, H = z.shape
+    return h, state_views(st, B, NH, H)
 
 
 class sLSTMStepwiseKernelCell(nn.Module):
@@ -51,5 +53,5 @@ class sLSTMStepwiseKernelCell(nn.Module):
             m = torch.zeros((B, NH), dtype=z.dtype, device=z.device)
         else:
             c, n, m = state
-        h, c, n, m = slstm_step_op(z, i_preact, f_preact, o_preact, c, n, m, float(self.eps))
-        return h, (c, n, m)
+        h, st = slstm_step_op(z, i_preact, f_preact, o_preact, c, n, m, float(self.eps))
+        return h, state_views(st, B, NH, H)
