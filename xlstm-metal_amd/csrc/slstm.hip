@@ -66,10 +66,24 @@ __global__ __launch_bounds__(256) void slstm_step_kernel(const TZ* __restrict__ 
 //    the last step writes the final states.  Without an initial n, n is the
 //    same for every d of a head and h = c * og / (|n| + eps) takes one
 //    multiply per element (the scale is formed per step in the gate phase).
-// z is read twice (the second read mostly hits the Infinity Cache); every
-// step of both passes keeps z loads SEQ_PF steps ahead.
+// z is read twice: for a 16-bit z pass 1 keeps the first 64 steps of every
+// segment in LDS (128 KB for 16 waves) and pass 2 reads them from there; the
+// rest of the second read often hits the Infinity Cache.  Every step of both
+// passes keeps z loads SEQ_PF steps ahead.
 constexpr int SEQ_WAVES = 16;
-constexpr int SEQ_PF = 32;
+constexpr int SEQ_PF = 16;
+// 16-bit z of the first 64 steps of every segment is kept in LDS by pass 1
+// and read from there by pass 2 (a quarter of the second z read at cfg4)
+constexpr int SEQ_ZC = 64;
+template <typename TZ> constexpr size_t seq_zc_bytes() { return sizeof(TZ) == 2 ? (size_t)SEQ_WAVES * SEQ_ZC * 64 * 2 : 0; }
+template <typename TZ> __device__ __forceinline__ TZ zc_get(uint16_t v) {
+  if constexpr (sizeof(TZ) == 2) return __builtin_bit_cast(TZ, v);
+  else return TZ{};
+}
+template <typename TZ> __device__ __forceinline__ uint16_t zc_put(TZ v) {
+  if constexpr (sizeof(TZ) == 2) return __builtin_bit_cast(uint16_t, v);
+  else return 0;
+}
 constexpr float SEQ_LOG2E = 1.4426950408889634f;
 
 // inclusive scan of the affine maps x -> F x + N (n from 0 and prod fg)
@@ -179,6 +193,8 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
   __shared__ float s_aff[SEQ_WAVES][2];        // F, n-from-0 of each segment
   __shared__ float s_cseg[SEQ_WAVES][64];      // c from 0 at each segment's end, per lane
   __shared__ SeqGateRow s_gate[SEQ_WAVES][64]; // gate rows of the wave's current chunk
+  extern __shared__ uint16_t s_zc[];            // [SEQ_WAVES][SEQ_ZC][64] raw 16-bit z (dynamic; 16-bit z only)
+  constexpr bool ZC = sizeof(TZ) == 2;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;  // w: wave-uniform
   const int bh = blockIdx.x / ndb, db = blockIdx.x - bh * ndb;
   const int b = bh / NH, hh = bh - b * NH;
@@ -227,10 +243,14 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
     const int tlast = max(t1 - 1, 0);
     // z of step t relative to the chunk starting at step cb (byte offsets < 2^31: checked at launch)
     auto zat = [&](__amdgpu_buffer_rsrc_t r, int cb, int t) { return buf_ld<TZ, 0>(r, zlb, (t - cb) * zrowb); };
+    // the segment's first chunk is kept in LDS (pass 1 writes, pass 2 reads) when it is a whole chunk
+    const bool zc_seg = ZC && t0 + SEQ_ZC <= t1;
+    uint16_t* zcw = s_zc + (size_t)w * SEQ_ZC * 64 + lane;
     {
-      const auto zr = seq_rsrc(z + zblk + (int64_t)t0 * zrow);
+      const int tp = (PASS == 2 && zc_seg) ? t0 + SEQ_ZC : t0;  // pass 2 prefetches past the kept steps
+      const auto zr = seq_rsrc(z + zblk + (int64_t)tp * zrow);
 #pragma unroll
-      for (int j = 0; j < SEQ_PF; ++j) zq[j] = zat(zr, t0, min(t0 + j, tlast));
+      for (int j = 0; j < SEQ_PF; ++j) zq[j] = zat(zr, tp, min(tp + j, tlast));
     }
     for (int cst = t0; cst < t1; cst += 64) {
       float fg, ig, og, ma, mb, ml;
@@ -285,17 +305,29 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
           if (decltype(store_tag)::value || dok) buf_st<SEQ_NT>(from_f32_fast<TH>(hv), hr, hlb, j * hrowb);
         }
       };
-      if (cst + 64 <= t1) {
+      if (PASS == 2 && zc_seg && cst == t0) {  // kept in LDS by pass 1 (the ring holds the next chunk)
         auto chunk = [&](auto store_tag) {
 #pragma unroll
           for (int j = 0; j < 64; ++j) {
-            const float zt = to_f32(zq[j % SEQ_PF]);
-            zq[j % SEQ_PF] = zat(zr, cst, min(cst + j + SEQ_PF, tlast));
-            step(j, zt, store_tag);
+            if (j % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // LDS reads at most 8 steps ahead (registers)
+            step(j, to_f32(zc_get<TZ>(zcw[64 * j])), store_tag);
           }
         };
         if (dfull) chunk(std::true_type{});
         else chunk(std::false_type{});
+      } else if (cst + 64 <= t1) {
+        auto chunk = [&](auto store_tag, auto keep_tag) {
+#pragma unroll
+          for (int j = 0; j < 64; ++j) {
+            const TZ zraw = zq[j % SEQ_PF];
+            if (decltype(keep_tag)::value) zcw[64 * j] = zc_put(zraw);
+            zq[j % SEQ_PF] = zat(zr, cst, min(cst + j + SEQ_PF, tlast));
+            step(j, to_f32(zraw), store_tag);
+          }
+        };
+        if (PASS == 1 && zc_seg && cst == t0) chunk(std::true_type{}, std::true_type{});  // pass 1: no h stores
+        else if (dfull) chunk(std::true_type{}, std::false_type{});
+        else chunk(std::false_type{}, std::false_type{});
       } else {  // partial chunk at the segment end: no prefetch
         for (int j = 0; j < t1 - cst; ++j) step(j, to_f32(zat(zr, cst, cst + j)), std::false_type{});
       }
@@ -351,7 +383,13 @@ static int launch_seq3(const void* z, const void* i, const void* f, const void* 
   const int ndb = (H + 63) / 64;  // 64-element d blocks per head
   const int64_t blocks = total / H * ndb;
   auto kern = n ? slstm_seq_kernel<TZ, TG, TH, false> : slstm_seq_kernel<TZ, TG, TH, true>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), 0, s, (const TZ*)z, (const TG*)i,
+  const size_t zc = seq_zc_bytes<TZ>();
+  if (zc) {
+    const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)zc);
+    if (e != hipSuccess)
+      return set_error(XL_ERR_LAUNCH, "xl_slstm_seq_fwd: LDS attribute failed: %s", hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), zc, s, (const TZ*)z, (const TG*)i,
                      (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H, ndb, eps);
   return check_launch("xl_slstm_seq_fwd");
 }
