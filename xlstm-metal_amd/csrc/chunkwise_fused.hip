@@ -123,6 +123,21 @@ __device__ __forceinline__ void split8(const LoOps& lk, f32x4 a, f32x4 b, bf16x8
   lo = __builtin_bit_cast(bf16x8, l);
 }
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+// Chunk-relative global access: a raw buffer resource per 64-token chunk
+// (wave-uniform base, num_records = the chunk's valid rows) and a per-thread
+// byte offset that stays the same for every chunk.  Rows past S (a ragged last
+// chunk) read as 0 and their stores are dropped by the buffer range check, so
+// no address needs clamping.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const bf16_t* base, int rows, int row_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, rows * row_bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 x) {
+  typedef unsigned int b128 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(b128, x), r, off, 0, 0);
+}
 __device__ __forceinline__ float exp_(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
 // log(sigmoid(x)) = min(x, 0) - log(1 + exp(-|x|)) via the hardware exp2/log2 (abs. error < 1e-7)
 __device__ __forceinline__ float logsig_fast(float x) {
@@ -255,20 +270,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const bf16_t* kh = k + (size_t)bh * S * DQK;
   const bf16_t* vh = v + (size_t)bh * S * DV;
   bf16_t* hh = h + (size_t)bh * S * DV;
+  auto rows_of = [&](int kc) { return min(L, S - kc * L); };  // valid rows of chunk kc
+  auto q_rsrc = [&](int kc) { return chunk_rsrc(qh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2); };
   const float m_init = m0 ? m0[bh] : 0.f;
 
   // ---- K staging: piece u of thread tid = u*NTHREADS + tid -> row piece / (DQK/8), 16-byte column group
-  // Rows past S (a ragged last chunk) read row 0 of the chunk instead: any
-  // finite values do, since those tokens carry alpha' = 0 and gate weight
+  // (rows past S read as 0: those tokens carry alpha' = 0 and gate weight
   // exp(-inf) = 0, their S columns are causally masked for real rows, and their
-  // own rows of h are not stored.
+  // own rows of h are not stored)
   auto load_k = [&](int kc, u32x4 (&Kst)[NKU]) {
-    const bf16_t* kb = kh + (size_t)kc * L * DQK;
+    const auto r = chunk_rsrc(kh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2);
 #pragma unroll
     for (int u = 0; u < NKU; ++u) {
       const int piece = u * NTHREADS + tid;
-      const int row = piece / (DQK / 8);
-      Kst[u] = *reinterpret_cast<const u32x4*>(kb + (size_t)(kc * L + row < S ? row : 0) * DQK + 8 * (piece % (DQK / 8)));
+      Kst[u] = ld16(r, (uint32_t)((piece / (DQK / 8)) * DQK * 2 + 16 * (piece % (DQK / 8))));
     }
   };
   auto store_k = [&](const u32x4 (&Kst)[NKU]) {
@@ -401,19 +416,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // rows dw0 + 16 s + 8 hh .. +7
     u32x4 Qs[2][QKS];
     auto load_v = [&](int kc) {
-      const bf16_t* vb = vh + (size_t)kc * L * DV + v0 + vcol;
+      const auto rv = chunk_rsrc(vh + (size_t)kc * L * DV, rows_of(kc), DV * 2);
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
-        Vst[r] = *reinterpret_cast<const u32x4*>(vb + (size_t)(kc * L + vrow + 2 * r < S ? vrow + 2 * r : 0) * DV);
+      for (int r = 0; r < 2; ++r) Vst[r] = ld16(rv, (uint32_t)(((vrow + 2 * r) * DV + v0 + vcol) * 2));
     };
     auto load_qs = [&](int kc) {
-      const bf16_t* qb = qh + (size_t)kc * L * DQK + dw0 + 8 * hh;
+      const auto rq = q_rsrc(kc);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int row = kc * L + 32 * tt + l32 < S ? 32 * tt + l32 : 0;
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int s = 0; s < QKS; ++s) Qs[tt][s] = *reinterpret_cast<const u32x4*>(qb + (size_t)row * DQK + 16 * s);
-      }
+        for (int s = 0; s < QKS; ++s)
+          Qs[tt][s] = ld16(rq, (uint32_t)(((32 * tt + l32) * DQK + dw0 + 8 * hh + 16 * s) * 2));
     };
     load_k(0, Kst);
     load_v(0);
@@ -561,9 +574,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
     // 16-byte load; the K operand below uses the same contiguous k order)
     auto load_q = [&](int kc) {
-      const bf16_t* qb = qh + ((size_t)kc * L + (kc * L + 16 * o + r16 < S ? 16 * o + r16 : 0)) * DQK + 8 * g;
+      const auto rq = q_rsrc(kc);
 #pragma unroll
-      for (int p = 0; p < KPD; ++p) Qf[p] = *reinterpret_cast<const u32x4*>(qb + 32 * p);
+      for (int p = 0; p < KPD; ++p) Qf[p] = ld16(rq, (uint32_t)(((16 * o + r16) * DQK + 8 * g + 32 * p) * 2));
     };
     load_k(0, Kst);
     load_q(0);
@@ -683,8 +696,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       const float mcr = gb[192 + 16 * o + r16];
       const float den = qb * qn + Hmv[NVT][0];
       const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr)) + eps);
-      bf16_t* hb = hh + ((size_t)kc * L + 16 * o + r16) * DV + v0 + 8 * g;
-      const bool hok = kc * L + 16 * o + r16 < S;  // rows past S (ragged last chunk) are not stored
+      // rows past S (ragged last chunk) are dropped by the range check
+      const auto rh = chunk_rsrc(hh + (size_t)kc * L * DV, rows_of(kc), DV * 2);
+      const uint32_t hoff = (uint32_t)(((16 * o + r16) * DV + v0 + 8 * g) * 2);
 #pragma unroll
       for (int h2 = 0; h2 < NVT / 2; ++h2) {
         u32x4 out;
@@ -694,7 +708,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           out[2 * b] = pack_bf16((qb * Hqc[vq][0] + Hmv[vq][0]) * inv, (qb * Hqc[vq][1] + Hmv[vq][1]) * inv);
           out[2 * b + 1] = pack_bf16((qb * Hqc[vq][2] + Hmv[vq][2]) * inv, (qb * Hqc[vq][3] + Hmv[vq][3]) * inv);
         }
-        if (hok) *reinterpret_cast<u32x4*>(hb + 32 * h2) = out;
+        st16(rh, hoff + 64 * h2, out);
       }
     }
     // ---- final n (undo the deferred rescale): even + odd column, lanes r16 = 0, 1
