@@ -329,6 +329,36 @@ def bench_slstm_sequence(args, dev):
             "roofline": dict(_hbm(slstm_bytes(), t["ms"]), traffic=load_traffic(SLSTM_KERNEL, wl))}
 
 
+SLSTM_STEPS = 32  # chained sLSTM steps per timed call
+
+
+def bench_slstm_step(args, dev):
+    """sLSTM decode step at config 4's sLSTM shape (B8 NH4 H512: bf16 z and gates, float32 c, n, m
+    carried from step to step): SLSTM_STEPS chained xl_slstm_step_fwd launches per timed call (one
+    HIP-graph replay).  Bytes per step: z (bf16) + three gates (bf16) + c, n, m in and out and h
+    (float32, the states' dtype).  A step moves ~0.3 MB, so it is launch-latency bound."""
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG4_SLSTM as c
+    g = torch.Generator("cpu").manual_seed(c.seed)
+    z = torch.randn(SLSTM_STEPS, c.B, c.NH, c.H, generator=g).to(c.dtype).to(dev)
+    gates = [(torch.randn(SLSTM_STEPS, c.B, c.NH, generator=g) + off).to(c.dtype).to(dev) for off in (0.0, 3.0, 0.0)]
+    st0 = (torch.zeros(c.B, c.NH, c.H, device=dev), torch.zeros(c.B, c.NH, c.H, device=dev),
+           torch.zeros(c.B, c.NH, device=dev))
+
+    def call():
+        cs, ns, ms = st0
+        for t in range(SLSTM_STEPS):
+            _, cs, ns, ms = xlstm_hip.slstm_step(z[t], gates[0][t], gates[1][t], gates[2][t], cs, ns, ms)
+
+    t = _timed(call, dev, max(5, args.steps))
+    el = c.B * c.NH * c.H
+    by = el * 2 + 3 * c.B * c.NH * 2 + 2 * (2 * el + c.B * c.NH) * 4 + el * 4
+    us = 1e3 * t["ms"] / SLSTM_STEPS
+    return {"workload": f"cfg4 sLSTM decode step B{c.B} NH{c.NH} H{c.H} (bf16 z/gates, fp32 states), "
+                        f"{SLSTM_STEPS} chained steps per call", "us_per_step": us, "mode": t["mode"],
+            "roofline": _hbm(by, us * 1e-3)}
+
+
 def bench_mlstm_sequence(args, dev):
     """Recurrent mLSTM time loop (xl_mlstm_sequence_fwd) over 64 tokens of config 2's heads
     (B4 NH8 DQK256 DV512, bf16 q/k/v/gates) from config-1-style float32 initial states, last
@@ -543,6 +573,7 @@ def main():
         out["soft_cap"] = bench_soft_cap(args, dev)
     if not args.no_extra:
         out["slstm_sequence"] = bench_slstm_sequence(args, dev)
+        out["slstm_step"] = bench_slstm_step(args, dev)
         out["mlstm_sequence"] = bench_mlstm_sequence(args, dev)
         out["arbitrary_length"] = bench_arbitrary_length(args, dev)
     if not args.no_cpu_baseline:
