@@ -252,7 +252,7 @@ def bench_soft_cap(args, dev):
                          "traffic": load_traffic(SOFT_CAP_KERNEL, "cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16")}}
 
 
-def _timed(call, dev, steps, warmup=3):
+def _timed(call, dev, steps, warmup=10):
     """Mean / median / min HIP-event ms of `call` over `steps` runs, each after a cache flush.
     The call is replayed from a HIP graph when it can be captured (host dispatch stays out of
     the timed region), else run eagerly."""
@@ -505,7 +505,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--chunk-size", type=int, default=64)
     ap.add_argument("--algo", default="auto", choices=["auto", "fused", "two_pass"])
     ap.add_argument("--decode-steps", type=int, default=1000)
