@@ -22,8 +22,11 @@ kernel that calibrates the rocprofv3 FETCH_SIZE / WRITE_SIZE counters.
 `slstm_sequence` (config 4's sLSTM layer, one time-loop launch),
 `mlstm_sequence` (the recurrent mLSTM time loop over 64 tokens of config 2's
 heads) and `arbitrary_length` (the any-S wrapper on config 2 with S = 8255)
-measure the remaining rows of the path; each is timed like the headline
-(cache flush, HIP graph replay, HIP events) and reported against HBM.
+measure the remaining rows of the path; `slstm_conv1d_silu` and
+`slstm_group_norm` the sLSTM layer's stages either side of its time loop at
+config 4 (conv K 4 + SiLU over [8, 4096, 2048]; GroupNorm NH 4 x H 512).  Each
+is timed like the headline (cache flush, HIP graph replay, HIP events) and
+reported against HBM.
 
 HBM traffic (`roofline.traffic`) cannot be measured from inside the process:
 it comes from two rocprofv3 --pmc passes over this script (FETCH_SIZE, then
@@ -62,6 +65,10 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 PREFILL_KERNEL = "chunkwise_fused_kernel"
 SOFT_CAP_KERNEL = "soft_cap_kernel"
+CONV_KERNEL = "causal_conv1d_kernel"
+GROUP_NORM_KERNEL = "group_norm_kernel"
+CFG4_D_MODEL = 2048  # config 4's d_model: the sLSTM projection conv runs over all of it
+CFG4_CONV_K = 4
 SOFT_CAP_SHAPE = (1, 2048, 50304)  # config 3 prefill logits
 SLSTM_KERNEL = "slstm_seq_kernel"
 SEQ_KERNEL = "mlstm_recurrent_kernel"
@@ -359,6 +366,52 @@ def bench_slstm_step(args, dev):
             "roofline": _hbm(by, us * 1e-3)}
 
 
+def _cfg4_layer_stage_inputs(dev):
+    from xlstm_hip.workloads import CFG4_SLSTM as c
+    g = torch.Generator(device=dev).manual_seed(c.seed)
+    D = CFG4_D_MODEL
+    x = torch.randn(c.B, c.S, D, generator=g, device=dev).to(c.dtype)
+    w = (0.5 * torch.randn(D, 1, CFG4_CONV_K, generator=g, device=dev)).to(c.dtype)
+    b = torch.randn(D, generator=g, device=dev).to(c.dtype)
+    return c, x, w, b
+
+
+def layer_stage_work():
+    """(workload, algorithmic bytes) of the cfg4 conv + SiLU and GroupNorm launches."""
+    from xlstm_hip.workloads import CFG4_SLSTM as c
+    D, NHH = CFG4_D_MODEL, c.NH * c.H
+    conv = (f"cfg4 sLSTM conv1d K{CFG4_CONV_K} + SiLU [B{c.B}, S{c.S}, {D}] bf16",
+            2 * c.B * c.S * D * 2 + D * (CFG4_CONV_K + 1) * 2)
+    gn = (f"cfg4 sLSTM GroupNorm NH{c.NH} x H{c.H} over [{c.B * c.S}, {NHH}] bf16", 2 * c.B * c.S * NHH * 2 + 2 * NHH * 2)
+    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn}
+
+
+def bench_slstm_conv(args, dev):
+    """Config 4's sLSTM projection conv: depthwise causal conv1d (K 4) + SiLU over x [B8, S4096,
+    d_model 2048] bf16, channels last (xl_causal_conv1d_fwd).  Bytes: x read and y written once,
+    plus the taps and bias."""
+    import xlstm_hip
+    c, x, w, b = _cfg4_layer_stage_inputs(dev)
+    t = _timed(lambda: xlstm_hip.causal_conv1d(x, w, b, activation="silu"), dev, max(5, args.steps))
+    wl, by = layer_stage_work()[CONV_KERNEL]
+    return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
+            "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(CONV_KERNEL, wl))}
+
+
+def bench_group_norm(args, dev):
+    """Config 4's sLSTM output GroupNorm: one group per head (NH 4 x H 512) over the kernel output
+    viewed as [B8 * S4096, 2048] bf16, affine (xl_group_norm_fwd).  Bytes: h read and y written
+    once, plus weight and bias."""
+    import xlstm_hip
+    c, x, w, b = _cfg4_layer_stage_inputs(dev)
+    h = x.view(c.B * c.S, c.NH * c.H)
+    gw, gb = w.reshape(-1)[: c.NH * c.H].contiguous(), b.clone()
+    t = _timed(lambda: xlstm_hip.group_norm(h, c.NH, gw, gb, 1e-6), dev, max(5, args.steps))
+    wl, by = layer_stage_work()[GROUP_NORM_KERNEL]
+    return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
+            "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(GROUP_NORM_KERNEL, wl))}
+
+
 def bench_mlstm_sequence(args, dev):
     """Recurrent mLSTM time loop (xl_mlstm_sequence_fwd) over 64 tokens of config 2's heads
     (B4 NH8 DQK256 DV512, bf16 q/k/v/gates) from config-1-style float32 initial states, last
@@ -434,7 +487,8 @@ def summarize_pmc(fetch_dir, write_dir):
                         continue
                     name = row["Kernel_Name"]
                     key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel",
-                                            SLSTM_KERNEL, SEQ_KERNEL) if k in name), None)
+                                            SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL)
+                                if k in name), None)
                     if key is None:
                         continue
                     acc.setdefault(key, {}).setdefault(row["Dispatch_Id"], 0.0)
@@ -455,7 +509,8 @@ def summarize_pmc(fetch_dir, write_dir):
             "mlstm_step_kernel": ("cfg1 mlstm decode step", decode_bytes(CFG1.B, CFG1.NH, CFG1.DQK, CFG1.DV)),
             # gate prep: reads i, f (bf16), writes 258 floats of per-chunk gate scans per 64 tokens
             "gate_prep_kernel": ("cfg2 chunkwise gate prep",
-                                 2 * CFG2.B * CFG2.NH * CFG2.S * 2 + CFG2.B * CFG2.NH * (CFG2.S // 64) * 258 * 4)}
+                                 2 * CFG2.B * CFG2.NH * CFG2.S * 2 + CFG2.B * CFG2.NH * (CFG2.S // 64) * 258 * 4),
+            **layer_stage_work()}
     out = {"calibration": {"kernel": SOFT_CAP_KERNEL, "bytes_read": sc_bytes, "bytes_written": sc_bytes,
                            "fetch_scale": f_scale, "write_scale": w_scale},
            "kernels": {}}
@@ -576,6 +631,8 @@ def main():
         out["slstm_step"] = bench_slstm_step(args, dev)
         out["mlstm_sequence"] = bench_mlstm_sequence(args, dev)
         out["arbitrary_length"] = bench_arbitrary_length(args, dev)
+        out["slstm_conv1d_silu"] = bench_slstm_conv(args, dev)
+        out["slstm_group_norm"] = bench_group_norm(args, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(out), flush=True)

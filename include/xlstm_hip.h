@@ -160,6 +160,36 @@ int xl_slstm_seq_fwd(const void* z, const void* i, const void* f, const void* o,
                      int B, int S, int NH, int H, float eps, int dtype_z, int dtype_gates, int dtype_h,
                      void* stream);
 
+/*
+ * Depthwise causal conv1d over time, channels last, with an optional SiLU.
+ * Replaces CausalConv1d.forward with groups == channels (xlstm_metal/
+ * torch_native/blocks/slstm/slstm_layers/causal_conv1d/causal_conv1d.py:51-67:
+ * left pad of K - 1 zeros, then nn.Conv1d) and, with act = 1, the nn.SiLU after
+ * it in sLSTMProjectionCell.forward (.../slstm_layers/slstm_projection_cell.py:
+ * 110-115), on the [B, S, D] input that cell permutes to [B, D, S].
+ *   x, y [B,S,D]; weight [D,K] (nn.Conv1d's [D,1,K]); bias [D] or NULL; all of
+ *   one dtype.  y[b,s,c] = act(bias[c] + sum_j weight[c,j] x[b, s-K+1+j, c]),
+ *   x = 0 before s = 0 (weight[c, K-1] multiplies the current step).  With a
+ *   16-bit dtype the convolution is rounded to that dtype before the SiLU, as
+ *   the two reference modules do.  1 <= K <= 8; act 0 = none, 1 = SiLU; y must
+ *   not overlap x.
+ */
+int xl_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, void* y,
+                         int B, int S, int D, int K, int act, int dtype, void* stream);
+
+/*
+ * GroupNorm of rows of G groups of CG channels: each group normalised by its
+ * own mean and biased variance, y = (x - mean) / sqrt(var + eps) * weight[c]
+ * + bias[c].  Replaces nn.GroupNorm(num_groups=NH, num_channels=NH*H) in
+ * sLSTMOutputCell.forward (xlstm_metal/torch_native/blocks/slstm/slstm_layers/
+ * slstm_output_cell.py:72-83), applied to the kernel output h [B,S,NH,H]
+ * viewed as [B*S, NH*H].
+ *   x, y [N, G*CG]; weight, bias [G*CG] (both given or both NULL: no affine);
+ *   all of one dtype; y may alias x.
+ */
+int xl_group_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                      int64_t N, int G, int CG, float eps, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,7 +36,8 @@ def lib():
 def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("xl_abi_version", "xl_last_error", "xl_soft_cap_fwd", "xl_mlstm_step_fwd", "xl_mlstm_chunkwise_fwd",
-              "xl_mlstm_chunkwise_workspace_size", "xl_mlstm_sequence_fwd", "xl_slstm_step_fwd", "xl_slstm_seq_fwd"):
+              "xl_mlstm_chunkwise_workspace_size", "xl_mlstm_sequence_fwd", "xl_slstm_step_fwd", "xl_slstm_seq_fwd",
+              "xl_causal_conv1d_fwd", "xl_group_norm_fwd"):
         assert n in names
 
 
@@ -105,6 +106,30 @@ def test_slstm_rejects_bad_args(lib):
     assert lib.xl_slstm_seq_fwd(p, p, p, p, p, None, None, p, None, None, None, 1, 3, 4, 8, 1e-6, 0, 0, 0, None) == -1
 
 
+def test_conv1d_and_group_norm_reject_bad_args(lib):
+    conv, gn = lib.xl_causal_conv1d_fwd, lib.xl_group_norm_fwd
+    p, q = ctypes.c_void_p(256), ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    assert conv(p, p, None, q, 1, -8, 16, 4, 1, 1, None) == -1
+    assert b"negative" in lib.xl_last_error()
+    assert conv(p, p, None, q, 1, 8, 16, 9, 1, 1, None) == -2
+    assert b"kernel size" in lib.xl_last_error()
+    assert conv(p, p, None, q, 1, 8, 16, 4, 2, 1, None) == -1
+    assert conv(p, p, None, q, 1, 8, 16, 4, 1, 5, None) == -1
+    assert conv(p, None, None, q, 1, 8, 16, 4, 1, 1, None) == -1
+    assert b"null" in lib.xl_last_error()
+    assert conv(p, p, None, ctypes.c_void_p(256 + 64), 1, 8, 16, 4, 1, 1, None) == -1  # y overlaps x
+    assert b"alias" in lib.xl_last_error()
+    assert conv(None, None, None, None, 0, 8, 16, 4, 1, 1, None) == 0  # empty input is a no-op
+    assert gn(p, None, None, q, 4, 0, 16, 1e-6, 1, None) == -1
+    assert gn(p, p, None, q, 4, 2, 16, 1e-6, 1, None) == -1
+    assert b"both" in lib.xl_last_error()
+    assert gn(p, None, None, q, 4, 2, 16, -1.0, 1, None) == -1
+    assert b"eps" in lib.xl_last_error()
+    assert gn(p, None, None, q, 4, 2, 16, 1e-6, 9, None) == -1
+    assert gn(None, None, None, None, 4, 2, 16, 1e-6, 1, None) == -1
+    assert gn(None, None, None, None, 0, 2, 16, 1e-6, 1, None) == 0
+
+
 def test_ops_refuse_cpu_tensors():
     import xlstm_hip
     x = torch.randn(8)
@@ -132,7 +157,7 @@ def test_registry_names():
 def test_ops_registered_with_torch_library():
     import xlstm_hip  # noqa: F401
     for name in ("soft_cap", "mlstm_step", "mlstm_step_", "mlstm_chunkwise", "mlstm_sequence", "slstm_step",
-                 "slstm_sequence"):
+                 "slstm_sequence", "causal_conv1d", "group_norm"):
         assert hasattr(torch.ops.xlstm_hip, name)
 
 
@@ -146,3 +171,9 @@ def test_fake_tensor_shapes():
         h, c, n, m = torch.ops.xlstm_hip.mlstm_chunkwise(q, q, v, g, g, None, None, None, 0.1, 64, 1e-6, True, 0)
         assert h.shape == (2, 4, 128, 48) and h.dtype == torch.bfloat16
         assert c.shape == (2, 4, 32, 48) and n.shape == (2, 4, 32) and m.shape == (2, 4, 1)
+        x = torch.empty(2, 100, 64, dtype=torch.bfloat16, device="cuda")
+        w = torch.empty(64, 1, 4, dtype=torch.bfloat16, device="cuda")
+        y = torch.ops.xlstm_hip.causal_conv1d(x, w, None, 1)
+        assert y.shape == x.shape and y.dtype == x.dtype
+        y = torch.ops.xlstm_hip.group_norm(x.view(200, 64), 4, None, None, 1e-6)
+        assert y.shape == (200, 64)

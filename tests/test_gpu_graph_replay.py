@@ -102,3 +102,18 @@ def test_soft_cap_graph_replays(gpu_case):
     import xlstm_hip
     x = (30 * torch.randn(3, 1000, 777, generator=torch.Generator().manual_seed(5))).to(torch.bfloat16).to(dev())
     _check_replays(lambda: (xlstm_hip.soft_cap(x, 30.0),))
+
+
+def test_slstm_layer_stages_graph_replays(gpu_case):
+    import xlstm_hip
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 300, 256, generator=g).to(torch.bfloat16).to(dev())
+    w = (0.5 * torch.randn(256, 1, 4, generator=g)).to(torch.bfloat16).to(dev())
+    b = torch.randn(256, generator=g).to(torch.bfloat16).to(dev())
+    gw = torch.randn(256, generator=g).to(torch.bfloat16).to(dev())
+
+    def fn():
+        y = xlstm_hip.causal_conv1d(x, w, b, activation="silu")
+        return y, xlstm_hip.group_norm(y.view(600, 256), 4, gw, b, 1e-6)
+
+    _check_replays(fn)

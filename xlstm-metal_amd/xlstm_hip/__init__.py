@@ -2,8 +2,9 @@
 
 Drop-in for the torch-native kernel API of MLXPorts/xLSTM-metal: chunkwise
 mLSTM prefill, recurrent decode step and sequence, sLSTM step and sequence,
-and soft_cap, each a ``torch.library`` op (``xlstm_hip::*``) calling
-hand-written HIP kernels in ``lib/libxlstm_hip.so`` through a C-ABI.
+the sLSTM layer's causal conv1d + SiLU and per-head GroupNorm, and soft_cap,
+each a ``torch.library`` op (``xlstm_hip::*``) calling hand-written HIP
+kernels in ``lib/libxlstm_hip.so`` through a C-ABI.
 """
 
 from . import _lib
@@ -17,6 +18,7 @@ from .recurrent import (
     mlstm_recurrent_step__native_fw,
 )
 from .slstm import sLSTMStepwiseKernelCell, slstm_sequence, slstm_step, slstm_step_pytorch
+from .slstm_layers import CausalConv1d, causal_conv1d, group_norm, sLSTMOutputCell, sLSTMProjectionCell
 from .soft_cap import SoftCapCell, soft_cap
 
 LIB_PATH = _lib.LIB_PATH
@@ -31,6 +33,7 @@ __all__ = [
     "mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "mlstm_recurrent_step__native",
     "mlstm_recurrent_step__native_fw", "mlstm_recurrent_step_", "mlstm_recurrent_sequence__native_fw",
     "slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell", "soft_cap", "SoftCapCell",
+    "causal_conv1d", "group_norm", "CausalConv1d", "sLSTMProjectionCell", "sLSTMOutputCell",
     "get_mlstm_kernel", "get_mlstm_step_kernel", "get_mlstm_sequence_kernel", "available_kernels",
     "wrap_chunkwise__arbitrary_sequence_length", "wrap_chunkwise__pad_zeros", "mLSTMBackendConfig",
     "mLSTMBackend", "load_library", "LIB_PATH",

@@ -18,7 +18,7 @@ from . import _lib
 
 __all__ = [
     "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
-    "slstm_step_op", "slstm_sequence_op", "chunkwise_workspace_bytes",
+    "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "chunkwise_workspace_bytes",
 ]
 
 _EMPTY_SHAPE = (0,)
@@ -319,3 +319,61 @@ def _(z, i, f, o, c0, n0, m0, eps):
     B, S, NH, H = z.shape
     out_dt = torch.promote_types(z.dtype, i.dtype) if c0 is None else _slstm_out_dtype(z, i, c0)
     return z.new_empty((B, S, NH, H), dtype=out_dt), z.new_empty((2 * B * NH * H + B * NH,), dtype=out_dt)
+
+
+# ------------------------------------------- sLSTM layer: causal conv1d + SiLU, GroupNorm
+CONV_ACTS = {None: 0, "silu": 1}
+
+
+@torch.library.custom_op("xlstm_hip::causal_conv1d", mutates_args=())
+def causal_conv1d_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], act: int) -> Tensor:
+    what = "causal_conv1d"
+    _lib.require_gpu(x, weight, bias, what=what)
+    _check(x.dim() == 3, what, f"x must be (B, S, D) channels last, got {tuple(x.shape)}")
+    B, S, D = x.shape
+    _check(weight.dim() in (2, 3) and weight.shape[0] == D and (weight.dim() == 2 or weight.shape[1] == 1), what,
+           f"weight must be (D, K) or (D, 1, K) with D = {D}, got {tuple(weight.shape)}")
+    _check(bias is None or tuple(bias.shape) == (D,), what, f"bias must be ({D},)")
+    _check(weight.dtype == x.dtype and (bias is None or bias.dtype == x.dtype), what,
+           "x, weight and bias must share a dtype (as nn.Conv1d requires)")
+    _check(act in (0, 1), what, f"act must be 0 (none) or 1 (SiLU), got {act}")
+    K = weight.shape[-1]
+    x, w = _prep(x), _prep(weight)
+    b = None if bias is None else _prep(bias)
+    y = torch.empty_like(x)
+    rc = _lib.load().xl_causal_conv1d_fwd(x.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), B, S, D, K,
+                                          int(act), _lib.dtype_code(x, what), _lib.stream_of(x))
+    _lib.check(rc, what)
+    return y
+
+
+@causal_conv1d_op.register_fake
+def _(x, weight, bias, act):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+@torch.library.custom_op("xlstm_hip::group_norm", mutates_args=())
+def group_norm_op(x: Tensor, num_groups: int, weight: Optional[Tensor], bias: Optional[Tensor],
+                  eps: float) -> Tensor:
+    what = "group_norm"
+    _lib.require_gpu(x, weight, bias, what=what)
+    _check(x.dim() == 2, what, f"x must be (N, C), got {tuple(x.shape)}")
+    N, C = x.shape
+    _check(num_groups >= 1 and C % num_groups == 0, what, f"C = {C} is not a multiple of num_groups = {num_groups}")
+    _check((weight is None) == (bias is None), what, "weight and bias must both be given or both be None")
+    if weight is not None:
+        _check(tuple(weight.shape) == (C,) and tuple(bias.shape) == (C,), what, f"weight and bias must be ({C},)")
+        _check(weight.dtype == x.dtype and bias.dtype == x.dtype, what, "x, weight and bias must share a dtype")
+    x = _prep(x)
+    w = None if weight is None else _prep(weight)
+    b = None if bias is None else _prep(bias)
+    y = torch.empty_like(x)
+    rc = _lib.load().xl_group_norm_fwd(x.data_ptr(), _lib.ptr(w), _lib.ptr(b), y.data_ptr(), N, int(num_groups),
+                                       C // num_groups, float(eps), _lib.dtype_code(x, what), _lib.stream_of(x))
+    _lib.check(rc, what)
+    return y
+
+
+@group_norm_op.register_fake
+def _(x, num_groups, weight, bias, eps):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
