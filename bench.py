@@ -259,17 +259,23 @@ def bench_soft_cap(args, dev):
                          "traffic": load_traffic(SOFT_CAP_KERNEL, "cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16")}}
 
 
-def _timed(call, dev, steps, warmup=10):
+def _timed(call, dev, steps, warmup=10, graph=True):
     """Mean / median / min HIP-event ms of `call` over `steps` runs, each after a cache flush.
-    The call is replayed from a HIP graph when it can be captured (host dispatch stays out of
-    the timed region), else run eagerly."""
+    graph=True: the call is replayed from a HIP graph when it can be captured (host dispatch of
+    several launches stays out of the timed region), else run eagerly.  graph=False (calls of one
+    kernel launch, at most followed by a small cast): the call runs eagerly; its host-side dispatch overlaps the ~0.1 ms
+    flush queued before it, and the events then bracket the kernel alone (a graph replay adds
+    ~12 us of its own between the events on this runtime, measured against rocprofv3's kernel
+    durations)."""
     flush = Flusher(dev)
     stream = torch.cuda.current_stream(dev)
     for _ in range(warmup):
         call()
     torch.cuda.synchronize(dev)
-    mode = "hip_graph"
+    mode = "hip_graph" if graph else "eager"
     try:
+        if not graph:
+            raise _Eager()
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
@@ -282,6 +288,8 @@ def _timed(call, dev, steps, warmup=10):
         graph.replay()
         torch.cuda.synchronize(dev)
         run = graph.replay
+    except _Eager:
+        run = call
     except Exception as exc:  # measurement method only; the kernels are the same
         mode, run = f"eager ({type(exc).__name__})", call
     times = []
@@ -295,6 +303,10 @@ def _timed(call, dev, steps, warmup=10):
         torch.cuda.synchronize(dev)
         times.append(e0.elapsed_time(e1))
     return {"ms": statistics.mean(times), "ms_median": statistics.median(times), "ms_min": min(times), "mode": mode}
+
+
+class _Eager(Exception):
+    """Selects eager timing in _timed."""
 
 
 def _hbm(by, ms):
@@ -329,7 +341,7 @@ def bench_slstm_sequence(args, dev):
     import xlstm_hip
     from xlstm_hip.workloads import CFG4_SLSTM as c, slstm_inputs
     z, i, f, o = slstm_inputs(c, device=dev)
-    t = _timed(lambda: xlstm_hip.slstm_sequence(z, i, f, o), dev, max(5, args.steps))
+    t = _timed(lambda: xlstm_hip.slstm_sequence(z, i, f, o), dev, max(5, args.steps), graph=False)
     wl = _workloads()[0]
     return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"],
             "tokens_per_s": c.B * c.S / (t["ms"] * 1e-3), "mode": t["mode"],
@@ -392,7 +404,7 @@ def bench_slstm_conv(args, dev):
     plus the taps and bias."""
     import xlstm_hip
     c, x, w, b = _cfg4_layer_stage_inputs(dev)
-    t = _timed(lambda: xlstm_hip.causal_conv1d(x, w, b, activation="silu"), dev, max(5, args.steps))
+    t = _timed(lambda: xlstm_hip.causal_conv1d(x, w, b, activation="silu"), dev, max(5, args.steps), graph=False)
     wl, by = layer_stage_work()[CONV_KERNEL]
     return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
             "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(CONV_KERNEL, wl))}
@@ -406,7 +418,7 @@ def bench_group_norm(args, dev):
     c, x, w, b = _cfg4_layer_stage_inputs(dev)
     h = x.view(c.B * c.S, c.NH * c.H)
     gw, gb = w.reshape(-1)[: c.NH * c.H].contiguous(), b.clone()
-    t = _timed(lambda: xlstm_hip.group_norm(h, c.NH, gw, gb, 1e-6), dev, max(5, args.steps))
+    t = _timed(lambda: xlstm_hip.group_norm(h, c.NH, gw, gb, 1e-6), dev, max(5, args.steps), graph=False)
     wl, by = layer_stage_work()[GROUP_NORM_KERNEL]
     return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
             "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(GROUP_NORM_KERNEL, wl))}
@@ -425,7 +437,7 @@ def bench_mlstm_sequence(args, dev):
     n = torch.randn(cfg.B, cfg.NH, cfg.DQK, generator=g).abs().to(dev)
     m = torch.randn(cfg.B, cfg.NH, 1, generator=g).to(dev)
     t = _timed(lambda: xlstm_hip.mlstm_recurrent_sequence__native_fw(q, k, v, i, f, C, n, m, return_last_states=True),
-               dev, max(5, args.steps))
+               dev, max(5, args.steps), graph=False)
     wl = _workloads()[1]
     return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "us_per_token": 1e3 * t["ms"] / S,
             "mode": t["mode"],
