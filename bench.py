@@ -24,7 +24,9 @@ kernel that calibrates the rocprofv3 FETCH_SIZE / WRITE_SIZE counters.
 heads) and `arbitrary_length` (the any-S wrapper on config 2 with S = 8255)
 measure the remaining rows of the path; `slstm_conv1d_silu` and
 `slstm_group_norm` the sLSTM layer's stages either side of its time loop at
-config 4 (conv K 4 + SiLU over [8, 4096, 2048]; GroupNorm NH 4 x H 512).  Each
+config 4 (conv K 4 + SiLU over [8, 4096, 2048]; GroupNorm NH 4 x H 512), and
+`mlstm_output_gate` the mLSTM output cell's RMSNorm x sigmoid(o) on config 2's
+kernel output.  Each
 is timed like the headline (cache flush, HIP graph replay, HIP events) and
 reported against HBM.
 
@@ -67,6 +69,7 @@ PREFILL_KERNEL = "chunkwise_fused_kernel"
 SOFT_CAP_KERNEL = "soft_cap_kernel"
 CONV_KERNEL = "causal_conv1d_kernel"
 GROUP_NORM_KERNEL = "group_norm_kernel"
+RMS_GATE_KERNEL = "mh_rmsnorm_gate_kernel"
 CFG4_D_MODEL = 2048  # config 4's d_model: the sLSTM projection conv runs over all of it
 CFG4_CONV_K = 4
 SOFT_CAP_SHAPE = (1, 2048, 50304)  # config 3 prefill logits
@@ -395,7 +398,11 @@ def layer_stage_work():
     conv = (f"cfg4 sLSTM conv1d K{CFG4_CONV_K} + SiLU [B{c.B}, S{c.S}, {D}] bf16",
             2 * c.B * c.S * D * 2 + D * (CFG4_CONV_K + 1) * 2)
     gn = (f"cfg4 sLSTM GroupNorm NH{c.NH} x H{c.H} over [{c.B * c.S}, {NHH}] bf16", 2 * c.B * c.S * NHH * 2 + 2 * NHH * 2)
-    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn}
+    from xlstm_hip.workloads import CFG2 as c2
+    nel = c2.B * c2.NH * c2.S * c2.DV
+    rms = (f"cfg2 mLSTM output norm x sigmoid(o) [B{c2.B}, NH{c2.NH}, S{c2.S}, DH{c2.DV}] bf16",
+           3 * nel * 2 + c2.NH * c2.DV * 2)
+    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn, RMS_GATE_KERNEL: rms}
 
 
 def bench_slstm_conv(args, dev):
@@ -422,6 +429,23 @@ def bench_group_norm(args, dev):
     wl, by = layer_stage_work()[GROUP_NORM_KERNEL]
     return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
             "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(GROUP_NORM_KERNEL, wl))}
+
+
+def bench_mlstm_output_gate(args, dev):
+    """The mLSTM output cell's stage after the chunkwise kernel on config 2's output: per-head
+    RMSNorm of h [B4, NH8, S8192, DH512] (read in the kernel's layout), the weight and sigmoid of
+    the gate pre-activation [B4, S8192, 4096], written as [B4, S8192, 4096] bf16
+    (xl_mh_rmsnorm_gate_fwd).  Bytes: h and o read once, y written once, plus the weight."""
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG2 as c
+    g = torch.Generator(device=dev).manual_seed(c.seed)
+    h = torch.randn(c.B, c.NH, c.S, c.DV, generator=g, device=dev).to(c.dtype)
+    w = torch.randn(c.NH * c.DV, generator=g, device=dev).to(c.dtype)
+    o = torch.randn(c.B, c.S, c.NH * c.DV, generator=g, device=dev).to(c.dtype)
+    t = _timed(lambda: xlstm_hip.mh_rmsnorm_gate(h, w, o, 1e-6), dev, max(5, args.steps), graph=False)
+    wl, by = layer_stage_work()[RMS_GATE_KERNEL]
+    return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
+            "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(RMS_GATE_KERNEL, wl))}
 
 
 def bench_mlstm_sequence(args, dev):
@@ -499,7 +523,8 @@ def summarize_pmc(fetch_dir, write_dir):
                         continue
                     name = row["Kernel_Name"]
                     key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel",
-                                            SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL)
+                                            SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL,
+                                            RMS_GATE_KERNEL)
                                 if k in name), None)
                     if key is None:
                         continue
@@ -645,6 +670,7 @@ def main():
         out["arbitrary_length"] = bench_arbitrary_length(args, dev)
         out["slstm_conv1d_silu"] = bench_slstm_conv(args, dev)
         out["slstm_group_norm"] = bench_group_norm(args, dev)
+        out["mlstm_output_gate"] = bench_mlstm_output_gate(args, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(out), flush=True)

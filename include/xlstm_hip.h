@@ -190,6 +190,26 @@ int xl_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, vo
 int xl_group_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
                       int64_t N, int G, int CG, float eps, int dtype, void* stream);
 
+/*
+ * The mLSTM output cell's stage before its output projection, fused: per-head
+ * RMS normalisation of the kernel output h, the per-channel weight and the
+ * output gate sigma(o).  Replaces MultiHeadRMSNorm.forward (xlstm_metal/
+ * torch_native/blocks/mlstm/multihead_norm/multihead_norm.py:56-64) and the
+ * permute, sigmoid and product around it in mLSTMOutputCell.forward
+ * (.../mlstm/mlstm_chunkwise/mlstm_output_cell.py:84-93).
+ *   h: [B,NH,S,DH] (h_layout 1, the chunkwise output) or [B,S,NH,DH]
+ *   (h_layout 0); weight [NH*DH] or NULL; o_preact [B,S,NH*DH] (the gate
+ *   projection before the sigmoid) or NULL (no gate: the norm alone);
+ *   y [B,S,NH*DH]; all of one dtype.
+ *   y = (h / sqrt(mean_DH(h^2) + eps)) * weight * sigmoid(o), with the
+ *   reference's roundings to a 16-bit dtype after the division, the weight
+ *   product and the sigmoid.  DH <= 8192 (16-bit) or 4096 (float32) when DH is
+ *   a multiple of 16 bytes, else DH <= 1024; y must not overlap h or o_preact.
+ */
+int xl_mh_rmsnorm_gate_fwd(const void* h, const void* weight, const void* o_preact, void* y,
+                           int B, int NH, int S, int DH, int h_layout, float eps, int dtype,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,7 +37,7 @@ def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("xl_abi_version", "xl_last_error", "xl_soft_cap_fwd", "xl_mlstm_step_fwd", "xl_mlstm_chunkwise_fwd",
               "xl_mlstm_chunkwise_workspace_size", "xl_mlstm_sequence_fwd", "xl_slstm_step_fwd", "xl_slstm_seq_fwd",
-              "xl_causal_conv1d_fwd", "xl_group_norm_fwd"):
+              "xl_causal_conv1d_fwd", "xl_group_norm_fwd", "xl_mh_rmsnorm_gate_fwd"):
         assert n in names
 
 
@@ -128,6 +128,15 @@ def test_conv1d_and_group_norm_reject_bad_args(lib):
     assert gn(p, None, None, q, 4, 2, 16, 1e-6, 9, None) == -1
     assert gn(None, None, None, None, 4, 2, 16, 1e-6, 1, None) == -1
     assert gn(None, None, None, None, 0, 2, 16, 1e-6, 1, None) == 0
+    rn = lib.xl_mh_rmsnorm_gate_fwd
+    assert rn(p, None, None, q, 1, -2, 4, 64, 1, 1e-6, 1, None) == -1
+    assert rn(p, None, None, q, 1, 2, 4, 64, 2, 1e-6, 1, None) == -1
+    assert b"h_layout" in lib.xl_last_error()
+    assert rn(p, None, None, q, 1, 2, 4, 64, 1, -1.0, 1, None) == -1
+    assert rn(p, None, None, ctypes.c_void_p(256 + 128), 1, 2, 4, 64, 1, 1e-6, 1, None) == -1
+    assert b"alias" in lib.xl_last_error()
+    assert rn(p, None, None, q, 1, 2, 4, 16384, 1, 1e-6, 1, None) == -2  # 32 vectors per lane
+    assert rn(None, None, None, None, 0, 2, 4, 64, 1, 1e-6, 1, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -157,7 +166,7 @@ def test_registry_names():
 def test_ops_registered_with_torch_library():
     import xlstm_hip  # noqa: F401
     for name in ("soft_cap", "mlstm_step", "mlstm_step_", "mlstm_chunkwise", "mlstm_sequence", "slstm_step",
-                 "slstm_sequence", "causal_conv1d", "group_norm"):
+                 "slstm_sequence", "causal_conv1d", "group_norm", "mh_rmsnorm_gate"):
         assert hasattr(torch.ops.xlstm_hip, name)
 
 

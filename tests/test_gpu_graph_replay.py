@@ -117,3 +117,12 @@ def test_slstm_layer_stages_graph_replays(gpu_case):
         return y, xlstm_hip.group_norm(y.view(600, 256), 4, gw, b, 1e-6)
 
     _check_replays(fn)
+
+
+def test_mh_rmsnorm_gate_graph_replays(gpu_case):
+    import xlstm_hip
+    g = torch.Generator().manual_seed(8)
+    h = torch.randn(2, 4, 100, 512, generator=g).to(torch.bfloat16).to(dev())
+    w = torch.randn(2048, generator=g).to(torch.bfloat16).to(dev())
+    o = torch.randn(2, 100, 2048, generator=g).to(torch.bfloat16).to(dev())
+    _check_replays(lambda: (xlstm_hip.mh_rmsnorm_gate(h, w, o, 1e-6),))

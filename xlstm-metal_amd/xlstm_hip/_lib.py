@@ -36,6 +36,7 @@ SIGNATURES = {
     "xl_slstm_seq_fwd": (_i, [_vp] * 4 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 4 + [_f] + [_i] * 3 + [_vp]),
     "xl_causal_conv1d_fwd": (_i, [_vp] * 4 + [_i] * 6 + [_vp]),
     "xl_group_norm_fwd": (_i, [_vp] * 4 + [_i64, _i, _i, _f, _i, _vp]),
+    "xl_mh_rmsnorm_gate_fwd": (_i, [_vp] * 4 + [_i] * 5 + [_f, _i, _vp]),
 }
 
 ABI_VERSION = 1

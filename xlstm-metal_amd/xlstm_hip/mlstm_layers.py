@@ -1,0 +1,81 @@
+"""The mLSTM output cell's stage after the chunkwise kernel, on HIP.
+
+Drop-ins (paths relative to the reference root, ``TNM`` =
+``xlstm_metal/torch_native/blocks/mlstm``):
+
+* ``MultiHeadRMSNorm`` (``TNM/multihead_norm/multihead_norm.py:43-64``): per-head
+  RMS normalisation of [B, S, NH, DH], flattened to [B, S, NH * DH], optional
+  per-channel weight.
+* ``mLSTMOutputCell`` (``TNM/mlstm_chunkwise/mlstm_output_cell.py:22-99``): the
+  permute of the kernel output, the norm, sigmoid(ogate_proj(x)) and the gate
+  product are one kernel (``mh_rmsnorm_gate_kernel``) reading h in the chunkwise
+  layout [B, NH, S, DH]; the two projections stay ``nn.Linear``.  The reference's
+  ``x_norm.view(B, S, -1)`` raises on the permuted (non-contiguous) tensor; the
+  kernel writes the flattening that ``reshape`` would give.
+
+State-dict keys match the reference modules.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from .ops import mh_rmsnorm_gate_op
+
+__all__ = ["mh_rmsnorm_gate", "MultiHeadRMSNorm", "mLSTMOutputCell"]
+
+
+def mh_rmsnorm_gate(h: Tensor, weight: Optional[Tensor] = None, o_preact: Optional[Tensor] = None,
+                    eps: float = 1e-6, heads_first: bool = True) -> Tensor:
+    """(h / rms(h over DH)) * weight * sigmoid(o_preact) as [B, S, NH * DH].
+
+    h is [B, NH, S, DH] (``heads_first``, the chunkwise output) or [B, S, NH, DH]; weight
+    [NH * DH] or None; o_preact [B, S, NH * DH] (the gate projection before its sigmoid) or None.
+    """
+    return mh_rmsnorm_gate_op(h, weight, o_preact, bool(heads_first), float(eps))
+
+
+class MultiHeadRMSNorm(nn.Module):
+    """``multihead_norm.py:43-64``: x [B, S, NH, DH] -> [B, S, NH * DH]."""
+
+    def __init__(self, num_heads: int, head_dim: int, eps: float = 1e-6, use_weight: bool = True) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.eps = eps
+        if use_weight:
+            self.weight = nn.Parameter(torch.ones(num_heads * head_dim))
+        else:
+            self.register_parameter("weight", None)
+
+    def forward(self, x: Tensor) -> Tensor:
+        B, S, NH, DH = x.shape
+        if NH != self.num_heads or DH != self.head_dim:
+            raise ValueError(f"Expected shape [B,S,{self.num_heads},{self.head_dim}], got {x.shape}")
+        return mh_rmsnorm_gate(x, self.weight, None, self.eps, heads_first=False)
+
+
+class mLSTMOutputCell(nn.Module):
+    """``mlstm_output_cell.py:22-99``: norm(h) * sigmoid(ogate_proj(x_orig)), then out_proj."""
+
+    def __init__(self, input_size: int, num_heads: int, v_dim_per_head: int, use_bias: bool = False,
+                 eps: float = 1e-6) -> None:
+        super().__init__()
+        self.input_size = input_size
+        self.num_heads = num_heads
+        self.v_dim_per_head = v_dim_per_head
+        v_dim = num_heads * v_dim_per_head
+        self.norm = MultiHeadRMSNorm(num_heads=num_heads, head_dim=v_dim_per_head, eps=eps)
+        self.ogate_proj = nn.Linear(input_size, v_dim, bias=use_bias)
+        self.out_proj = nn.Linear(v_dim, input_size, bias=use_bias)
+
+    def gated(self, h: Tensor, x_orig: Tensor) -> Tensor:
+        """h [B, NH, S, DH_v] (the kernel output), x_orig [B, S, input_size] -> [B, S, NH * DH_v]."""
+        return mh_rmsnorm_gate(h, self.norm.weight, self.ogate_proj(x_orig), self.norm.eps, heads_first=True)
+
+    def forward(self, h: Tensor, x_orig: Tensor) -> Tensor:
+        return self.out_proj(self.gated(h, x_orig))

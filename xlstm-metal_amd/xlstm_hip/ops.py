@@ -18,7 +18,8 @@ from . import _lib
 
 __all__ = [
     "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
-    "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "chunkwise_workspace_bytes",
+    "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "mh_rmsnorm_gate_op",
+    "chunkwise_workspace_bytes",
 ]
 
 _EMPTY_SHAPE = (0,)
@@ -377,3 +378,39 @@ def group_norm_op(x: Tensor, num_groups: int, weight: Optional[Tensor], bias: Op
 @group_norm_op.register_fake
 def _(x, num_groups, weight, bias, eps):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+# ------------------------------------------- mLSTM output cell: multi-head RMSNorm x sigmoid(o)
+@torch.library.custom_op("xlstm_hip::mh_rmsnorm_gate", mutates_args=())
+def mh_rmsnorm_gate_op(h: Tensor, weight: Optional[Tensor], o_preact: Optional[Tensor], heads_first: bool,
+                       eps: float) -> Tensor:
+    what = "mh_rmsnorm_gate"
+    _lib.require_gpu(h, weight, o_preact, what=what)
+    _check(h.dim() == 4, what, f"h must be 4-D, got {tuple(h.shape)}")
+    if heads_first:
+        B, NH, S, DH = h.shape
+    else:
+        B, S, NH, DH = h.shape
+    _check(weight is None or tuple(weight.shape) == (NH * DH,), what, f"weight must be ({NH * DH},)")
+    _check(o_preact is None or tuple(o_preact.shape) in ((B, S, NH * DH), (B, S, NH, DH)), what,
+           f"o_preact must be (B, S, NH*DH) = {(B, S, NH * DH)}")
+    for name, t in (("weight", weight), ("o_preact", o_preact)):
+        _check(t is None or t.dtype == h.dtype, what, f"{name} must have h's dtype {h.dtype}")
+    h = _prep(h)
+    w = None if weight is None else _prep(weight)
+    o = None if o_preact is None else _prep(o_preact)
+    y = torch.empty((B, S, NH * DH), dtype=h.dtype, device=h.device)
+    rc = _lib.load().xl_mh_rmsnorm_gate_fwd(h.data_ptr(), _lib.ptr(w), _lib.ptr(o), y.data_ptr(), B, NH, S, DH,
+                                            1 if heads_first else 0, float(eps), _lib.dtype_code(h, what),
+                                            _lib.stream_of(h))
+    _lib.check(rc, what)
+    return y
+
+
+@mh_rmsnorm_gate_op.register_fake
+def _(h, weight, o_preact, heads_first, eps):
+    if heads_first:
+        B, NH, S, DH = h.shape
+    else:
+        B, S, NH, DH = h.shape
+    return h.new_empty((B, S, NH * DH))
