@@ -184,8 +184,10 @@ int xl_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, vo
  * sLSTMOutputCell.forward (xlstm_metal/torch_native/blocks/slstm/slstm_layers/
  * slstm_output_cell.py:72-83), applied to the kernel output h [B,S,NH,H]
  * viewed as [B*S, NH*H].
- *   x, y [N, G*CG]; weight, bias [G*CG] (both given or both NULL: no affine);
- *   all of one dtype; y may alias x.
+ *   x, y [N, G*CG]; weight, bias [G*CG], each optional (NULL: 1 / 0); all of
+ *   one dtype; y may alias x.  With the weight alone it is also the
+ *   MultiHeadLayerNorm of xlstm_metal/torch_native/blocks/mlstm/multihead_norm/
+ *   multihead_norm.py:27-40 on x [B,S,NH,DH] viewed as [B*S, NH*DH].
  */
 int xl_group_norm_fwd(const void* x, const void* weight, const void* bias, void* y,
                       int64_t N, int G, int CG, float eps, int dtype, void* stream);

@@ -121,8 +121,8 @@ def test_conv1d_and_group_norm_reject_bad_args(lib):
     assert b"alias" in lib.xl_last_error()
     assert conv(None, None, None, None, 0, 8, 16, 4, 1, 1, None) == 0  # empty input is a no-op
     assert gn(p, None, None, q, 4, 0, 16, 1e-6, 1, None) == -1
-    assert gn(p, p, None, q, 4, 2, 16, 1e-6, 1, None) == -1
-    assert b"both" in lib.xl_last_error()
+    assert gn(p, p, None, q, 4, 2, -16, 1e-6, 1, None) == -1
+    assert b"bad size" in lib.xl_last_error()
     assert gn(p, None, None, q, 4, 2, 16, -1.0, 1, None) == -1
     assert b"eps" in lib.xl_last_error()
     assert gn(p, None, None, q, 4, 2, 16, 1e-6, 9, None) == -1

@@ -89,3 +89,24 @@ def test_rejections(gpu_case):
     x = torch.randn(1, 2, 4, 64, device=dev())
     rc = lib.xl_mh_rmsnorm_gate_fwd(x.data_ptr(), None, None, x.data_ptr(), 1, 2, 4, 64, 1, 1e-6, 0, None)
     assert rc == -1 and b"alias" in lib.xl_last_error()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("use_bias", [False, True])
+def test_multihead_layernorm(gpu_case, dtype, use_bias):
+    """MultiHeadLayerNorm (per-head LayerNorm, weight and optional bias) on the GroupNorm kernel."""
+    import xlstm_hip
+    from oracle import slstm_layers as osl
+    torch.manual_seed(6)
+    B, S, NH, DH = 2, 40, 4, 128
+    m = xlstm_hip.MultiHeadLayerNorm(NH, DH, use_bias=use_bias)
+    with torch.no_grad():
+        m.weight.normal_()
+        if use_bias:
+            m.bias.normal_()
+    m = m.to(dtype)
+    x = (2 * torch.randn(B, S, NH, DH) + 1).to(dtype)
+    want = osl.group_norm(x.reshape(B * S, NH * DH), NH, m.weight, m.bias, 1e-6).reshape(B, S, NH * DH)
+    y = m.to(dev())(x.to(dev()))
+    assert y.shape == (B, S, NH * DH)
+    assert_parity(y.cpu(), torch.from_numpy(want), dtype, f"MultiHeadLayerNorm {dtype} bias={use_bias}")

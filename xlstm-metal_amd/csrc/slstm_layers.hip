@@ -241,12 +241,13 @@ __global__ __launch_bounds__(GN_BLOCK) void group_norm_kernel(const T* x, const 
   const float inv_n = 1.0f / (float)CG;
 
   // rows are G * CG wide, so group `team` starts at team * CG.  The affine
-  // parameters are loaded without a branch (a load under a branch makes the
-  // compiler wait for every earlier load at the join): without them, the same
-  // offsets of x (c < G * CG <= N * G * CG) are read and the values dropped.
-  const bool aff = w != nullptr;
-  const T* wsrc = aff ? w : x;
-  const T* bsrc = aff ? bias : x;
+  // parameters (each optional) are loaded without a branch (a load under a
+  // branch makes the compiler wait for every earlier load at the join): a
+  // missing one reads the same offsets of x (c < G * CG <= N * G * CG) and the
+  // values are dropped.
+  const bool has_w = w != nullptr, has_b = bias != nullptr;
+  const T* wsrc = has_w ? w : x;
+  const T* bsrc = has_b ? bias : x;
   auto affine = [&](const Row<T, VW>& in, int64_t team, int v, float mean, float rstd) {
     float o[VW];
     const int c = (int)(team % G) * CG + v * VW;
@@ -254,7 +255,7 @@ __global__ __launch_bounds__(GN_BLOCK) void group_norm_kernel(const T* x, const 
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
       const float xn = (to_f32(in.e[j]) - mean) * rstd;
-      o[j] = aff ? fmaf(xn, to_f32(wr.e[j]), to_f32(br.e[j])) : xn;
+      o[j] = fmaf(xn, has_w ? to_f32(wr.e[j]) : 1.0f, has_b ? to_f32(br.e[j]) : 0.0f);
     }
     return pack_row<T, VW>(o);
   };
@@ -427,7 +428,6 @@ extern "C" int xl_group_norm_fwd(const void* x, const void* weight, const void* 
     return set_error(XL_ERR_INVALID_ARG, "xl_group_norm_fwd: bad size (N=%lld G=%d CG=%d)", (long long)N, G, CG);
   if (!dtype_ok(dtype)) return set_error(XL_ERR_INVALID_ARG, "xl_group_norm_fwd: unknown dtype %d", dtype);
   if (!(eps >= 0.0f) || eps == INFINITY) return set_error(XL_ERR_INVALID_ARG, "xl_group_norm_fwd: eps must be finite and >= 0");
-  if (!weight != !bias) return set_error(XL_ERR_INVALID_ARG, "xl_group_norm_fwd: weight and bias must both be given or both NULL");
   if (N == 0) return XL_OK;
   if (!x || !y) return set_error(XL_ERR_INVALID_ARG, "xl_group_norm_fwd: null pointer");
   hipStream_t st = (hipStream_t)stream;

@@ -3,6 +3,8 @@
 Drop-ins (paths relative to the reference root, ``TNM`` =
 ``xlstm_metal/torch_native/blocks/mlstm``):
 
+* ``MultiHeadLayerNorm`` (``TNM/multihead_norm/multihead_norm.py:5-40``): per-head
+  LayerNorm, on the GroupNorm kernel with one group per head.
 * ``MultiHeadRMSNorm`` (``TNM/multihead_norm/multihead_norm.py:43-64``): per-head
   RMS normalisation of [B, S, NH, DH], flattened to [B, S, NH * DH], optional
   per-channel weight.
@@ -26,7 +28,9 @@ from torch import Tensor
 
 from .ops import mh_rmsnorm_gate_op
 
-__all__ = ["mh_rmsnorm_gate", "MultiHeadRMSNorm", "mLSTMOutputCell"]
+from .slstm_layers import group_norm
+
+__all__ = ["mh_rmsnorm_gate", "MultiHeadRMSNorm", "MultiHeadLayerNorm", "mLSTMOutputCell"]
 
 
 def mh_rmsnorm_gate(h: Tensor, weight: Optional[Tensor] = None, o_preact: Optional[Tensor] = None,
@@ -57,6 +61,36 @@ class MultiHeadRMSNorm(nn.Module):
         if NH != self.num_heads or DH != self.head_dim:
             raise ValueError(f"Expected shape [B,S,{self.num_heads},{self.head_dim}], got {x.shape}")
         return mh_rmsnorm_gate(x, self.weight, None, self.eps, heads_first=False)
+
+
+class MultiHeadLayerNorm(nn.Module):
+    """``multihead_norm.py:5-40``: per-head LayerNorm of x [B, S, NH, DH] -> [B, S, NH * DH], optional
+    weight and bias.  Runs ``group_norm_kernel`` (one group per head) on the [B * S, NH * DH] view,
+    with float32 statistics and one rounding of the output; the reference takes the mean and
+    variance in x's own dtype."""
+
+    def __init__(self, num_heads: int, head_dim: int, eps: float = 1e-6, use_weight: bool = True,
+                 use_bias: bool = False) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.eps = eps
+        self.use_weight = use_weight
+        self.use_bias = use_bias
+        if use_weight:
+            self.weight = nn.Parameter(torch.ones(num_heads * head_dim))
+        else:
+            self.register_parameter("weight", None)
+        if use_bias:
+            self.bias = nn.Parameter(torch.zeros(num_heads * head_dim))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: Tensor) -> Tensor:
+        B, S, NH, DH = x.shape
+        if NH != self.num_heads or DH != self.head_dim:
+            raise ValueError(f"Expected shape [B,S,{self.num_heads},{self.head_dim}], got {x.shape}")
+        return group_norm(x.reshape(B * S, NH * DH), NH, self.weight, self.bias, self.eps).view(B, S, NH * DH)
 
 
 class mLSTMOutputCell(nn.Module):

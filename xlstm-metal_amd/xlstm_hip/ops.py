@@ -361,10 +361,10 @@ def group_norm_op(x: Tensor, num_groups: int, weight: Optional[Tensor], bias: Op
     _check(x.dim() == 2, what, f"x must be (N, C), got {tuple(x.shape)}")
     N, C = x.shape
     _check(num_groups >= 1 and C % num_groups == 0, what, f"C = {C} is not a multiple of num_groups = {num_groups}")
-    _check((weight is None) == (bias is None), what, "weight and bias must both be given or both be None")
-    if weight is not None:
-        _check(tuple(weight.shape) == (C,) and tuple(bias.shape) == (C,), what, f"weight and bias must be ({C},)")
-        _check(weight.dtype == x.dtype and bias.dtype == x.dtype, what, "x, weight and bias must share a dtype")
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None:
+            _check(tuple(t.shape) == (C,), what, f"{name} must be ({C},)")
+            _check(t.dtype == x.dtype, what, f"{name} must have x's dtype {x.dtype}")
     x = _prep(x)
     w = None if weight is None else _prep(weight)
     b = None if bias is None else _prep(bias)
