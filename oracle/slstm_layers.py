@@ -75,10 +75,10 @@ def causal_conv1d(x, weight, bias=None, activation=None, dtype=None):
 
 
 def group_norm(x, num_groups, weight=None, bias=None, eps=1e-5):
-    """x [N, C] with C = num_groups * CG; weight, bias [C] or None (each optional: the
-    MultiHeadLayerNorm of ``xlstm_metal/torch_native/blocks/mlstm/multihead_norm/multihead_norm.py:27-40``
-    has a weight
-    and no bias by default).  Returns float64 [N, C]."""
+    """x [N, C] with C = num_groups * CG; weight, bias [C] or None, each optional (the
+    MultiHeadLayerNorm of
+    ``xlstm_metal/torch_native/blocks/mlstm/multihead_norm/multihead_norm.py:27-40`` has a
+    weight and no bias by default).  Returns float64 [N, C]."""
     xv = _np64(x)
     N, C = xv.shape
     G = int(num_groups)
