@@ -30,6 +30,10 @@ How each function is pinned (tests/test_oracle_*.py):
   the gate known-answer values of ``tests/test_mlx_torch_numerical_parity.py``
   and the committed float64 fixtures under ``tests/golden``.
 * ``mlstm_parallel_fw``: equals the brute-force closed form.
+* ``mlstm_recurrent_kernel_cell``: equals ``mlstm_recurrent_sequence`` in
+  float64 (the cell and ``native_sequence.py`` are the same recurrence; the
+  cell's softplus-form log-sigmoid agrees with ``F.logsigmoid`` there), with and
+  without a carried state.
 * ``arbitrary_length``: equals the plain sequence loop for every S.
 """
 
@@ -43,6 +47,7 @@ __all__ = [
     "parallel_fw_H",
     "mlstm_chunkwise_fw",
     "mlstm_chunkwise",
+    "mlstm_recurrent_kernel_cell",
     "mlstm_recurrent_step",
     "mlstm_recurrent_sequence",
     "mlstm_parallel_fw",
@@ -236,6 +241,44 @@ def mlstm_recurrent_sequence(q, k, v, i, f, c_initial=None, n_initial=None, m_in
         hs.append(h)
     H = torch.stack(hs, dim=-2)
     return (H, (C, n, m)) if return_last_states else H
+
+
+def mlstm_recurrent_kernel_cell(q, k, v, i, f, state=None, eps=1e-6):
+    """``mLSTMRecurrentKernelCell.forward`` (``xlstm_metal/torch_native/blocks/mlstm/mlstm_chunkwise/
+    mlstm_recurrent_kernel_cell.py:53-161``) with its default float32 compute and state dtypes.
+
+    q, k [B, NH, S, DHQK], v [B, NH, S, DHV], i, f [B, NH, S]; state (C, n, m [B, NH]) or None
+    (zeros, ``:99-102``).  Per step: ``f_log = -log(1 + exp(-f))`` (``:129``, the softplus form,
+    not ``F.logsigmoid``), ``m' = max(f_log + m, i)``, ``fg = exp(f_log + m - m')``, ``ig = exp(i -
+    m')`` (``:130-134``), ``C' = fg C + ig k v^T``, ``n' = fg n + ig k`` (``:138-146``), ``q_s = q
+    rsqrt(DHQK)`` (``:152``), ``h = sum(C' q_s) / (max(|n' . q_s|, exp(-m')) + eps)``
+    (``:155-163``).  Returns (h [B, NH, S, DHV], (C, n, m [B, NH])).
+    """
+    B, NH, S, DHQK = q.shape
+    DHV = v.shape[-1]
+    dt = q.dtype
+    if state is None:
+        C = torch.zeros((B, NH, DHQK, DHV), dtype=dt)
+        n = torch.zeros((B, NH, DHQK), dtype=dt)
+        m = torch.zeros((B, NH), dtype=dt)
+    else:
+        C, n, m = (t.to(dt) for t in state)
+    hs = []
+    for t in range(S):
+        q_t, k_t, v_t, i_t, f_t = q[:, :, t], k[:, :, t], v[:, :, t], i[:, :, t], f[:, :, t]
+        f_log = -torch.log(1.0 + torch.exp(-f_t))
+        m_new = torch.maximum(f_log + m, i_t)
+        fg = torch.exp(f_log + m - m_new)
+        ig = torch.exp(i_t - m_new)
+        C = fg[:, :, None, None] * C + ig[:, :, None, None] * (k_t[:, :, :, None] * v_t[:, :, None, :])
+        n = fg[:, :, None] * n + ig[:, :, None] * k_t
+        m = m_new
+        q_s = q_t * DHQK ** -0.5
+        h_num = (C * q_s[:, :, :, None]).sum(dim=2)
+        qn = (n * q_s).sum(dim=2, keepdim=True)
+        h_den = torch.maximum(qn.abs(), torch.exp(-m)[:, :, None]) + eps
+        hs.append(h_num / h_den)
+    return torch.stack(hs, dim=2), (C, n, m)
 
 
 def mlstm_parallel_fw(matQ, matK, matV, vecI, vecF, eps=1e-6):

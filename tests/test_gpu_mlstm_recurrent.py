@@ -166,3 +166,29 @@ def test_sequence_kernel_heads_and_strong_gates(gpu_case, DQK, DV, S):
     hr, (Cr, nr, mr) = om.mlstm_recurrent_sequence(q, k, v, i, f, C0, n0, m0, return_last_states=True)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got, want, torch.float32, f"DQK={DQK} DV={DV} S={S} {name}")
+
+
+@pytest.mark.parametrize("S,with_state", [(1, True), (1, False), (7, True), (70, False)])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+def test_recurrent_kernel_cell(gpu_case, S, with_state, in_dtype):
+    """mLSTMRecurrentKernelCell (the model-level decode caller, float32 compute and states by
+    default): one token with a state runs the step kernel, the rest the sequence kernel; both
+    against the cell's own restatement (mlstm_recurrent_kernel_cell.py:53-161) on the inputs cast
+    to float32, as the cell casts them."""
+    import xlstm_hip
+    B, NH, DQK, DV = 2, 4, 256, 512
+    g = torch.Generator().manual_seed(S + 100 * with_state)
+    q, k = (torch.randn(B, NH, S, DQK, generator=g).to(in_dtype) for _ in range(2))
+    v = torch.randn(B, NH, S, DV, generator=g).to(in_dtype)
+    i = (15 * torch.tanh(torch.randn(B, NH, S, generator=g) / 15)).to(in_dtype)
+    f = (15 * torch.tanh((torch.randn(B, NH, S, generator=g) + 3) / 15)).to(in_dtype)
+    state = None
+    if with_state:
+        state = (0.1 * torch.randn(B, NH, DQK, DV, generator=g), torch.randn(B, NH, DQK, generator=g).abs(),
+                 torch.randn(B, NH, generator=g))
+    cell = xlstm_hip.mLSTMRecurrentKernelCell(NH, DQK, DV)
+    h, (C, n, m) = cell(*_to((q, k, v, i, f)), None if state is None else tuple(_to(state)))
+    hr, (Cr, nr, mr) = om.mlstm_recurrent_kernel_cell(*(t.float() for t in (q, k, v, i, f)), state)
+    assert h.shape == (B, NH, S, DV) and h.dtype == torch.float32 and m.shape == (B, NH)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert relerr(got, want) <= FP32_REL, f"S={S} state={with_state} {in_dtype} {name}"

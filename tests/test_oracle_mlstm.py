@@ -183,3 +183,25 @@ def test_golden_fixture_small():
         np.testing.assert_allclose(C.numpy(), z[f"{name}_C"], rtol=1e-9, atol=1e-11)
         np.testing.assert_allclose(n.numpy(), z[f"{name}_n"], rtol=1e-9, atol=1e-11)
         np.testing.assert_allclose(m.numpy(), z[f"{name}_m"], rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+def test_recurrent_kernel_cell_equals_sequence(with_state):
+    """mLSTMRecurrentKernelCell (mlstm_recurrent_kernel_cell.py:53-161) and native_sequence.py are the
+    same recurrence: the two restatements agree in float64 (m carried as [B, NH] vs [B, NH, 1])."""
+    g = torch.Generator().manual_seed(17)
+    B, NH, S, DQK, DV = 2, 3, 11, 16, 8
+    dt = torch.float64
+    q, k = (torch.randn(B, NH, S, DQK, generator=g, dtype=dt) for _ in range(2))
+    v = torch.randn(B, NH, S, DV, generator=g, dtype=dt)
+    i = 3 * torch.randn(B, NH, S, generator=g, dtype=dt)
+    f = 3 * torch.randn(B, NH, S, generator=g, dtype=dt) + 1
+    state = None
+    if with_state:
+        state = (0.3 * torch.randn(B, NH, DQK, DV, generator=g, dtype=dt),
+                 torch.randn(B, NH, DQK, generator=g, dtype=dt).abs(), torch.randn(B, NH, generator=g, dtype=dt))
+    h, (C, n, m) = om.mlstm_recurrent_kernel_cell(q, k, v, i, f, state)
+    init = (None, None, None) if state is None else (state[0], state[1], state[2][:, :, None])
+    hr, (Cr, nr, mr) = om.mlstm_recurrent_sequence(q, k, v, i, f, *init, return_last_states=True, dtype_state=dt)
+    for a, b in ((h, hr), (C, Cr), (n, nr), (m, mr[:, :, 0])):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)

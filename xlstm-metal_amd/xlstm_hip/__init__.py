@@ -16,8 +16,8 @@ from .backend import (
 from .chunkwise import mlstm_chunkwise, mlstm_chunkwise__native_autograd
 from .mlstm_layers import MultiHeadLayerNorm, MultiHeadRMSNorm, mLSTMOutputCell, mh_rmsnorm_gate
 from .recurrent import (
-    mlstm_recurrent_sequence__native_fw, mlstm_recurrent_step_, mlstm_recurrent_step__native,
-    mlstm_recurrent_step__native_fw,
+    mLSTMRecurrentKernelCell, mlstm_recurrent_sequence__native_fw, mlstm_recurrent_step_,
+    mlstm_recurrent_step__native, mlstm_recurrent_step__native_fw,
 )
 from .slstm import sLSTMStepwiseKernelCell, slstm_sequence, slstm_step, slstm_step_pytorch
 from .slstm_layers import CausalConv1d, causal_conv1d, group_norm, sLSTMOutputCell, sLSTMProjectionCell
@@ -34,6 +34,7 @@ def load_library():
 __all__ = [
     "mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "mlstm_recurrent_step__native",
     "mlstm_recurrent_step__native_fw", "mlstm_recurrent_step_", "mlstm_recurrent_sequence__native_fw",
+    "mLSTMRecurrentKernelCell",
     "slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell", "soft_cap", "SoftCapCell",
     "causal_conv1d", "group_norm", "CausalConv1d", "sLSTMProjectionCell", "sLSTMOutputCell",
     "mh_rmsnorm_gate", "MultiHeadRMSNorm", "MultiHeadLayerNorm", "mLSTMOutputCell",

@@ -4,16 +4,25 @@ Drop-in for ``mlstm_recurrent_step__native`` / ``mlstm_recurrent_step__native_fw
 (kernel_development/xlstm/mlstm_block/mlstm_recurrent/recurrent/native_step.py:
 8-133) and ``mlstm_recurrent_sequence__native_fw`` (.../native_sequence.py:
 131-170).  States are float32 (``dtype_state`` other than float32 raises).
+
+``mLSTMRecurrentKernelCell`` is the model-level decode caller
+(xlstm_metal/torch_native/blocks/mlstm/mlstm_chunkwise/
+mlstm_recurrent_kernel_cell.py:19-161): one token with a carried state runs the
+decode-step kernel, longer inputs (or no state) the sequence kernel.
 """
 
 from __future__ import annotations
 
+from typing import Optional, Tuple
+
 import torch
+import torch.nn as nn
+from torch import Tensor
 
 from .ops import mlstm_sequence_op, mlstm_step_inplace_op, mlstm_step_op
 
 __all__ = ["mlstm_recurrent_step__native", "mlstm_recurrent_step__native_fw", "mlstm_recurrent_step_",
-           "mlstm_recurrent_sequence__native_fw"]
+           "mlstm_recurrent_sequence__native_fw", "mLSTMRecurrentKernelCell"]
 
 
 def _state_dtype(dtype_state):
@@ -50,3 +59,44 @@ def mlstm_recurrent_sequence__native_fw(q, k, v, i, f, c_initial=None, n_initial
     if return_last_states:
         return h, (C, n, m)
     return h
+
+
+class mLSTMRecurrentKernelCell(nn.Module):
+    """``mlstm_recurrent_kernel_cell.py:19-161``: q, k [B, NH, S, DHQK], v [B, NH, S, DHV], gates
+    [B, NH, S], state (C, n, m [B, NH]) or None -> (h [B, NH, S, DHV], (C, n, m)).
+
+    Inputs are cast to ``compute_dtype`` as the reference does (``:87-91``); h comes back in it.
+    The kernels carry the state in float32 from step to step and cast it to ``state_dtype`` once at
+    the end (the reference rounds it to ``state_dtype`` every step), and use the stable
+    log-sigmoid where the reference's ``-log(1 + exp(-f))`` (``:129``) overflows (f < -88 in
+    float32).
+    """
+
+    def __init__(self, num_heads: int, qk_dim_per_head: int, v_dim_per_head: int, eps: float = 1e-6,
+                 compute_dtype: torch.dtype = torch.float32, state_dtype: torch.dtype = torch.float32) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.qk_dim_per_head = qk_dim_per_head
+        self.v_dim_per_head = v_dim_per_head
+        self.eps = eps
+        self.compute_dtype = compute_dtype
+        self.state_dtype = state_dtype
+
+    def forward(self, q: Tensor, k: Tensor, v: Tensor, i_preact: Tensor, f_preact: Tensor,
+                state: Optional[Tuple[Tensor, Tensor, Tensor]] = None) -> Tuple[Tensor, Tuple[Tensor, Tensor, Tensor]]:
+        B, NH, S, _ = q.shape
+        cd = self.compute_dtype
+        q, k, v, i, f = (t.to(dtype=cd) for t in (q, k, v, i_preact, f_preact))
+        if state is not None:
+            C0, n0, m0 = state
+            C0, n0, m0 = C0.to(torch.float32), n0.to(torch.float32), m0.to(torch.float32).reshape(B, NH, 1)
+        if S == 1 and state is not None:  # one decode step: the HBM-bound step kernel
+            h, (C, n, m) = mlstm_recurrent_step__native_fw(C0, n0, m0, q[:, :, 0], k[:, :, 0], v[:, :, 0],
+                                                           i[:, :, :1], f[:, :, :1], eps=self.eps)
+            h = h[:, :, None]
+        else:
+            init = (None, None, None) if state is None else (C0, n0, m0)
+            h, (C, n, m) = mlstm_recurrent_sequence__native_fw(q, k, v, i, f, *init, return_last_states=True,
+                                                               eps=self.eps)
+        sd = self.state_dtype
+        return h, (C.to(sd), n.to(sd), m.reshape(B, NH).to(sd))
