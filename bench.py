@@ -26,7 +26,8 @@ measure the remaining rows of the path; `slstm_conv1d_silu` and
 `slstm_group_norm` the sLSTM layer's stages either side of its time loop at
 config 4 (conv K 4 + SiLU over [8, 4096, 2048]; GroupNorm NH 4 x H 512), and
 `mlstm_output_gate` the mLSTM output cell's RMSNorm x sigmoid(o) on config 2's
-kernel output.  Each
+kernel output, `slstm_gate_proj` config 4's i/f gate projection with its
+soft-cap (beside the reference's Linear + soft-cap composition on the GPU).  Each
 is timed like the headline (cache flush, HIP graph replay, HIP events) and
 reported against HBM.
 
@@ -70,6 +71,7 @@ SOFT_CAP_KERNEL = "soft_cap_kernel"
 CONV_KERNEL = "causal_conv1d_kernel"
 GROUP_NORM_KERNEL = "group_norm_kernel"
 RMS_GATE_KERNEL = "mh_rmsnorm_gate_kernel"
+GATE_PROJ_KERNEL = "gate_proj_kernel"
 CFG4_D_MODEL = 2048  # config 4's d_model: the sLSTM projection conv runs over all of it
 CFG4_CONV_K = 4
 SOFT_CAP_SHAPE = (1, 2048, 50304)  # config 3 prefill logits
@@ -402,7 +404,9 @@ def layer_stage_work():
     nel = c2.B * c2.NH * c2.S * c2.DV
     rms = (f"cfg2 mLSTM output norm x sigmoid(o) [B{c2.B}, NH{c2.NH}, S{c2.S}, DH{c2.DV}] bf16",
            3 * nel * 2 + c2.NH * c2.DV * 2)
-    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn, RMS_GATE_KERNEL: rms}
+    gp = (f"cfg4 sLSTM i/f gate projection + soft-cap 15 [{c.B * c.S}, {D}] x [{2 * c.NH}, {D}] bf16",
+          c.B * c.S * D * 2 + 2 * c.NH * D * 2 + c.B * c.S * 2 * c.NH * 2)
+    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn, RMS_GATE_KERNEL: rms, GATE_PROJ_KERNEL: gp}
 
 
 def bench_slstm_conv(args, dev):
@@ -446,6 +450,28 @@ def bench_mlstm_output_gate(args, dev):
     wl, by = layer_stage_work()[RMS_GATE_KERNEL]
     return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
             "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(RMS_GATE_KERNEL, wl))}
+
+
+def bench_gate_proj(args, dev):
+    """Config 4's sLSTM i and f gates: x_conv [B8 * S4096, 2048] bf16 times the stacked gate weights
+    [8, 2048] plus bias, soft-capped at 15 (xl_gate_proj_softcap_fwd).  Bytes: x read once, the
+    weights, the [32768, 8] output.  The reference's composition on the same GPU (two nn.Linear
+    calls and two soft-caps, torch + hipBLASLt) is timed beside it."""
+    import torch.nn.functional as F
+    import xlstm_hip
+    c, x, _, _ = _cfg4_layer_stage_inputs(dev)
+    x2 = x.view(c.B * c.S, CFG4_D_MODEL)
+    g = torch.Generator(device=dev).manual_seed(c.seed + 1)
+    w = (0.05 * torch.randn(2 * c.NH, CFG4_D_MODEL, generator=g, device=dev)).to(c.dtype)
+    b = torch.randn(2 * c.NH, generator=g, device=dev).to(c.dtype)
+    t = _timed(lambda: xlstm_hip.gate_proj_softcap(x2, w, b, 15.0), dev, max(5, args.steps), graph=False)
+    wi, wf, bi, bf = w[:c.NH], w[c.NH:], b[:c.NH], b[c.NH:]
+    tr = _timed(lambda: (xlstm_hip.soft_cap(F.linear(x2, wi, bi), 15.0), xlstm_hip.soft_cap(F.linear(x2, wf, bf), 15.0)),
+                dev, max(5, args.steps))
+    wl, by = layer_stage_work()[GATE_PROJ_KERNEL]
+    return {"workload": wl, "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
+            "reference_composition_us": 1e3 * tr["ms"],
+            "roofline": dict(_hbm(by, t["ms"]), traffic=load_traffic(GATE_PROJ_KERNEL, wl))}
 
 
 def bench_mlstm_sequence(args, dev):
@@ -524,7 +550,7 @@ def summarize_pmc(fetch_dir, write_dir):
                     name = row["Kernel_Name"]
                     key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel",
                                             SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL,
-                                            RMS_GATE_KERNEL)
+                                            RMS_GATE_KERNEL, GATE_PROJ_KERNEL)
                                 if k in name), None)
                     if key is None:
                         continue
@@ -671,6 +697,7 @@ def main():
         out["slstm_conv1d_silu"] = bench_slstm_conv(args, dev)
         out["slstm_group_norm"] = bench_group_norm(args, dev)
         out["mlstm_output_gate"] = bench_mlstm_output_gate(args, dev)
+        out["slstm_gate_proj"] = bench_gate_proj(args, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(out), flush=True)

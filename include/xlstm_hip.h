@@ -212,6 +212,22 @@ int xl_mh_rmsnorm_gate_fwd(const void* h, const void* weight, const void* o_prea
                            int B, int NH, int S, int DH, int h_layout, float eps, int dtype,
                            void* stream);
 
+/*
+ * Gate projection with the soft-cap epilogue: y[m, n] = cap * tanh(z / cap),
+ * z = (b[n] + sum_d x[m, d] w[n, d]) rounded to the dtype (the Linear's output),
+ * for the gate pre-activations of the projection cells.  Replaces
+ * soft_cap(igate_proj(x)), soft_cap(fgate_proj(x)) in mLSTMProjectionCell.
+ * forward (xlstm_metal/torch_native/blocks/mlstm/mlstm_chunkwise/
+ * mlstm_projection_cell.py:97-103) and the i, f (on the conv output) and o
+ * gates of sLSTMProjectionCell.forward (.../slstm/slstm_layers/
+ * slstm_projection_cell.py:118-121), with the gates' weights stacked.
+ *   x [M, D], w [G, D] (nn.Linear's weight), bias [G] or NULL, y [M, G]; bf16
+ *   or f16 (float32: XL_ERR_UNSUPPORTED); G <= 64; D a multiple of 8; x and
+ *   w 16-byte aligned; cap <= 0: no soft-cap.
+ */
+int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias, void* y,
+                             int M, int D, int G, float cap, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

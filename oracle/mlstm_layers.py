@@ -17,6 +17,13 @@ Reference (paths relative to the MLXPorts/xLSTM-metal root, ``TNM`` =
   The reference's ``view`` of the permuted tensor raises; the oracle flattens
   as ``reshape`` would.
 
+* ``gate_proj_softcap``: the gate projections of the projection cells with
+  their soft-cap, ``soft_cap(igate_proj(x))`` etc.
+  (``TNM/mlstm_chunkwise/mlstm_projection_cell.py:97-103``,
+  ``xlstm_metal/torch_native/blocks/slstm/slstm_layers/slstm_projection_cell.py:
+  118-121``): x w^T + b rounded to the module dtype (the Linear's output),
+  then cap * tanh(z / cap).
+
 Pinned (tests/test_oracle_mlstm_layers.py) against torch's CPU
 ``F.rms_norm`` in float64, the closed forms of a constant head (x / rms =
 sign(x) for eps = 0) and of the output's root mean square, ``math.exp`` for the
@@ -28,7 +35,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-__all__ = ["mh_rmsnorm_gate"]
+__all__ = ["mh_rmsnorm_gate", "gate_proj_softcap"]
 
 
 def _np64(t):
@@ -62,3 +69,15 @@ def mh_rmsnorm_gate(h, weight=None, o_preact=None, eps=1e-6, heads_first=True, d
         o = _np64(o_preact).reshape(B, S, NH * DH)
         y = y * _round_to(1.0 / (1.0 + np.exp(-o)), dtype)  # mlstm_output_cell.py:90-93
     return y
+
+
+def gate_proj_softcap(x, weight, bias=None, cap=15.0, dtype=None):
+    """x [..., D], weight [G, D], bias [G] or None.  Returns float64 [..., G] before the final
+    rounding: the Linear's output rounded to ``dtype`` (x's by default), then the soft-cap."""
+    if dtype is None and isinstance(x, torch.Tensor):
+        dtype = x.dtype
+    z = _np64(x) @ _np64(weight).T
+    if bias is not None:
+        z = z + _np64(bias)
+    z = _round_to(z, dtype)
+    return cap * np.tanh(z / cap) if cap > 0 else z

@@ -37,7 +37,7 @@ def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("xl_abi_version", "xl_last_error", "xl_soft_cap_fwd", "xl_mlstm_step_fwd", "xl_mlstm_chunkwise_fwd",
               "xl_mlstm_chunkwise_workspace_size", "xl_mlstm_sequence_fwd", "xl_slstm_step_fwd", "xl_slstm_seq_fwd",
-              "xl_causal_conv1d_fwd", "xl_group_norm_fwd", "xl_mh_rmsnorm_gate_fwd"):
+              "xl_causal_conv1d_fwd", "xl_group_norm_fwd", "xl_mh_rmsnorm_gate_fwd", "xl_gate_proj_softcap_fwd"):
         assert n in names
 
 
@@ -137,6 +137,14 @@ def test_conv1d_and_group_norm_reject_bad_args(lib):
     assert b"alias" in lib.xl_last_error()
     assert rn(p, None, None, q, 1, 2, 4, 16384, 1, 1e-6, 1, None) == -2  # 32 vectors per lane
     assert rn(None, None, None, None, 0, 2, 4, 64, 1, 1e-6, 1, None) == 0
+    gp = lib.xl_gate_proj_softcap_fwd
+    assert gp(p, p, None, q, 4, 64, 8, 15.0, 0, None) == -2  # float32
+    assert gp(p, p, None, q, 4, 64, 65, 15.0, 1, None) == -2
+    assert gp(p, p, None, q, 4, 12, 8, 15.0, 1, None) == -2
+    assert gp(p, p, None, q, -4, 64, 8, 15.0, 1, None) == -1
+    assert gp(ctypes.c_void_p(264), p, None, q, 4, 64, 8, 15.0, 1, None) == -1  # misaligned x
+    assert b"aligned" in lib.xl_last_error()
+    assert gp(None, None, None, None, 0, 64, 8, 15.0, 1, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -166,7 +174,7 @@ def test_registry_names():
 def test_ops_registered_with_torch_library():
     import xlstm_hip  # noqa: F401
     for name in ("soft_cap", "mlstm_step", "mlstm_step_", "mlstm_chunkwise", "mlstm_sequence", "slstm_step",
-                 "slstm_sequence", "causal_conv1d", "group_norm", "mh_rmsnorm_gate"):
+                 "slstm_sequence", "causal_conv1d", "group_norm", "mh_rmsnorm_gate", "gate_proj_softcap"):
         assert hasattr(torch.ops.xlstm_hip, name)
 
 

@@ -126,3 +126,12 @@ def test_mh_rmsnorm_gate_graph_replays(gpu_case):
     w = torch.randn(2048, generator=g).to(torch.bfloat16).to(dev())
     o = torch.randn(2, 100, 2048, generator=g).to(torch.bfloat16).to(dev())
     _check_replays(lambda: (xlstm_hip.mh_rmsnorm_gate(h, w, o, 1e-6),))
+
+
+def test_gate_proj_graph_replays(gpu_case):
+    import xlstm_hip
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(300, 2048, generator=g).to(torch.bfloat16).to(dev())
+    w = (0.1 * torch.randn(8, 2048, generator=g)).to(torch.bfloat16).to(dev())
+    b = torch.randn(8, generator=g).to(torch.bfloat16).to(dev())
+    _check_replays(lambda: (xlstm_hip.gate_proj_softcap(x, w, b, 15.0),))

@@ -68,3 +68,29 @@ def test_bf16_roundings_match_torch_promotion():
     ref = ref.double()
     ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
     assert bool(((got - ref).abs() <= ulp).all())
+
+
+def test_gate_proj_matches_torch_linear_and_tanh():
+    """float64: the oracle is torch's F.linear followed by the soft-cap closed form with math.tanh."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(3, 5, 40, generator=g, dtype=torch.float64)
+    w = torch.randn(6, 40, generator=g, dtype=torch.float64)
+    b = torch.randn(6, generator=g, dtype=torch.float64)
+    lin = F.linear(x, w, b).numpy()
+    got = oml.gate_proj_softcap(x, w, b, 15.0)
+    for idx in np.ndindex(got.shape):
+        assert math.isclose(got[idx], 15.0 * math.tanh(lin[idx] / 15.0), rel_tol=1e-12, abs_tol=1e-15)
+    np.testing.assert_allclose(oml.gate_proj_softcap(x, w, None, 0.0), F.linear(x, w).numpy(), rtol=1e-12)
+
+
+def test_gate_proj_bf16_linear_rounding_matches_torch():
+    """The Linear's output is rounded to bf16 before the soft-cap, as torch's bf16 F.linear returns it
+    (within one bf16 ulp of torch, whose summation order differs)."""
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(64, 256, generator=g).to(torch.bfloat16)
+    w = (0.3 * torch.randn(8, 256, generator=g)).to(torch.bfloat16)
+    b = torch.randn(8, generator=g).to(torch.bfloat16)
+    lin = F.linear(x, w, b).double()
+    got = torch.from_numpy(oml.gate_proj_softcap(x, w, b, 0.0))
+    ulp = torch.exp2(torch.floor(torch.log2(lin.abs().clamp_min(1e-30))) - 7)
+    assert bool(((got - lin).abs() <= ulp).all())

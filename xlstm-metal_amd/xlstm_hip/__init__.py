@@ -14,7 +14,9 @@ from .backend import (
     mLSTMBackendConfig, wrap_chunkwise__arbitrary_sequence_length, wrap_chunkwise__pad_zeros,
 )
 from .chunkwise import mlstm_chunkwise, mlstm_chunkwise__native_autograd
-from .mlstm_layers import MultiHeadLayerNorm, MultiHeadRMSNorm, mLSTMOutputCell, mh_rmsnorm_gate
+from .mlstm_layers import (
+    MultiHeadLayerNorm, MultiHeadRMSNorm, gate_proj_softcap, mh_rmsnorm_gate, mLSTMOutputCell, mLSTMProjectionCell,
+)
 from .recurrent import (
     mLSTMRecurrentKernelCell, mlstm_recurrent_sequence__native_fw, mlstm_recurrent_step_,
     mlstm_recurrent_step__native, mlstm_recurrent_step__native_fw,
@@ -37,7 +39,8 @@ __all__ = [
     "mLSTMRecurrentKernelCell",
     "slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell", "soft_cap", "SoftCapCell",
     "causal_conv1d", "group_norm", "CausalConv1d", "sLSTMProjectionCell", "sLSTMOutputCell",
-    "mh_rmsnorm_gate", "MultiHeadRMSNorm", "MultiHeadLayerNorm", "mLSTMOutputCell",
+    "mh_rmsnorm_gate", "MultiHeadRMSNorm", "MultiHeadLayerNorm", "mLSTMOutputCell", "gate_proj_softcap",
+    "mLSTMProjectionCell",
     "get_mlstm_kernel", "get_mlstm_step_kernel", "get_mlstm_sequence_kernel", "available_kernels",
     "wrap_chunkwise__arbitrary_sequence_length", "wrap_chunkwise__pad_zeros", "mLSTMBackendConfig",
     "mLSTMBackend", "load_library", "LIB_PATH",

@@ -15,6 +15,10 @@ Drop-ins (paths relative to the reference root, ``TNM`` =
   ``x_norm.view(B, S, -1)`` raises on the permuted (non-contiguous) tensor; the
   kernel writes the flattening that ``reshape`` would give.
 
+* ``mLSTMProjectionCell`` (``TNM/mlstm_chunkwise/mlstm_projection_cell.py:18-106``): the
+  q, k, v projections stay ``nn.Linear``; the two gate projections and their soft-cap are one
+  kernel (``gate_proj_kernel``) over the stacked gate weights.
+
 State-dict keys match the reference modules.
 """
 
@@ -24,13 +28,39 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 from torch import Tensor
 
-from .ops import mh_rmsnorm_gate_op
+from .ops import gate_proj_softcap_op, mh_rmsnorm_gate_op
+from .soft_cap import soft_cap
 
-from .slstm_layers import group_norm
+__all__ = ["mh_rmsnorm_gate", "gate_proj_softcap", "stacked_linears", "MultiHeadRMSNorm", "MultiHeadLayerNorm",
+           "mLSTMProjectionCell", "mLSTMOutputCell"]
 
-__all__ = ["mh_rmsnorm_gate", "MultiHeadRMSNorm", "MultiHeadLayerNorm", "mLSTMOutputCell"]
+
+def gate_proj_softcap(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None,
+                      cap: Optional[float] = None) -> Tensor:
+    """``cap * tanh(F.linear(x, weight, bias) / cap)`` for a few gate outputs (weight [G, D], G <= 64).
+
+    bf16 / f16: one kernel reading x once (the Linear's output rounded to x's dtype before the
+    soft-cap, as the reference's two modules do); float32: ``F.linear`` then the soft-cap kernel.
+    ``cap`` None or <= 0: no soft-cap.
+    """
+    c = 0.0 if cap is None else float(cap)
+    if x.dtype == torch.float32:
+        y = F.linear(x, weight, bias)
+        return soft_cap(y, c) if c > 0 else y
+    return gate_proj_softcap_op(x, weight, bias, c)
+
+
+def stacked_linears(*linears: nn.Linear):
+    """(weight, bias) of several Linear layers over the same input, stacked row-wise (a missing bias
+    is zeros; None when none has one)."""
+    w = torch.cat([lin.weight for lin in linears])
+    if all(lin.bias is None for lin in linears):
+        return w, None
+    b = torch.cat([lin.bias if lin.bias is not None else lin.weight.new_zeros(lin.out_features) for lin in linears])
+    return w, b
 
 
 def mh_rmsnorm_gate(h: Tensor, weight: Optional[Tensor] = None, o_preact: Optional[Tensor] = None,
@@ -63,6 +93,35 @@ class MultiHeadRMSNorm(nn.Module):
         return mh_rmsnorm_gate(x, self.weight, None, self.eps, heads_first=False)
 
 
+class mLSTMProjectionCell(nn.Module):
+    """``mlstm_projection_cell.py:18-106``: q, k, v [B, NH, S, DH] (permuted views) and the soft-capped
+    gate pre-activations i, f [B, NH, S] (permuted views) of x [B, S, input_size]."""
+
+    def __init__(self, input_size: int, num_heads: int, qk_dim_per_head: int, v_dim_per_head: int,
+                 use_bias: bool = False, gate_soft_cap: Optional[float] = None) -> None:
+        super().__init__()
+        self.input_size = input_size
+        self.num_heads = num_heads
+        self.qk_dim_per_head = qk_dim_per_head
+        self.v_dim_per_head = v_dim_per_head
+        self.gate_soft_cap = gate_soft_cap
+        qk_dim, v_dim = num_heads * qk_dim_per_head, num_heads * v_dim_per_head
+        self.q_proj = nn.Linear(input_size, qk_dim, bias=use_bias)
+        self.k_proj = nn.Linear(input_size, qk_dim, bias=use_bias)
+        self.v_proj = nn.Linear(input_size, v_dim, bias=use_bias)
+        self.igate_proj = nn.Linear(input_size, num_heads)
+        self.fgate_proj = nn.Linear(input_size, num_heads)
+
+    def forward(self, x: Tensor):
+        B, S, _ = x.shape
+        NH = self.num_heads
+        q = self.q_proj(x).view(B, S, NH, self.qk_dim_per_head).permute(0, 2, 1, 3)
+        k = self.k_proj(x).view(B, S, NH, self.qk_dim_per_head).permute(0, 2, 1, 3)
+        v = self.v_proj(x).view(B, S, NH, self.v_dim_per_head).permute(0, 2, 1, 3)
+        g = gate_proj_softcap(x, *stacked_linears(self.igate_proj, self.fgate_proj), self.gate_soft_cap)
+        return q, k, v, g[..., :NH].permute(0, 2, 1), g[..., NH:].permute(0, 2, 1)
+
+
 class MultiHeadLayerNorm(nn.Module):
     """``multihead_norm.py:5-40``: per-head LayerNorm of x [B, S, NH, DH] -> [B, S, NH * DH], optional
     weight and bias.  Runs ``group_norm_kernel`` (one group per head) on the [B * S, NH * DH] view,
@@ -90,6 +149,7 @@ class MultiHeadLayerNorm(nn.Module):
         B, S, NH, DH = x.shape
         if NH != self.num_heads or DH != self.head_dim:
             raise ValueError(f"Expected shape [B,S,{self.num_heads},{self.head_dim}], got {x.shape}")
+        from .slstm_layers import group_norm
         return group_norm(x.reshape(B * S, NH * DH), NH, self.weight, self.bias, self.eps).view(B, S, NH * DH)
 
 

@@ -19,7 +19,7 @@ from . import _lib
 __all__ = [
     "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
     "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "mh_rmsnorm_gate_op",
-    "chunkwise_workspace_bytes",
+    "gate_proj_softcap_op", "chunkwise_workspace_bytes",
 ]
 
 _EMPTY_SHAPE = (0,)
@@ -414,3 +414,32 @@ def _(h, weight, o_preact, heads_first, eps):
     else:
         B, S, NH, DH = h.shape
     return h.new_empty((B, S, NH * DH))
+
+
+# ------------------------------------------- projection cells: gate projection + soft-cap epilogue
+@torch.library.custom_op("xlstm_hip::gate_proj_softcap", mutates_args=())
+def gate_proj_softcap_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], cap: float) -> Tensor:
+    what = "gate_proj_softcap"
+    _lib.require_gpu(x, weight, bias, what=what)
+    _check(x.dim() >= 1 and weight.dim() == 2 and weight.shape[1] == x.shape[-1], what,
+           f"weight must be (G, D) with D = x.shape[-1], got {tuple(weight.shape)} for x {tuple(x.shape)}")
+    G, D = weight.shape
+    _check(bias is None or tuple(bias.shape) == (G,), what, f"bias must be ({G},)")
+    _check(weight.dtype == x.dtype and (bias is None or bias.dtype == x.dtype), what,
+           "x, weight and bias must share a dtype")
+    lead = tuple(x.shape[:-1])
+    M = 1
+    for d in lead:
+        M *= d
+    x2, w = _prep(x.reshape(M, D)), _prep(weight)
+    b = None if bias is None else _prep(bias)
+    y = torch.empty(lead + (G,), dtype=x.dtype, device=x.device)
+    rc = _lib.load().xl_gate_proj_softcap_fwd(x2.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), M, D, G,
+                                              float(cap), _lib.dtype_code(x, what), _lib.stream_of(x))
+    _lib.check(rc, what)
+    return y
+
+
+@gate_proj_softcap_op.register_fake
+def _(x, weight, bias, cap):
+    return x.new_empty(tuple(x.shape[:-1]) + (weight.shape[0],))

@@ -9,8 +9,9 @@ reference root, ``SL`` = ``xlstm_metal/torch_native/blocks/slstm/slstm_layers``)
   ``NotImplementedError`` (no CPU path).
 * ``sLSTMProjectionCell`` (``SL/slstm_projection_cell.py:25-126``): the conv and
   its SiLU are one kernel on the channels-last input (no permuted copies); the
-  gate and z projections are ``nn.Linear`` (library GEMMs); the gate soft-cap
-  runs ``soft_cap_kernel``.
+  gate projections with their soft-cap are ``gate_proj_kernel`` (i and f
+  stacked over the conv output, o over the input; float32 takes ``nn.Linear``
+  and ``soft_cap_kernel``); the z projection is ``nn.Linear`` (a library GEMM).
 * ``sLSTMOutputCell`` (``SL/slstm_output_cell.py:18-91``): the per-head
   ``nn.GroupNorm`` runs ``group_norm_kernel``; ``out_proj`` is ``nn.Linear``.
 
@@ -107,14 +108,17 @@ class sLSTMProjectionCell(nn.Module):
         return x if self.gate_soft_cap is None else soft_cap(x, float(self.gate_soft_cap))
 
     def forward(self, x: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-        """x [B, S, D] -> z [B, S, NH, H], i, f, o pre-activations [B, S, NH], x_conv [B, S, D]."""
+        """x [B, S, D] -> z [B, S, NH, H], i, f, o pre-activations [B, S, NH], x_conv [B, S, D].
+
+        i and f are one gate-projection kernel over x_conv (their weights stacked), o one over x."""
+        from .mlstm_layers import gate_proj_softcap, stacked_linears
         B, S, _ = x.shape
+        NH = self.num_heads
         x_conv = x if self.conv1d is None else self.conv1d.forward_channels_last(x, activation="silu")
-        i_preact = self.soft_cap(self.igate_proj(x_conv))
-        f_preact = self.soft_cap(self.fgate_proj(x_conv))
-        o_preact = self.soft_cap(self.ogate_proj(x))
-        z = self.z_proj(x).view(B, S, self.num_heads, self.head_dim)
-        return z, i_preact, f_preact, o_preact, x_conv
+        gif = gate_proj_softcap(x_conv, *stacked_linears(self.igate_proj, self.fgate_proj), self.gate_soft_cap)
+        o_preact = gate_proj_softcap(x, self.ogate_proj.weight, self.ogate_proj.bias, self.gate_soft_cap)
+        z = self.z_proj(x).view(B, S, NH, self.head_dim)
+        return z, gif[..., :NH], gif[..., NH:], o_preact, x_conv
 
 
 class sLSTMOutputCell(nn.Module):
