@@ -194,3 +194,9 @@ def test_fake_tensor_shapes():
         assert y.shape == x.shape and y.dtype == x.dtype
         y = torch.ops.xlstm_hip.group_norm(x.view(200, 64), 4, None, None, 1e-6)
         assert y.shape == (200, 64)
+        h = torch.empty(2, 4, 100, 16, dtype=torch.bfloat16, device="cuda")
+        y = torch.ops.xlstm_hip.mh_rmsnorm_gate(h, None, None, True, 1e-6)
+        assert y.shape == (2, 100, 64) and y.dtype == torch.bfloat16
+        y = torch.ops.xlstm_hip.gate_proj_softcap(x, torch.empty(8, 64, dtype=torch.bfloat16, device="cuda"), None,
+                                                  15.0)
+        assert y.shape == (2, 100, 8)
