@@ -556,7 +556,10 @@ def summarize_pmc(fetch_dir, write_dir):
                         continue
                     acc.setdefault(key, {}).setdefault(row["Dispatch_Id"], 0.0)
                     acc[key][row["Dispatch_Id"]] += float(row["Counter_Value"])  # summed over TCC instances
-        return {k: statistics.median(v.values()) * 1024 for k, v in acc.items()}  # KiB -> bytes
+        # KiB -> bytes; the median dispatch of each kernel, except the calibration stream, whose
+        # largest dispatch is the known-size one (smaller soft-cap launches run in other entries)
+        return {k: (max(v.values()) if k == SOFT_CAP_KERNEL else statistics.median(v.values())) * 1024
+                for k, v in acc.items()}
 
     fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
     if SOFT_CAP_KERNEL not in fetch or SOFT_CAP_KERNEL not in write:
