@@ -103,17 +103,25 @@ __global__ __launch_bounds__(GP_BLOCK) void gate_proj_kernel(const T* __restrict
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  // Two blocks per trip keep the buffer indices compile-time constants.  The
-  // prefetches are unconditional (past the range they re-read a valid k-step,
-  // and the MFMAs of those steps see zeros): a load under a branch makes the
-  // compiler wait for every load at the join.
+  // Two blocks per trip keep the buffer indices compile-time constants.  In the
+  // loop both blocks ahead exist, so the prefetches need no branch (a load under
+  // a branch makes the compiler wait for every load at the join); the last one
+  // or two blocks run after it, each branch consuming what it loads.
   const int nblk = (max(kend - kbeg, 0) + KB - 1) / KB;
   load_block(0, B0{});
-  for (int blk = 0; blk < nblk; blk += 2) {
+  int blk = 0;
+  for (; blk + 2 < nblk; blk += 2) {
     load_block(blk + 1, B1{});
     run_block(blk, B0{});
     load_block(blk + 2, B0{});
     run_block(blk + 1, B1{});
+  }
+  if (blk + 1 < nblk) {
+    load_block(blk + 1, B1{});
+    run_block(blk, B0{});
+    run_block(blk + 1, B1{});
+  } else {
+    run_block(blk, B0{});  // no k-steps left for this wave when nblk == 0: the block is all zeros
   }
   if (wv > 0) {
 #pragma unroll
