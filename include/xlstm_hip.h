@@ -116,6 +116,27 @@ int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* v, const vo
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Chunkwise mLSTM forward that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc).  Same arguments and results as xl_mlstm_chunkwise_fwd
+ * with algo = XL_CHUNKWISE_FUSED (bf16 q/k/v, DQK 128 or 256, DV % 64 == 0,
+ * any S >= 1); the fused algorithm's gate-prep scratch lives in a static
+ * device array of XL_NOALLOC_SCRATCH_BYTES per GPU (1280 bytes per 64 tokens
+ * of every head: B*NH*ceil(S/64) <= 13107), held until the process ends.
+ * Larger requests return XL_ERR_UNSUPPORTED.  The stream's device must be the
+ * current device.  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (concurrent streams or threads) race.
+ */
+#define XL_NOALLOC_SCRATCH_BYTES (16u * 1024u * 1024u)
+size_t xl_mlstm_chunkwise_noalloc_max_bytes(void);
+int xl_mlstm_chunkwise_fwd_noalloc(const void* q, const void* k, const void* v, const void* i, const void* f,
+                                   const float* c0, const float* n0, const float* m0,
+                                   void* h, float* c_last, float* n_last, float* m_last,
+                                   int B, int NH, int S, int DQK, int DV, int L, float qk_scale, float eps,
+                                   int dtype_qkv, int dtype_gates, void* stream);
+
+/*
  * Recurrent mLSTM over a whole sequence in one launch (the time loop runs on
  * the GPU, states stay on chip).  Replaces mlstm_recurrent_sequence__native_fw
  * (kernel_development/xlstm/mlstm_block/mlstm_recurrent/recurrent/

@@ -1,0 +1,109 @@
+"""xl_mlstm_chunkwise_fwd_noalloc: the chunkwise forward whose gate-prep scratch is a static
+device array (for callers that cannot allocate).
+
+* CPU: the entry point is exported, states its maximum, and rejects requests beyond it (and
+  shapes the fused algorithm does not take) before any GPU work;
+* GPU: through the C-ABI, two calls in a row (the second on a smaller input, so the array
+  holds the first call's larger contents) each equal xl_mlstm_chunkwise_fwd with the fused
+  algorithm and a caller workspace, bit for bit (same kernels, same inputs), on h and on
+  the last C, n, m; and both also meet the bf16 parity bar against the CPU oracle.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from helpers import assert_parity, gpu_available
+
+FUSED = 2
+BF16, F32 = 1, 0
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from xlstm_hip import _lib
+    return _lib.load()
+
+
+def test_noalloc_max_and_rejections(lib):
+    from xlstm_hip import _lib
+    mx = lib.xl_mlstm_chunkwise_noalloc_max_bytes()
+    assert mx == 16 * 1024 * 1024
+    per_chunk = lib.xl_mlstm_chunkwise_workspace_size(1, 1, 64, 256, 512, 64, BF16, FUSED)
+    assert per_chunk == 1280
+    f = lib.xl_mlstm_chunkwise_fwd_noalloc
+    p = ctypes.c_void_p(256)  # never dereferenced: the checks fail before any GPU call
+    # 4 * 8 * ceil(32768 / 64) = 16384 head-chunks > 13107
+    rc = f(p, p, p, p, p, None, None, None, p, None, None, None, 4, 8, 32768, 256, 512, 64, 0.0625, 1e-6,
+           BF16, BF16, None)
+    assert rc == -2
+    msg = lib.xl_last_error()
+    assert b"scratch" in msg and b"13107" in msg
+    # float32 q/k/v: the fused algorithm (the only one without a workspace) does not take them
+    rc = f(p, p, p, p, p, None, None, None, p, None, None, None, 1, 2, 128, 256, 512, 64, 0.0625, 1e-6,
+           F32, F32, None)
+    assert rc == -2 and b"fused" in lib.xl_last_error()
+    # the usual argument checks still apply
+    rc = f(p, p, p, p, None, None, None, None, p, None, None, None, 1, 2, 128, 256, 512, 64, 0.0625, 1e-6,
+           BF16, BF16, None)
+    assert rc == -1 and b"null" in lib.xl_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(-1, "noalloc")
+
+
+def _inputs(B, NH, S, DQK, DV, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, NH, S, DQK, generator=g) / DQK ** 0.5).to(torch.bfloat16)
+    k = torch.randn(B, NH, S, DQK, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, NH, S, DV, generator=g).to(torch.bfloat16)
+    i = torch.randn(B, NH, S, generator=g).to(torch.bfloat16)
+    f = (torch.randn(B, NH, S, generator=g) + 3).to(torch.bfloat16)
+    c0 = 0.1 * torch.randn(B, NH, DQK, DV, generator=g)
+    n0 = torch.randn(B, NH, DQK, generator=g).abs()
+    m0 = torch.randn(B, NH, generator=g)
+    return [t.to(dev) for t in (q, k, v, i, f, c0, n0, m0)]
+
+
+def _run(lib, fn, x, B, NH, S, DQK, DV, workspace=None):
+    q, k, v, i, f, c0, n0, m0 = x
+    dev = q.device
+    h = torch.full((B, NH, S, DV), float("nan"), dtype=torch.bfloat16, device=dev)
+    cl = torch.full((B, NH, DQK, DV), float("nan"), device=dev)
+    nl = torch.full((B, NH, DQK), float("nan"), device=dev)
+    ml = torch.full((B, NH), float("nan"), device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    common = [q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(), c0.data_ptr(), n0.data_ptr(),
+              m0.data_ptr(), h.data_ptr(), cl.data_ptr(), nl.data_ptr(), ml.data_ptr(), B, NH, S, DQK, DV, 64,
+              DQK ** -0.5, 1e-6, BF16, BF16]
+    if workspace is None:
+        rc = fn(*common, st)
+    else:
+        rc = fn(*common, FUSED, workspace.data_ptr(), workspace.numel(), st)
+    assert rc == 0, lib.xl_last_error()
+    torch.cuda.synchronize(dev)
+    return h, cl, nl, ml
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+def test_noalloc_matches_workspace_entry_point(lib, gpu_case):
+    from oracle import mlstm as om
+    dev = torch.device("cuda:0")
+    # second call smaller than the first: the array still holds the first call's gate prep
+    for (B, NH, S, DQK, DV, seed) in ((2, 4, 1000, 256, 128, 11), (1, 2, 300, 128, 64, 12)):
+        print(f"[noalloc] B{B} NH{NH} S{S} DQK{DQK} DV{DV} seed {seed}", flush=True)
+        x = _inputs(B, NH, S, DQK, DV, seed, dev)
+        ws_bytes = lib.xl_mlstm_chunkwise_workspace_size(B, NH, S, DQK, DV, 64, BF16, FUSED)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        want = _run(lib, lib.xl_mlstm_chunkwise_fwd, x, B, NH, S, DQK, DV, workspace=ws)
+        got = _run(lib, lib.xl_mlstm_chunkwise_fwd_noalloc, x, B, NH, S, DQK, DV)
+        for a, b, name in zip(got, want, ("h", "C", "n", "m")):
+            assert torch.equal(a, b), f"noalloc {name} differs from the workspace entry point"
+        # and both meet the parity bar against the oracle
+        q, k, v, i, f, c0, n0, m0 = (t.cpu().float() for t in x)
+        hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, c0, n0, m0[..., None], chunk_size=64)
+        assert_parity(got[0], hr, torch.bfloat16, "noalloc h")
+        assert_parity(got[1], Cr, torch.bfloat16, "noalloc C")
+        assert_parity(got[2], nr, torch.bfloat16, "noalloc n")
+        assert_parity(got[3], mr.reshape(B, NH), torch.bfloat16, "noalloc m")

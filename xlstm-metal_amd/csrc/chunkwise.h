@@ -18,6 +18,9 @@ struct ChunkwiseArgs {
   void* stream;
 };
 
+// Argument checks of xl_mlstm_chunkwise_fwd for the given algorithm (0 or an XL_ERR_* code).
+int chunkwise_check_args(const ChunkwiseArgs& a, int algo);
+
 // Two-pass algorithm (states pass + output pass), float32 arithmetic.
 size_t chunkwise_two_pass_workspace(int B, int NH, int S, int DQK, int DV, int L);
 int chunkwise_two_pass(const ChunkwiseArgs& a);

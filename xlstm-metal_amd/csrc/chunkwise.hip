@@ -6,7 +6,7 @@ namespace xl {
 
 static bool valid_L(int L) { return L == 16 || L == 32 || L == 64 || L == 128; }
 
-static int check_args(const ChunkwiseArgs& a, int algo) {
+int chunkwise_check_args(const ChunkwiseArgs& a, int algo) {
   const char* who = "xl_mlstm_chunkwise_fwd";
   if (a.B <= 0 || a.NH <= 0 || a.S <= 0 || a.DQK <= 0 || a.DV <= 0)
     return set_error(XL_ERR_INVALID_ARG, "%s: dimensions must be positive (B=%d NH=%d S=%d DQK=%d DV=%d)", who, a.B,
@@ -68,7 +68,7 @@ extern "C" int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* 
   clear_error();
   ChunkwiseArgs a = {q, k, v, i, f, c0, n0, m0, h, c_last, n_last, m_last, B, NH, S, DQK, DV, L,
                      qk_scale, eps, dtype_qkv, dtype_gates, workspace, workspace_bytes, stream};
-  int rc = check_args(a, algo);
+  int rc = chunkwise_check_args(a, algo);
   if (rc) return rc;
   int chosen = XL_CHUNKWISE_TWO_PASS;
   rc = pick(a, algo, &chosen);

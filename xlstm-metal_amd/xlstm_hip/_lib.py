@@ -31,6 +31,9 @@ SIGNATURES = {
     "xl_mlstm_chunkwise_workspace_size": (_sz, [_i] * 8),
     "xl_mlstm_chunkwise_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 6 + [_f, _f] + [_i] * 3
                                + [_vp, _sz, _vp]),
+    "xl_mlstm_chunkwise_noalloc_max_bytes": (_sz, []),
+    "xl_mlstm_chunkwise_fwd_noalloc": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 6 + [_f, _f] + [_i] * 2
+                                       + [_vp]),
     "xl_mlstm_sequence_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 5 + [_f, _f] + [_i, _i, _vp]),
     "xl_slstm_step_fwd": (_i, [_vp] * 4 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 3 + [_f] + [_i] * 3 + [_vp]),
     "xl_slstm_seq_fwd": (_i, [_vp] * 4 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 4 + [_f] + [_i] * 3 + [_vp]),
