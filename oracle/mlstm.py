@@ -189,7 +189,7 @@ def mlstm_chunkwise(matQ, matK, matV, vecI, vecF, matC_initial=None, vecN_initia
     return (H, last) if return_last_states else H
 
 
-def mlstm_recurrent_step(q, k, v, i, f, c, n, m, eps=1e-6, dtype_state=torch.float32):
+def mlstm_recurrent_step(q, k, v, i, f, c, n, m, eps=1e-6, dtype_state=torch.float32, gate_exp=torch.exp):
     """One recurrent decode step, ``REC/native_step.py:8-133``.
 
     ``m' = max(logsigmoid(f) + m, i)`` (``:70-73``); ``fa = exp(logsig f + m
@@ -197,7 +197,9 @@ def mlstm_recurrent_step(q, k, v, i, f, c, n, m, eps=1e-6, dtype_state=torch.flo
     (``:78``); ``C' = fa C + ia (k v^T)`` (``:79-81``); ``n' = fa n + ia k``
     (``:82``); ``h = q_s C'.to(q.dtype) / (max(|q_s n'.to(q.dtype)|,
     exp(-m')) + eps)`` (``:83-96``).  h is returned in q's dtype and the
-    states in ``dtype_state`` (``:98-101``).
+    states in ``dtype_state`` (``:98-101``).  ``gate_exp`` computes the three
+    exponentials (fa, ia, exp(-m')); tests pass a perturbed one to measure how
+    far the reference's roundings move h under 1-ulp changes of them.
     """
     dtype_qkv = q.dtype
     C_old = c.to(dtype=dtype_state)
@@ -206,20 +208,20 @@ def mlstm_recurrent_step(q, k, v, i, f, c, n, m, eps=1e-6, dtype_state=torch.flo
     B, NH, DHQK = q.shape
     lsf = F.logsigmoid(f)
     m_new = torch.max(lsf + m_old, i)
-    fa = torch.exp(lsf + m_old - m_new)
-    ia = torch.exp(i - m_new)
+    fa = gate_exp(lsf + m_old - m_new)
+    ia = gate_exp(i - m_new)
     q_s = q * (DHQK ** (-0.5))
     C_new = fa[:, :, :, None] * C_old + ia[:, :, :, None] * (k[:, :, :, None] @ v[:, :, None, :])
     n_new = fa * n_old + ia * k
     h_num = (q_s[:, :, None, :] @ C_new.to(dtype=dtype_qkv)).squeeze(2).to(dtype=dtype_state)
     qn = (q_s[:, :, None, :] @ n_new[:, :, :, None].to(dtype=dtype_qkv)).squeeze(2)
-    h_den = (torch.maximum(qn.abs(), torch.exp(-m_new)) + eps).to(dtype=dtype_state)
+    h_den = (torch.maximum(qn.abs(), gate_exp(-m_new)) + eps).to(dtype=dtype_state)
     h = (h_num / h_den).to(dtype=dtype_qkv)
     return h, (C_new.to(dtype=dtype_state), n_new.to(dtype=dtype_state), m_new.to(dtype=dtype_state))
 
 
 def mlstm_recurrent_sequence(q, k, v, i, f, c_initial=None, n_initial=None, m_initial=None,
-                             return_last_states=False, eps=1e-6, dtype_state=torch.float32):
+                             return_last_states=False, eps=1e-6, dtype_state=torch.float32, gate_exp=torch.exp):
     """Time loop over :func:`mlstm_recurrent_step`, ``REC/native_sequence.py:18-170``.
 
     Zero initial states (m = 0) when none are given (``:63-69``).
@@ -237,7 +239,7 @@ def mlstm_recurrent_sequence(q, k, v, i, f, c_initial=None, n_initial=None, m_in
     for t in range(S):
         h, (C, n, m) = mlstm_recurrent_step(
             q[:, :, t, :], k[:, :, t, :], v[:, :, t, :], i[:, :, t, None], f[:, :, t, None],
-            C, n, m, eps=eps, dtype_state=dtype_state)
+            C, n, m, eps=eps, dtype_state=dtype_state, gate_exp=gate_exp)
         hs.append(h)
     H = torch.stack(hs, dim=-2)
     return (H, (C, n, m)) if return_last_states else H

@@ -123,11 +123,14 @@ def test_sequence_kernel(gpu_case, S, dtype):
     h, (C, n, m) = xlstm_hip.mlstm_recurrent_sequence__native_fw(*_to((q, k, v, i, f, C0, n0, m0)),
                                                                 return_last_states=True)
     hr, (Cr, nr, mr) = om.mlstm_recurrent_sequence(q, k, v, i, f, C0, n0, m0, return_last_states=True)
-    # With a 16-bit q the reference rounds q . n' to q's dtype before dividing by it
-    # (native_step.py:86-96), so a 1-ulp difference of the float32 gate exponentials (GPU
-    # and CPU exp) can flip that rounding and move h by one bf16 ulp of its own: over long
-    # sequences h is held to 2e-2 beyond two bf16 roundings (its own and the denominator's).
-    rnd = 2 if S > 64 else 1
+    # With a 16-bit q the reference rounds q C' and q n' to q's dtype before dividing one by
+    # the other and rounds h once more (native_step.py:83-96).  The GPU's and the CPU's
+    # float32 exponentials differ by up to one ulp, which can flip the first two roundings:
+    # tests/test_oracle_bf16_sensitivity.py shows the oracle alone, under seeded 1-ulp
+    # changes of its gate exponentials, moving its own h beyond 2e-2 past one rounding (at
+    # this test's S = 130 inputs) and never beyond 2e-2 past three.  So h is held to 2e-2
+    # beyond the reference's three roundings of it, for every S.
+    rnd = 3
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got, want, dtype, f"S={S} {dtype} {name}", roundings=rnd if name == "h" else 1)
     h0 = xlstm_hip.mlstm_recurrent_sequence__native_fw(*_to((q, k, v, i, f)))
