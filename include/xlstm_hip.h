@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define XL_ABI_VERSION 1
+#define XL_ABI_VERSION 2
 
 enum xl_dtype { XL_DTYPE_F32 = 0, XL_DTYPE_BF16 = 1, XL_DTYPE_F16 = 2 };
 
@@ -108,6 +108,15 @@ int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i
  */
 size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, int L,
                                          int dtype_qkv, int algo);
+/*
+ * The algorithm xl_mlstm_chunkwise_fwd takes for these arguments:
+ * XL_CHUNKWISE_TWO_PASS or XL_CHUNKWISE_FUSED, or a negative XL_ERR_* code for
+ * arguments it rejects.  When algo = XL_CHUNKWISE_AUTO falls back to the
+ * two-pass algorithm, xl_last_error() says why the fused one was not taken.
+ * (The reference has no algorithm choice: its torch-native chunkwise is one
+ * code path, VTN fw.py:257-369.)
+ */
+int xl_mlstm_chunkwise_algo(int B, int NH, int S, int DQK, int DV, int L, int dtype_qkv, int algo);
 int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
                            const float* c0, const float* n0, const float* m0,
                            void* h, float* c_last, float* n_last, float* m_last,
@@ -236,7 +245,12 @@ int xl_mh_rmsnorm_gate_fwd(const void* h, const void* weight, const void* o_prea
 /*
  * Gate projection with the soft-cap epilogue: y[m, n] = cap * tanh(z / cap),
  * z = (b[n] + sum_d x[m, d] w[n, d]) rounded to the dtype (the Linear's output),
- * for the gate pre-activations of the projection cells.  Replaces
+ * for the gate pre-activations of the projection cells.  cap_rounding 0: the
+ * soft-cap in float32, rounded once (SoftCapCell, which the mLSTM projection
+ * cell uses); 1: cap, z / cap, tanh and the product each rounded to the dtype,
+ * as torch evaluates cap * tanh(x / cap) on 16-bit tensors in
+ * sLSTMProjectionCell.soft_cap (xlstm_metal/torch_native/blocks/slstm/
+ * slstm_layers/slstm_projection_cell.py:84-89).  Replaces
  * soft_cap(igate_proj(x)), soft_cap(fgate_proj(x)) in mLSTMProjectionCell.
  * forward (xlstm_metal/torch_native/blocks/mlstm/mlstm_chunkwise/
  * mlstm_projection_cell.py:97-103) and the i, f (on the conv output) and o
@@ -247,7 +261,7 @@ int xl_mh_rmsnorm_gate_fwd(const void* h, const void* weight, const void* o_prea
  *   w 16-byte aligned; cap <= 0: no soft-cap.
  */
 int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias, void* y,
-                             int M, int D, int G, float cap, int dtype, void* stream);
+                             int M, int D, int G, float cap, int cap_rounding, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

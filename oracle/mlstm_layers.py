@@ -22,7 +22,11 @@ Reference (paths relative to the MLXPorts/xLSTM-metal root, ``TNM`` =
   (``TNM/mlstm_chunkwise/mlstm_projection_cell.py:97-103``,
   ``xlstm_metal/torch_native/blocks/slstm/slstm_layers/slstm_projection_cell.py:
   118-121``): x w^T + b rounded to the module dtype (the Linear's output),
-  then cap * tanh(z / cap).
+  then cap * tanh(z / cap): in float64 for the mLSTM cell's SoftCapCell (which
+  computes in float32 and casts once), or with cap, z / cap, tanh and the product
+  each rounded to the dtype (``cap_in_dtype``) for the sLSTM cell, which
+  evaluates ``cap * torch.tanh(x / cap)`` on tensors of x's dtype
+  (``slstm_projection_cell.py:84-89``).
 
 Pinned (tests/test_oracle_mlstm_layers.py) against torch's CPU
 ``F.rms_norm`` in float64, the closed forms of a constant head (x / rms =
@@ -71,13 +75,19 @@ def mh_rmsnorm_gate(h, weight=None, o_preact=None, eps=1e-6, heads_first=True, d
     return y
 
 
-def gate_proj_softcap(x, weight, bias=None, cap=15.0, dtype=None):
+def gate_proj_softcap(x, weight, bias=None, cap=15.0, dtype=None, cap_in_dtype=False):
     """x [..., D], weight [G, D], bias [G] or None.  Returns float64 [..., G] before the final
-    rounding: the Linear's output rounded to ``dtype`` (x's by default), then the soft-cap."""
+    rounding: the Linear's output rounded to ``dtype`` (x's by default), then the soft-cap
+    (with ``cap_in_dtype``: cap, z / cap and tanh each rounded to ``dtype`` first)."""
     if dtype is None and isinstance(x, torch.Tensor):
         dtype = x.dtype
     z = _np64(x) @ _np64(weight).T
     if bias is not None:
         z = z + _np64(bias)
     z = _round_to(z, dtype)
-    return cap * np.tanh(z / cap) if cap > 0 else z
+    if cap <= 0:
+        return z
+    if cap_in_dtype:
+        capr = float(_round_to(np.float64(cap), dtype))
+        return capr * _round_to(np.tanh(_round_to(z / capr, dtype)), dtype)
+    return cap * np.tanh(z / cap)

@@ -138,13 +138,15 @@ def test_conv1d_and_group_norm_reject_bad_args(lib):
     assert rn(p, None, None, q, 1, 2, 4, 16384, 1, 1e-6, 1, None) == -2  # 32 vectors per lane
     assert rn(None, None, None, None, 0, 2, 4, 64, 1, 1e-6, 1, None) == 0
     gp = lib.xl_gate_proj_softcap_fwd
-    assert gp(p, p, None, q, 4, 64, 8, 15.0, 0, None) == -2  # float32
-    assert gp(p, p, None, q, 4, 64, 65, 15.0, 1, None) == -2
-    assert gp(p, p, None, q, 4, 12, 8, 15.0, 1, None) == -2
-    assert gp(p, p, None, q, -4, 64, 8, 15.0, 1, None) == -1
-    assert gp(ctypes.c_void_p(264), p, None, q, 4, 64, 8, 15.0, 1, None) == -1  # misaligned x
+    assert gp(p, p, None, q, 4, 64, 8, 15.0, 0, 0, None) == -2  # float32
+    assert gp(p, p, None, q, 4, 64, 65, 15.0, 0, 1, None) == -2
+    assert gp(p, p, None, q, 4, 12, 8, 15.0, 0, 1, None) == -2
+    assert gp(p, p, None, q, -4, 64, 8, 15.0, 0, 1, None) == -1
+    assert gp(p, p, None, q, 4, 64, 8, 15.0, 2, 1, None) == -1  # cap_rounding 0 or 1
+    assert b"cap_rounding" in lib.xl_last_error()
+    assert gp(ctypes.c_void_p(264), p, None, q, 4, 64, 8, 15.0, 0, 1, None) == -1  # misaligned x
     assert b"aligned" in lib.xl_last_error()
-    assert gp(None, None, None, None, 0, 64, 8, 15.0, 1, None) == 0
+    assert gp(None, None, None, None, 0, 64, 8, 15.0, 0, 1, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -200,3 +202,20 @@ def test_fake_tensor_shapes():
         y = torch.ops.xlstm_hip.gate_proj_softcap(x, torch.empty(8, 64, dtype=torch.bfloat16, device="cuda"), None,
                                                   15.0)
         assert y.shape == (2, 100, 8)
+
+
+def test_chunkwise_algorithm_query(lib):
+    """xl_mlstm_chunkwise_algo names the algorithm auto picks and why it left the fused one."""
+    from xlstm_hip import chunkwise_algorithm
+    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 64, torch.bfloat16) == "fused"
+    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 128, torch.bfloat16) == "fused"
+    assert chunkwise_algorithm(1, 8, 256, 256, 512, 64, torch.float32) == "two_pass"
+    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 64, torch.bfloat16, algo="two_pass") == "two_pass"
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 2, 0) == 1  # float16 q/k/v
+    assert b"bfloat16" in lib.xl_last_error()
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 96, 512, 64, 1, 0) == 1  # DQK 96
+    assert b"DQK" in lib.xl_last_error()
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 100, 256, 512, 64, 1, 0) == -1  # S % L
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 100, 256, 512, 64, 1, 2) == 2  # fused takes any S
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 48, 1, 0) == -2
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 96, 512, 64, 1, 2) == -2

@@ -237,3 +237,20 @@ def test_backend_any_length_bf16(gpu_case, S):
     hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, chunk_size=64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got, want, torch.bfloat16, f"backend any-S bf16 S={S} {name}")
+
+
+def test_auto_fallback_warns_once(gpu_case):
+    """algo="auto" with float16 q/k/v runs the float32 two-pass kernels and says so once (a
+    RuntimeWarning naming the reason), still within the parity bar."""
+    import warnings
+
+    import xlstm_hip
+    from xlstm_hip import ops
+    ops._fallback_warned.clear()
+    x, st = _inputs(1, 2, 128, 64, 64, torch.float16, seed=77)
+    with pytest.warns(RuntimeWarning, match="two-pass"):
+        h = xlstm_hip.mlstm_chunkwise(*_gpu(x))
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        xlstm_hip.mlstm_chunkwise(*_gpu(x))  # the same reason is not repeated
+    assert_parity(h.cpu(), _oracle(x, st, 64)[0], torch.float16, "f16 two-pass h")

@@ -94,3 +94,25 @@ def test_gate_proj_bf16_linear_rounding_matches_torch():
     got = torch.from_numpy(oml.gate_proj_softcap(x, w, b, 0.0))
     ulp = torch.exp2(torch.floor(torch.log2(lin.abs().clamp_min(1e-30))) - 7)
     assert bool(((got - lin).abs() <= ulp).all())
+
+
+def test_gate_proj_softcap_in_dtype_matches_torch_bf16_expression():
+    """cap_in_dtype: the sLSTM projection cell's ``cap * torch.tanh(x / cap)`` with cap a tensor of
+    x's dtype (slstm_projection_cell.py:84-89), evaluated by torch on bf16 tensors, equals the
+    oracle's per-operation roundings bit for bit except where torch's float32 tanh and the
+    float64 one round to different bf16 neighbours (one ulp, rarely); and the three roundings are
+    really there: the float64 soft-cap rounded once differs on many inputs."""
+    g = torch.Generator().manual_seed(23)
+    x = torch.eye(512, dtype=torch.bfloat16)
+    w = (40 * torch.randn(512, 512, generator=g)).to(torch.bfloat16)  # outputs = the rows of w
+    z = F.linear(x, w).double()
+    got = torch.from_numpy(oml.gate_proj_softcap(x, w, None, 15.0, cap_in_dtype=True)).to(torch.bfloat16).double()
+    cap_t = torch.tensor(15.0, dtype=torch.bfloat16)
+    want = (cap_t * torch.tanh(F.linear(x, w) / cap_t)).double()
+    ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp_min(1e-30))) - 7)
+    diff = (got - want).abs()
+    assert bool((diff <= ulp).all())
+    assert float((diff > 0).double().mean()) < 0.01
+    once = torch.from_numpy(oml.gate_proj_softcap(x, w, None, 15.0)).to(torch.bfloat16).double()
+    assert float((once != want).double().mean()) > 0.05
+    assert bool((z.abs() > 15).any())

@@ -59,6 +59,30 @@ extern "C" size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQ
                                      : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
 }
 
+extern "C" int xl_mlstm_chunkwise_algo(int B, int NH, int S, int DQK, int DV, int L, int dtype_qkv, int algo) {
+  using namespace xl;
+  clear_error();
+  if (B <= 0 || NH <= 0 || S <= 0 || DQK <= 0 || DV <= 0)
+    return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: dimensions must be positive");
+  if (!valid_L(L)) return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_algo: chunk_size=%d not in {16,32,64,128}", L);
+  if (!dtype_ok(dtype_qkv)) return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: unknown dtype");
+  if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_FUSED)
+    return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: unknown algo %d", algo);
+  if (S % L && algo != XL_CHUNKWISE_FUSED)
+    return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: Sequence length %d is not divisible by chunk size %d.",
+                     S, L);
+  ChunkwiseArgs a = {};
+  a.B = B; a.NH = NH; a.S = S; a.DQK = DQK; a.DV = DV; a.L = L;
+  a.dtype_qkv = dtype_qkv; a.dtype_gates = dtype_qkv;
+  int chosen = XL_CHUNKWISE_TWO_PASS;
+  const int rc = pick(a, algo, &chosen);
+  if (rc) return rc;
+  const char* why = nullptr;
+  if (chosen == XL_CHUNKWISE_TWO_PASS && algo == XL_CHUNKWISE_AUTO && !chunkwise_fused_supported(a, &why))
+    set_error(XL_OK, "fused algorithm not taken: %s", why);  // informational: why auto fell back
+  return chosen;
+}
+
 extern "C" int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,
                                       const float* c0, const float* n0, const float* m0, void* h, float* c_last,
                                       float* n_last, float* m_last, int B, int NH, int S, int DQK, int DV, int L,

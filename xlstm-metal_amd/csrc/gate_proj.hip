@@ -11,7 +11,11 @@
 // continues the row), the weights come from the caches (W is a few KB to a few
 // tens of KB and every wave re-reads it), one block of k-steps ahead.  The
 // epilogue adds the bias, rounds to the Linear's output dtype and applies
-// cap * tanh(x / cap) in float32 with one more rounding.
+// cap * tanh(x / cap), either in float32 with one more rounding (cap_rounding 0:
+// SoftCapCell, which computes in float32 and casts once) or with every
+// operation rounded to the dtype (cap_rounding 1: cap * torch.tanh(x / cap) on
+// 16-bit tensors, as sLSTMProjectionCell.soft_cap evaluates it,
+// xlstm_metal/torch_native/blocks/slstm/slstm_layers/slstm_projection_cell.py:84-89).
 #include "common.h"
 
 #include <type_traits>
@@ -52,7 +56,8 @@ constexpr int GP_BLOCK = 64 * GP_WAVES;
 template <typename T, int NT>
 __global__ __launch_bounds__(GP_BLOCK) void gate_proj_kernel(const T* __restrict__ x, const T* __restrict__ w,
                                                              const T* __restrict__ bias, T* __restrict__ y, int M,
-                                                             int D, int G, float cap, float inv_cap) {
+                                                             int D, int G, float cap, float inv_cap,
+                                                             int cap_rounding) {
   __shared__ f32x4 s_part[GP_WAVES - 1][NT][64];
   const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15, wv = threadIdx.x >> 6;
   const int m0 = blockIdx.x * 16;
@@ -144,14 +149,22 @@ __global__ __launch_bounds__(GP_BLOCK) void gate_proj_kernel(const T* __restrict
       const int m = m0 + 4 * g + e;
       if (m >= M) continue;
       float v = round_to<T>(acc[nt][e] + bn);  // the Linear's output in its dtype
-      if (cap > 0.0f) v = soft_cap16(v, cap, inv_cap);
+      if (cap > 0.0f) {
+        if (cap_rounding) {  // cap, x / cap, tanh and the product each in the dtype
+          const float capr = round_to<T>(cap);
+          v = capr * round_to<T>(tanh_f32(round_to<T>(v / capr)));
+        } else {
+          v = soft_cap16(v, cap, inv_cap);
+        }
+      }
       y[(size_t)m * G + n] = from_f32<T>(v);
     }
   }
 }
 
 template <typename T>
-int launch(const void* x, const void* w, const void* b, void* y, int M, int D, int G, float cap, hipStream_t st) {
+int launch(const void* x, const void* w, const void* b, void* y, int M, int D, int G, float cap, int cap_rounding,
+           hipStream_t st) {
   const int64_t blocks = ((int64_t)M + 15) / 16;
   if (blocks > 0x7fffffff) return set_error(XL_ERR_UNSUPPORTED, "xl_gate_proj_softcap_fwd: M=%d too large", M);
   const float inv_cap = cap > 0.0f ? 1.0f / cap : 0.0f;
@@ -159,10 +172,10 @@ int launch(const void* x, const void* w, const void* b, void* y, int M, int D, i
   T* yp = (T*)y;
   const dim3 grid((unsigned)blocks), blk(GP_BLOCK);
   switch ((G + 15) / 16) {
-    case 1: hipLaunchKernelGGL((gate_proj_kernel<T, 1>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap); break;
-    case 2: hipLaunchKernelGGL((gate_proj_kernel<T, 2>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap); break;
-    case 3: hipLaunchKernelGGL((gate_proj_kernel<T, 3>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap); break;
-    default: hipLaunchKernelGGL((gate_proj_kernel<T, 4>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap); break;
+    case 1: hipLaunchKernelGGL((gate_proj_kernel<T, 1>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap, cap_rounding); break;
+    case 2: hipLaunchKernelGGL((gate_proj_kernel<T, 2>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap, cap_rounding); break;
+    case 3: hipLaunchKernelGGL((gate_proj_kernel<T, 3>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap, cap_rounding); break;
+    default: hipLaunchKernelGGL((gate_proj_kernel<T, 4>), grid, blk, 0, st, xp, wp, bp, yp, M, D, G, cap, inv_cap, cap_rounding); break;
   }
   return check_launch("xl_gate_proj_softcap_fwd");
 }
@@ -171,7 +184,7 @@ int launch(const void* x, const void* w, const void* b, void* y, int M, int D, i
 }  // namespace xl
 
 extern "C" int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias, void* y, int M, int D,
-                                        int G, float cap, int dtype, void* stream) {
+                                        int G, float cap, int cap_rounding, int dtype, void* stream) {
   using namespace xl;
   clear_error();
   if (M < 0 || D < 0 || G < 0)
@@ -183,11 +196,13 @@ extern "C" int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const
   if (D % 8 != 0 || (D == 0 && M > 0 && G > 0))
     return set_error(XL_ERR_UNSUPPORTED, "xl_gate_proj_softcap_fwd: D=%d (a positive multiple of 8)", D);
   if (!(cap == cap) || cap == INFINITY) return set_error(XL_ERR_INVALID_ARG, "xl_gate_proj_softcap_fwd: cap must be finite");
+  if (cap_rounding != 0 && cap_rounding != 1)
+    return set_error(XL_ERR_INVALID_ARG, "xl_gate_proj_softcap_fwd: cap_rounding must be 0 or 1");
   if ((int64_t)M * G == 0) return XL_OK;
   if (!x || !weight || !y) return set_error(XL_ERR_INVALID_ARG, "xl_gate_proj_softcap_fwd: null pointer");
   if ((((uintptr_t)x) | ((uintptr_t)weight)) & 15u)
     return set_error(XL_ERR_INVALID_ARG, "xl_gate_proj_softcap_fwd: x and weight must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == XL_DTYPE_BF16) return launch<bf16_t>(x, weight, bias, y, M, D, G, cap, st);
-  return launch<f16_t>(x, weight, bias, y, M, D, G, cap, st);
+  if (dtype == XL_DTYPE_BF16) return launch<bf16_t>(x, weight, bias, y, M, D, G, cap, cap_rounding, st);
+  return launch<f16_t>(x, weight, bias, y, M, D, G, cap, cap_rounding, st);
 }

@@ -14,6 +14,7 @@ from .backend import (
     mLSTMBackendConfig, wrap_chunkwise__arbitrary_sequence_length, wrap_chunkwise__pad_zeros,
 )
 from .chunkwise import mlstm_chunkwise, mlstm_chunkwise__native_autograd
+from .ops import chunkwise_algorithm
 from .mlstm_layers import (
     MultiHeadLayerNorm, MultiHeadRMSNorm, gate_proj_softcap, mh_rmsnorm_gate, mLSTMOutputCell, mLSTMProjectionCell,
 )
@@ -34,7 +35,7 @@ def load_library():
 
 
 __all__ = [
-    "mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "mlstm_recurrent_step__native",
+    "mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "chunkwise_algorithm", "mlstm_recurrent_step__native",
     "mlstm_recurrent_step__native_fw", "mlstm_recurrent_step_", "mlstm_recurrent_sequence__native_fw",
     "mLSTMRecurrentKernelCell",
     "slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell", "soft_cap", "SoftCapCell",

@@ -29,6 +29,7 @@ SIGNATURES = {
     "xl_soft_cap_fwd": (_i, [_vp, _vp, _i64, _f, _i, _vp]),
     "xl_mlstm_step_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 4 + [_f, _f] + [_i, _i, _vp]),
     "xl_mlstm_chunkwise_workspace_size": (_sz, [_i] * 8),
+    "xl_mlstm_chunkwise_algo": (_i, [_i] * 8),
     "xl_mlstm_chunkwise_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 6 + [_f, _f] + [_i] * 3
                                + [_vp, _sz, _vp]),
     "xl_mlstm_chunkwise_noalloc_max_bytes": (_sz, []),
@@ -40,10 +41,10 @@ SIGNATURES = {
     "xl_causal_conv1d_fwd": (_i, [_vp] * 4 + [_i] * 6 + [_vp]),
     "xl_group_norm_fwd": (_i, [_vp] * 4 + [_i64, _i, _i, _f, _i, _vp]),
     "xl_mh_rmsnorm_gate_fwd": (_i, [_vp] * 4 + [_i] * 5 + [_f, _i, _vp]),
-    "xl_gate_proj_softcap_fwd": (_i, [_vp] * 4 + [_i] * 3 + [_f, _i, _vp]),
+    "xl_gate_proj_softcap_fwd": (_i, [_vp] * 4 + [_i] * 3 + [_f, _i, _i, _vp]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()

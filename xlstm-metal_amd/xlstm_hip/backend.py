@@ -104,8 +104,10 @@ def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequ
     n_state = n_initial if n_initial is not None else torch.zeros(B, NH, DHQK, device=dev, dtype=torch.float32)
     m_state = m_initial if m_initial is not None else torch.zeros(B, NH, 1, device=dev, dtype=torch.float32)
     if S > 1 and mlstm_chunkwise_kernel is mlstm_chunkwise__native_autograd and _fused_takes_any_length(q, k, v):
+        # the fused kernel runs 64-token chunks whatever chunk_size names (the forward is
+        # chunk-size invariant), so it is called with the size its support was checked for
         h_out, (c_state, n_state, m_state) = mlstm_chunkwise_kernel(
-            q=q, k=k, v=v, f=f, i=i, c_initial=c_state, n_initial=n_state, m_initial=m_state, chunk_size=chunk_size,
+            q=q, k=k, v=v, f=f, i=i, c_initial=c_state, n_initial=n_state, m_initial=m_state, chunk_size=64,
             return_last_states=True, eps=eps, algo="fused")
     elif S > 1:
         h_outs = []

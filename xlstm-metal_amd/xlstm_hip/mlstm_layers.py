@@ -39,18 +39,21 @@ __all__ = ["mh_rmsnorm_gate", "gate_proj_softcap", "stacked_linears", "MultiHead
 
 
 def gate_proj_softcap(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None,
-                      cap: Optional[float] = None) -> Tensor:
+                      cap: Optional[float] = None, cap_in_dtype: bool = False) -> Tensor:
     """``cap * tanh(F.linear(x, weight, bias) / cap)`` for a few gate outputs (weight [G, D], G <= 64).
 
     bf16 / f16: one kernel reading x once (the Linear's output rounded to x's dtype before the
     soft-cap, as the reference's two modules do); float32: ``F.linear`` then the soft-cap kernel.
-    ``cap`` None or <= 0: no soft-cap.
+    ``cap_in_dtype``: the soft-cap's operations are each rounded to x's dtype, as torch evaluates
+    ``cap * tanh(x / cap)`` on 16-bit tensors (sLSTMProjectionCell.soft_cap,
+    slstm_projection_cell.py:84-89); otherwise it is computed in float32 and rounded once
+    (SoftCapCell, which mLSTMProjectionCell uses).  ``cap`` None or <= 0: no soft-cap.
     """
     c = 0.0 if cap is None else float(cap)
     if x.dtype == torch.float32:
         y = F.linear(x, weight, bias)
         return soft_cap(y, c) if c > 0 else y
-    return gate_proj_softcap_op(x, weight, bias, c)
+    return gate_proj_softcap_op(x, weight, bias, c, 1 if cap_in_dtype else 0)
 
 
 def stacked_linears(*linears: nn.Linear):

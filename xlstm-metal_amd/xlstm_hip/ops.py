@@ -9,6 +9,7 @@ no CPU path: CPU tensors raise.
 
 from __future__ import annotations
 
+import warnings
 from typing import Optional
 
 import torch
@@ -19,7 +20,7 @@ from . import _lib
 __all__ = [
     "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
     "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "mh_rmsnorm_gate_op",
-    "gate_proj_softcap_op", "chunkwise_workspace_bytes",
+    "gate_proj_softcap_op", "chunkwise_workspace_bytes", "chunkwise_algorithm",
 ]
 
 _EMPTY_SHAPE = (0,)
@@ -155,6 +156,33 @@ def _seq_shapes(q, k, v, i, f, c0, n0, m0, what):
     return B, NH, S, DQK, DV
 
 
+_ALGO_NAMES = {1: "two_pass", 2: "fused"}
+_fallback_warned: set = set()
+
+
+def chunkwise_algorithm(B, NH, S, DQK, DV, L, dtype, algo="auto") -> str:
+    """The algorithm ("fused" or "two_pass") xl_mlstm_chunkwise_fwd takes for these arguments."""
+    lib = _lib.load()
+    rc = int(lib.xl_mlstm_chunkwise_algo(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype], _lib.ALGO[algo]))
+    if rc < 0:
+        _lib.check(rc, "mlstm_chunkwise")
+    return _ALGO_NAMES[rc]
+
+
+def _warn_slow_fallback(B, NH, S, DQK, DV, L, dtype) -> None:
+    """One warning per reason when algo="auto" leaves 16-bit inputs on the float32 two-pass kernels
+    (an order of magnitude slower than the fused kernel, with a workspace of every chunk's state)."""
+    lib = _lib.load()
+    if int(lib.xl_mlstm_chunkwise_algo(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype], 0)) != 1:
+        return
+    why = lib.xl_last_error().decode(errors="replace")
+    if why not in _fallback_warned:
+        _fallback_warned.add(why)
+        warnings.warn(f"xlstm_hip.mlstm_chunkwise: {dtype} inputs run the two-pass float32 kernels ({why}); "
+                      "bf16 q/k/v with DQK 128 or 256 and DV a multiple of 64 take the fused kernel",
+                      RuntimeWarning, stacklevel=3)
+
+
 def chunkwise_workspace_bytes(B, NH, S, DQK, DV, L, dtype, algo="auto") -> int:
     return int(_lib.load().xl_mlstm_chunkwise_workspace_size(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype],
                                                              _lib.ALGO[algo]))
@@ -183,6 +211,8 @@ def mlstm_chunkwise_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c0
     cl, nl, ml = _state_outs(return_last_states, B, NH, DQK, DV, q.device)
     lib = _lib.load()
     dq = _lib.dtype_code(q, what)
+    if algo == _lib.ALGO["auto"] and q.dtype != torch.float32:
+        _warn_slow_fallback(B, NH, S, DQK, DV, chunk_size, q.dtype)
     ws_bytes = int(lib.xl_mlstm_chunkwise_workspace_size(B, NH, S, DQK, DV, chunk_size, dq, int(algo)))
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device) if ws_bytes else None
     rc = lib.xl_mlstm_chunkwise_fwd(
@@ -418,7 +448,8 @@ def _(h, weight, o_preact, heads_first, eps):
 
 # ------------------------------------------- projection cells: gate projection + soft-cap epilogue
 @torch.library.custom_op("xlstm_hip::gate_proj_softcap", mutates_args=())
-def gate_proj_softcap_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], cap: float) -> Tensor:
+def gate_proj_softcap_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], cap: float,
+                         cap_rounding: int = 0) -> Tensor:
     what = "gate_proj_softcap"
     _lib.require_gpu(x, weight, bias, what=what)
     _check(x.dim() >= 1 and weight.dim() == 2 and weight.shape[1] == x.shape[-1], what,
@@ -435,11 +466,12 @@ def gate_proj_softcap_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], cap:
     b = None if bias is None else _prep(bias)
     y = torch.empty(lead + (G,), dtype=x.dtype, device=x.device)
     rc = _lib.load().xl_gate_proj_softcap_fwd(x2.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), M, D, G,
-                                              float(cap), _lib.dtype_code(x, what), _lib.stream_of(x))
+                                              float(cap), int(cap_rounding), _lib.dtype_code(x, what),
+                                              _lib.stream_of(x))
     _lib.check(rc, what)
     return y
 
 
 @gate_proj_softcap_op.register_fake
-def _(x, weight, bias, cap):
+def _(x, weight, bias, cap, cap_rounding=0):
     return x.new_empty(tuple(x.shape[:-1]) + (weight.shape[0],))

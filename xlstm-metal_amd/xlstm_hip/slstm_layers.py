@@ -115,8 +115,11 @@ class sLSTMProjectionCell(nn.Module):
         B, S, _ = x.shape
         NH = self.num_heads
         x_conv = x if self.conv1d is None else self.conv1d.forward_channels_last(x, activation="silu")
-        gif = gate_proj_softcap(x_conv, *stacked_linears(self.igate_proj, self.fgate_proj), self.gate_soft_cap)
-        o_preact = gate_proj_softcap(x, self.ogate_proj.weight, self.ogate_proj.bias, self.gate_soft_cap)
+        # the reference soft-caps with torch ops in x's dtype (slstm_projection_cell.py:84-89)
+        gif = gate_proj_softcap(x_conv, *stacked_linears(self.igate_proj, self.fgate_proj), self.gate_soft_cap,
+                                cap_in_dtype=True)
+        o_preact = gate_proj_softcap(x, self.ogate_proj.weight, self.ogate_proj.bias, self.gate_soft_cap,
+                                     cap_in_dtype=True)
         z = self.z_proj(x).view(B, S, NH, self.head_dim)
         return z, gif[..., :NH], gif[..., NH:], o_preact, x_conv
 
