@@ -519,6 +519,54 @@ def bench_arbitrary_length(args, dev):
             "roofline_hbm": _hbm(by, t["ms"])}
 
 
+def bench_stack(args, dev, which):
+    """BASELINE config 3 or 4 end to end on the random-init stack (xlstm_hip.stack): prefill tokens/s
+    of the whole prompt (B x S tokens through every block, the final norm, the lm_head and the logit
+    soft-cap of the last position) and greedy-decode tokens/s (one HIP-graph replay per token: every
+    block's step kernels, the lm_head, the soft-cap and the argmax), both timed with HIP events."""
+    from xlstm_hip.stack import CFG3_STACK, CFG4_STACK, DecodeGraph, xLSTMStack
+    cfg, B, S, steps = (CFG3_STACK, 1, 2048, 256) if which == "cfg3" else (CFG4_STACK, 8, 4096, 128)
+    model = xLSTMStack.random(cfg, dev, seed=3 if which == "cfg3" else 4)
+    g = torch.Generator(device=dev).manual_seed(11)
+    prompt = torch.randint(0, cfg.vocab, (B, S), generator=g, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(2):
+        logits, states = model.prefill(prompt)
+    torch.cuda.synchronize(dev)
+    times = []
+    for _ in range(max(3, args.steps // 4)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        logits, states = model.prefill(prompt)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1))
+    pre_ms = statistics.median(times)
+    dg = DecodeGraph(model, states, logits.argmax(-1))
+    for _ in range(4):
+        dg.step()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        dg.graph.replay()
+        dg.token.copy_(dg.next_token)
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    dec_ms = e0.elapsed_time(e1) / steps
+    nparams = sum(p.numel() for p in model.parameters())
+    n_sl = sum(cfg.is_slstm(b) for b in range(cfg.num_blocks))
+    del model, states, dg
+    torch.cuda.empty_cache()
+    return {"workload": f"{which} random-init stack: {cfg.num_blocks} blocks ({cfg.num_blocks - n_sl} mLSTM, {n_sl} "
+                        f"sLSTM), d {cfg.d_model}, vocab {cfg.vocab}, {nparams / 1e9:.2f}B params, bf16; B{B}, "
+                        f"prefill {S} tokens, then {steps} greedy decode steps",
+            "prefill_ms": pre_ms, "prefill_tokens_per_s": B * S / (pre_ms * 1e-3),
+            "decode_ms_per_step": dec_ms, "decode_tokens_per_s": B / (dec_ms * 1e-3), "decode_steps": steps,
+            "decode_mode": "hip_graph (one replay per token)",
+            "data": "synthetic: random token ids, weights N(0, 0.02), forget-gate bias 3"}
+
+
 def load_traffic(kernel, workload):
     """Calibrated HBM bytes per launch of `kernel` on `workload` from profiles/hbm_traffic.json, else None."""
     try:
@@ -589,10 +637,44 @@ def summarize_pmc(fetch_dir, write_dir):
     print(json.dumps(out, indent=1))
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _blas() -> str:
+    """The BLAS torch was built with and, where torch names it, the library version."""
+    import re
+    cfg = torch.__config__.show()
+    blas = re.search(r"BLAS_INFO=([^,\s]+)", cfg)
+    ver = re.search(r"(Intel\(R\) [^\n]*Math Kernel Library[^\n]*)", cfg)
+    out = blas.group(1) if blas else "unknown"
+    return f"{out} ({ver.group(1).strip()})" if ver else out
+
+
+def bench_cfg0(args, dev):
+    """BASELINE config 0 on the GPU: one float32 mlstm_chunkwise call (B1 NH8 S256 DQK256 DV512, L 64,
+    last states returned), the two-pass float32 kernels, replayed from a HIP graph, HIP events."""
+    import xlstm_hip
+    from xlstm_hip.workloads import CFG0, chunkwise_inputs
+    x = chunkwise_inputs(CFG0, device=dev)
+    t = _timed(lambda: xlstm_hip.mlstm_chunkwise(*x, return_last_states=True, chunk_size=CFG0.L), dev,
+               max(20, args.steps))
+    return {"workload": "cfg0 mlstm_chunkwise fp32 B1 NH8 S256 DQK256 DV512 L64", "us_per_call": 1e3 * t["ms"],
+            "us_min": 1e3 * t["ms_min"], "mode": t["mode"], "algo": "two_pass (float32)"}
+
+
 def cpu_baseline(args):
-    """Oracle (torch on the host) on a bounded sample: prefill tokens/s and decode us/step."""
+    """Oracle (torch on the host) on bounded samples: cfg2 prefill tokens/s (the headline's unit),
+    cfg0 us per call, cfg1 decode us per step."""
     from oracle import mlstm as om
-    from xlstm_hip.workloads import CFG1, CFG2, chunkwise_inputs, step_inputs
+    from xlstm_hip.workloads import CFG0, CFG1, CFG2, chunkwise_inputs, step_inputs
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     # prefill sample: batch row 0 of cfg2 (all 8 heads, full S; bf16 inputs upcast, fp32 states)
@@ -605,20 +687,34 @@ def cpu_baseline(args):
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     pre_tps = S / dt
-    # decode sample: cfg1 step, 10 chained steps
+    # cfg0: the whole config, >= 20 reps, median
+    x0 = chunkwise_inputs(CFG0)
+    for _ in range(2):
+        om.mlstm_chunkwise(*x0, return_last_states=True, chunk_size=CFG0.L)
+    c0 = []
+    while len(c0) < 20:
+        t1 = time.perf_counter()
+        om.mlstm_chunkwise(*x0, return_last_states=True, chunk_size=CFG0.L)
+        c0.append(time.perf_counter() - t1)
+    # decode sample: cfg1 step, 100 chained steps (the 1000-step figure is this rate x 1000)
     q, k, v, i, f, C, n, m = step_inputs(CFG1)
     om.mlstm_recurrent_step(q, k, v, i, f, C, n, m)
     t0 = time.perf_counter()
-    nst = 10
+    nst = 100
     for _ in range(nst):
         _, (C, n, m) = om.mlstm_recurrent_step(q, k, v, i, f, C, n, m)
     dec_us = 1e6 * (time.perf_counter() - t0) / nst
     return {
         "value": pre_tps, "unit": "tokens/s", "cores": cores, "kind": "port",
-        "sample": f"oracle.mlstm.mlstm_chunkwise (torch {torch.__version__} CPU, fp32) on cfg2 batch row 0, "
-                  f"8 heads, S={S}, L={args.chunk_size}: {reps} reps, {dt * 1e3:.1f} ms each",
+        "cpu_model": _cpu_model(), "blas": _blas(), "torch": torch.__version__,
+        "sample": f"oracle.mlstm.mlstm_chunkwise (torch {torch.__version__} CPU, fp32, {cores} threads) on cfg2 "
+                  f"batch row 0, 8 heads, S={S}, L={args.chunk_size}: {reps} reps, {dt * 1e3:.1f} ms each",
+        "cfg0_us_per_call": 1e6 * statistics.median(c0),
+        "cfg0_sample": "oracle.mlstm.mlstm_chunkwise on all of cfg0 (fp32 B1 NH8 S256 DQK256 DV512 L64, last "
+                       "states), 20 reps after 2 warm-ups, median",
         "decode_us_per_step": dec_us,
-        "decode_sample": f"oracle.mlstm.mlstm_recurrent_step on cfg1, {nst} chained steps",
+        "decode_sample": f"oracle.mlstm.mlstm_recurrent_step on cfg1, {nst} chained steps after 1 warm-up (1000 "
+                         f"steps extrapolate to {dec_us * 1e-3:.0f} ms)",
     }
 
 
@@ -634,6 +730,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-soft-cap", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the sLSTM, recurrent-sequence and any-S entries")
+    ap.add_argument("--no-stacks", action="store_true", help="skip the config 3 / 4 end-to-end stacks")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
     if args.summarize_pmc:
@@ -701,6 +798,11 @@ def main():
         out["slstm_group_norm"] = bench_group_norm(args, dev)
         out["mlstm_output_gate"] = bench_mlstm_output_gate(args, dev)
         out["slstm_gate_proj"] = bench_gate_proj(args, dev)
+    if not args.no_extra:
+        out["cfg0"] = bench_cfg0(args, dev)
+    if not args.no_stacks:
+        out["cfg3_stack"] = bench_stack(args, dev, "cfg3")
+        out["cfg4_stack"] = bench_stack(args, dev, "cfg4")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(out), flush=True)
