@@ -494,6 +494,38 @@ def bench_mlstm_sequence(args, dev):
             "roofline": dict(_hbm(mlstm_sequence_bytes(), t["ms"]), traffic=load_traffic(SEQ_KERNEL, wl))}
 
 
+def bench_cfg3_heads(args, dev):
+    """The chunkwise call of one config 3 mLSTM layer (B1 NH8 S2048 DQK256 DV512, bf16, config 0's value
+    distributions, last states): 8 heads x 8 column tiles are 64 workgroups for 256 CUs, so the fused
+    kernel splits the sequence into 4 segments (a states-only pass over the first three, the segment
+    combine, then all four from their start states).  Beside it the same call unsplit (the
+    no-allocation entry point, which never splits)."""
+    import xlstm_hip
+    from xlstm_hip import _lib
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    B, NH, S, DQK, DV = 1, 8, 2048, CFG2.DQK, CFG2.DV
+    q, k, v, i, f = chunkwise_inputs(CFG2, device=dev, S=S, B=B)
+    lib = _lib.load()
+    h = torch.empty(B, NH, S, DV, dtype=q.dtype, device=dev)
+    cl = torch.empty(B, NH, DQK, DV, device=dev)
+    nl = torch.empty(B, NH, DQK, device=dev)
+    ml = torch.empty(B, NH, device=dev)
+
+    def unsplit():
+        _lib.check(lib.xl_mlstm_chunkwise_fwd_noalloc(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(), None, None, None, h.data_ptr(),
+            cl.data_ptr(), nl.data_ptr(), ml.data_ptr(), B, NH, S, DQK, DV, 64, DQK ** -0.5, 1e-6, 1, 1,
+            torch.cuda.current_stream(dev).cuda_stream), "noalloc")
+
+    t = _timed(lambda: xlstm_hip.mlstm_chunkwise(q, k, v, i, f, return_last_states=True), dev, max(10, args.steps))
+    tu = _timed(unsplit, dev, max(10, args.steps))
+    fl = prefill_flops(B, NH, S, DQK, DV, 64)
+    return {"workload": f"cfg3 mLSTM layer chunkwise B{B} NH{NH} S{S} DQK{DQK} DV{DV} bf16",
+            "us_per_call": 1e3 * t["ms"], "us_min": 1e3 * t["ms_min"], "mode": t["mode"],
+            "tokens_per_s": B * S / (t["ms"] * 1e-3), "tflops": fl / (t["ms"] * 1e-3) / 1e12,
+            "unsplit_us_per_call": 1e3 * tu["ms"], "split_speedup": tu["ms"] / t["ms"]}
+
+
 def bench_arbitrary_length(args, dev):
     """Any-S inference wrapper (wrap_chunkwise__arbitrary_sequence_length) on config 2 with
     S = 8192 + 63, the reference's worst tail (its split: chunk sizes 64, 32, 16 and a 15-token
@@ -794,6 +826,7 @@ def main():
         out["slstm_step"] = bench_slstm_step(args, dev)
         out["mlstm_sequence"] = bench_mlstm_sequence(args, dev)
         out["arbitrary_length"] = bench_arbitrary_length(args, dev)
+        out["cfg3_heads_chunkwise"] = bench_cfg3_heads(args, dev)
         out["slstm_conv1d_silu"] = bench_slstm_conv(args, dev)
         out["slstm_group_norm"] = bench_group_norm(args, dev)
         out["mlstm_output_gate"] = bench_mlstm_output_gate(args, dev)

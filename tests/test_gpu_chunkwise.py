@@ -254,3 +254,27 @@ def test_auto_fallback_warns_once(gpu_case):
         warnings.simplefilter("error")
         xlstm_hip.mlstm_chunkwise(*_gpu(x))  # the same reason is not repeated
     assert_parity(h.cpu(), _oracle(x, st, 64)[0], torch.float16, "f16 two-pass h")
+
+
+@pytest.mark.parametrize("B,NH,S,DQK,DV,with_state", [
+    (1, 2, 2048, 256, 128, False),   # 4 (head, tile) pairs: 8 segments of 4 chunks
+    (1, 2, 2048, 256, 128, True),
+    (2, 1, 1000, 128, 64, True),     # ragged last chunk inside the last segment
+    (1, 8, 2048, 256, 512, True),    # config 3's heads: 4 segments of 8 chunks
+    (1, 1, 300, 256, 64, False),     # 5 chunks: too short to split
+])
+def test_fused_sequence_split(gpu_case, B, NH, S, DQK, DV, with_state):
+    """Few heads: the fused kernel splits the sequence into segments (a states-only pass, the
+    segment combine, then all segments at once from their start states).  h and the last C, n, m
+    against the oracle's any-S driver, and the workspace grows by the per-segment states."""
+    import xlstm_hip
+    from xlstm_hip.ops import chunkwise_workspace_bytes
+    x, st = _inputs(B, NH, S, DQK, DV, torch.bfloat16, seed=S + NH, with_state=with_state)
+    ws = chunkwise_workspace_bytes(B, NH, S, DQK, DV, 64, torch.bfloat16, algo="fused")
+    prep = ((B * NH * ((S + 63) // 64) * 1280 + 255) // 256) * 256
+    assert (ws > prep) == (B * NH * DV // 64 < 256 and (S + 63) // 64 >= 8)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, algo="fused")
+    q, k, v, i, f = (t.float() for t in x)
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got.cpu(), want, torch.bfloat16, f"split B{B} NH{NH} S{S} DQK{DQK} DV{DV} {name}")

@@ -5,8 +5,9 @@ device array (for callers that cannot allocate).
   shapes the fused algorithm does not take) before any GPU work;
 * GPU: through the C-ABI, two calls in a row (the second on a smaller input, so the array
   holds the first call's larger contents) each equal xl_mlstm_chunkwise_fwd with the fused
-  algorithm and a caller workspace, bit for bit (same kernels, same inputs), on h and on
-  the last C, n, m; and both also meet the bf16 parity bar against the CPU oracle.
+  algorithm and a caller workspace, on h and on the last C, n, m: bit for bit where that call
+  runs the same unsplit kernels, within the bf16 parity bar where it splits the sequence into
+  segments (few heads); and both also meet the bf16 parity bar against the CPU oracle.
 """
 
 import ctypes
@@ -90,7 +91,8 @@ def _run(lib, fn, x, B, NH, S, DQK, DV, workspace=None):
 def test_noalloc_matches_workspace_entry_point(lib, gpu_case):
     from oracle import mlstm as om
     dev = torch.device("cuda:0")
-    # second call smaller than the first: the array still holds the first call's gate prep
+    # second call smaller than the first: the array still holds the first call's gate prep;
+    # the first shape also makes the workspace entry point split the sequence, the second not
     for (B, NH, S, DQK, DV, seed) in ((2, 4, 1000, 256, 128, 11), (1, 2, 300, 128, 64, 12)):
         print(f"[noalloc] B{B} NH{NH} S{S} DQK{DQK} DV{DV} seed {seed}", flush=True)
         x = _inputs(B, NH, S, DQK, DV, seed, dev)
@@ -98,8 +100,16 @@ def test_noalloc_matches_workspace_entry_point(lib, gpu_case):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         want = _run(lib, lib.xl_mlstm_chunkwise_fwd, x, B, NH, S, DQK, DV, workspace=ws)
         got = _run(lib, lib.xl_mlstm_chunkwise_fwd_noalloc, x, B, NH, S, DQK, DV)
+        # with few heads the workspace entry point splits the sequence into segments (its
+        # workspace then holds per-segment states besides the gate prep); the static scratch
+        # holds the gate prep only, so the no-allocation call runs unsplit: the same kernels
+        # bit for bit when the other call does not split, the parity bar when it does
+        prep_only = ((B * NH * ((S + 63) // 64) * 1280 + 255) // 256) * 256
         for a, b, name in zip(got, want, ("h", "C", "n", "m")):
-            assert torch.equal(a, b), f"noalloc {name} differs from the workspace entry point"
+            if ws_bytes == prep_only:
+                assert torch.equal(a, b), f"noalloc {name} differs from the workspace entry point"
+            else:
+                assert_parity(a.cpu(), b.cpu().float(), torch.bfloat16, f"noalloc vs split {name}")
         # and both meet the parity bar against the oracle
         q, k, v, i, f, c0, n0, m0 = (t.cpu().float() for t in x)
         hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, c0, n0, m0[..., None], chunk_size=64)

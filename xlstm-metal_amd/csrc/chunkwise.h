@@ -16,6 +16,7 @@ struct ChunkwiseArgs {
   void* workspace;
   size_t workspace_bytes;
   void* stream;
+  int max_segments;  // fused algorithm: at most this many sequence segments (1: no split)
 };
 
 // Argument checks of xl_mlstm_chunkwise_fwd for the given algorithm (0 or an XL_ERR_* code).
@@ -28,7 +29,12 @@ int chunkwise_two_pass(const ChunkwiseArgs& a);
 // Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a
 // shape/dtype is covered (and why not, in `why`, when it is not).
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why);
-size_t chunkwise_fused_workspace(int B, int NH, int S);  // gate prep: 1280 bytes per 64-token chunk
+// Workspace of the fused algorithm: the gate prep (1280 bytes per 64-token chunk of every
+// head) and, when the sequence is split into segments (few heads), two sets of per-segment
+// states.  max_segments 1 disables the split.
+constexpr int kChunkwiseMaxSegments = 16;
+size_t chunkwise_fused_workspace(int B, int NH, int S, int DQK, int DV, int max_segments);
+int chunkwise_fused_segments(int B, int NH, int S, int DQK, int DV, int max_segments);
 int chunkwise_fused(const ChunkwiseArgs& a);
 
 }  // namespace xl

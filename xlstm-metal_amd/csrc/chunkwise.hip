@@ -55,7 +55,7 @@ extern "C" size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQ
   a.dtype_qkv = dtype_qkv; a.dtype_gates = dtype_qkv;
   int chosen = XL_CHUNKWISE_TWO_PASS;
   if (pick(a, algo, &chosen) != XL_OK) return 0;
-  return chosen == XL_CHUNKWISE_FUSED ? chunkwise_fused_workspace(B, NH, S)
+  return chosen == XL_CHUNKWISE_FUSED ? chunkwise_fused_workspace(B, NH, S, DQK, DV, kChunkwiseMaxSegments)
                                      : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
 }
 
@@ -91,14 +91,16 @@ extern "C" int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* 
   using namespace xl;
   clear_error();
   ChunkwiseArgs a = {q, k, v, i, f, c0, n0, m0, h, c_last, n_last, m_last, B, NH, S, DQK, DV, L,
-                     qk_scale, eps, dtype_qkv, dtype_gates, workspace, workspace_bytes, stream};
+                     qk_scale, eps, dtype_qkv, dtype_gates, workspace, workspace_bytes, stream,
+                     kChunkwiseMaxSegments};
   int rc = chunkwise_check_args(a, algo);
   if (rc) return rc;
   int chosen = XL_CHUNKWISE_TWO_PASS;
   rc = pick(a, algo, &chosen);
   if (rc) return rc;
   const bool fused = chosen == XL_CHUNKWISE_FUSED;
-  const size_t need = fused ? chunkwise_fused_workspace(B, NH, S) : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
+  const size_t need = fused ? chunkwise_fused_workspace(B, NH, S, DQK, DV, kChunkwiseMaxSegments)
+                            : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
   if (!workspace || workspace_bytes < need)
     return set_error(XL_ERR_WORKSPACE, "xl_mlstm_chunkwise_fwd: %s workspace needs %zu bytes, got %zu",
                      fused ? "fused" : "two-pass", need, workspace ? workspace_bytes : (size_t)0);

@@ -80,6 +80,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
 constexpr int PREP_STRIDE = 320;  // floats per chunk of gate prep: b, a, cummax(i - b), (i - b) log2e, [g, max a]
+constexpr int kMaxSegmentsDev = 16;  // most sequence segments of one call (few heads)
 constexpr int GROWS = 7;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G], alpha' bf16 hi | lo
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -231,13 +232,29 @@ struct Smem {
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int DQK>
+// Sequence segments (for few heads: B * NH * DV / 64 workgroups leave CUs idle).
+// The grid covers nseg segments of kc_per_seg chunks per (head, column tile).
+// Segment 0 starts from (c0, n0, m0) (zeros and m = 0 when absent, the
+// reference's zero state); segment s >= 1 starts from the s-1'th entry of
+// (sc, sn, sm) or, when sc is null, from the empty state (C = n = 0, m = -inf,
+// so its end state is the segment's own contribution).  With ec set, every
+// segment writes its end state to entry s of (ec, en, em); otherwise the last
+// segment writes (c_last, n_last, m_last).  STATES_ONLY launches skip q C and
+// the outputs (h is not written).
+struct SegArgs {
+  int nseg, kc_per_seg;
+  const float *sc, *sn, *sm;
+  float *ec, *en, *em;
+};
+
+template <int DQK, bool STATES_ONLY>
 __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const float* __restrict__ c0,
     const float* __restrict__ n0, const float* __restrict__ m0, bf16_t* __restrict__ h,
     float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last,
-    const float* __restrict__ prep, int S, int NC, int DV, int BNH, int nvtile, float qk_scale, float eps) {
+    const float* __restrict__ prep, int S, int NC, int DV, int BNH, int nvtile, float qk_scale, float eps,
+    SegArgs sg) {
   using SM = Smem<DQK>;
   constexpr int KPD = SM::KPD;
   constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
@@ -253,11 +270,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const LoOps lk = lo_ops();
 
   // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
-  const int nwg = BNH * nvtile;
+  const int nwg = BNH * nvtile * sg.nseg;
   int lin = blockIdx.x;
   if ((nwg & 7) == 0) lin = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
-  const int bh = lin / nvtile;
-  const int v0 = (lin - bh * nvtile) * DVT;
+  const int bhs = lin / nvtile;  // segment * BNH + head
+  const int v0 = (lin - bhs * nvtile) * DVT;
+  const int seg = bhs / BNH, bh = bhs - seg * BNH;
+  const int kc0 = seg * sg.kc_per_seg, kc1 = min(NC, kc0 + sg.kc_per_seg);  // this segment's chunks
+  // initial state of this segment (see SegArgs)
+  const size_t cst = (size_t)BNH * DQK * DV, nst = (size_t)BNH * DQK;
+  const float* ci = seg == 0 ? c0 : (sg.sc ? sg.sc + (seg - 1) * cst : nullptr);
+  const float* ni = seg == 0 ? n0 : (sg.sn ? sg.sn + (seg - 1) * nst : nullptr);
+  const float m_init = seg == 0 ? (m0 ? m0[bh] : 0.f) : (sg.sm ? sg.sm[(seg - 1) * BNH + bh] : -INFINITY);
+  // where the end state goes: every segment's (ec) or the last segment's (c_last)
+  float* ce = sg.ec ? sg.ec + seg * cst : (seg == sg.nseg - 1 ? c_last : nullptr);
+  float* ne = sg.ec ? sg.en + seg * nst : n_last;
+  float* me = sg.ec ? sg.em + (size_t)seg * BNH : m_last;
 
   char* kn = smem + SM::KN;
   char* vn = smem + SM::VN;
@@ -272,7 +300,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   bf16_t* hh = h + (size_t)bh * S * DV;
   auto rows_of = [&](int kc) { return min(L, S - kc * L); };  // valid rows of chunk kc
   auto q_rsrc = [&](int kc) { return chunk_rsrc(qh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2); };
-  const float m_init = m0 ? m0[bh] : 0.f;
 
   // ---- K staging: piece u of thread tid = u*NTHREADS + tid -> row piece / (DQK/8), 16-byte column group
   // (rows past S read as 0: those tokens carry alpha' = 0 and gate weight
@@ -372,13 +399,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
     for (int dt = 0; dt < NTO; ++dt)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        nacc[dt][e] = (n0 && (r16 & 1) == 0) ? n0[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] : 0.f;
-    store_nparts(0);
+        nacc[dt][e] = (ni && (r16 & 1) == 0) ? ni[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] : 0.f;
+    store_nparts(kc0 & 1);
   }
   if (w == NSW) {
     float pv[5];
-    prep_load(0, pv);
-    gate_rows(0, pv);
+    prep_load(kc0, pv);
+    gate_rows(kc0, pv);
   }
   __syncthreads();  // B0: gate rows and n parts of chunk 0
 
@@ -407,7 +434,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          acc[dt][vt][e] = c0 ? c0[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] : 0.f;
+          acc[dt][vt][e] = ci ? ci[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] : 0.f;
 
     // V staging (state threads): rows t0 = 4*(tid>>4) + ((tid>>3)&1) and t0 + 2, columns 8*(tid&7)
     const int vrow = 4 * (tid >> 4) + ((tid >> 3) & 1), vcol = 8 * (tid & 7);
@@ -428,10 +455,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int s = 0; s < QKS; ++s)
           Qs[tt][s] = ld16(rq, (uint32_t)(((32 * tt + l32) * DQK + dw0 + 8 * hh + 16 * s) * 2));
     };
-    load_k(0, Kst);
-    load_v(0);
-    load_qs(0);
-    for (int kc = 0; kc < NC; ++kc) {
+    load_k(kc0, Kst);
+    load_v(kc0);
+    if (!STATES_ONLY) load_qs(kc0);
+    for (int kc = kc0; kc < kc1; ++kc) {
       const float* gb = gbuf + (kc & 1) * GROWS * 64;
       store_k(Kst);
       // V natural and alpha' V hi / lo (natural layout, 16-byte rows)
@@ -451,7 +478,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 128 + 2 * vcol) = lv;
       }
       __syncthreads();  // B1: the chunk's tiles are visible; the previous chunk's partials have been read
-      if (kc + 1 < NC) {  // staging registers are free: prefetch (q after its last use below)
+      if (kc + 1 < kc1) {  // staging registers are free: prefetch (q after its last use below)
         load_k(kc + 1, Kst);
         load_v(kc + 1);
       }
@@ -462,7 +489,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       // Software pipelined: the split of k-step q+1 (VALU) is interleaved with
       // the four MFMAs of k-step q, and the partials of column tile 0 are
       // stored one k-step into tile 1, when their MFMAs have retired.
-      {
+      if (!STATES_ONLY) {
         constexpr int NQ = 2 * QKS;
         bf16x8 bsp[2][2];
         f32x16 P[2][2];
@@ -505,7 +532,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         }
         store_p(1);
       }
-      if (kc + 1 < NC) load_qs(kc + 1);
+      if (!STATES_ONLY && kc + 1 < kc1) load_qs(kc + 1);
       if (gb[323] != 0.f) {  // renormalise the stored state (wave-uniform)
         const float sc = gb[320];
 #pragma unroll
@@ -546,8 +573,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       __syncthreads();  // B2: partials complete; the chunk's tiles may be overwritten
     }
     // ---- final states (undo the deferred rescale)
-    if (c_last) {
-      const float* gl = gbuf + ((NC - 1) & 1) * GROWS * 64;
+    if (ce) {
+      const float* gl = gbuf + ((kc1 - 1) & 1) * GROWS * 64;
       const float sc = exp_(gl[322]);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
@@ -555,8 +582,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
-            c_last[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] = acc[dt][vt][e] * sc;
-      if (v0 == 0 && tid == 0) m_last[bh] = gl[321];
+            ce[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] = acc[dt][vt][e] * sc;
+      if (v0 == 0 && tid == 0) me[bh] = gl[321];
     }
   } else {
     // =====================================================================
@@ -578,16 +605,36 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
 #pragma unroll
       for (int p = 0; p < KPD; ++p) Qf[p] = ld16(rq, (uint32_t)(((16 * o + r16) * DQK + 8 * g + 32 * p) * 2));
     };
-    load_k(0, Kst);
-    load_q(0);
-    for (int kc = 0; kc < NC; ++kc) {
+    load_k(kc0, Kst);
+    if (!STATES_ONLY) load_q(kc0);
+    for (int kc = kc0; kc < kc1; ++kc) {
       const float* gb = gbuf + (kc & 1) * GROWS * 64;
       const bf16_t* nbk = nbuf + (kc & 1) * 4 * SM::NB_PITCH;
       store_k(Kst);
       __syncthreads();  // B1
-      if (kc + 1 < NC) {
+      if (kc + 1 < kc1) {
         load_k(kc + 1, Kst);
         if (o == 0) prep_load(kc + 1, pv);
+      }
+      if (STATES_ONLY) {  // the n update and the next gate rows only
+        if (gb[323] != 0.f) {
+          const float sc = gb[320];
+#pragma unroll
+          for (int dt = 0; dt < NTO; ++dt) nacc[dt] *= sc;
+        }
+        const uint16_t* ar = reinterpret_cast<const uint16_t*>(gb + 384) + 64 * (r16 & 1);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const bf16x8 ab = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ar + 32 * p + 8 * g));
+#pragma unroll
+          for (int dt = 0; dt < NTO; ++dt) {
+            const char* base = kn + (32 * p + 8 * g + 2 * (r16 >> 2)) * SM::KN_PITCH + 2 * (nd0 + 16 * dt + 4 * (r16 & 3));
+            nacc[dt] = mfma(tr8(base, base + SM::KN_PITCH), ab, nacc[dt]);
+          }
+        }
+        if (o == 0 && kc + 1 < kc1) gate_rows(kc + 1, pv);
+        __syncthreads();  // B2
+        continue;
       }
 
       // S^T tiles over the whole DQK: A = K rows 16jt + r16, B = q rows; only the
@@ -615,7 +662,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           if (jt == 4 || jt <= o)  // j-tiles above the diagonal are all masked (compile-time)
             Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
       }
-      if (kc + 1 < NC) load_q(kc + 1);  // q fragments are dead: prefetch
+      if (kc + 1 < kc1) load_q(kc + 1);  // q fragments are dead: prefetch
       const float qn = (Sacc[4][0] + Sacc[4][1]) + (Sacc[4][2] + Sacc[4][3]);  // q . n (stored state)
       // gate the scores of row i = 16o + r16, then M [V | 1] with M split hi + lo
       const int i = 16 * o + r16;
@@ -676,7 +723,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       }
       // the gate wave forms the gate rows of chunk kc + 1 (buffer (kc + 1) & 1,
       // last read before B2 of the previous chunk)
-      if (o == 0 && kc + 1 < NC) gate_rows(kc + 1, pv);
+      if (o == 0 && kc + 1 < kc1) gate_rows(kc + 1, pv);
       __syncthreads();  // B2: the state waves' partial Q C of this chunk are complete
       // Q C of row 16o + r16, columns vcol_of(vq, 4g + e): sum of the four state
       // waves' partials (two 16-byte runs of 4 columns per tile pair)
@@ -712,8 +759,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       }
     }
     // ---- final n (undo the deferred rescale): even + odd column, lanes r16 = 0, 1
-    if (c_last && v0 == 0) {
-      const float* gl = gbuf + ((NC - 1) & 1) * GROWS * 64;
+    if (ce && v0 == 0) {
+      const float* gl = gbuf + ((kc1 - 1) & 1) * GROWS * 64;
       const float sc = exp_(gl[322]);
 #pragma unroll
       for (int dt = 0; dt < NTO; ++dt)
@@ -722,7 +769,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           const float na = nacc[dt][e];
           // quad_perm [1, 0, 3, 2]: lane 4q gets lane 4q + 1
           const float nb = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, na), 0xB1, 0xf, 0xf, false));
-          if (r16 == 0) n_last[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] = (na + nb) * sc;
+          if (r16 == 0) ne[(size_t)bh * DQK + nd0 + 16 * dt + 4 * g + e] = (na + nb) * sc;
         }
     }
     };
@@ -735,23 +782,140 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   }
 }
 
+// Start states of segments 1 .. P-1 from the end states of the first pass:
+// start(1) = E_0 (segment 0 ran from the caller's initial state), and
+// start(s + 1) = compose(start(s), E_s), E_s being segment s's own
+// contribution (run from the empty state) and g_s its total log forget gate
+// (the sum of its chunks' g from the gate prep):
+//   m' = max(g_s + m, m_s),  X' = e^{g_s + m - m'} X + e^{m_s - m'} X_s  (X = C, n).
+// This is the inter-chunk recurrence of fw.py:115-133 applied to whole
+// segments.  Block (head, part): lanes 0 .. P-2 sum their segment's g, lane 0
+// runs the m recurrence, then one float4 of [C | n] per thread.
+__global__ __launch_bounds__(256) void segment_combine_kernel(const float* __restrict__ prep, const float* __restrict__ ec,
+                                                              const float* __restrict__ en, const float* __restrict__ em,
+                                                              float* __restrict__ sc, float* __restrict__ sn,
+                                                              float* __restrict__ sm, int P, int kc_per_seg, int NC,
+                                                              int BNH, int DQK, int DV) {
+  __shared__ float s_g[kMaxSegmentsDev], s_a[kMaxSegmentsDev], s_b[kMaxSegmentsDev];
+  const int bh = blockIdx.y;
+  const int t = threadIdx.x;
+  if (t < P - 1) {
+    float gsum = 0.f;
+    const int c1 = min(NC, (t + 1) * kc_per_seg);
+    for (int c = t * kc_per_seg; c < c1; ++c) gsum += prep[((size_t)bh * NC + c) * PREP_STRIDE + 256];
+    s_g[t] = gsum;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float m = em[bh];  // start(1) = E_0
+    if (blockIdx.x == 0) sm[bh] = m;
+    for (int sgi = 1; sgi + 1 < P; ++sgi) {
+      const float ms = em[(size_t)sgi * BNH + bh];
+      const float mn = fmaxf(s_g[sgi] + m, ms);
+      s_a[sgi] = exp_(s_g[sgi] + m - mn);
+      s_b[sgi] = exp_(ms - mn);
+      m = mn;
+      if (blockIdx.x == 0) sm[(size_t)sgi * BNH + bh] = m;
+    }
+  }
+  __syncthreads();
+  const size_t cst = (size_t)BNH * DQK * DV, nst = (size_t)BNH * DQK;
+  const int per4 = (DQK * DV + DQK) / 4;  // float4 elements of [C | n] per head
+  {
+    const int e4 = blockIdx.x * 256 + t;
+    if (e4 >= per4) return;
+    const bool isc = e4 < DQK * DV / 4;
+    const size_t off = isc ? (size_t)bh * DQK * DV + 4 * (size_t)e4 : (size_t)bh * DQK + 4 * (size_t)(e4 - DQK * DV / 4);
+    const float* src = isc ? ec : en;
+    float* dst = isc ? sc : sn;
+    const size_t st = isc ? cst : nst;
+    f32x4 x = *reinterpret_cast<const f32x4*>(src + off);
+    *reinterpret_cast<f32x4*>(dst + off) = x;
+    for (int sgi = 1; sgi + 1 < P; ++sgi) {
+      x = s_a[sgi] * x + s_b[sgi] * *reinterpret_cast<const f32x4*>(src + sgi * st + off);
+      *reinterpret_cast<f32x4*>(dst + sgi * st + off) = x;
+    }
+  }
+}
+
+// Workgroups the fused kernel needs to occupy an MI355X (256 CUs, one
+// workgroup per CU).  With fewer (head, column tile) pairs the sequence is
+// split into segments: P = min(256 / pairs, chunks / 4, 16).
+constexpr int kTargetWorkgroups = 256;
+constexpr int kMaxSegments = kMaxSegmentsDev;
+
+static int segments_for(int B, int NH, int S, int DV, int max_seg) {
+  const long long pairs = (long long)B * NH * (DV / DVT);
+  const int NC = (S + L - 1) / L;
+  if (pairs <= 0 || pairs >= kTargetWorkgroups || max_seg < 2) return 1;
+  int P = (int)(kTargetWorkgroups / pairs);
+  P = min(P, NC / 4);
+  P = min(P, min(kMaxSegments, max_seg));
+  return P < 2 ? 1 : P;
+}
+
+struct Layout {  // workspace: gate prep, then (split only) the end states and start states
+  int P, kc_per_seg;
+  size_t prep_bytes, states_bytes, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+static Layout layout_for(int B, int NH, int S, int DQK, int DV, int max_seg) {
+  Layout l;
+  const int NC = (S + L - 1) / L;
+  l.P = segments_for(B, NH, S, DV, max_seg);
+  l.kc_per_seg = (NC + l.P - 1) / l.P;
+  l.P = (NC + l.kc_per_seg - 1) / l.kc_per_seg;  // no empty segment
+  l.prep_bytes = align256((size_t)B * NH * NC * PREP_STRIDE * sizeof(float));
+  const size_t per = (size_t)B * NH * ((size_t)DQK * DV + DQK + 1);
+  l.states_bytes = l.P > 1 ? align256((size_t)(l.P - 1) * per * sizeof(float)) : 0;
+  l.total = l.prep_bytes + 2 * l.states_bytes;
+  return l;
+}
+
 template <typename TG, int DQK>
 static int launch(const ChunkwiseArgs& A) {
   const int BNH = A.B * A.NH;
   const int nvtile = A.DV / DVT;
   const int NC = (A.S + L - 1) / L;  // the last chunk may be ragged
+  const Layout lay = layout_for(A.B, A.NH, A.S, A.DQK, A.DV, A.max_segments);
+  hipStream_t st = (hipStream_t)A.stream;
   float* prep = (float*)A.workspace;
   const int total = BNH * NC;
-  hipLaunchKernelGGL(gate_prep_kernel<TG>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, (hipStream_t)A.stream,
-                     (const TG*)A.i, (const TG*)A.f, prep, total, NC, A.S);
-  auto kern = chunkwise_fused_kernel<DQK>;
+  hipLaunchKernelGGL(gate_prep_kernel<TG>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, st, (const TG*)A.i,
+                     (const TG*)A.f, prep, total, NC, A.S);
   const size_t smem = Smem<DQK>::BYTES;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  if (e != hipSuccess)
-    return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvtile)), dim3(NTHREADS), smem, (hipStream_t)A.stream,
-                     (const bf16_t*)A.q, (const bf16_t*)A.k, (const bf16_t*)A.v, A.c0, A.n0, A.m0, (bf16_t*)A.h,
-                     A.c_last, A.n_last, A.m_last, prep, A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps);
+  for (auto kern : {chunkwise_fused_kernel<DQK, false>, chunkwise_fused_kernel<DQK, true>}) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess)
+      return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
+  }
+  const bf16_t *q = (const bf16_t*)A.q, *k = (const bf16_t*)A.k, *v = (const bf16_t*)A.v;
+  SegArgs sg = {1, NC, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  if (lay.P > 1) {
+    // pass 1: every segment but the last, states only (segment 0 from the caller's initial
+    // state, the others from the empty state), end states into the workspace
+    const size_t cst = (size_t)BNH * A.DQK * A.DV, nst = (size_t)BNH * A.DQK;
+    char* base = (char*)A.workspace + lay.prep_bytes;
+    float* ec = (float*)base;
+    float* en = ec + (lay.P - 1) * cst;
+    float* em = en + (lay.P - 1) * nst;
+    float* scs = (float*)(base + lay.states_bytes);
+    float* sns = scs + (lay.P - 1) * cst;
+    float* sms = sns + (lay.P - 1) * nst;
+    SegArgs s1 = {lay.P - 1, lay.kc_per_seg, nullptr, nullptr, nullptr, ec, en, em};
+    hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, true>), dim3((unsigned)(BNH * nvtile * (lay.P - 1))),
+                       dim3(NTHREADS), smem, st, q, k, v, A.c0, A.n0, A.m0, (bf16_t*)nullptr, nullptr, nullptr,
+                       nullptr, prep, A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, s1);
+    const int per4 = (A.DQK * A.DV + A.DQK) / 4;
+    hipLaunchKernelGGL(segment_combine_kernel, dim3((unsigned)((per4 + 255) / 256), (unsigned)BNH), dim3(256), 0,
+                       st, prep, ec, en, em, scs, sns, sms, lay.P, lay.kc_per_seg, NC, BNH, A.DQK, A.DV);
+    sg = SegArgs{lay.P, lay.kc_per_seg, scs, sns, sms, nullptr, nullptr, nullptr};
+  }
+  hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, false>), dim3((unsigned)(BNH * nvtile * sg.nseg)), dim3(NTHREADS),
+                     smem, st, q, k, v, A.c0, A.n0, A.m0, (bf16_t*)A.h, A.c_last, A.n_last, A.m_last, prep, A.S, NC,
+                     A.DV, BNH, nvtile, A.qk_scale, A.eps, sg);
   return check_launch("xl_mlstm_chunkwise_fwd(fused)");
 }
 
@@ -762,8 +926,12 @@ static int launch_d(const ChunkwiseArgs& A) {
 
 }  // namespace fused
 
-size_t chunkwise_fused_workspace(int B, int NH, int S) {
-  return ((size_t)B * NH * ((S + fused::L - 1) / fused::L) * fused::PREP_STRIDE * sizeof(float) + 255) / 256 * 256;
+size_t chunkwise_fused_workspace(int B, int NH, int S, int DQK, int DV, int max_segments) {
+  return fused::layout_for(B, NH, S, DQK, DV, max_segments).total;
+}
+
+int chunkwise_fused_segments(int B, int NH, int S, int DQK, int DV, int max_segments) {
+  return fused::layout_for(B, NH, S, DQK, DV, max_segments).P;
 }
 
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why) {

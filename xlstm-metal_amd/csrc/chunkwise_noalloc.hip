@@ -66,20 +66,21 @@ extern "C" int xl_mlstm_chunkwise_fwd_noalloc(const void* q, const void* k, cons
                                               int dtype_qkv, int dtype_gates, void* stream) {
   using namespace xl;
   clear_error();
+  // no sequence split: the static scratch holds the gate prep only
   ChunkwiseArgs a = {q, k, v, i, f, c0, n0, m0, h, c_last, n_last, m_last, B, NH, S, DQK, DV, L,
-                     qk_scale, eps, dtype_qkv, dtype_gates, nullptr, 0, stream};
+                     qk_scale, eps, dtype_qkv, dtype_gates, nullptr, 0, stream, 1};
   int rc = chunkwise_check_args(a, XL_CHUNKWISE_FUSED);
   if (rc) return rc;
   const char* why = nullptr;
   if (!chunkwise_fused_supported(a, &why))
     return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_fwd_noalloc: fused algorithm unsupported here: %s", why);
-  const size_t need = chunkwise_fused_workspace(B, NH, S);
+  const size_t need = chunkwise_fused_workspace(B, NH, S, DQK, DV, 1);
   if (need > (size_t)XL_NOALLOC_SCRATCH_BYTES)
     return set_error(XL_ERR_UNSUPPORTED,
                      "xl_mlstm_chunkwise_fwd_noalloc: B*NH*ceil(S/64) = %lld chunks need %zu bytes of scratch, "
                      "more than the static %zu (at most %zu chunks); use xl_mlstm_chunkwise_fwd with a workspace",
                      (long long)B * NH * ((S + 63) / 64), need, (size_t)XL_NOALLOC_SCRATCH_BYTES,
-                     (size_t)XL_NOALLOC_SCRATCH_BYTES / chunkwise_fused_workspace(1, 1, 64));
+                     (size_t)XL_NOALLOC_SCRATCH_BYTES / chunkwise_fused_workspace(1, 1, 64, DQK, DV, 1));
   void* ws = nullptr;
   rc = scratch_address(stream, &ws);
   if (rc) return rc;
