@@ -50,7 +50,9 @@ def test_cfg1_decode_step_bf16(gpu_case):
     assert relerr(C, Cr) <= 1e-6 and relerr(n, nr) <= 1e-6
 
 
-@pytest.mark.parametrize("shape", [(2, 3, 64, 64), (1, 1, 48, 72), (3, 2, 512, 260), (1, 4, 16, 4)])
+@pytest.mark.parametrize("shape", [(2, 3, 64, 64), (1, 1, 48, 72), (3, 2, 512, 260), (1, 4, 16, 4),
+                                   # 256-column tiles (DV a multiple of 256, >= 256 workgroups, DQK <= 256)
+                                   (32, 8, 64, 256), (64, 4, 128, 256), (16, 16, 200, 512)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_step_shapes_dtypes(gpu_case, shape, dtype):
     import xlstm_hip
