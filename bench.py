@@ -586,6 +586,23 @@ def bench_stack(args, dev, which):
     e1.record(stream)
     torch.cuda.synchronize(dev)
     dec_ms = e0.elapsed_time(e1) / steps
+    # the decode step's logit projection: the fused lm_head + soft-cap kernel against torch's Linear
+    # (hipBLASLt) then the soft_cap kernel, on the same normalised rows and weights
+    xl = torch.randn(B, 1, cfg.d_model, generator=g, device=dev).to(cfg.dtype)
+    lm_us = {}
+    for fused in (True, False):
+        model.fused_lm_head = fused
+        for _ in range(5):
+            model.logits(xl)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(50):
+            model.logits(xl)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        lm_us[fused] = e0.elapsed_time(e1) * 1e3 / 50
+    model.fused_lm_head = True
+    w_bytes = model.lm_head.weight.numel() * model.lm_head.weight.element_size()
     nparams = sum(p.numel() for p in model.parameters())
     n_sl = sum(cfg.is_slstm(b) for b in range(cfg.num_blocks))
     del model, states, dg
@@ -596,6 +613,11 @@ def bench_stack(args, dev, which):
             "prefill_ms": pre_ms, "prefill_tokens_per_s": B * S / (pre_ms * 1e-3),
             "decode_ms_per_step": dec_ms, "decode_tokens_per_s": B / (dec_ms * 1e-3), "decode_steps": steps,
             "decode_mode": "hip_graph (one replay per token)",
+            "lm_head_decode": {"rows": B, "weight_bytes": w_bytes,
+                               "final_norm_plus_lm_head_softcap_fused_us": lm_us[True],
+                               "final_norm_plus_linear_then_soft_cap_us": lm_us[False],
+                               "fused_weight_stream_TBps": w_bytes / (lm_us[True] * 1e-6) / 1e12,
+                               "note": "eager, 50 calls, HIP events; both include the final RMSNorm"},
             "data": "synthetic: random token ids, weights N(0, 0.02), forget-gate bias 3"}
 
 

@@ -263,6 +263,25 @@ int xl_mh_rmsnorm_gate_fwd(const void* h, const void* weight, const void* o_prea
 int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias, void* y,
                              int M, int D, int G, float cap, int cap_rounding, int dtype, void* stream);
 
+/*
+ * Logit projection with the soft-cap epilogue: y[m, v] = cap * tanh(z / cap),
+ * z = (sum_d x[m, d] w[v, d]) rounded to the dtype, the soft-cap in float32 and
+ * rounded once.  Replaces soft_cap(lm_head(out_norm(x)), output_logit_soft_cap)
+ * for the rows a decoder needs logits of (a decode step's tokens, a prompt's
+ * last positions): nn.Linear(embedding_dim, vocab_size, bias=False)
+ * (xlstm_metal/torch_native/models/wired_xlstm.py:123-131,176) followed by
+ * soft_cap (xlstm_metal/torch_native/generate.py:131;
+ * xlstm_metal/mlx_jit/generate.py:201).  The weights are streamed from HBM once
+ * for all M rows.
+ *   x [M, D], w [V, D] (nn.Linear's weight), y [M, V]; bf16 or f16 (float32:
+ *   XL_ERR_UNSUPPORTED); M <= 16 and M * (D + 8) * 2 <= 160 KiB (the token
+ *   rows are staged in LDS; logits of every position of a prompt are a GEMM:
+ *   XL_ERR_UNSUPPORTED); D a multiple of 8; x and w 16-byte aligned; cap <= 0:
+ *   no soft-cap.
+ */
+int xl_lm_head_softcap_fwd(const void* x, const void* weight, void* y, int M, int D, int V, float cap,
+                           int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,6 +94,16 @@ __device__ __forceinline__ float tanh_f32(float x) {
   return copysignf(t, x);
 }
 
+// cap * tanh(x / cap) for a 16-bit output: tanh(z) = 1 - 2 / (1 + e^{2z}) from
+// the hardware exp2 and reciprocal (absolute error < 5e-7, far under half an
+// ulp), and z itself below |z| = 2^-6, where the subtraction cancels (relative
+// error z^2 / 3 < 1e-4).
+__device__ __forceinline__ float soft_cap16(float x, float cap, float inv_cap) {
+  const float z = x * inv_cap;
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * 2.8853900817779268f));
+  return cap * (fabsf(z) < 0.015625f ? z : t);
+}
+
 // ------------------------------------------------------- wavefront reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -38,15 +38,6 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                   0);
 }
 
-// cap * tanh(x / cap) with tanh(z) = 1 - 2 / (1 + e^{2z}) (hardware exp2 and
-// reciprocal) and z itself below |z| = 2^-6, where the subtraction cancels
-// (relative error < 1e-4, far under a 16-bit rounding).
-__device__ __forceinline__ float soft_cap16(float x, float cap, float inv_cap) {
-  const float z = x * inv_cap;
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * 2.8853900817779268f));
-  return cap * (fabsf(z) < 0.015625f ? z : t);
-}
-
 constexpr int GP_WAVES = 4;  // waves per 16-row tile, each over a quarter of the k-steps
 constexpr int GP_BLOCK = 64 * GP_WAVES;
 

@@ -3,7 +3,8 @@
 Drop-in for the torch-native kernel API of MLXPorts/xLSTM-metal: chunkwise
 mLSTM prefill, recurrent decode step and sequence, sLSTM step and sequence,
 the sLSTM layer's causal conv1d + SiLU and per-head GroupNorm, the mLSTM
-output cell's multi-head RMSNorm x sigmoid(o), and soft_cap,
+output cell's multi-head RMSNorm x sigmoid(o), soft_cap and the logit
+projection with its soft-cap epilogue,
 each a ``torch.library`` op (``xlstm_hip::*``) calling hand-written HIP
 kernels in ``lib/libxlstm_hip.so`` through a C-ABI.
 """
@@ -24,7 +25,7 @@ from .recurrent import (
 )
 from .slstm import sLSTMStepwiseKernelCell, slstm_sequence, slstm_step, slstm_step_pytorch
 from .slstm_layers import CausalConv1d, causal_conv1d, group_norm, sLSTMOutputCell, sLSTMProjectionCell
-from .soft_cap import SoftCapCell, soft_cap
+from .soft_cap import SoftCapCell, lm_head_softcap, soft_cap
 
 LIB_PATH = _lib.LIB_PATH
 
@@ -39,6 +40,7 @@ __all__ = [
     "mlstm_recurrent_step__native_fw", "mlstm_recurrent_step_", "mlstm_recurrent_sequence__native_fw",
     "mLSTMRecurrentKernelCell",
     "slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell", "soft_cap", "SoftCapCell",
+    "lm_head_softcap",
     "causal_conv1d", "group_norm", "CausalConv1d", "sLSTMProjectionCell", "sLSTMOutputCell",
     "mh_rmsnorm_gate", "MultiHeadRMSNorm", "MultiHeadLayerNorm", "mLSTMOutputCell", "gate_proj_softcap",
     "mLSTMProjectionCell",

@@ -42,6 +42,7 @@ SIGNATURES = {
     "xl_group_norm_fwd": (_i, [_vp] * 4 + [_i64, _i, _i, _f, _i, _vp]),
     "xl_mh_rmsnorm_gate_fwd": (_i, [_vp] * 4 + [_i] * 5 + [_f, _i, _vp]),
     "xl_gate_proj_softcap_fwd": (_i, [_vp] * 4 + [_i] * 3 + [_f, _i, _i, _vp]),
+    "xl_lm_head_softcap_fwd": (_i, [_vp] * 3 + [_i] * 3 + [_f, _i, _vp]),
 }
 
 ABI_VERSION = 2

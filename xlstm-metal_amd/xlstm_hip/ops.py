@@ -20,7 +20,7 @@ from . import _lib
 __all__ = [
     "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
     "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "mh_rmsnorm_gate_op",
-    "gate_proj_softcap_op", "chunkwise_workspace_bytes", "chunkwise_algorithm",
+    "gate_proj_softcap_op", "lm_head_softcap_op", "chunkwise_workspace_bytes", "chunkwise_algorithm",
 ]
 
 _EMPTY_SHAPE = (0,)
@@ -474,4 +474,37 @@ def gate_proj_softcap_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], cap:
 
 @gate_proj_softcap_op.register_fake
 def _(x, weight, bias, cap, cap_rounding=0):
+    return x.new_empty(tuple(x.shape[:-1]) + (weight.shape[0],))
+
+
+# ------------------------------------------- logit projection + soft-cap epilogue
+LM_HEAD_MAX_ROWS = 16
+LM_HEAD_MAX_LDS = 160 * 1024  # the kernel stages rows * (D + 8) 16-bit values in LDS
+
+
+@torch.library.custom_op("xlstm_hip::lm_head_softcap", mutates_args=())
+def lm_head_softcap_op(x: Tensor, weight: Tensor, cap: float) -> Tensor:
+    what = "lm_head_softcap"
+    _lib.require_gpu(x, weight, what=what)
+    _check(x.dim() >= 1 and weight.dim() == 2 and weight.shape[1] == x.shape[-1], what,
+           f"weight must be (V, D) with D = x.shape[-1], got {tuple(weight.shape)} for x {tuple(x.shape)}")
+    _check(weight.dtype == x.dtype, what, "x and weight must share a dtype")
+    V, D = weight.shape
+    lead = tuple(x.shape[:-1])
+    M = 1
+    for d in lead:
+        M *= d
+    _check(M <= LM_HEAD_MAX_ROWS, what, f"{M} rows (at most {LM_HEAD_MAX_ROWS}; logits of every position are a "
+                                        "GEMM: use the Linear and soft_cap)")
+    _check(M * (D + 8) * 2 <= LM_HEAD_MAX_LDS, what, f"{M} rows of D={D} exceed the kernel's LDS staging")
+    x2, w = _prep(x.reshape(M, D)), _prep(weight)
+    y = torch.empty(lead + (V,), dtype=x.dtype, device=x.device)
+    rc = _lib.load().xl_lm_head_softcap_fwd(x2.data_ptr(), w.data_ptr(), y.data_ptr(), M, D, V, float(cap),
+                                            _lib.dtype_code(x, what), _lib.stream_of(x))
+    _lib.check(rc, what)
+    return y
+
+
+@lm_head_softcap_op.register_fake
+def _(x, weight, cap):
     return x.new_empty(tuple(x.shape[:-1]) + (weight.shape[0],))

@@ -15,8 +15,10 @@ the gate soft-cap) -> the chunkwise kernel over the prompt (the any-length wrapp
 recurrent step kernel per decoded token -> mLSTMOutputCell (``mh_rmsnorm_gate_kernel`` with
 sigma(o), then out_proj).  The sLSTM layer is sLSTMProjectionCell (conv1d + SiLU kernel, gate
 kernels, z Linear) -> the sLSTM sequence kernel over the prompt and the step kernel per token
--> sLSTMOutputCell (``group_norm_kernel``, out_proj).  Projections, FFN, norms, embedding and
-lm_head are torch (hipBLASLt GEMMs); every mLSTM/sLSTM kernel is this library's.
+-> sLSTMOutputCell (``group_norm_kernel``, out_proj).  The lm_head and the logit soft-cap are
+one kernel of this library (``lm_head_softcap``; ``fused_lm_head = False`` runs torch's Linear and
+then the soft_cap kernel instead).  Projections, FFN, norms and embedding are torch (hipBLASLt
+GEMMs); every mLSTM/sLSTM kernel is this library's.
 
 Weights are N(0, init_std) in the model dtype (there is no checkpoint); the mLSTM forget-gate
 bias starts at +3 and the input-gate bias at 0, so the gates sit where a trained model keeps
@@ -43,7 +45,7 @@ from .mlstm_layers import mLSTMOutputCell, mLSTMProjectionCell
 from .recurrent import mlstm_recurrent_step_
 from .slstm import slstm_sequence, slstm_step
 from .slstm_layers import sLSTMOutputCell, sLSTMProjectionCell
-from .soft_cap import soft_cap
+from .soft_cap import lm_head_softcap, soft_cap
 
 __all__ = ["StackConfig", "CFG3_STACK", "CFG4_STACK", "xLSTMStack", "DecodeGraph"]
 
@@ -227,6 +229,8 @@ class xLSTMStack(nn.Module):
             [_sLSTMBlock(cfg) if cfg.is_slstm(b) else _mLSTMBlock(cfg) for b in range(cfg.num_blocks)])
         self.out_norm = _RMSNorm(cfg.d_model, cfg.norm_eps)
         self.lm_head = nn.Linear(cfg.d_model, cfg.vocab, bias=False)
+        # the lm_head with the soft-cap in its epilogue (False: torch's Linear, then soft_cap)
+        self.fused_lm_head = True
 
     @classmethod
     def random(cls, cfg: StackConfig, device, seed: int = 0) -> "xLSTMStack":
@@ -248,7 +252,10 @@ class xLSTMStack(nn.Module):
         return model.eval()
 
     def logits(self, x: Tensor) -> Tensor:
-        return soft_cap(self.lm_head(self.out_norm(x)), self.cfg.logit_soft_cap)
+        xn = self.out_norm(x)
+        if self.fused_lm_head:
+            return lm_head_softcap(xn, self.lm_head.weight, self.cfg.logit_soft_cap)
+        return soft_cap(self.lm_head(xn), self.cfg.logit_soft_cap)
 
     @torch.no_grad()
     def prefill(self, tokens: Tensor):
