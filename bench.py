@@ -27,9 +27,13 @@ measure the remaining rows of the path; `slstm_conv1d_silu` and
 config 4 (conv K 4 + SiLU over [8, 4096, 2048]; GroupNorm NH 4 x H 512), and
 `mlstm_output_gate` the mLSTM output cell's RMSNorm x sigmoid(o) on config 2's
 kernel output, `slstm_gate_proj` config 4's i/f gate projection with its
-soft-cap (beside the reference's Linear + soft-cap composition on the GPU).  Each
-is timed like the headline (cache flush, HIP graph replay, HIP events) and
-reported against HBM.
+soft-cap (beside the reference's Linear + soft-cap composition on the GPU), and
+`chunkwise_bwd` the chunkwise backward on config 2's shape (float32 arithmetic,
+against the fp32 peak).  Each is timed like the headline (cache flush, HIP graph
+replay, HIP events) and reported against HBM.  `cfg3_stack` / `cfg4_stack` run
+the random-init stacks end to end (prefill and graph-replayed greedy decode
+tokens/s, and the decode step's lm_head with its soft-cap against hipBLASLt's
+Linear then the soft-cap kernel).
 
 HBM traffic (`roofline.traffic`) cannot be measured from inside the process:
 it comes from two rocprofv3 --pmc passes over this script (FETCH_SIZE, then
@@ -64,6 +68,7 @@ sys.path.insert(0, ROOT)
 import torch  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 PREFILL_KERNEL = "chunkwise_fused_kernel"
@@ -526,6 +531,39 @@ def bench_cfg3_heads(args, dev):
             "unsplit_us_per_call": 1e3 * tu["ms"], "split_speedup": tu["ms"] / t["ms"]}
 
 
+def bwd_flops(B, NH, S, DQK, DV, L):
+    """FLOP of the reference's custom backward as xl_mlstm_chunkwise_bwd runs it, per chunk: the
+    recomputed states (L DQK DV), the dC recurrence (L DQK DV), the inter-chunk dV, dK, dQ products
+    (3 L DQK DV), the intra-chunk Q K^T twice, dS Q and dS^T K (4 L^2 DQK) and dH~ V^T, Sbar^T dH~
+    (2 L^2 DV); 2 FLOP per multiply-add."""
+    NC = S // L
+    return 2.0 * B * NH * NC * (5 * L * DQK * DV + 4 * L * L * DQK + 2 * L * L * DV)
+
+
+def bench_chunkwise_bwd(args, dev):
+    """The chunkwise backward (xl_mlstm_chunkwise_bwd, the reference's custom backward) on config 2's
+    shape: B4 NH8 S8192 DQK256 DV512 bf16, last-state gradient included; float32 arithmetic."""
+    from xlstm_hip.ops import mlstm_chunkwise_bwd_op
+    from xlstm_hip.workloads import CFG2, chunkwise_inputs
+    cfg = CFG2
+    q, k, v, i, f = chunkwise_inputs(cfg, device=dev)
+    g = torch.Generator("cpu").manual_seed(12)
+    dh = torch.randn(cfg.B, cfg.NH, cfg.S, cfg.DV, generator=g).to(cfg.dtype).to(dev)
+    dcl = torch.randn(cfg.B, cfg.NH, cfg.DQK, cfg.DV, generator=g).to(dev)
+
+    def call():
+        return mlstm_chunkwise_bwd_op(q, k, v, i, f, None, None, None, dh, dcl, cfg.DQK ** -0.5, 64, 1e-6)
+
+    t = _timed(call, dev, max(3, args.steps // 4), warmup=2)
+    fl = bwd_flops(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, 64)
+    tf = fl / (t["ms"] * 1e-3) / 1e12
+    return {"workload": f"cfg2 chunkwise backward B{cfg.B} NH{cfg.NH} S{cfg.S} DQK{cfg.DQK} DV{cfg.DV} bf16 in, "
+                        "float32 arithmetic", "ms_per_call": t["ms"], "ms_min": t["ms_min"], "mode": t["mode"],
+            "tokens_per_s": cfg.B * cfg.S / (t["ms"] * 1e-3), "flops_per_call": fl,
+            "roofline": {"bound": "fp32", "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / PEAK_FP32_TFLOPS}}
+
+
 def bench_arbitrary_length(args, dev):
     """Any-S inference wrapper (wrap_chunkwise__arbitrary_sequence_length) on config 2 with
     S = 8192 + 63, the reference's worst tail (its split: chunk sizes 64, 32, 16 and a 15-token
@@ -853,6 +891,7 @@ def main():
         out["slstm_group_norm"] = bench_group_norm(args, dev)
         out["mlstm_output_gate"] = bench_mlstm_output_gate(args, dev)
         out["slstm_gate_proj"] = bench_gate_proj(args, dev)
+        out["chunkwise_bwd"] = bench_chunkwise_bwd(args, dev)
     if not args.no_extra:
         out["cfg0"] = bench_cfg0(args, dev)
     if not args.no_stacks:

@@ -264,6 +264,29 @@ int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias
                              int M, int D, int G, float cap, int cap_rounding, int dtype, void* stream);
 
 /*
+ * Chunkwise mLSTM backward: the reference's custom backward mlstm_chunkwise_bw
+ * (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/vendored/torch/native/
+ * bw.py:198-352, wrapped by _mlstm_chunkwise_fwbw.backward, fwbw.py:102-173 and
+ * mlstm_chunkwise__native_custbw, fwbw.py:232-281), float32 arithmetic.  The
+ * states are recomputed from the inputs (recompute_states_in_bw) and the
+ * per-token denominator max(|q n|, exp(-m)) + eps is treated as a constant, as
+ * there.  Inputs as for xl_mlstm_chunkwise_fwd plus dh [B,NH,S,DV] (dtype_qkv)
+ * and dc_last [B,NH,DQK,DV] float32 or NULL (the gradient of the last C state).
+ * Outputs: dq, dk [B,NH,S,DQK], dv [B,NH,S,DV] in dtype_qkv; di, df [B,NH,S] in
+ * dtype_gates; dc0 [B,NH,DQK,DV] float32 or NULL (only with initial states; the
+ * gradients of n0 and m0 are zero in the reference).  S % L == 0, L in
+ * {16, 32, 64}.  Workspace: xl_mlstm_chunkwise_bwd_workspace_size bytes,
+ * 256-byte aligned (every chunk's state and its gradient in float32).
+ */
+size_t xl_mlstm_chunkwise_bwd_workspace_size(int B, int NH, int S, int DQK, int DV, int L);
+int xl_mlstm_chunkwise_bwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                           const float* c0, const float* n0, const float* m0, const void* dh,
+                           const float* dc_last, void* dq, void* dk, void* dv, void* di, void* df,
+                           float* dc0, int B, int NH, int S, int DQK, int DV, int L, float qk_scale,
+                           float eps, int dtype_qkv, int dtype_gates, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
  * Logit projection with the soft-cap epilogue: y[m, v] = cap * tanh(z / cap),
  * z = (sum_d x[m, d] w[v, d]) rounded to the dtype, the soft-cap in float32 and
  * rounded once.  Replaces soft_cap(lm_head(out_norm(x)), output_logit_soft_cap)

@@ -35,6 +35,15 @@ How each function is pinned (tests/test_oracle_*.py):
   cell's softplus-form log-sigmoid agrees with ``F.logsigmoid`` there), with and
   without a carried state.
 * ``arbitrary_length``: equals the plain sequence loop for every S.
+* ``mlstm_chunkwise_bw`` (the reference's custom backward): in float64 it equals
+  torch.autograd through ``mlstm_chunkwise_fw`` wherever the reference's
+  simplification is exact — a loss that depends on h only through each row's
+  direction (h / |h|, what the layer's multi-head norm sees), with and without
+  initial states (dq, dk, dv, di, df, dc0, dn0 = 0); and a loss
+  <G, C_last exp(m_last)> on the last state, where dq, dk, dv, di and dc0 equal
+  autograd's and df equals autograd's minus <G, C_last exp(m_last)> sigmoid(-f)
+  (the constant the reference's suffix-sum formula for df leaves out on that
+  path); it is invariant to the chunk size.
 """
 
 from __future__ import annotations
@@ -52,6 +61,7 @@ __all__ = [
     "mlstm_recurrent_sequence",
     "mlstm_parallel_fw",
     "arbitrary_length",
+    "mlstm_chunkwise_bw",
 ]
 
 
@@ -354,3 +364,80 @@ def arbitrary_length(q, k, v, f, i, c_initial=None, n_initial=None, m_initial=No
                                             dtype_state=dtype_state)
         H = h[:, :, None, :]
     return (H, (C, n, m)) if return_last_states else H
+
+
+def mlstm_chunkwise_bw(matQ, matK, matV, vecI, vecF, matDeltaH, matC_initial=None, vecN_initial=None,
+                       scaM_initial=None, matDeltaC_last=None, qk_scale=None, chunk_size=64, eps=1e-6):
+    """The reference's custom chunkwise backward, ``VTN/bw.py:198-352``.
+
+    States are recomputed from the inputs (``:242-258``) and the forward's
+    per-token divisor ``N = max(|den|, exp(-m))`` and stabiliser ``m`` are taken
+    as constants (``:44-47``).  Reverse recurrence (``:31-115``):
+    ``dC_{c} = exp(g_c + m_c - m_{c+1}) dC_{c+1} + Qbar_c^T (dH_c / (N_c + eps))``
+    with ``Qbar = Q exp(b + m_c - m) s``.  Per chunk (``:118-195``):
+    ``Dbar = exp(logD - m)``, ``Sbar = Q K^T s Dbar``, ``dS = (dH~ V^T) Dbar``,
+    ``dV = Sbar^T dH~ + (K Abar) dC_{c+1}``, ``dK = dS^T Q s + (V Abar) dC_{c+1}^T``,
+    ``dQ = dS K s + (dH~ Bbar) (C_c s)^T`` with ``Abar = exp(b_L - b + i - m_{c+1})``,
+    ``Bbar = exp(b + m_c - m)``.  Gates (``:330-338``): ``dF = sigmoid(-f)`` times the
+    suffix sum over the sequence of ``sum_d (q dq - k dk)``, ``dI = sum_d v dv``.
+    Returns ``(dq, dk, dv, di, df, dc0 | None, dn0 | None, dm0 | None)``; dn0 and dm0
+    are zeros, as there (``:340-342``).
+    """
+    B, NH, S, DHQK = matQ.shape
+    DHV = matV.shape[-1]
+    L = chunk_size
+    assert S % L == 0, f"Sequence length {S} is not divisible by chunk size {L}."
+    NC = S // L
+    if qk_scale is None:
+        qk_scale = DHQK ** -0.5
+    vecB = F.logsigmoid(vecF.reshape(B, NH, NC, L)).cumsum(-1)
+    vecIr = vecI.reshape(B, NH, NC, L)
+    C_states, n_states, m_states = recurrent_fw_C(matK, matV, vecB, vecIr, matC_initial, vecN_initial,
+                                                  scaM_initial, chunk_size=L, num_chunks=NC)
+    _, n_out, m_out = parallel_fw_H(matQ, matK, matV, C_states[:, :, :-DHQK, :], n_states[:, :, :-DHQK],
+                                    m_states[:, :, :-1], vecIr, vecB, qk_scale, chunk_size=L, num_chunks=NC,
+                                    eps=eps)
+    Cs = C_states.reshape(B, NH, NC + 1, DHQK, DHV)
+    dH_t = matDeltaH / (n_out + eps)[..., None]  # dH~, (B, NH, S, DHV)
+
+    def chunk(x, c):
+        return x[:, :, c * L:(c + 1) * L]
+
+    # reverse recurrence over the chunks
+    g = vecB[..., -1]
+    dC = (matDeltaC_last.to(matQ.dtype) if matDeltaC_last is not None
+          else torch.zeros((B, NH, DHQK, DHV), dtype=matQ.dtype, device=matQ.device))
+    dC_after = [None] * NC  # gradient of the state after chunk c
+    for c in range(NC - 1, -1, -1):
+        dC_after[c] = dC
+        m_c, m_n = m_states[:, :, c], m_states[:, :, c + 1]
+        gbar = torch.exp(g[:, :, c] + m_c - m_n)[:, :, None, None]
+        bbar = torch.exp(vecB[:, :, c] + m_c[..., None] - chunk(m_out, c))[..., None]
+        Qbar = chunk(matQ, c) * bbar * qk_scale
+        dC = gbar * dC + Qbar.transpose(-2, -1) @ chunk(dH_t, c)
+    dC_initial = dC
+
+    causal = torch.tril(torch.ones((L, L), dtype=torch.bool, device=matQ.device))
+    dQ, dK, dV = torch.empty_like(matQ), torch.empty_like(matK), torch.empty_like(matV)
+    for c in range(NC):
+        Qc, Kc, Vc, dHc = chunk(matQ, c), chunk(matK, c), chunk(matV, c), chunk(dH_t, c)
+        b, ic, mc = vecB[:, :, c], vecIr[:, :, c], chunk(m_out, c)
+        m_c, m_n = m_states[:, :, c], m_states[:, :, c + 1]
+        logD = torch.where(causal, b[..., :, None] - b[..., None, :], -float("inf")) + ic[..., None, :]
+        Dbar = torch.exp(logD - mc[..., None])
+        Sbar = (Qc @ Kc.transpose(-2, -1)) * qk_scale * Dbar
+        dS = (dHc @ Vc.transpose(-2, -1)) * Dbar
+        Abar = torch.exp(b[..., -1:] - b + ic - m_n[..., None])[..., None]
+        Bbar = torch.exp(b + m_c[..., None] - mc)[..., None]
+        dV[:, :, c * L:(c + 1) * L] = Sbar.transpose(-2, -1) @ dHc + (Kc * Abar) @ dC_after[c]
+        dK[:, :, c * L:(c + 1) * L] = (dS.transpose(-2, -1) @ Qc) * qk_scale + (Vc * Abar) @ dC_after[c].transpose(-2, -1)
+        dQ[:, :, c * L:(c + 1) * L] = (dS @ Kc) * qk_scale + (dHc * Bbar) @ (Cs[:, :, c] * qk_scale).transpose(-2, -1)
+
+    per_token = (matQ * dQ - matK * dK).sum(-1)
+    suffix = per_token.flip(-1).cumsum(-1).flip(-1)
+    dF = suffix * torch.sigmoid(-vecF)
+    dI = (matV * dV).sum(-1)
+    dc0 = dC_initial if matC_initial is not None else None
+    dn0 = torch.zeros_like(vecN_initial) if vecN_initial is not None else None
+    dm0 = torch.zeros_like(scaM_initial) if scaM_initial is not None else None
+    return dQ, dK, dV, dI, dF, dc0, dn0, dm0

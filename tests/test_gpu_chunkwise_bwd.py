@@ -1,0 +1,119 @@
+"""Chunkwise backward on the GPU (xl_mlstm_chunkwise_bwd through torch.autograd) against the oracle's
+restatement of the reference's custom backward (oracle.mlstm.mlstm_chunkwise_bw, itself pinned to
+torch.autograd in tests/test_oracle_chunkwise_bw.py), run in float64 on the same inputs.
+
+Bars, per gradient, relative to the largest magnitude of the expected tensor:
+* float32 inputs (two-pass float32 forward, float32 backward): |got - want| <= 1e-4 max|want|;
+* bf16 inputs (the gradients come back in bf16): |got - want| <= 2^-8 |want| + 2e-3 max|want|
+  (the output's own rounding, one ulp, plus float32 accumulation over the chunk).
+
+Cases: with and without initial states, the last-state gradient, chunk sizes 16 / 32 / 64, DQK and
+DV that are not multiples of the 64-wide tiles, several heads and chunks, bf16 and f16 inputs, and
+the registry form mlstm_chunkwise__native_custbw.
+"""
+
+import pytest
+import torch
+
+from helpers import dev
+from oracle import mlstm as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, NH, S, DQK, DV, seed, states):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, NH, S, DQK, generator=g)
+    k = torch.randn(B, NH, S, DQK, generator=g)
+    v = torch.randn(B, NH, S, DV, generator=g)
+    i = torch.randn(B, NH, S, generator=g)
+    f = torch.randn(B, NH, S, generator=g) + 3.0
+    st = None
+    if states:
+        st = (0.3 * torch.randn(B, NH, DQK, DV, generator=g), torch.rand(B, NH, DQK, generator=g) + 0.5,
+              0.5 * torch.randn(B, NH, 1, generator=g))
+    dh = torch.randn(B, NH, S, DV, generator=g)
+    dcl = torch.randn(B, NH, DQK, DV, generator=g)
+    return (q, k, v, i, f), st, dh, dcl
+
+
+def _check(got, want, dtype, what):
+    got, want = got.detach().double().cpu(), want.detach().double().cpu()
+    scale = float(want.abs().max())
+    if dtype == torch.float32:
+        err = float((got - want).abs().max()) / scale
+        assert err <= 1e-4, f"{what}: rel-err {err:.3e}"
+    else:
+        excess = float(((got - want).abs() - 2.0 ** -8 * want.abs()).max()) / scale
+        assert excess <= 2e-3, f"{what}: {excess:.3e} of max beyond one rounding"
+
+
+def _run(B, NH, S, DQK, DV, L, dtype, states, last, seed, algo="auto"):
+    import xlstm_hip
+    x, st, dh, dcl = _inputs(B, NH, S, DQK, DV, seed, states)
+    xd = [t.to(dtype).to(dev()).requires_grad_(True) for t in x]
+    std = [t.to(dev()).requires_grad_(True) for t in st] if states else [None, None, None]
+    out = xlstm_hip.mlstm_chunkwise(*xd, *std, return_last_states=last, chunk_size=L, algo=algo)
+    h, (C, _, _) = out if last else (out, (None, None, None))
+    loss = (h.float() * dh.to(dev())).sum()
+    if last:
+        loss = loss + (C * dcl.to(dev())).sum()
+    loss.backward()
+    # oracle on the same (rounded) inputs in float64; h is in q's dtype, so the gradient reaching it
+    # is dh rounded to that dtype
+    x64 = [t.to(dtype).double() for t in x]
+    st64 = [t.double() for t in st] if states else [None, None, None]
+    want = om.mlstm_chunkwise_bw(*x64, dh.to(dtype).double(), *st64, matDeltaC_last=dcl.double() if last else None,
+                                 chunk_size=L)
+    for nm, t, w in zip(["dq", "dk", "dv", "di", "df"], xd, want[:5]):
+        assert t.grad.dtype == dtype
+        _check(t.grad, w, dtype, f"{nm} B{B} NH{NH} S{S} DQK{DQK} DV{DV} L{L} {dtype} states={states} last={last}")
+    if states:
+        _check(std[0].grad, want[5], torch.float32, "dc0")
+        assert float(std[1].grad.abs().max()) == 0.0 and float(std[2].grad.abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("B,NH,S,DQK,DV,L", [(1, 2, 128, 64, 64, 64), (2, 3, 96, 48, 80, 32), (1, 1, 64, 16, 16, 16),
+                                             (1, 2, 192, 128, 96, 64), (2, 2, 128, 200, 72, 16)])
+@pytest.mark.parametrize("states,last", [(False, False), (True, True), (True, False), (False, True)])
+def test_fp32_vs_oracle(gpu_case, B, NH, S, DQK, DV, L, states, last):
+    _run(B, NH, S, DQK, DV, L, torch.float32, states, last, seed=B * 100 + S + DQK + L + 2 * states + last)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,NH,S,DQK,DV", [(1, 2, 256, 128, 128), (2, 2, 128, 256, 64)])
+def test_lowp_vs_oracle(gpu_case, dtype, B, NH, S, DQK, DV):
+    _run(B, NH, S, DQK, DV, 64, dtype, True, True, seed=7 + S)
+
+
+def test_larger_fp32(gpu_case):
+    _run(2, 4, 512, 128, 256, 64, torch.float32, True, True, seed=77)
+
+
+def test_registry_form_and_gate_dtypes(gpu_case):
+    """mlstm_chunkwise__native_custbw with bf16 q/k/v and float32 gates: the gate gradients come back
+    in float32, dq/dk/dv in bf16, all within the bars above."""
+    import xlstm_hip
+    B, NH, S, DQK, DV = 1, 2, 128, 64, 64
+    x, st, dh, _ = _inputs(B, NH, S, DQK, DV, 5, False)
+    q, k, v = (t.bfloat16().to(dev()).requires_grad_(True) for t in x[:3])
+    i, f = (t.to(dev()).requires_grad_(True) for t in x[3:])
+    h = xlstm_hip.mlstm_chunkwise__native_custbw(q, k, v, i, f)
+    (h.float() * dh.to(dev())).sum().backward()
+    want = om.mlstm_chunkwise_bw(*(t.bfloat16().double() for t in x[:3]), x[3].double(), x[4].double(),
+                                 dh.bfloat16().double())
+    for nm, t, w, dt in (("dq", q, want[0], torch.bfloat16), ("dk", k, want[1], torch.bfloat16),
+                         ("dv", v, want[2], torch.bfloat16), ("di", i, want[3], torch.float32),
+                         ("df", f, want[4], torch.float32)):
+        assert t.grad.dtype == dt
+        _check(t.grad, w, dt if dt == torch.float32 else torch.bfloat16, nm)
+
+
+def test_ragged_sequence_backward_raises(gpu_case):
+    import xlstm_hip
+    x, _, _, _ = _inputs(1, 1, 100, 128, 64, 1, False)
+    xd = [t.to(dev()).requires_grad_(True) for t in x]
+    h = xlstm_hip.mlstm_chunkwise(*(t.bfloat16() if j < 3 else t for j, t in enumerate(xd)), chunk_size=64,
+                                  algo="fused")
+    with pytest.raises(Exception, match="not divisible"):
+        h.float().sum().backward()

@@ -19,12 +19,38 @@ struct ChunkwiseArgs {
   int max_segments;  // fused algorithm: at most this many sequence segments (1: no split)
 };
 
+// Per-chunk gate prefix: sb[t] = sum_{u<=t} logsig(f_u) in sequential order
+// (torch's CPU cumsum order), si[t] = i_t, for the L tokens from g0.  Called by
+// every thread of the block; needs 2 barriers.
+template <typename TG, int L>
+__device__ __forceinline__ void chunk_gate_prefix(const TG* __restrict__ ig, const TG* __restrict__ fg, size_t g0,
+                                                  float* sb, float* si) {
+  const int tid = threadIdx.x;
+  if (tid < L) {
+    sb[tid] = logsigmoid(to_f32(fg[g0 + tid]));
+    si[tid] = to_f32(ig[g0 + tid]);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float acc = 0.f;
+    for (int t = 0; t < L; ++t) {
+      acc += sb[t];
+      sb[t] = acc;
+    }
+  }
+  __syncthreads();
+}
+
 // Argument checks of xl_mlstm_chunkwise_fwd for the given algorithm (0 or an XL_ERR_* code).
 int chunkwise_check_args(const ChunkwiseArgs& a, int algo);
 
 // Two-pass algorithm (states pass + output pass), float32 arithmetic.
 size_t chunkwise_two_pass_workspace(int B, int NH, int S, int DQK, int DV, int L);
 int chunkwise_two_pass(const ChunkwiseArgs& a);
+// The states pass alone (S % L == 0): the state entering every chunk into Cst [BNH][NC][DQK][DV],
+// nst [BNH][NC][DQK], mst [BNH][NC], the state after the last chunk into c_fin, n_fin, m_fin.
+int chunkwise_states_pass(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst, float* c_fin, float* n_fin,
+                          float* m_fin);
 
 // Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a
 // shape/dtype is covered (and why not, in `why`, when it is not).

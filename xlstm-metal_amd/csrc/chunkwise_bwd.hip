@@ -1,0 +1,672 @@
+// Chunkwise mLSTM backward (float32 arithmetic): the reference's custom backward
+// mlstm_chunkwise_bw (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/
+// vendored/torch/native/bw.py:198-352), which treats the per-token
+// denominator max(|q n|, exp(-m)) + eps as a constant (the mLSTM layer's
+// multi-head norm removes any per-row scale of h, so its gradient does not
+// reach the loss there).  Five launches after the states pass:
+//
+//   1. the states pass of the two-pass forward recomputes the state entering
+//      every chunk (bw.py:242-258, recompute_states_in_bw);
+//   2. bw_stats_kernel: per chunk, the combined stabiliser m_t and the divisor
+//      max(|den_t|, exp(-m_t)) + eps of every token (the forward's vecM_out and
+//      vecN_out + eps, fw.py:204-253);
+//   3. bw_dC_kernel: the reverse recurrence dC_{k-1} = exp(g_k + m_{k-1} - m_k) dC_k
+//      + Qbar_k^T (dH_k / (N_k + eps)) over the chunks, one workgroup per 64 x 64
+//      tile of dC (bw.py:31-115);
+//   4. bw_dv_kernel: dV = Sbar^T dH~ + (K * Abar) dC_k per chunk and 64-column tile
+//      of V, and the per-token partial sums v . dV of dI (bw.py:159,182,338);
+//   5. bw_dqk_kernel: dQ = (dS K) s + (dH~ * Bbar) (C_{k-1} s)^T and
+//      dK = (dS^T Q) s + (V * Abar) dC_k^T per chunk and 64-column tile of DQK,
+//      with dS = (dH~ V^T) * Dbar, and the per-token partial sums q . dQ - k . dK
+//      (bw.py:161-185, 333);
+//   6. bw_gates_kernel: dI = sum of the partials, dF = (reverse cumulative sum of
+//      the q . dQ - k . dK partials) * sigmoid(-f) (bw.py:332-338).
+//
+// Workspace (float32, each region 256-byte aligned): the entering states C, n, m
+// [BNH][NC](...), the final state, m_comb and the divisor [BNH][S], dC
+// [BNH][NC + 1][DQK][DV] (index k: the gradient of the state after chunk k - 1;
+// 0 is dC_initial), the dF partials [BNH][S][ceil(DQK/64)] and the dI partials
+// [BNH][S][ceil(DV/64)].
+#include "chunkwise.h"
+
+namespace xl {
+namespace {
+
+constexpr int BW_THREADS = 256;
+constexpr int BW_T = 64;   // DQK / DV tile
+constexpr int BW_KT = 32;  // contraction tile
+
+__device__ __forceinline__ float sum16(float v) {  // over the 16 lanes of a tx group
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 16);
+  return v;
+}
+
+struct BwLayout {
+  size_t Cst, nst, mst, cfin, nfin, mfin, vm, vn, dC, dfp, dip, total;
+};
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+BwLayout bw_layout(int B, int NH, int S, int DQK, int DV, int L) {
+  const size_t BNH = (size_t)B * NH, NC = (size_t)(S / L);
+  const size_t ndt = (DQK + BW_T - 1) / BW_T, nvt = (DV + BW_T - 1) / BW_T;
+  BwLayout o{};
+  size_t off = 0;
+  auto take = [&](size_t floats) {
+    const size_t at = off;
+    off += align256(floats * sizeof(float));
+    return at;
+  };
+  o.Cst = take(BNH * NC * DQK * DV);
+  o.nst = take(BNH * NC * DQK);
+  o.mst = take(BNH * NC);
+  o.cfin = take(BNH * DQK * DV);
+  o.nfin = take(BNH * DQK);
+  o.mfin = take(BNH);
+  o.vm = take(BNH * S);
+  o.vn = take(BNH * S);
+  o.dC = take(BNH * (NC + 1) * DQK * DV);
+  o.dfp = take(BNH * S * ndt);
+  o.dip = take(BNH * S * nvt);
+  o.total = off;
+  return o;
+}
+
+// combined stabiliser of token i of a chunk entering with m_prev: max(b_i + m_prev,
+// max_{j<=i} b_i - b_j + i_j) (fw.py:204-217)
+template <int L>
+__device__ __forceinline__ float m_combine(const float* sb, const float* si, int i, float m_prev) {
+  float mi = -INFINITY;
+  for (int j = 0; j <= i; ++j) mi = fmaxf(mi, sb[i] - sb[j] + si[j]);
+  return fmaxf(sb[i] + m_prev, mi);
+}
+
+// ------------------------------------------------------------------ 2. stats
+template <typename TQ, typename TG, int L>
+__global__ __launch_bounds__(BW_THREADS) void bw_stats_kernel(const TQ* __restrict__ q, const TQ* __restrict__ k,
+                                                               const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                               const float* __restrict__ nst,
+                                                               const float* __restrict__ mst, float* __restrict__ vm,
+                                                               float* __restrict__ vn, int NC, int DQK,
+                                                               float qk_scale, float eps) {
+  constexpr int RS = L / 16;
+  __shared__ float sQt[BW_KT][L], sKt[BW_KT][L], sn[BW_KT];
+  __shared__ float sM[L][L + 1];
+  __shared__ float sb[L], si[L], smc[L], sqb[L];
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  const int bh = blockIdx.x / NC, kc = blockIdx.x - bh * NC;
+  const size_t row0 = (size_t)bh * NC * L + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  if (tid < L) {
+    const float mp = mst[sidx];
+    const float mc = m_combine<L>(sb, si, tid, mp);
+    smc[tid] = mc;
+    sqb[tid] = expf(sb[tid] + mp - mc) * qk_scale;  // fw.py:230-231
+  }
+  float accS[RS][RS] = {};
+  float qn = 0.f;
+  for (int dd = 0; dd < DQK; dd += BW_KT) {
+    __syncthreads();
+    for (int e = tid; e < L * BW_KT; e += BW_THREADS) {
+      const int t = e / BW_KT, c = e - t * BW_KT;
+      const bool ok = dd + c < DQK;
+      sQt[c][t] = ok ? to_f32(q[(row0 + t) * DQK + dd + c]) : 0.f;
+      sKt[c][t] = ok ? to_f32(k[(row0 + t) * DQK + dd + c]) : 0.f;
+    }
+    if (tid < BW_KT) sn[tid] = (dd + tid < DQK) ? nst[sidx * DQK + dd + tid] : 0.f;
+    __syncthreads();
+#pragma unroll 4
+    for (int d = 0; d < BW_KT; ++d) {
+      float qv[RS], kv[RS];
+#pragma unroll
+      for (int a = 0; a < RS; ++a) qv[a] = sQt[d][ty * RS + a];
+#pragma unroll
+      for (int b = 0; b < RS; ++b) kv[b] = sKt[d][tx * RS + b];
+#pragma unroll
+      for (int a = 0; a < RS; ++a)
+#pragma unroll
+        for (int b = 0; b < RS; ++b) accS[a][b] += qv[a] * kv[b];
+    }
+    if (tid < L)
+      for (int d = 0; d < BW_KT; ++d) qn += sQt[d][tid] * sn[d];
+  }
+  // M = S s exp(b_i - b_j + i_j - m_i) on j <= i (fw.py:219-227)
+#pragma unroll
+  for (int a = 0; a < RS; ++a) {
+    const int i = ty * RS + a;
+#pragma unroll
+    for (int b = 0; b < RS; ++b) {
+      const int j = tx * RS + b;
+      sM[i][j] = (j <= i) ? accS[a][b] * qk_scale * expf(sb[i] - sb[j] + si[j] - smc[i]) : 0.f;
+    }
+  }
+  __syncthreads();
+  if (tid < L) {  // den = qbar (q . n) + sum_j M_ij; divisor max(|den|, exp(-m)) + eps (fw.py:237-245)
+    float rs = 0.f;
+    for (int j = 0; j < L; ++j) rs += sM[tid][j];
+    const float den = sqb[tid] * qn + rs;
+    vm[row0 + tid] = smc[tid];
+    vn[row0 + tid] = fmaxf(fabsf(den), expf(-smc[tid])) + eps;
+  }
+}
+
+// --------------------------------------------------------------- 3. dC pass
+template <typename TQ, typename TG, int L>
+__global__ __launch_bounds__(BW_THREADS) void bw_dC_kernel(const TQ* __restrict__ q, const TQ* __restrict__ dh,
+                                                            const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                            const float* __restrict__ mst,
+                                                            const float* __restrict__ mfin,
+                                                            const float* __restrict__ vm,
+                                                            const float* __restrict__ vn,
+                                                            const float* __restrict__ dc_last,
+                                                            float* __restrict__ dCst, float* __restrict__ dc0,
+                                                            int NC, int DQK, int DV, int ndt, int nvt,
+                                                            float qk_scale) {
+  __shared__ float sQ[L][BW_T + 1], sH[L][BW_T + 1];
+  __shared__ float sb[L], si[L], scoef[L];
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  const int per_bh = ndt * nvt;
+  const int bh = blockIdx.x / per_bh, rem = blockIdx.x - bh * per_bh;
+  const int d0 = (rem / nvt) * BW_T, v0 = (rem % nvt) * BW_T;
+  const size_t S = (size_t)NC * L;
+  float dC[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int d = d0 + 4 * ty + a, v = v0 + 4 * tx + b;
+      dC[a][b] = (dc_last && d < DQK && v < DV) ? dc_last[((size_t)bh * DQK + d) * DV + v] : 0.f;
+    }
+  auto store = [&](float* dst) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int d = d0 + 4 * ty + a, v = v0 + 4 * tx + b;
+        if (d < DQK && v < DV) dst[(size_t)d * DV + v] = dC[a][b];
+      }
+  };
+  for (int kc = NC - 1; kc >= 0; --kc) {
+    store(dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV);  // bw.py:81
+    const size_t row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+    chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+    const float mp = mst[sidx];
+    const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+    // Qbar dH~ = q exp(b + m_{k-1} - m_comb) s / (N + eps) (bw.py:92-101)
+    if (tid < L) scoef[tid] = expf(sb[tid] + mp - vm[row0 + tid]) * qk_scale / vn[row0 + tid];
+    for (int e = tid; e < L * BW_T; e += BW_THREADS) {
+      const int t = e / BW_T, c = e - t * BW_T;
+      sQ[t][c] = (d0 + c < DQK) ? to_f32(q[(row0 + t) * DQK + d0 + c]) : 0.f;
+      sH[t][c] = (v0 + c < DV) ? to_f32(dh[(row0 + t) * DV + v0 + c]) : 0.f;
+    }
+    __syncthreads();
+    const float gbar = expf(sb[L - 1] + mp - mn);  // bw.py:86-89
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) dC[a][b] *= gbar;
+    for (int t = 0; t < L; ++t) {  // bw.py:104
+      const float co = scoef[t];
+      float qd[4], hv[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) qd[a] = sQ[t][4 * ty + a] * co;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) hv[b] = sH[t][4 * tx + b];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) dC[a][b] += qd[a] * hv[b];
+    }
+    __syncthreads();  // LDS reused by the next chunk
+  }
+  store(dCst + (size_t)bh * (NC + 1) * DQK * DV);  // bw.py:110
+  if (dc0) store(dc0 + (size_t)bh * DQK * DV);
+}
+
+// --------------------------------------------------------------- 4. dV pass
+template <int L>
+struct DvSmem {
+  // phase 1 (contraction over DQK): Q^T, K^T tiles and the dC tile
+  static constexpr int QT = 0, KT = QT + BW_KT * L, DC = KT + BW_KT * L, P1 = DC + BW_KT * BW_T;
+  // phase 2: Sbar [L][L + 1] and dH~ [L][BW_T + 1]
+  static constexpr int SB = 0, H = SB + L * (L + 1), P2 = H + L * (BW_T + 1);
+  static constexpr int TOTAL = P1 > P2 ? P1 : P2;
+};
+
+template <typename TQ, typename TG, int L>
+__global__ __launch_bounds__(BW_THREADS) void bw_dv_kernel(const TQ* __restrict__ q, const TQ* __restrict__ k,
+                                                            const TQ* __restrict__ v, const TQ* __restrict__ dh,
+                                                            const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                            const float* __restrict__ mst,
+                                                            const float* __restrict__ mfin,
+                                                            const float* __restrict__ vm,
+                                                            const float* __restrict__ vn,
+                                                            const float* __restrict__ dCst, TQ* __restrict__ dv,
+                                                            float* __restrict__ dip, int NC, int DQK, int DV,
+                                                            int nvt, float qk_scale) {
+  constexpr int RS = L / 16;
+  using SM = DvSmem<L>;
+  __shared__ float smem[SM::TOTAL];
+  __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L];
+  float* sQt = smem + SM::QT;
+  float* sKt = smem + SM::KT;
+  float* sdC = smem + SM::DC;
+  float* sSb = smem + SM::SB;
+  float* sH = smem + SM::H;
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  const int per_bh = NC * nvt;
+  const int bh = blockIdx.x / per_bh, rem = blockIdx.x - bh * per_bh;
+  const int kc = rem / nvt, vt = rem - kc * nvt, v0 = vt * BW_T;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  const float* dCk = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // gradient of the state after chunk kc
+  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  if (tid < L) {
+    const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+    smc[tid] = vm[row0 + tid];
+    sinv[tid] = 1.0f / vn[row0 + tid];
+    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - mn);  // Abar = exp(b_L - b + i - m_k) (bw.py:168-176)
+  }
+  float accS[RS][RS] = {}, accV[RS][4] = {};
+  for (int dd = 0; dd < DQK; dd += BW_KT) {
+    __syncthreads();
+    for (int e = tid; e < L * BW_KT; e += BW_THREADS) {
+      const int t = e / BW_KT, c = e - t * BW_KT;
+      const bool ok = dd + c < DQK;
+      sQt[c * L + t] = ok ? to_f32(q[(row0 + t) * DQK + dd + c]) : 0.f;
+      sKt[c * L + t] = ok ? to_f32(k[(row0 + t) * DQK + dd + c]) : 0.f;
+    }
+    for (int e = tid; e < BW_KT * BW_T; e += BW_THREADS) {
+      const int r = e / BW_T, c = e - r * BW_T;
+      sdC[r * BW_T + c] = (dd + r < DQK && v0 + c < DV) ? dCk[(size_t)(dd + r) * DV + v0 + c] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int d = 0; d < BW_KT; ++d) {
+      float qv[RS], kv[RS], kr[RS], cv[4];
+#pragma unroll
+      for (int a = 0; a < RS; ++a) {
+        qv[a] = sQt[d * L + ty * RS + a];
+        kr[a] = sKt[d * L + ty * RS + a];
+      }
+#pragma unroll
+      for (int b = 0; b < RS; ++b) kv[b] = sKt[d * L + tx * RS + b];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cv[c] = sdC[d * BW_T + tx * 4 + c];
+#pragma unroll
+      for (int a = 0; a < RS; ++a) {
+#pragma unroll
+        for (int b = 0; b < RS; ++b) accS[a][b] += qv[a] * kv[b];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) accV[a][c] += kr[a] * cv[c];
+      }
+    }
+  }
+  __syncthreads();  // phase-1 tiles dead
+  // inter: (K * Abar) dC_k (bw.py:179); Sbar = S s Dbar on j <= i (bw.py:146-153)
+#pragma unroll
+  for (int a = 0; a < RS; ++a) {
+    const int t = ty * RS + a;
+    const float ab = sab[t];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) accV[a][c] *= ab;
+#pragma unroll
+    for (int b = 0; b < RS; ++b) {
+      const int j = tx * RS + b;
+      sSb[t * (L + 1) + j] = (j <= t) ? accS[a][b] * qk_scale * expf(sb[t] - sb[j] + si[j] - smc[t]) : 0.f;
+    }
+  }
+  for (int e = tid; e < L * BW_T; e += BW_THREADS) {
+    const int t = e / BW_T, c = e - t * BW_T;
+    sH[t * (BW_T + 1) + c] = (v0 + c < DV) ? to_f32(dh[(row0 + t) * DV + v0 + c]) * sinv[t] : 0.f;
+  }
+  __syncthreads();
+  // intra: dV_j = sum_t Sbar_tj dH~_t (bw.py:156)
+  for (int t = 0; t < L; ++t) {
+    float sv[RS], hv[4];
+#pragma unroll
+    for (int a = 0; a < RS; ++a) sv[a] = sSb[t * (L + 1) + ty * RS + a];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) hv[c] = sH[t * (BW_T + 1) + tx * 4 + c];
+#pragma unroll
+    for (int a = 0; a < RS; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) accV[a][c] += sv[a] * hv[c];
+  }
+#pragma unroll
+  for (int a = 0; a < RS; ++a) {
+    const size_t row = row0 + ty * RS + a;
+    float part = 0.f;  // v . dV over this tile (bw.py:338)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int vv = v0 + tx * 4 + c;
+      if (vv < DV) {
+        dv[row * DV + vv] = from_f32<TQ>(accV[a][c]);
+        part += to_f32(v[row * DV + vv]) * accV[a][c];
+      }
+    }
+    part = sum16(part);
+    if (tx == 0) dip[row * nvt + vt] = part;
+  }
+}
+
+// ------------------------------------------------------------ 5. dQ, dK pass
+template <int L>
+struct DqkSmem {
+  // phase 1 (contraction over DV): dH~^T, V^T tiles, C_{k-1} and dC_k tiles (transposed)
+  static constexpr int HT = 0, VT = HT + BW_KT * L, CT = VT + BW_KT * L, DCT = CT + BW_KT * BW_T,
+                       P1 = DCT + BW_KT * BW_T;
+  // phase 2: dS [L][L + 1], Q and K tiles [L][BW_T + 1]
+  static constexpr int DS = 0, Q = DS + L * (L + 1), K = Q + L * (BW_T + 1), P2 = K + L * (BW_T + 1);
+  static constexpr int TOTAL = P1 > P2 ? P1 : P2;
+};
+
+template <typename TQ, typename TG, int L>
+__global__ __launch_bounds__(BW_THREADS) void bw_dqk_kernel(const TQ* __restrict__ q, const TQ* __restrict__ k,
+                                                             const TQ* __restrict__ v, const TQ* __restrict__ dh,
+                                                             const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                             const float* __restrict__ Cst,
+                                                             const float* __restrict__ mst,
+                                                             const float* __restrict__ mfin,
+                                                             const float* __restrict__ vm,
+                                                             const float* __restrict__ vn,
+                                                             const float* __restrict__ dCst, TQ* __restrict__ dq,
+                                                             TQ* __restrict__ dk, float* __restrict__ dfp, int NC,
+                                                             int DQK, int DV, int ndt, float qk_scale) {
+  constexpr int RS = L / 16;
+  using SM = DqkSmem<L>;
+  __shared__ float smem[SM::TOTAL];
+  __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L], sbb[L];
+  float* sHt = smem + SM::HT;
+  float* sVt = smem + SM::VT;
+  float* sCt = smem + SM::CT;
+  float* sdCt = smem + SM::DCT;
+  float* sdS = smem + SM::DS;
+  float* sQ = smem + SM::Q;
+  float* sK = smem + SM::K;
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  const int per_bh = NC * ndt;
+  const int bh = blockIdx.x / per_bh, rem = blockIdx.x - bh * per_bh;
+  const int kc = rem / ndt, dt = rem - kc * ndt, d0 = dt * BW_T;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  const float* Ck = Cst + sidx * DQK * DV;                                   // state entering chunk kc
+  const float* dCk = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // gradient of the state after it
+  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  if (tid < L) {
+    const float mp = mst[sidx];
+    const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+    const float mc = vm[row0 + tid];
+    smc[tid] = mc;
+    sinv[tid] = 1.0f / vn[row0 + tid];
+    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - mn);  // Abar (bw.py:168-176)
+    sbb[tid] = expf(sb[tid] + mp - mc) * qk_scale;        // Bbar s (bw.py:175, 182)
+  }
+  float accS[RS][RS] = {}, accQ[RS][4] = {}, accK[RS][4] = {};
+  for (int vv = 0; vv < DV; vv += BW_KT) {
+    __syncthreads();
+    for (int e = tid; e < L * BW_KT; e += BW_THREADS) {
+      const int t = e / BW_KT, c = e - t * BW_KT;
+      const bool ok = vv + c < DV;
+      sHt[c * L + t] = ok ? to_f32(dh[(row0 + t) * DV + vv + c]) * sinv[t] : 0.f;
+      sVt[c * L + t] = ok ? to_f32(v[(row0 + t) * DV + vv + c]) : 0.f;
+    }
+    for (int e = tid; e < BW_KT * BW_T; e += BW_THREADS) {
+      const int r = e / BW_KT, c = e - r * BW_KT;  // r: d row of the tile, c: v column
+      const bool ok = d0 + r < DQK && vv + c < DV;
+      sCt[c * BW_T + r] = ok ? Ck[(size_t)(d0 + r) * DV + vv + c] : 0.f;
+      sdCt[c * BW_T + r] = ok ? dCk[(size_t)(d0 + r) * DV + vv + c] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int r = 0; r < BW_KT; ++r) {
+      float hv[RS], vj[RS], vr[RS], cv[4], dcv[4];
+#pragma unroll
+      for (int a = 0; a < RS; ++a) {
+        hv[a] = sHt[r * L + ty * RS + a];
+        vr[a] = sVt[r * L + ty * RS + a];
+      }
+#pragma unroll
+      for (int b = 0; b < RS; ++b) vj[b] = sVt[r * L + tx * RS + b];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        cv[c] = sCt[r * BW_T + tx * 4 + c];
+        dcv[c] = sdCt[r * BW_T + tx * 4 + c];
+      }
+#pragma unroll
+      for (int a = 0; a < RS; ++a) {
+#pragma unroll
+        for (int b = 0; b < RS; ++b) accS[a][b] += hv[a] * vj[b];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          accQ[a][c] += hv[a] * cv[c];
+          accK[a][c] += vr[a] * dcv[c];
+        }
+      }
+    }
+  }
+  __syncthreads();  // phase-1 tiles dead
+  // inter terms (bw.py:181-182); dS = (dH~ V^T) Dbar on j <= i (bw.py:158-159)
+#pragma unroll
+  for (int a = 0; a < RS; ++a) {
+    const int t = ty * RS + a;
+    const float bb = sbb[t], ab = sab[t];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      accQ[a][c] *= bb;
+      accK[a][c] *= ab;
+    }
+#pragma unroll
+    for (int b = 0; b < RS; ++b) {
+      const int j = tx * RS + b;
+      sdS[t * (L + 1) + j] = (j <= t) ? accS[a][b] * expf(sb[t] - sb[j] + si[j] - smc[t]) : 0.f;
+    }
+  }
+  for (int e = tid; e < L * BW_T; e += BW_THREADS) {
+    const int t = e / BW_T, c = e - t * BW_T;
+    const bool ok = d0 + c < DQK;
+    sQ[t * (BW_T + 1) + c] = ok ? to_f32(q[(row0 + t) * DQK + d0 + c]) : 0.f;
+    sK[t * (BW_T + 1) + c] = ok ? to_f32(k[(row0 + t) * DQK + d0 + c]) : 0.f;
+  }
+  __syncthreads();
+  // intra: dQ_t = s sum_j dS_tj K_j, dK_j = s sum_t dS_tj Q_t (bw.py:161-162)
+  float iq[RS][4] = {}, ik[RS][4] = {};
+  for (int j = 0; j < L; ++j) {
+    float dsq[RS], dsk[RS], kv[4], qv[4];
+#pragma unroll
+    for (int a = 0; a < RS; ++a) {
+      dsq[a] = sdS[(ty * RS + a) * (L + 1) + j];  // dS[t = row][j]
+      dsk[a] = sdS[j * (L + 1) + ty * RS + a];    // dS[t = j][row]
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kv[c] = sK[j * (BW_T + 1) + tx * 4 + c];
+      qv[c] = sQ[j * (BW_T + 1) + tx * 4 + c];
+    }
+#pragma unroll
+    for (int a = 0; a < RS; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        iq[a][c] += dsq[a] * kv[c];
+        ik[a][c] += dsk[a] * qv[c];
+      }
+  }
+#pragma unroll
+  for (int a = 0; a < RS; ++a) {
+    const int t = ty * RS + a;
+    const size_t row = row0 + t;
+    float part = 0.f;  // q . dQ - k . dK over this tile (bw.py:333)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = d0 + tx * 4 + c;
+      const float gq = accQ[a][c] + qk_scale * iq[a][c];
+      const float gk = accK[a][c] + qk_scale * ik[a][c];
+      if (d < DQK) {
+        dq[row * DQK + d] = from_f32<TQ>(gq);
+        dk[row * DQK + d] = from_f32<TQ>(gk);
+        part += sQ[t * (BW_T + 1) + tx * 4 + c] * gq - sK[t * (BW_T + 1) + tx * 4 + c] * gk;
+      }
+    }
+    part = sum16(part);
+    if (tx == 0) dfp[row * ndt + dt] = part;
+  }
+}
+
+// --------------------------------------------------------------- 6. gates
+// One workgroup per head: dI_t = sum of its dV partials; dF_t = sigmoid(-f_t) times
+// the suffix sum over u >= t of the q . dQ - k . dK partials, 256 tokens per step
+// from the end of the sequence (a block-wide inclusive scan, then the carry).
+template <typename TG>
+__global__ __launch_bounds__(BW_THREADS) void bw_gates_kernel(const TG* __restrict__ fg,
+                                                               const float* __restrict__ dfp,
+                                                               const float* __restrict__ dip, TG* __restrict__ di,
+                                                               TG* __restrict__ df, int S, int ndt, int nvt) {
+  __shared__ float sx[BW_THREADS];
+  const int tid = threadIdx.x;
+  const size_t base = (size_t)blockIdx.x * S;
+  float carry = 0.f;
+  for (int end = S; end > 0; end -= BW_THREADS) {
+    // position tid counts back from the end of this block of tokens
+    const int t = end - 1 - tid;
+    float x = 0.f;
+    if (t >= 0) {
+      for (int j = 0; j < ndt; ++j) x += dfp[(base + t) * ndt + j];
+      float s = 0.f;
+      for (int j = 0; j < nvt; ++j) s += dip[(base + t) * nvt + j];
+      di[base + t] = from_f32<TG>(s);
+    }
+    sx[tid] = x;
+    __syncthreads();
+    for (int o = 1; o < BW_THREADS; o <<= 1) {  // inclusive scan over the reversed positions
+      const float y = tid >= o ? sx[tid - o] : 0.f;
+      __syncthreads();
+      sx[tid] += y;
+      __syncthreads();
+    }
+    if (t >= 0) {
+      const float suffix = carry + sx[tid];
+      const float fv = to_f32(fg[base + t]);
+      df[base + t] = from_f32<TG>(suffix / (1.0f + expf(fv)));  // * sigmoid(-f)
+    }
+    carry += sx[BW_THREADS - 1];
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+struct BwArgs {
+  ChunkwiseArgs fw;
+  const void* dh;
+  const float* dc_last;
+  void *dq, *dk, *dv, *di, *df;
+  float* dc0;
+};
+
+template <typename TQ, typename TG, int L>
+int bw_launch(const BwArgs& A, const BwLayout& lay) {
+  const ChunkwiseArgs& F = A.fw;
+  const int BNH = F.B * F.NH, NC = F.S / L;
+  const int ndt = (F.DQK + BW_T - 1) / BW_T, nvt = (F.DV + BW_T - 1) / BW_T;
+  char* ws = (char*)F.workspace;
+  float *Cst = (float*)(ws + lay.Cst), *nst = (float*)(ws + lay.nst), *mst = (float*)(ws + lay.mst);
+  float *cfin = (float*)(ws + lay.cfin), *nfin = (float*)(ws + lay.nfin), *mfin = (float*)(ws + lay.mfin);
+  float *vm = (float*)(ws + lay.vm), *vn = (float*)(ws + lay.vn), *dC = (float*)(ws + lay.dC);
+  float *dfp = (float*)(ws + lay.dfp), *dip = (float*)(ws + lay.dip);
+  hipStream_t s = (hipStream_t)F.stream;
+  const TQ *q = (const TQ*)F.q, *k = (const TQ*)F.k, *v = (const TQ*)F.v, *dh = (const TQ*)A.dh;
+  const TG *ig = (const TG*)F.i, *fg = (const TG*)F.f;
+  int rc = chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
+  if (rc) return rc;
+  hipLaunchKernelGGL((bw_stats_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC)), dim3(BW_THREADS), 0, s, q, k, ig, fg,
+                     nst, mst, vm, vn, NC, F.DQK, F.qk_scale, F.eps);
+  if ((rc = check_launch("xl_mlstm_chunkwise_bwd(stats)"))) return rc;
+  hipLaunchKernelGGL((bw_dC_kernel<TQ, TG, L>), dim3((unsigned)(BNH * ndt * nvt)), dim3(BW_THREADS), 0, s, q, dh, ig,
+                     fg, mst, mfin, vm, vn, A.dc_last, dC, A.dc0, NC, F.DQK, F.DV, ndt, nvt, F.qk_scale);
+  if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dC)"))) return rc;
+  hipLaunchKernelGGL((bw_dv_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * nvt)), dim3(BW_THREADS), 0, s, q, k, v, dh,
+                     ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DQK, F.DV, nvt, F.qk_scale);
+  if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dV)"))) return rc;
+  hipLaunchKernelGGL((bw_dqk_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * ndt)), dim3(BW_THREADS), 0, s, q, k, v,
+                     dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DQK, F.DV, ndt,
+                     F.qk_scale);
+  if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dQ, dK)"))) return rc;
+  hipLaunchKernelGGL((bw_gates_kernel<TG>), dim3((unsigned)BNH), dim3(BW_THREADS), 0, s, fg, dfp, dip, (TG*)A.di,
+                     (TG*)A.df, F.S, ndt, nvt);
+  return check_launch("xl_mlstm_chunkwise_bwd(gates)");
+}
+
+template <typename TQ, typename TG>
+int bw_l(const BwArgs& A, const BwLayout& lay) {
+  switch (A.fw.L) {
+    case 16: return bw_launch<TQ, TG, 16>(A, lay);
+    case 32: return bw_launch<TQ, TG, 32>(A, lay);
+    default: return bw_launch<TQ, TG, 64>(A, lay);
+  }
+}
+
+template <typename TQ>
+int bw_g(const BwArgs& A, const BwLayout& lay) {
+  switch (A.fw.dtype_gates) {
+    case XL_DTYPE_F32: return bw_l<TQ, float>(A, lay);
+    case XL_DTYPE_BF16: return bw_l<TQ, bf16_t>(A, lay);
+    default: return bw_l<TQ, f16_t>(A, lay);
+  }
+}
+
+bool bw_shape_ok(int B, int NH, int S, int DQK, int DV, int L) {
+  return B > 0 && NH > 0 && S > 0 && DQK > 0 && DV > 0 && (L == 16 || L == 32 || L == 64) && S % L == 0;
+}
+
+}  // namespace
+}  // namespace xl
+
+extern "C" size_t xl_mlstm_chunkwise_bwd_workspace_size(int B, int NH, int S, int DQK, int DV, int L) {
+  using namespace xl;
+  if (!bw_shape_ok(B, NH, S, DQK, DV, L)) return 0;
+  return bw_layout(B, NH, S, DQK, DV, L).total;
+}
+
+extern "C" int xl_mlstm_chunkwise_bwd(const void* q, const void* k, const void* v, const void* i, const void* f,
+                                      const float* c0, const float* n0, const float* m0, const void* dh,
+                                      const float* dc_last, void* dq, void* dk, void* dv, void* di, void* df,
+                                      float* dc0, int B, int NH, int S, int DQK, int DV, int L, float qk_scale,
+                                      float eps, int dtype_qkv, int dtype_gates, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  using namespace xl;
+  clear_error();
+  const char* who = "xl_mlstm_chunkwise_bwd";
+  if (B <= 0 || NH <= 0 || S <= 0 || DQK <= 0 || DV <= 0)
+    return set_error(XL_ERR_INVALID_ARG, "%s: dimensions must be positive (B=%d NH=%d S=%d DQK=%d DV=%d)", who, B, NH,
+                     S, DQK, DV);
+  if (L != 16 && L != 32 && L != 64) return set_error(XL_ERR_UNSUPPORTED, "%s: chunk_size=%d not in {16,32,64}", who, L);
+  if (S % L) return set_error(XL_ERR_INVALID_ARG, "%s: Sequence length %d is not divisible by chunk size %d.", who, S, L);
+  if (!dtype_ok(dtype_qkv) || !dtype_ok(dtype_gates)) return set_error(XL_ERR_INVALID_ARG, "%s: unknown dtype", who);
+  if (!q || !k || !v || !i || !f || !dh || !dq || !dk || !dv || !di || !df)
+    return set_error(XL_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!((c0 && n0 && m0) || (!c0 && !n0 && !m0)))
+    return set_error(XL_ERR_INVALID_ARG, "%s: initial states must be given together", who);
+  if (dc0 && !c0) return set_error(XL_ERR_INVALID_ARG, "%s: dc0 asks for the gradient of an initial state not given", who);
+  const long long BNH = (long long)B * NH;
+  if (BNH * (S / L) * ((DV + 63) / 64) > 0x7fffffffLL || BNH * (S / L) * ((DQK + 63) / 64) > 0x7fffffffLL)
+    return set_error(XL_ERR_INVALID_ARG, "%s: too large", who);
+  const BwLayout lay = bw_layout(B, NH, S, DQK, DV, L);
+  if (!workspace || workspace_bytes < lay.total)
+    return set_error(XL_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", who, lay.total,
+                     workspace ? workspace_bytes : (size_t)0);
+  if (((uintptr_t)workspace) & 255u) return set_error(XL_ERR_INVALID_ARG, "%s: workspace must be 256-byte aligned", who);
+  BwArgs A;
+  A.fw = ChunkwiseArgs{q, k, v, i, f, c0, n0, m0, nullptr, nullptr, nullptr, nullptr, B, NH, S, DQK, DV, L,
+                       qk_scale, eps, dtype_qkv, dtype_gates, workspace, workspace_bytes, stream, 1};
+  A.dh = dh;
+  A.dc_last = dc_last;
+  A.dq = dq;
+  A.dk = dk;
+  A.dv = dv;
+  A.di = di;
+  A.df = df;
+  A.dc0 = dc0;
+  switch (dtype_qkv) {
+    case XL_DTYPE_F32: return bw_g<float>(A, lay);
+    case XL_DTYPE_BF16: return bw_g<bf16_t>(A, lay);
+    default: return bw_g<f16_t>(A, lay);
+  }
+}

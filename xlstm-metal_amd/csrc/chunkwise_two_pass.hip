@@ -19,28 +19,6 @@ constexpr int CW_THREADS = 256;
 constexpr int CW_TILE = 64;  // d and v tile of the states pass, v tile of the output pass
 constexpr int CW_DTILE = 32; // contraction tile of the output pass
 
-// ------------------------------------------------------------- gate helpers
-// Per-chunk gate prefix: sb[t] = sum_{u<=t} logsig(f_u) in sequential order
-// (torch's CPU cumsum order), si[t] = i_t.  Needs 2 barriers.
-template <typename TG, int L>
-__device__ __forceinline__ void chunk_gate_prefix(const TG* __restrict__ ig, const TG* __restrict__ fg, size_t g0,
-                                                  float* sb, float* si) {
-  const int tid = threadIdx.x;
-  if (tid < L) {
-    sb[tid] = logsigmoid(to_f32(fg[g0 + tid]));
-    si[tid] = to_f32(ig[g0 + tid]);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int t = 0; t < L; ++t) {
-      acc += sb[t];
-      sb[t] = acc;
-    }
-  }
-  __syncthreads();
-}
-
 // ------------------------------------------------------------ states pass
 template <typename TQ, typename TG, int L>
 __global__ __launch_bounds__(CW_THREADS) void chunk_states_kernel(
@@ -357,6 +335,44 @@ static int two_pass_g(const ChunkwiseArgs& A) {
     case XL_DTYPE_F32: return two_pass_l<TQ, float>(A);
     case XL_DTYPE_BF16: return two_pass_l<TQ, bf16_t>(A);
     default: return two_pass_l<TQ, f16_t>(A);
+  }
+}
+
+template <typename TQ, typename TG>
+static int states_pass_l(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst, float* c_fin, float* n_fin,
+                         float* m_fin) {
+  const int BNH = A.B * A.NH;
+  const int ndt = (A.DQK + CW_TILE - 1) / CW_TILE;
+  const int nvt = (A.DV + CW_TILE - 1) / CW_TILE;
+  const dim3 grid((unsigned)(BNH * ndt * nvt)), blk(CW_THREADS);
+  hipStream_t s = (hipStream_t)A.stream;
+  const TQ *k = (const TQ*)A.k, *v = (const TQ*)A.v;
+  const TG *ig = (const TG*)A.i, *fg = (const TG*)A.f;
+  switch (A.L) {
+    case 16: hipLaunchKernelGGL((chunk_states_kernel<TQ, TG, 16>), grid, blk, 0, s, k, v, ig, fg, A.c0, A.n0, A.m0, Cst, nst, mst, c_fin, n_fin, m_fin, A.S / 16, A.DQK, A.DV, ndt, nvt); break;
+    case 32: hipLaunchKernelGGL((chunk_states_kernel<TQ, TG, 32>), grid, blk, 0, s, k, v, ig, fg, A.c0, A.n0, A.m0, Cst, nst, mst, c_fin, n_fin, m_fin, A.S / 32, A.DQK, A.DV, ndt, nvt); break;
+    case 64: hipLaunchKernelGGL((chunk_states_kernel<TQ, TG, 64>), grid, blk, 0, s, k, v, ig, fg, A.c0, A.n0, A.m0, Cst, nst, mst, c_fin, n_fin, m_fin, A.S / 64, A.DQK, A.DV, ndt, nvt); break;
+    default: hipLaunchKernelGGL((chunk_states_kernel<TQ, TG, 128>), grid, blk, 0, s, k, v, ig, fg, A.c0, A.n0, A.m0, Cst, nst, mst, c_fin, n_fin, m_fin, A.S / 128, A.DQK, A.DV, ndt, nvt); break;
+  }
+  return check_launch("chunkwise states pass");
+}
+
+template <typename TQ>
+static int states_pass_g(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst, float* c_fin, float* n_fin,
+                         float* m_fin) {
+  switch (A.dtype_gates) {
+    case XL_DTYPE_F32: return states_pass_l<TQ, float>(A, Cst, nst, mst, c_fin, n_fin, m_fin);
+    case XL_DTYPE_BF16: return states_pass_l<TQ, bf16_t>(A, Cst, nst, mst, c_fin, n_fin, m_fin);
+    default: return states_pass_l<TQ, f16_t>(A, Cst, nst, mst, c_fin, n_fin, m_fin);
+  }
+}
+
+int chunkwise_states_pass(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst, float* c_fin, float* n_fin,
+                          float* m_fin) {
+  switch (A.dtype_qkv) {
+    case XL_DTYPE_F32: return states_pass_g<float>(A, Cst, nst, mst, c_fin, n_fin, m_fin);
+    case XL_DTYPE_BF16: return states_pass_g<bf16_t>(A, Cst, nst, mst, c_fin, n_fin, m_fin);
+    default: return states_pass_g<f16_t>(A, Cst, nst, mst, c_fin, n_fin, m_fin);
   }
 }
 

@@ -1,7 +1,7 @@
 """xlstm_hip — MI355X (gfx950) mLSTM/sLSTM kernel backend.
 
 Drop-in for the torch-native kernel API of MLXPorts/xLSTM-metal: chunkwise
-mLSTM prefill, recurrent decode step and sequence, sLSTM step and sequence,
+mLSTM prefill and its custom backward, recurrent decode step and sequence, sLSTM step and sequence,
 the sLSTM layer's causal conv1d + SiLU and per-head GroupNorm, the mLSTM
 output cell's multi-head RMSNorm x sigmoid(o), soft_cap and the logit
 projection with its soft-cap epilogue,
@@ -14,7 +14,7 @@ from .backend import (
     available_kernels, get_mlstm_kernel, get_mlstm_sequence_kernel, get_mlstm_step_kernel, mLSTMBackend,
     mLSTMBackendConfig, wrap_chunkwise__arbitrary_sequence_length, wrap_chunkwise__pad_zeros,
 )
-from .chunkwise import mlstm_chunkwise, mlstm_chunkwise__native_autograd
+from .chunkwise import mlstm_chunkwise, mlstm_chunkwise__native_autograd, mlstm_chunkwise__native_custbw
 from .ops import chunkwise_algorithm
 from .mlstm_layers import (
     MultiHeadLayerNorm, MultiHeadRMSNorm, gate_proj_softcap, mh_rmsnorm_gate, mLSTMOutputCell, mLSTMProjectionCell,
@@ -36,7 +36,8 @@ def load_library():
 
 
 __all__ = [
-    "mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "chunkwise_algorithm", "mlstm_recurrent_step__native",
+    "mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "mlstm_chunkwise__native_custbw",
+    "chunkwise_algorithm", "mlstm_recurrent_step__native",
     "mlstm_recurrent_step__native_fw", "mlstm_recurrent_step_", "mlstm_recurrent_sequence__native_fw",
     "mLSTMRecurrentKernelCell",
     "slstm_step", "slstm_step_pytorch", "slstm_sequence", "sLSTMStepwiseKernelCell", "soft_cap", "SoftCapCell",

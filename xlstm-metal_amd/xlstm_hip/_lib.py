@@ -32,6 +32,9 @@ SIGNATURES = {
     "xl_mlstm_chunkwise_algo": (_i, [_i] * 8),
     "xl_mlstm_chunkwise_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 6 + [_f, _f] + [_i] * 3
                                + [_vp, _sz, _vp]),
+    "xl_mlstm_chunkwise_bwd_workspace_size": (_sz, [_i] * 6),
+    "xl_mlstm_chunkwise_bwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp, _fp] + [_vp] * 5 + [_fp] + [_i] * 6 + [_f, _f]
+                               + [_i, _i, _vp, _sz, _vp]),
     "xl_mlstm_chunkwise_noalloc_max_bytes": (_sz, []),
     "xl_mlstm_chunkwise_fwd_noalloc": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 6 + [_f, _f] + [_i] * 2
                                        + [_vp]),

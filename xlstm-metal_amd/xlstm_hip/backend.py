@@ -19,7 +19,7 @@ from typing import Callable, Literal
 import torch
 from torch import nn
 
-from .chunkwise import mlstm_chunkwise__native_autograd
+from .chunkwise import mlstm_chunkwise__native_autograd, mlstm_chunkwise__native_custbw
 from .ops import chunkwise_workspace_bytes
 from .recurrent import mlstm_recurrent_sequence__native_fw, mlstm_recurrent_step__native
 
@@ -40,9 +40,10 @@ DtypeType = Literal["float32", "bfloat16", "float16"]
 BackendModeType = Literal["train", "train_with_padding", "inference"]
 
 _CHUNKWISE = {
-    # both torch-native names run the same HIP forward (forward-only)
+    # both torch-native names run the same HIP forward and, under autograd, the reference's custom
+    # backward (bw.py:198-352; equal to autograd's gradient behind the layer's multi-head norm)
     "chunkwise--native_autograd": mlstm_chunkwise__native_autograd,
-    "chunkwise--native_custbw": mlstm_chunkwise__native_autograd,
+    "chunkwise--native_custbw": mlstm_chunkwise__native_custbw,
 }
 _SEQUENCE = {"native_sequence__native": mlstm_recurrent_sequence__native_fw}
 _STEP = {"native": mlstm_recurrent_step__native}
@@ -103,7 +104,8 @@ def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequ
     c_state = c_initial if c_initial is not None else torch.zeros(B, NH, DHQK, DHHV, device=dev, dtype=torch.float32)
     n_state = n_initial if n_initial is not None else torch.zeros(B, NH, DHQK, device=dev, dtype=torch.float32)
     m_state = m_initial if m_initial is not None else torch.zeros(B, NH, 1, device=dev, dtype=torch.float32)
-    if S > 1 and mlstm_chunkwise_kernel is mlstm_chunkwise__native_autograd and _fused_takes_any_length(q, k, v):
+    if S > 1 and mlstm_chunkwise_kernel in (mlstm_chunkwise__native_autograd, mlstm_chunkwise__native_custbw) \
+            and _fused_takes_any_length(q, k, v):
         # the fused kernel runs 64-token chunks whatever chunk_size names (the forward is
         # chunk-size invariant), so it is called with the size its support was checked for
         h_out, (c_state, n_state, m_state) = mlstm_chunkwise_kernel(

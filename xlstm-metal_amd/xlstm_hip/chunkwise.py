@@ -1,12 +1,23 @@
-"""Chunkwise mLSTM forward with the reference's signatures, on HIP.
+"""Chunkwise mLSTM with the reference's signatures, on HIP.
 
 Drop-in for ``mlstm_chunkwise`` (kernel_development/xlstm/mlstm_block/
-mlstm_chunkwise/vendored/torch/native/fw.py:372-412) and the registry form
-``mlstm_chunkwise__native_autograd`` (.../native/fwbw.py:192-229).
+mlstm_chunkwise/vendored/torch/native/fw.py:372-412) and the registry forms
+``mlstm_chunkwise__native_autograd`` and ``mlstm_chunkwise__native_custbw``
+(.../native/fwbw.py:192-281).
+
+The op's backward is the reference's custom backward (bw.py:198-352, the one
+``__native_custbw`` uses): the states are recomputed from the inputs, the
+per-token divisor max(|q n|, exp(-m)) + eps is a constant, the gradients of the
+last n and m are dropped and those of the initial n and m are zero.  For the
+mLSTM layer (the multi-head norm after h removes each row's scale) it equals
+autograd's gradient, which ``__native_autograd`` gets in the reference by
+differentiating its forward; a loss that sees the scale of h, m0 or the
+last-state path's df (see ``oracle.mlstm.mlstm_chunkwise_bw``) differs from
+autograd there.  S must be a multiple of ``chunk_size`` (16, 32 or 64) for the
+backward.
 
 Differences from the reference, by design: the states are always float32
-(the reference keeps them in ``matK.dtype``, fw.py:65), and the op is
-forward-only (no autograd formula is registered; calling backward raises).
+(the reference keeps them in ``matK.dtype``, fw.py:65).
 
 ``chunk_size`` keeps the reference's contract (S must be a multiple of it,
 fw.py:303-305).  The forward is chunk-size invariant, so with bf16 q/k/v and
@@ -22,7 +33,7 @@ import torch
 from . import _lib
 from .ops import mlstm_chunkwise_op
 
-__all__ = ["mlstm_chunkwise", "mlstm_chunkwise__native_autograd"]
+__all__ = ["mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "mlstm_chunkwise__native_custbw"]
 
 
 def mlstm_chunkwise(matQ, matK, matV, vecI, vecF, matC_initial=None, vecN_initial=None, scaM_initial=None,
@@ -45,3 +56,16 @@ def mlstm_chunkwise__native_autograd(q, k, v, i, f, c_initial=None, n_initial=No
     return mlstm_chunkwise(q, k, v, i, f, c_initial, n_initial, m_initial, qk_scale=None,
                            return_last_states=return_last_states, chunk_size=chunk_size, eps=eps,
                            algo=kwargs.get("algo", "auto"))
+
+
+def mlstm_chunkwise__native_custbw(q, k, v, i, f, c_initial=None, n_initial=None, m_initial=None,
+                                   return_last_states=False, eps=1e-6, chunk_size=64,
+                                   autocast_kernel_dtype=torch.float32, **kwargs):
+    """Registry form with the custom backward (fwbw.py:232-281).  ``autocast_kernel_dtype`` casts
+    q, k, v, i, f to that dtype when autocast is on, as the reference's custom_fwd does."""
+    if torch.is_autocast_enabled():
+        q, k, v, i, f = (t.to(autocast_kernel_dtype) for t in (q, k, v, i, f))
+    h = mlstm_chunkwise(q, k, v, i, f, c_initial, n_initial, m_initial, qk_scale=None,
+                        return_last_states=return_last_states, chunk_size=chunk_size, eps=eps,
+                        algo=kwargs.get("algo", "auto"))
+    return h

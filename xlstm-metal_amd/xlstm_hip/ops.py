@@ -18,7 +18,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = [
-    "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_sequence_op",
+    "soft_cap_op", "mlstm_step_op", "mlstm_step_inplace_op", "mlstm_chunkwise_op", "mlstm_chunkwise_bwd_op", "mlstm_sequence_op",
     "slstm_step_op", "slstm_sequence_op", "causal_conv1d_op", "group_norm_op", "mh_rmsnorm_gate_op",
     "gate_proj_softcap_op", "lm_head_softcap_op", "chunkwise_workspace_bytes", "chunkwise_algorithm",
 ]
@@ -235,6 +235,76 @@ def _(q, k, v, i, f, c0, n0, m0, qk_scale, chunk_size, eps, return_last_states, 
         return (h,) + tuple(q.new_empty(_EMPTY_SHAPE, dtype=torch.float32) for _ in range(3))
     return (h, q.new_empty((B, NH, DQK, DV), dtype=torch.float32), q.new_empty((B, NH, DQK), dtype=torch.float32),
             q.new_empty((B, NH, 1), dtype=torch.float32))
+
+
+# ----------------------------------------------------------- chunkwise backward
+@torch.library.custom_op("xlstm_hip::mlstm_chunkwise_bwd", mutates_args=())
+def mlstm_chunkwise_bwd_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c0: Optional[Tensor],
+                           n0: Optional[Tensor], m0: Optional[Tensor], dh: Tensor, dc_last: Optional[Tensor],
+                           qk_scale: float, chunk_size: int, eps: float
+                           ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The reference's custom backward (mlstm_chunkwise_bw, bw.py:198-352): dq, dk, dv (q's dtype),
+    di, df (the gates' dtype) and dc0 (float32; an empty placeholder without initial states)."""
+    what = "mlstm_chunkwise_bwd"
+    _lib.require_gpu(q, k, v, i, f, c0, n0, m0, dh, dc_last, what=what)
+    B, NH, S, DQK, DV = _seq_shapes(q, k, v, i, f, c0, n0, m0, what)
+    _check(tuple(dh.shape) == (B, NH, S, DV), what, f"dh must be (B, NH, S, DHV), got {tuple(dh.shape)}")
+    _check(dc_last is None or tuple(dc_last.shape) == (B, NH, DQK, DV), what, "dC_last must be (B, NH, DHQK, DHV)")
+    if S % chunk_size != 0:
+        raise AssertionError(f"Sequence length {S} is not divisible by chunk size {chunk_size}.")
+    q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
+    dh = _prep(dh.to(q.dtype))
+    c0, n0, m0, dcl = _f32(c0), _f32(n0), _f32(m0), _f32(dc_last)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    di, df = torch.empty_like(i), torch.empty_like(f)
+    dc0 = (torch.empty((B, NH, DQK, DV), dtype=torch.float32, device=q.device) if c0 is not None
+           else torch.empty(_EMPTY_SHAPE, dtype=torch.float32, device=q.device))
+    lib = _lib.load()
+    ws_bytes = int(lib.xl_mlstm_chunkwise_bwd_workspace_size(B, NH, S, DQK, DV, int(chunk_size)))
+    _check(ws_bytes > 0, what, f"unsupported shape or chunk_size {chunk_size} (16, 32 or 64)")
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device)
+    rc = lib.xl_mlstm_chunkwise_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(),
+        _lib.ptr(c0), _lib.ptr(n0), _lib.ptr(m0), dh.data_ptr(), _lib.ptr(dcl),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), di.data_ptr(), df.data_ptr(),
+        dc0.data_ptr() if c0 is not None else None,
+        B, NH, S, DQK, DV, int(chunk_size), float(qk_scale), float(eps), _lib.dtype_code(q, what),
+        _lib.dtype_code(i, what), ws.data_ptr(), ws_bytes, _lib.stream_of(q))
+    _lib.check(rc, what)
+    return dq, dk, dv, di, df, dc0
+
+
+@mlstm_chunkwise_bwd_op.register_fake
+def _(q, k, v, i, f, c0, n0, m0, dh, dc_last, qk_scale, chunk_size, eps):
+    dc0 = (q.new_empty(tuple(c0.shape), dtype=torch.float32) if c0 is not None
+           else q.new_empty(_EMPTY_SHAPE, dtype=torch.float32))
+    return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape), i.new_empty(i.shape), \
+        f.new_empty(f.shape), dc0
+
+
+def _chunkwise_setup_context(ctx, inputs, output):
+    q, k, v, i, f, c0, n0, m0, qk_scale, chunk_size, eps, return_last_states, algo = inputs
+    ctx.save_for_backward(q, k, v, i, f, c0, n0, m0)
+    ctx.params = (qk_scale, chunk_size, eps, return_last_states)
+
+
+def _chunkwise_backward(ctx, dh, dC, dn, dm):
+    """Gradients of (h, C_last) through the reference's custom backward; those of n_last and m_last
+    are dropped and the initial n and m get zeros, as there (bw.py:340-342)."""
+    q, k, v, i, f, c0, n0, m0 = ctx.saved_tensors
+    qk_scale, chunk_size, eps, return_last_states = ctx.params
+    if dh is None:
+        dh = torch.zeros(q.shape[:3] + (v.shape[-1],), dtype=q.dtype, device=q.device)
+    dcl = dC if (return_last_states and dC is not None) else None
+    dq, dk, dv, di, df, dc0 = mlstm_chunkwise_bwd_op(q, k, v, i, f, c0, n0, m0, dh, dcl, qk_scale, chunk_size, eps)
+    g_c0 = dc0.to(c0.dtype) if c0 is not None else None
+    g_n0 = torch.zeros_like(n0) if n0 is not None else None
+    g_m0 = torch.zeros_like(m0) if m0 is not None else None
+    return dq, dk, dv, di, df, g_c0, g_n0, g_m0, None, None, None, None, None
+
+
+torch.library.register_autograd("xlstm_hip::mlstm_chunkwise", _chunkwise_backward,
+                                setup_context=_chunkwise_setup_context)
 
 
 @torch.library.custom_op("xlstm_hip::mlstm_sequence", mutates_args=())
