@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--chunk-size 64] [--algo auto]
                     [--decode-steps 1000] [--no-cpu-baseline] [--no-decode] [--no-soft-cap] [--no-extra]
     python bench.py --summarize-pmc FETCH_DIR WRITE_DIR      (no GPU: reads rocprofv3 CSVs)
+    python bench.py --summarize-trace TRACE_DIR              (no GPU: per-kernel durations of a kernel trace)
 
 Prints ONE JSON line.  Headline (`value`): chunkwise mLSTM prefill tokens/s
 at BASELINE config 2 (bf16 q/k/v/gates, float32 states, B4 NH8 S8192 DQK256
@@ -233,7 +234,32 @@ def bench_decode(args, dev):
     steps = reps * per_graph
     us = 1e3 * e0.elapsed_time(e1) / steps
     by = decode_bytes(B, NH, DQK, DV)
-    return {"us_per_step": us, "steps": steps, "bytes": by, "mode": mode, "state_sets": nsets, "cfg": cfg}
+    # the practical ceiling for a step's bytes: a plain device copy of each set's C (67 MB read,
+    # 67 MB written), the same rotation over the 6 sets, replayed from a HIP graph
+    dsts = [torch.empty_like(c) for c in Cs]
+    copy_graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for s in range(nsets):
+            dsts[s].copy_(Cs[s])
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    with torch.cuda.graph(copy_graph):
+        for s in range(nsets):
+            dsts[s].copy_(Cs[s])
+    for _ in range(3):
+        copy_graph.replay()
+    torch.cuda.synchronize(dev)
+    creps = max(1, args.decode_steps // nsets)
+    e0.record(stream)
+    for _ in range(creps):
+        copy_graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    copy_us = 1e3 * e0.elapsed_time(e1) / (creps * nsets)
+    return {"us_per_step": us, "steps": steps, "bytes": by, "mode": mode, "state_sets": nsets, "cfg": cfg,
+            "copy_us": copy_us, "copy_bytes": 2 * Cs[0].numel() * Cs[0].element_size()}
 
 
 def bench_soft_cap(args, dev):
@@ -625,22 +651,40 @@ def bench_stack(args, dev, which):
     torch.cuda.synchronize(dev)
     dec_ms = e0.elapsed_time(e1) / steps
     # the decode step's logit projection: the fused lm_head + soft-cap kernel against torch's Linear
-    # (hipBLASLt) then the soft_cap kernel, on the same normalised rows and weights
-    xl = torch.randn(B, 1, cfg.d_model, generator=g, device=dev).to(cfg.dtype)
+    # (hipBLASLt) then the soft_cap kernel, on the same normalised rows; three copies of the weights
+    # used in turn (more than the 256 MB last-level cache holds), as in decoding, where every other
+    # weight of the model streams between two lm_head calls; each variant replayed from a HIP graph
+    from xlstm_hip.soft_cap import lm_head_softcap, soft_cap
+    xn = model.out_norm(torch.randn(B, 1, cfg.d_model, generator=g, device=dev).to(cfg.dtype))
+    W0 = model.lm_head.weight
+    Ws = [W0, W0.clone(), W0.clone()]
+    variants = {True: lambda w: lm_head_softcap(xn, w, cfg.logit_soft_cap),
+                False: lambda w: soft_cap(torch.nn.functional.linear(xn, w), cfg.logit_soft_cap)}
     lm_us = {}
-    for fused in (True, False):
-        model.fused_lm_head = fused
-        for _ in range(5):
-            model.logits(xl)
+    for fused, fn in variants.items():
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for w in Ws:
+                fn(w)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        lg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(lg):
+            for w in Ws:
+                fn(w)
+        for _ in range(3):
+            lg.replay()
+        torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(50):
-            model.logits(xl)
+        for _ in range(20):
+            lg.replay()
         e1.record(stream)
         torch.cuda.synchronize(dev)
-        lm_us[fused] = e0.elapsed_time(e1) * 1e3 / 50
-    model.fused_lm_head = True
-    w_bytes = model.lm_head.weight.numel() * model.lm_head.weight.element_size()
+        lm_us[fused] = e0.elapsed_time(e1) * 1e3 / (20 * len(Ws))
+    del Ws, variants
+    w_bytes = W0.numel() * W0.element_size()
     nparams = sum(p.numel() for p in model.parameters())
     n_sl = sum(cfg.is_slstm(b) for b in range(cfg.num_blocks))
     del model, states, dg
@@ -652,10 +696,12 @@ def bench_stack(args, dev, which):
             "decode_ms_per_step": dec_ms, "decode_tokens_per_s": B / (dec_ms * 1e-3), "decode_steps": steps,
             "decode_mode": "hip_graph (one replay per token)",
             "lm_head_decode": {"rows": B, "weight_bytes": w_bytes,
-                               "final_norm_plus_lm_head_softcap_fused_us": lm_us[True],
-                               "final_norm_plus_linear_then_soft_cap_us": lm_us[False],
+                               "lm_head_softcap_fused_us": lm_us[True],
+                               "linear_then_soft_cap_us": lm_us[False],
                                "fused_weight_stream_TBps": w_bytes / (lm_us[True] * 1e-6) / 1e12,
-                               "note": "eager, 50 calls, HIP events; both include the final RMSNorm"},
+                               "speedup": lm_us[False] / lm_us[True],
+                               "note": "HIP-graph replays of 3 calls on 3 weight copies (cold in the caches), "
+                                       "HIP events"},
             "data": "synthetic: random token ids, weights N(0, 0.02), forget-gate bias 3"}
 
 
@@ -670,6 +716,45 @@ def load_traffic(kernel, workload):
     if not ent or ent.get("workload") != workload:
         return None
     return ent.get("hbm_bytes_per_launch")
+
+
+def _progress(what):
+    """One line on stderr per finished entry (stdout carries only the JSON line)."""
+    print(f"[bench] {what} done", file=sys.stderr, flush=True)
+
+
+def summarize_trace(trace_dir, headline_calls):
+    """Markdown table of a rocprofv3 --kernel-trace run of this script: calls, mean, min and max
+    duration per kernel, the fused chunkwise kernel's first `headline_calls` dispatches (the
+    headline: warm-up, the graph warm replay and the timed steps) listed on their own line."""
+    import csv
+    import glob
+    import re
+    files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"summarize-trace: no *kernel_trace.csv under {trace_dir}")
+    rows = []
+    for fn in files:
+        with open(fn) as fh:
+            rows += [(int(r["Start_Timestamp"]), r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                     for r in csv.DictReader(fh)]
+    rows.sort()
+
+    def short(name):
+        name = name.replace("(anonymous namespace)::", "").replace("xl::fused::", "").replace("xl::", "")
+        name = re.sub(r"\(.*$", "", name)  # drop the parameter list
+        return re.sub(r"^void ", "", name)
+
+    per = {}
+    for _, name, us in rows:
+        per.setdefault(short(name), []).append(us)
+    print("| kernel | calls | mean us | min us | max us |\n|---|---|---|---|---|")
+    for name, ts in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        if name.startswith("chunkwise_fused_kernel<256, false>"):
+            head = ts[:headline_calls]
+            print(f"| {name}, first {len(head)} dispatches (cfg2 headline) | {len(head)} | "
+                  f"{statistics.mean(head):.1f} | {min(head):.1f} | {max(head):.1f} |")
+        print(f"| {name} | {len(ts)} | {statistics.mean(ts):.1f} | {min(ts):.1f} | {max(ts):.1f} |")
 
 
 def summarize_pmc(fetch_dir, write_dir):
@@ -824,9 +909,14 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the sLSTM, recurrent-sequence and any-S entries")
     ap.add_argument("--no-stacks", action="store_true", help="skip the config 3 / 4 end-to-end stacks")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--summarize-trace", metavar="TRACE_DIR",
+                    help="per-kernel durations of a rocprofv3 --kernel-trace run of this script (no GPU)")
     args = ap.parse_args()
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
+        return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.warmup + 2 + args.steps)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on ONE GPU only (no collectives); use --gpus 1", file=sys.stderr)
@@ -839,6 +929,7 @@ def main():
     xlstm_hip.load_library()
 
     pre = bench_prefill(args, dev)
+    _progress("prefill")
     cfg = pre["cfg"]
     value = pre["tokens"] / (pre["ms"] * 1e-3)
     tflops = pre["flops"] / (pre["ms"] * 1e-3) / 1e12
@@ -872,33 +963,53 @@ def main():
             "flops_per_call_reference_L128": p128["flops"]}
     if not args.no_decode:
         dec = bench_decode(args, dev)
+        _progress("decode")
         dgbs = dec["bytes"] / (dec["us_per_step"] * 1e-6) / 1e9
         out["decode"] = {"workload": "cfg1 mlstm decode step", "us_per_step": dec["us_per_step"],
                          "tokens_per_s": dec["cfg"].B / (dec["us_per_step"] * 1e-6), "steps": dec["steps"],
                          "mode": dec["mode"], "state_sets": dec["state_sets"],
                          "roofline": {"bound": "hbm", "achieved": dgbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                       "frac": dgbs / PEAK_HBM_GBS, "bytes_per_step": dec["bytes"],
-                                      "traffic": load_traffic("mlstm_step_kernel", "cfg1 mlstm decode step")}}
+                                      "traffic": load_traffic("mlstm_step_kernel", "cfg1 mlstm decode step")},
+                         "copy_ceiling": {"what": "device copy of each step's C (torch copy_, same 6-set "
+                                                  "rotation, HIP graph)", "bytes": dec["copy_bytes"],
+                                          "us": dec["copy_us"],
+                                          "step_fraction_of_copy": dec["copy_us"] / dec["us_per_step"]}}
     if not args.no_soft_cap:
         out["soft_cap"] = bench_soft_cap(args, dev)
+        _progress("soft_cap")
     if not args.no_extra:
         out["slstm_sequence"] = bench_slstm_sequence(args, dev)
+        _progress("slstm_sequence")
         out["slstm_step"] = bench_slstm_step(args, dev)
+        _progress("slstm_step")
         out["mlstm_sequence"] = bench_mlstm_sequence(args, dev)
+        _progress("mlstm_sequence")
         out["arbitrary_length"] = bench_arbitrary_length(args, dev)
+        _progress("arbitrary_length")
         out["cfg3_heads_chunkwise"] = bench_cfg3_heads(args, dev)
+        _progress("cfg3_heads_chunkwise")
         out["slstm_conv1d_silu"] = bench_slstm_conv(args, dev)
+        _progress("slstm_conv1d_silu")
         out["slstm_group_norm"] = bench_group_norm(args, dev)
+        _progress("slstm_group_norm")
         out["mlstm_output_gate"] = bench_mlstm_output_gate(args, dev)
+        _progress("mlstm_output_gate")
         out["slstm_gate_proj"] = bench_gate_proj(args, dev)
+        _progress("slstm_gate_proj")
         out["chunkwise_bwd"] = bench_chunkwise_bwd(args, dev)
+        _progress("chunkwise_bwd")
     if not args.no_extra:
         out["cfg0"] = bench_cfg0(args, dev)
+        _progress("cfg0")
     if not args.no_stacks:
         out["cfg3_stack"] = bench_stack(args, dev, "cfg3")
+        _progress("cfg3_stack")
         out["cfg4_stack"] = bench_stack(args, dev, "cfg4")
+        _progress("cfg4_stack")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args)
+        _progress("cpu_baseline")
     print(json.dumps(out), flush=True)
 
 
