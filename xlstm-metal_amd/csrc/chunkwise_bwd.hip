@@ -73,6 +73,34 @@ BwLayout bw_layout(int B, int NH, int S, int DQK, int DV, int L) {
   return o;
 }
 
+// inclusive sum over the 64 lanes of a wave (lane order)
+__device__ __forceinline__ float wave_incl_sum(float x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Per-chunk gate prefix of the backward kernels: sb[t] = sum_{u<=t} logsig f_u, si[t] = i_t
+// for the L tokens from g0, scanned by wave 0 (lane = token); called by every thread, one
+// barrier.
+template <typename TG, int L>
+__device__ __forceinline__ void chunk_gate_scan(const TG* __restrict__ ig, const TG* __restrict__ fg, size_t g0,
+                                                float* sb, float* si) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    const float x = tid < L ? logsigmoid(to_f32(fg[g0 + tid])) : 0.f;
+    const float b = wave_incl_sum(x, tid);
+    if (tid < L) {
+      sb[tid] = b;
+      si[tid] = to_f32(ig[g0 + tid]);
+    }
+  }
+  __syncthreads();
+}
+
 // combined stabiliser of token i of a chunk entering with m_prev: max(b_i + m_prev,
 // max_{j<=i} b_i - b_j + i_j) (fw.py:204-217)
 template <int L>
@@ -97,7 +125,7 @@ __global__ __launch_bounds__(BW_THREADS) void bw_stats_kernel(const TQ* __restri
   const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
   const int bh = blockIdx.x / NC, kc = blockIdx.x - bh * NC;
   const size_t row0 = (size_t)bh * NC * L + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
-  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);
   if (tid < L) {
     const float mp = mst[sidx];
     const float mc = m_combine<L>(sb, si, tid, mp);
@@ -190,7 +218,7 @@ __global__ __launch_bounds__(BW_THREADS) void bw_dC_kernel(const TQ* __restrict_
   for (int kc = NC - 1; kc >= 0; --kc) {
     store(dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV);  // bw.py:81
     const size_t row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
-    chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+    chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);
     const float mp = mst[sidx];
     const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
     // Qbar dH~ = q exp(b + m_{k-1} - m_comb) s / (N + eps) (bw.py:92-101)
@@ -260,7 +288,7 @@ __global__ __launch_bounds__(BW_THREADS) void bw_dv_kernel(const TQ* __restrict_
   const int kc = rem / nvt, vt = rem - kc * nvt, v0 = vt * BW_T;
   const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
   const float* dCk = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // gradient of the state after chunk kc
-  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);
   if (tid < L) {
     const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
     smc[tid] = vm[row0 + tid];
@@ -391,7 +419,7 @@ __global__ __launch_bounds__(BW_THREADS) void bw_dqk_kernel(const TQ* __restrict
   const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
   const float* Ck = Cst + sidx * DQK * DV;                                   // state entering chunk kc
   const float* dCk = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // gradient of the state after it
-  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);
   if (tid < L) {
     const float mp = mst[sidx];
     const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
@@ -552,6 +580,216 @@ __global__ __launch_bounds__(BW_THREADS) void bw_gates_kernel(const TG* __restri
   }
 }
 
+// --------------------------------------------------- MFMA chunk scans (1, 3)
+// The two chunk-sequential passes on v_mfma_f32_16x16x4f32: float32 operands and
+// accumulation, the arithmetic of the FMA form at the matrix cores' rate.  One
+// workgroup of 4 waves per (head, 64 columns of DV); wave w holds rows
+// [16 NRT w, 16 NRT (w + 1)) of the DQK x 64 state as NRT x 4 accumulator tiles of
+// 16 x 16.  Per chunk, X (K forward, Q reverse) is staged in LDS in its own dtype and
+// Y (V forward, dH reverse) in float32 with the per-token coefficient folded in, then
+//   state = decay state + sum_t X[t][rows]^T (coef_t Y[t][cols]),
+// four tokens per MFMA: lane (g, r) supplies X[t0 + g][row r of the tile] and
+// coef Y[t0 + g][column r of the tile] (16x16x4: A[i][k] in lane i + 16 k, B[k][j] in
+// lane j + 16 k, D[i][j] in lane j + 16 (i / 4), element i % 4).  The next chunk's
+// X, Y and gates are loaded into registers while the MFMAs run.
+//  * forward (REV false): X = K, Y = V, coef_t = exp(a_t - m'), decay = exp(g + m - m');
+//    stores the state entering every chunk (recurrent_fw_C, fw.py:98-143), with n (v
+//    tile 0) and m beside it, and the state after the last chunk;
+//  * reverse (REV true): X = Q, Y = dH, coef_t = exp(b_t + m_{k-1} - m_t) s / (N_t + eps),
+//    decay = exp(g + m_{k-1} - m_k); stores the gradient of the state after every chunk
+//    and, last, of the initial state (bw.py:31-115).
+constexpr int SC_V = 64;          // DV columns per workgroup
+constexpr int SC_YP = SC_V + 16;  // floats per staged Y row (16 mod 64 dwords: 4 rows, distinct banks)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <typename T>
+union Piece16 {
+  u32x4 raw;
+  T v[16 / sizeof(T)];
+};
+
+template <typename TQ, typename TG, int L, int NRT, bool REV>
+__global__ __launch_bounds__(256) void bw_scan_kernel(
+    const TQ* __restrict__ X, const TQ* __restrict__ Y, const TG* __restrict__ ig, const TG* __restrict__ fg,
+    const float* __restrict__ s0, const float* __restrict__ n0, const float* __restrict__ m0,
+    const float* __restrict__ vm, const float* __restrict__ vn, float* __restrict__ Sst, float* __restrict__ nst,
+    float* __restrict__ mst, float* __restrict__ sfin, float* __restrict__ nfin, float* __restrict__ mfin,
+    float* __restrict__ s_init, int NC, int DV, int nvt, float qk_scale) {
+  constexpr int DQK = 64 * NRT;
+  constexpr int XP = DQK + 16;  // elements per staged X row (see the bank note above)
+  constexpr int EPV = 16 / sizeof(TQ);
+  constexpr int PRX = DQK / EPV, NX = L * PRX, NXP = (NX + 255) / 256;
+  constexpr int PRY = SC_V / EPV, NY = L * PRY, NYP = (NY + 255) / 256;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  TQ* sX = reinterpret_cast<TQ*>(smem_raw);
+  float* sY = reinterpret_cast<float*>(smem_raw + (size_t)L * XP * sizeof(TQ));
+  __shared__ float scoef[L];
+  __shared__ float s_mn, s_g;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int bh = blockIdx.x / nvt, vt = blockIdx.x - bh * nvt, v0 = vt * SC_V;
+  const size_t S = (size_t)NC * L;
+  const int row0 = w * 16 * NRT;
+  const int nslots = REV ? NC + 1 : NC;
+
+  f32x4 acc[NRT][4];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[rt][ct][e] = s0 ? s0[((size_t)bh * DQK + row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] : 0.f;
+  auto store_state = [&](float* dst) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(size_t)(row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] = acc[rt][ct][e];
+  };
+  const bool owns_n = !REV && vt == 0 && tid < DQK;
+  float nn = (owns_n && n0) ? n0[(size_t)bh * DQK + tid] : 0.f;
+  float m = (!REV && m0) ? m0[bh] : 0.f;
+
+  // prefetch registers: X, Y pieces and this thread's token gates (tid < L)
+  u32x4 px[NXP], py[NYP];
+  float pf = 0.f, pi = 0.f, pvm = 0.f, pvn = 1.f, pmp = 0.f;
+  auto fetch = [&](int kc) {
+    const size_t t0 = (size_t)bh * S + (size_t)kc * L;
+#pragma unroll
+    for (int u = 0; u < NXP; ++u) {
+      const int p = u * 256 + tid;
+      if (NX % 256 == 0 || p < NX)
+        px[u] = *reinterpret_cast<const u32x4*>(X + (t0 + p / PRX) * DQK + (p % PRX) * EPV);
+    }
+#pragma unroll
+    for (int u = 0; u < NYP; ++u) {
+      const int p = u * 256 + tid;
+      if (NY % 256 == 0 || p < NY)
+        py[u] = *reinterpret_cast<const u32x4*>(Y + (t0 + p / PRY) * DV + v0 + (p % PRY) * EPV);
+    }
+    if (tid < L) {
+      pf = to_f32(fg[t0 + tid]);
+      pi = to_f32(ig[t0 + tid]);
+      if (REV) {
+        pvm = vm[t0 + tid];
+        pvn = vn[t0 + tid];
+      }
+    }
+    if (REV) pmp = mst[(size_t)bh * NC + kc];  // m entering chunk kc
+  };
+  float mnext = REV ? mfin[bh] : 0.f;  // reverse: m after the chunk being processed
+  const int kfirst = REV ? NC - 1 : 0;
+  fetch(kfirst);
+  for (int it = 0; it < NC; ++it) {
+    const int kc = REV ? NC - 1 - it : it;
+    const size_t sidx = (size_t)bh * NC + kc;
+    const int slot = REV ? kc + 1 : kc;
+    // gates of this chunk from the prefetched values, wave 0 (lane = token): b = cumsum logsig f,
+    // then the coefficients and the decay
+    const float cvm = pvm, cvn = pvn, cmp = pmp;
+    if (w == 0) {
+      const float b = wave_incl_sum(lane < L ? logsigmoid(pf) : 0.f, lane);
+      const float gl = __shfl(b, L - 1, 64);
+      if (!REV) {
+        const float a = lane < L ? gl - b + pi : -INFINITY;
+        const float mn = fmaxf(gl + m, wave_max(a));  // fw.py:115
+        if (lane < L) scoef[lane] = expf(a - mn);     // fw.py:121
+        if (lane == 0) {
+          s_mn = mn;
+          s_g = gl;
+        }
+      } else {
+        if (lane < L) scoef[lane] = expf(b + cmp - cvm) * qk_scale / cvn;  // bw.py:92-101
+        if (lane == 0) s_g = gl;
+      }
+    }
+    __syncthreads();
+    const float gch = s_g;
+    float decay;
+    const float m_in = m;
+    if (!REV) {
+      const float mn = s_mn;
+      decay = expf(gch + m - mn);  // fw.py:125
+      m = mn;
+    } else {
+      decay = expf(gch + cmp - mnext);  // bw.py:86-89
+      mnext = cmp;
+    }
+    // stage X (own dtype) and coef Y (float32)
+#pragma unroll
+    for (int u = 0; u < NXP; ++u) {
+      const int p = u * 256 + tid;
+      if (NX % 256 == 0 || p < NX) *reinterpret_cast<u32x4*>(sX + (p / PRX) * XP + (p % PRX) * EPV) = px[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NYP; ++u) {
+      const int p = u * 256 + tid;
+      if (NY % 256 == 0 || p < NY) {
+        const int t = p / PRY, c = (p % PRY) * EPV;
+        Piece16<TQ> pc;
+        pc.raw = py[u];
+        const float co = scoef[t];
+        float* dst = sY + t * SC_YP + c;
+#pragma unroll
+        for (int e = 0; e < EPV; e += 4)
+          *reinterpret_cast<f32x4*>(dst + e) =
+              f32x4{co * to_f32(pc.v[e]), co * to_f32(pc.v[e + 1]), co * to_f32(pc.v[e + 2]), co * to_f32(pc.v[e + 3])};
+      }
+    }
+    if (it + 1 < NC) fetch(REV ? kc - 1 : kc + 1);
+    __syncthreads();
+    // the state entering this chunk (forward) / after it (reverse), stored here, after the
+    // waits for the staged data, so that the next wait (one chunk later) finds them done
+    store_state(Sst + ((size_t)bh * nslots + slot) * DQK * DV);
+    if (owns_n) nst[sidx * DQK + tid] = nn;
+    if (!REV && vt == 0 && tid == 0) mst[sidx] = m_in;
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) acc[rt][ct] *= decay;
+#pragma unroll 4
+    for (int t0 = 0; t0 < L; t0 += 4) {
+      float a[NRT], b[4];
+      const TQ* xr = sX + (t0 + g) * XP + row0 + r;
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) a[rt] = to_f32(xr[16 * rt]);
+      const float* yr = sY + (t0 + g) * SC_YP + r;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) b[ct] = yr[16 * ct];
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = mfma4(a[rt], b[ct], acc[rt][ct]);
+    }
+    if (owns_n) {  // n' = decay n + sum_t coef_t k_t (fw.py:133)
+      float sacc = 0.f;
+      for (int t = 0; t < L; ++t) sacc += scoef[t] * to_f32(sX[t * XP + tid]);
+      nn = decay * nn + sacc;
+    }
+    __syncthreads();  // the staged tiles are read; the next chunk may overwrite them
+  }
+  if (!REV) {
+    store_state(sfin + (size_t)bh * DQK * DV);
+    if (owns_n) nfin[(size_t)bh * DQK + tid] = nn;
+    if (vt == 0 && tid == 0) mfin[bh] = m;
+  } else {
+    store_state(Sst + (size_t)bh * nslots * DQK * DV);
+    if (s_init) store_state(s_init + (size_t)bh * DQK * DV);
+  }
+}
+
+template <typename TQ, int L>
+constexpr size_t scan_smem(int NRT) {
+  return (size_t)L * (64 * NRT + 16) * sizeof(TQ) + (size_t)L * SC_YP * sizeof(float);
+}
+
 // ---------------------------------------------------------------- launchers
 struct BwArgs {
   ChunkwiseArgs fw;
@@ -560,6 +798,131 @@ struct BwArgs {
   void *dq, *dk, *dv, *di, *df;
   float* dc0;
 };
+
+// ------------------------------------------------------- MFMA dV pass (4)
+// dV on v_mfma_f32_16x16x4f32 for 16-bit q/k/v/dH and 64-token chunks: one workgroup of
+// 4 waves per (head, chunk, 64 columns of DV) as in bw_dv_kernel.  Wave w owns columns
+// [16 w, 16 w + 16) of the tile and the j-tile w of Sbar, for all 64 tokens (4 row tiles):
+//   over d (4 per MFMA): A = K[t][d] (K staged in LDS), B = Q[16 w + r][d] (Sbar^T) and
+//     dC_k[d][v] (the inter term), both straight from global memory;
+//   Sbar^T gated (fw.py:204-227) into LDS; dV rows scaled by Abar_t (bw.py:179);
+//   over j: A = Sbar^T[t][j] (LDS), B = dH[j][v] / (N_j + eps) (bw.py:156).
+// Lane (g, r) ends with dV[16 tt + 4 g + e][16 w + r]; the v . dV partials of dI are summed
+// over the 16 lanes of a column group, then over the 4 waves in LDS.
+constexpr int DVM_SP = 68;  // floats per row of the staged Sbar^T
+
+template <typename TQ, typename TG, int NRT>
+__global__ __launch_bounds__(256) void bw_dv_mfma_kernel(const TQ* __restrict__ q, const TQ* __restrict__ k,
+                                                          const TQ* __restrict__ v, const TQ* __restrict__ dh,
+                                                          const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                          const float* __restrict__ mst,
+                                                          const float* __restrict__ mfin,
+                                                          const float* __restrict__ vm,
+                                                          const float* __restrict__ vn,
+                                                          const float* __restrict__ dCst, TQ* __restrict__ dv,
+                                                          float* __restrict__ dip, int NC, int DV, int nvt,
+                                                          float qk_scale) {
+  constexpr int L = 64;
+  constexpr int DQK = 64 * NRT;
+  constexpr int XP = DQK + 8;  // elements per staged K row (16-byte rows, 4 mod 64 dwords apart)
+  constexpr int EPV = 16 / sizeof(TQ);
+  constexpr int PRX = DQK / EPV;
+  static_assert(sizeof(TQ) == 2, "16-bit operands");
+  __shared__ __attribute__((aligned(16))) TQ sK[L * XP];
+  __shared__ float sS[L * DVM_SP];
+  __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L];
+  __shared__ float s_part[4][L];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int per_bh = NC * nvt;
+  const int bh = blockIdx.x / per_bh, rem = blockIdx.x - bh * per_bh;
+  const int kc = rem / nvt, vt = rem - kc * nvt, v0 = vt * 64;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  const float* dCk = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // gradient of the state after chunk kc
+  // stage K of the chunk
+  for (int p = tid; p < L * PRX; p += 256) {
+    const int t = p / PRX, c = (p % PRX) * EPV;
+    *reinterpret_cast<u32x4*>(sK + t * XP + c) = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + c);
+  }
+  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);  // its barrier also covers the K tile
+  if (tid < L) {
+    const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+    smc[tid] = vm[row0 + tid];
+    sinv[tid] = 1.0f / vn[row0 + tid];
+    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - mn);  // Abar (bw.py:168-176)
+  }
+  f32x4 accS[4], accV[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    accS[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accV[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const TQ* qrow = q + (row0 + 16 * w + r) * DQK;
+  const float* dcol = dCk + v0 + 16 * w + r;
+#pragma unroll 8
+  for (int d0 = 0; d0 < DQK; d0 += 4) {
+    const float bq = to_f32(qrow[d0 + g]);
+    const float bc = dcol[(size_t)(d0 + g) * DV];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const float a = to_f32(sK[(16 * tt + r) * XP + d0 + g]);
+      accS[tt] = mfma4(a, bq, accS[tt]);
+      accV[tt] = mfma4(a, bc, accV[tt]);
+    }
+  }
+  __syncthreads();  // gate rows (smc, sab) visible
+  // Sbar^T[t][j] = S[j][t] Dbar[j][t] on t <= j; inter rows scaled by Abar_t
+  const int j = 16 * w + r;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * g + e;
+      sS[t * DVM_SP + j] = (t <= j) ? accS[tt][e] * qk_scale * expf(sb[j] - sb[t] + si[t] - smc[j]) : 0.f;
+      accV[tt][e] *= sab[t];
+    }
+  __syncthreads();
+  // intra: dV[t][v] += sum_j Sbar^T[t][j] dH[j][v] / (N_j + eps)
+  const TQ* hcol = dh + row0 * DV + v0 + 16 * w + r;
+#pragma unroll 4
+  for (int j0 = 0; j0 < L; j0 += 4) {
+    const float b = to_f32(hcol[(size_t)(j0 + g) * DV]) * sinv[j0 + g];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) accV[tt] = mfma4(sS[(16 * tt + r) * DVM_SP + j0 + g], b, accV[tt]);
+  }
+  // store dV; v . dV partials of dI (bw.py:338)
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * g + e;
+      const size_t off = (row0 + t) * DV + v0 + 16 * w + r;
+      dv[off] = from_f32<TQ>(accV[tt][e]);
+      const float part = sum16(to_f32(v[off]) * accV[tt][e]);
+      if (r == 0) s_part[w][t] = part;
+    }
+  __syncthreads();
+  if (tid < L) dip[(row0 + tid) * nvt + vt] = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+}
+
+template <typename TQ, typename TG, int L, bool REV>
+int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* s0, const float* n0,
+                const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst, float* sfin,
+                float* nfin, float* mfin, float* s_init, int BNH, int NC, int DV, float qk_scale, hipStream_t st) {
+  const int nvt = DV / SC_V;
+  auto go = [&](auto kern, size_t smem) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess)
+      return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_bwd: LDS attribute failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvt)), dim3(256), smem, st, X, Y, ig, fg, s0, n0, m0, vm, vn, Sst,
+                       nst, mst, sfin, nfin, mfin, s_init, NC, DV, nvt, qk_scale);
+    return check_launch(REV ? "xl_mlstm_chunkwise_bwd(dC scan)" : "xl_mlstm_chunkwise_bwd(states scan)");
+  };
+  switch (DQK) {
+    case 64: return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1));
+    case 128: return go(bw_scan_kernel<TQ, TG, L, 2, REV>, scan_smem<TQ, L>(2));
+    default: return go(bw_scan_kernel<TQ, TG, L, 4, REV>, scan_smem<TQ, L>(4));
+  }
+}
 
 template <typename TQ, typename TG, int L>
 int bw_launch(const BwArgs& A, const BwLayout& lay) {
@@ -574,16 +937,41 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   hipStream_t s = (hipStream_t)F.stream;
   const TQ *q = (const TQ*)F.q, *k = (const TQ*)F.k, *v = (const TQ*)F.v, *dh = (const TQ*)A.dh;
   const TG *ig = (const TG*)F.i, *fg = (const TG*)F.f;
-  int rc = chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
+  // the chunk scans on the matrix cores when the state tiles fit their layout
+  const bool scan_mfma = F.DV % SC_V == 0 && (F.DQK == 64 || F.DQK == 128 || F.DQK == 256);
+  int rc = scan_mfma ? launch_scan<TQ, TG, L, false>(F.DQK, k, v, ig, fg, F.c0, F.n0, F.m0, nullptr, nullptr, Cst,
+                                                     nst, mst, cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s)
+                     : chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
   if (rc) return rc;
   hipLaunchKernelGGL((bw_stats_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC)), dim3(BW_THREADS), 0, s, q, k, ig, fg,
                      nst, mst, vm, vn, NC, F.DQK, F.qk_scale, F.eps);
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(stats)"))) return rc;
-  hipLaunchKernelGGL((bw_dC_kernel<TQ, TG, L>), dim3((unsigned)(BNH * ndt * nvt)), dim3(BW_THREADS), 0, s, q, dh, ig,
-                     fg, mst, mfin, vm, vn, A.dc_last, dC, A.dc0, NC, F.DQK, F.DV, ndt, nvt, F.qk_scale);
-  if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dC)"))) return rc;
-  hipLaunchKernelGGL((bw_dv_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * nvt)), dim3(BW_THREADS), 0, s, q, k, v, dh,
-                     ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DQK, F.DV, nvt, F.qk_scale);
+  if (scan_mfma) {
+    rc = launch_scan<TQ, TG, L, true>(F.DQK, q, dh, ig, fg, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr, mst,
+                                      nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
+  } else {
+    hipLaunchKernelGGL((bw_dC_kernel<TQ, TG, L>), dim3((unsigned)(BNH * ndt * nvt)), dim3(BW_THREADS), 0, s, q, dh,
+                       ig, fg, mst, mfin, vm, vn, A.dc_last, dC, A.dc0, NC, F.DQK, F.DV, ndt, nvt, F.qk_scale);
+    rc = check_launch("xl_mlstm_chunkwise_bwd(dC)");
+  }
+  if (rc) return rc;
+  // dV and dQ/dK on the matrix cores for 16-bit operands, 64-token chunks and whole 64-wide tiles
+  bool tiles_mfma = false;
+  if constexpr (sizeof(TQ) == 2 && L == 64) {
+    tiles_mfma = scan_mfma;
+    if (tiles_mfma) {
+      const dim3 grid((unsigned)(BNH * NC * nvt));
+      switch (F.DQK) {
+        case 64: hipLaunchKernelGGL((bw_dv_mfma_kernel<TQ, TG, 1>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
+        case 128: hipLaunchKernelGGL((bw_dv_mfma_kernel<TQ, TG, 2>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
+        default: hipLaunchKernelGGL((bw_dv_mfma_kernel<TQ, TG, 4>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
+      }
+    }
+  }
+  if (!tiles_mfma) {
+    hipLaunchKernelGGL((bw_dv_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * nvt)), dim3(BW_THREADS), 0, s, q, k, v,
+                       dh, ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DQK, F.DV, nvt, F.qk_scale);
+  }
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dV)"))) return rc;
   hipLaunchKernelGGL((bw_dqk_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * ndt)), dim3(BW_THREADS), 0, s, q, k, v,
                      dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DQK, F.DV, ndt,
