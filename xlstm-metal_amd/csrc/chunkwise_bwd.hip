@@ -904,6 +904,163 @@ __global__ __launch_bounds__(256) void bw_dv_mfma_kernel(const TQ* __restrict__ 
   if (tid < L) dip[(row0 + tid) * nvt + vt] = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
 }
 
+// ---------------------------------------------------- MFMA dQ, dK pass (5)
+// dQ and dK on v_mfma_f32_16x16x4f32 for 16-bit q/k/v/dH and 64-token chunks: one workgroup
+// of 4 waves per (head, chunk, 64 columns of DQK) as in bw_dqk_kernel.  Wave w owns columns
+// [16 w, 16 w + 16) of the tile and the j-tile w of dS~, for all 64 tokens.
+//  Phase 1, over DV in blocks of 64 (dH and V staged in LDS, C_{k-1} and dC_k rows from
+//  global memory one block ahead), 4 v per MFMA in the order v = 16 g + ks of a block
+//  (lane group g, k-step ks; any order of the contraction serves, and this one makes the
+//  C / dC operands of a lane 16 consecutive floats):
+//    dS~[t][j] = sum_v dH[t][v] V[j][v],  Q~[t][d] = sum_v dH[t][v] C[d][v],
+//    K~[t][d] = sum_v V[t][v] dC[d][v].
+//  Then dS = dS~ / (N_t + eps) Dbar[t][j] s (bw.py:158-159) into LDS, dQ = Q~ Bbar_t s /
+//  (N_t + eps) (bw.py:182), dK = K~ Abar_t (bw.py:181), and phase 2 adds dS K and dS^T Q over
+//  the chunk's tokens (bw.py:161-162), K and Q of the tile staged in LDS.
+constexpr int DQM_P = 72;   // elements per staged 64-wide bf16 row (144 bytes: 36 mod 64 dwords)
+constexpr int DQM_SP = 68;  // floats per staged dS row
+
+template <typename TQ, typename TG, int NRT>
+__global__ __launch_bounds__(256) void bw_dqk_mfma_kernel(const TQ* __restrict__ q, const TQ* __restrict__ k,
+                                                           const TQ* __restrict__ v, const TQ* __restrict__ dh,
+                                                           const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                           const float* __restrict__ Cst,
+                                                           const float* __restrict__ mst,
+                                                           const float* __restrict__ mfin,
+                                                           const float* __restrict__ vm,
+                                                           const float* __restrict__ vn,
+                                                           const float* __restrict__ dCst, TQ* __restrict__ dq,
+                                                           TQ* __restrict__ dk, float* __restrict__ dfp, int NC, int DV,
+                                                           int ndt, float qk_scale) {
+  constexpr int L = 64;
+  constexpr int DQK = 64 * NRT;
+  static_assert(sizeof(TQ) == 2, "16-bit operands");
+  // phase 1: sA = dH block, sB = V block; phase 2: sA = K tile, sB = Q tile
+  __shared__ __attribute__((aligned(16))) TQ sA[L * DQM_P];
+  __shared__ __attribute__((aligned(16))) TQ sB[L * DQM_P];
+  __shared__ float sdS[L * DQM_SP];
+  __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L], sbb[L];
+  __shared__ float s_part[4][L];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int per_bh = NC * ndt;
+  const int bh = blockIdx.x / per_bh, rem = blockIdx.x - bh * per_bh;
+  const int kc = rem / ndt, dt = rem - kc * ndt, d0 = dt * 64;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  const float* crow = Cst + sidx * DQK * DV + (size_t)(d0 + 16 * w + r) * DV;  // C_{k-1} row d
+  const float* dcrow = dCst + (((size_t)bh * (NC + 1) + kc + 1) * DQK + d0 + 16 * w + r) * DV;  // dC_k row d
+  // 64 x 64 bf16 tiles: 512 pieces of 16 bytes, 2 per thread (rows p / 8, 8 elements at 8 (p % 8))
+  u32x4 pa[2], pb[2];
+  auto fetch_tiles = [&](const TQ* A, const TQ* Bm, int stride, int col) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      pa[u] = *reinterpret_cast<const u32x4*>(A + (row0 + t) * stride + col + c);
+      pb[u] = *reinterpret_cast<const u32x4*>(Bm + (row0 + t) * stride + col + c);
+    }
+  };
+  auto store_tiles = [&]() {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      *reinterpret_cast<u32x4*>(sA + t * DQM_P + c) = pa[u];
+      *reinterpret_cast<u32x4*>(sB + t * DQM_P + c) = pb[u];
+    }
+  };
+  // this lane's C and dC operands of a block: v = vb + 16 g + 0..15
+  f32x4 pc[4], pd[4];
+  auto fetch_cd = [&](int vb) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      pc[u] = *reinterpret_cast<const f32x4*>(crow + vb + 16 * g + 4 * u);
+      pd[u] = *reinterpret_cast<const f32x4*>(dcrow + vb + 16 * g + 4 * u);
+    }
+  };
+  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);
+  if (tid < L) {
+    const float mp = mst[sidx];
+    const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+    const float mc = vm[row0 + tid];
+    smc[tid] = mc;
+    sinv[tid] = 1.0f / vn[row0 + tid];
+    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - mn);  // Abar (bw.py:168-176)
+    sbb[tid] = expf(sb[tid] + mp - mc) * qk_scale;        // Bbar s (bw.py:175, 182)
+  }
+  f32x4 accS[4], accQ[4], accK[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    accS[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accQ[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accK[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  fetch_tiles(dh, v, DV, 0);
+  fetch_cd(0);
+  for (int vb = 0; vb < DV; vb += 64) {
+    store_tiles();
+    const f32x4 cc[4] = {pc[0], pc[1], pc[2], pc[3]}, cd[4] = {pd[0], pd[1], pd[2], pd[3]};
+    __syncthreads();
+    if (vb + 64 < DV) {
+      fetch_tiles(dh, v, DV, vb + 64);
+      fetch_cd(vb + 64);
+    } else {  // phase 2's K and Q tiles
+      fetch_tiles(k, q, DQK, d0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const int vv = 16 * g + ks;
+      const float bV = to_f32(sB[(16 * w + r) * DQM_P + vv]);
+      const float bC = cc[ks >> 2][ks & 3], bD = cd[ks >> 2][ks & 3];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float aH = to_f32(sA[(16 * tt + r) * DQM_P + vv]);
+        const float aV = to_f32(sB[(16 * tt + r) * DQM_P + vv]);
+        accS[tt] = mfma4(aH, bV, accS[tt]);
+        accQ[tt] = mfma4(aH, bC, accQ[tt]);
+        accK[tt] = mfma4(aV, bD, accK[tt]);
+      }
+    }
+    __syncthreads();  // the blocks are read; the next staging may overwrite them
+  }
+  // dS into LDS; inter terms scaled
+  const int j = 16 * w + r;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * g + e;
+      sdS[t * DQM_SP + j] =
+          (j <= t) ? accS[tt][e] * sinv[t] * expf(sb[t] - sb[j] + si[j] - smc[t]) * qk_scale : 0.f;
+      accQ[tt][e] *= sbb[t] * sinv[t];
+      accK[tt][e] *= sab[t];
+    }
+  store_tiles();  // sA = K[t][d0 ..], sB = Q[t][d0 ..]
+  __syncthreads();
+  const int dc = 16 * w + r;  // this lane's column of the tile
+#pragma unroll 4
+  for (int c0 = 0; c0 < L; c0 += 4) {
+    const float bK = to_f32(sA[(c0 + g) * DQM_P + dc]);
+    const float bQ = to_f32(sB[(c0 + g) * DQM_P + dc]);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      accQ[tt] = mfma4(sdS[(16 * tt + r) * DQM_SP + c0 + g], bK, accQ[tt]);  // dS[t][j] K[j][d]
+      accK[tt] = mfma4(sdS[(c0 + g) * DQM_SP + 16 * tt + r], bQ, accK[tt]);  // dS[t][j'] Q[t][d]
+    }
+  }
+  // store dQ, dK; q . dQ - k . dK partials of dF (bw.py:333)
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * g + e;
+      const size_t off = (row0 + t) * DQK + d0 + dc;
+      dq[off] = from_f32<TQ>(accQ[tt][e]);
+      dk[off] = from_f32<TQ>(accK[tt][e]);
+      const float part = sum16(to_f32(sB[t * DQM_P + dc]) * accQ[tt][e] - to_f32(sA[t * DQM_P + dc]) * accK[tt][e]);
+      if (r == 0) s_part[w][t] = part;
+    }
+  __syncthreads();
+  if (tid < L) dfp[(row0 + tid) * ndt + dt] = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+}
+
 template <typename TQ, typename TG, int L, bool REV>
 int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* s0, const float* n0,
                 const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst, float* sfin,
@@ -973,9 +1130,20 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
                        dh, ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DQK, F.DV, nvt, F.qk_scale);
   }
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dV)"))) return rc;
-  hipLaunchKernelGGL((bw_dqk_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * ndt)), dim3(BW_THREADS), 0, s, q, k, v,
-                     dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DQK, F.DV, ndt,
-                     F.qk_scale);
+  if (tiles_mfma) {
+    if constexpr (sizeof(TQ) == 2 && L == 64) {
+      const dim3 grid((unsigned)(BNH * NC * ndt));
+      switch (F.DQK) {
+        case 64: hipLaunchKernelGGL((bw_dqk_mfma_kernel<TQ, TG, 1>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
+        case 128: hipLaunchKernelGGL((bw_dqk_mfma_kernel<TQ, TG, 2>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
+        default: hipLaunchKernelGGL((bw_dqk_mfma_kernel<TQ, TG, 4>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
+      }
+    }
+  } else {
+    hipLaunchKernelGGL((bw_dqk_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC * ndt)), dim3(BW_THREADS), 0, s, q, k, v,
+                       dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DQK, F.DV, ndt,
+                       F.qk_scale);
+  }
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dQ, dK)"))) return rc;
   hipLaunchKernelGGL((bw_gates_kernel<TG>), dim3((unsigned)BNH), dim3(BW_THREADS), 0, s, fg, dfp, dip, (TG*)A.di,
                      (TG*)A.df, F.S, ndt, nvt);
