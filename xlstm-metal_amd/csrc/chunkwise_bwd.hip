@@ -620,9 +620,9 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     const float* __restrict__ s0, const float* __restrict__ n0, const float* __restrict__ m0,
     const float* __restrict__ vm, const float* __restrict__ vn, float* __restrict__ Sst, float* __restrict__ nst,
     float* __restrict__ mst, float* __restrict__ sfin, float* __restrict__ nfin, float* __restrict__ mfin,
-    float* __restrict__ s_init, int NC, int DV, int nvt, float qk_scale) {
-  constexpr int DQK = 64 * NRT;
-  constexpr int XP = DQK + 16;  // elements per staged X row (see the bank note above)
+    float* __restrict__ s_init, int NC, int DQKf, int DV, int nvt, float qk_scale) {
+  constexpr int DQK = 64 * NRT;  // state rows of this workgroup (DQKf / DQK workgroups share a state)
+  constexpr int XP = DQK + 16;   // elements per staged X row (see the bank note above)
   constexpr int EPV = 16 / sizeof(TQ);
   constexpr int PRX = DQK / EPV, NX = L * PRX, NXP = (NX + 255) / 256;
   constexpr int PRY = SC_V / EPV, NY = L * PRY, NYP = (NY + 255) / 256;
@@ -632,9 +632,12 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
   __shared__ float scoef[L];
   __shared__ float s_mn, s_g;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
-  const int bh = blockIdx.x / nvt, vt = blockIdx.x - bh * nvt, v0 = vt * SC_V;
+  const int nrs = DQKf / DQK;
+  const int bhv = blockIdx.x / nrs, rs = blockIdx.x - bhv * nrs;
+  const int bh = bhv / nvt, vt = bhv - bh * nvt, v0 = vt * SC_V;
+  const int d_off = rs * DQK;  // this workgroup's first state row
   const size_t S = (size_t)NC * L;
-  const int row0 = w * 16 * NRT;
+  const int row0 = d_off + w * 16 * NRT;  // this wave's first state row
   const int nslots = REV ? NC + 1 : NC;
 
   f32x4 acc[NRT][4];
@@ -644,7 +647,7 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        acc[rt][ct][e] = s0 ? s0[((size_t)bh * DQK + row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] : 0.f;
+        acc[rt][ct][e] = s0 ? s0[((size_t)bh * DQKf + row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] : 0.f;
   auto store_state = [&](float* dst) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
@@ -654,7 +657,7 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
         for (int e = 0; e < 4; ++e) dst[(size_t)(row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] = acc[rt][ct][e];
   };
   const bool owns_n = !REV && vt == 0 && tid < DQK;
-  float nn = (owns_n && n0) ? n0[(size_t)bh * DQK + tid] : 0.f;
+  float nn = (owns_n && n0) ? n0[(size_t)bh * DQKf + d_off + tid] : 0.f;
   float m = (!REV && m0) ? m0[bh] : 0.f;
 
   // prefetch registers: X, Y pieces and this thread's token gates (tid < L)
@@ -666,7 +669,7 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     for (int u = 0; u < NXP; ++u) {
       const int p = u * 256 + tid;
       if (NX % 256 == 0 || p < NX)
-        px[u] = *reinterpret_cast<const u32x4*>(X + (t0 + p / PRX) * DQK + (p % PRX) * EPV);
+        px[u] = *reinterpret_cast<const u32x4*>(X + (t0 + p / PRX) * DQKf + d_off + (p % PRX) * EPV);
     }
 #pragma unroll
     for (int u = 0; u < NYP; ++u) {
@@ -747,9 +750,9 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     __syncthreads();
     // the state entering this chunk (forward) / after it (reverse), stored here, after the
     // waits for the staged data, so that the next wait (one chunk later) finds them done
-    store_state(Sst + ((size_t)bh * nslots + slot) * DQK * DV);
-    if (owns_n) nst[sidx * DQK + tid] = nn;
-    if (!REV && vt == 0 && tid == 0) mst[sidx] = m_in;
+    store_state(Sst + ((size_t)bh * nslots + slot) * DQKf * DV);
+    if (owns_n) nst[sidx * DQKf + d_off + tid] = nn;
+    if (!REV && vt == 0 && rs == 0 && tid == 0) mst[sidx] = m_in;
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -757,7 +760,7 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
 #pragma unroll 4
     for (int t0 = 0; t0 < L; t0 += 4) {
       float a[NRT], b[4];
-      const TQ* xr = sX + (t0 + g) * XP + row0 + r;
+      const TQ* xr = sX + (t0 + g) * XP + (row0 - d_off) + r;
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt) a[rt] = to_f32(xr[16 * rt]);
       const float* yr = sY + (t0 + g) * SC_YP + r;
@@ -776,12 +779,12 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     __syncthreads();  // the staged tiles are read; the next chunk may overwrite them
   }
   if (!REV) {
-    store_state(sfin + (size_t)bh * DQK * DV);
-    if (owns_n) nfin[(size_t)bh * DQK + tid] = nn;
-    if (vt == 0 && tid == 0) mfin[bh] = m;
+    store_state(sfin + (size_t)bh * DQKf * DV);
+    if (owns_n) nfin[(size_t)bh * DQKf + d_off + tid] = nn;
+    if (vt == 0 && rs == 0 && tid == 0) mfin[bh] = m;
   } else {
-    store_state(Sst + (size_t)bh * nslots * DQK * DV);
-    if (s_init) store_state(s_init + (size_t)bh * DQK * DV);
+    store_state(Sst + (size_t)bh * nslots * DQKf * DV);
+    if (s_init) store_state(s_init + (size_t)bh * DQKf * DV);
   }
 }
 
@@ -803,12 +806,14 @@ struct BwArgs {
 // dV on v_mfma_f32_16x16x4f32 for 16-bit q/k/v/dH and 64-token chunks: one workgroup of
 // 4 waves per (head, chunk, 64 columns of DV) as in bw_dv_kernel.  Wave w owns columns
 // [16 w, 16 w + 16) of the tile and the j-tile w of Sbar, for all 64 tokens (4 row tiles):
-//   over d (4 per MFMA): A = K[t][d] (K staged in LDS), B = Q[16 w + r][d] (Sbar^T) and
-//     dC_k[d][v] (the inter term), both straight from global memory;
+//   over DQK in blocks of 64 (K and Q of the block staged in LDS, the dC_k column values
+//   of a lane and the next block's tiles loaded a block ahead), 4 d per MFMA:
+//     A = K[t][d], B = Q[16 w + r][d] (Sbar^T) and dC_k[d][v] (the inter term);
 //   Sbar^T gated (fw.py:204-227) into LDS; dV rows scaled by Abar_t (bw.py:179);
 //   over j: A = Sbar^T[t][j] (LDS), B = dH[j][v] / (N_j + eps) (bw.py:156).
 // Lane (g, r) ends with dV[16 tt + 4 g + e][16 w + r]; the v . dV partials of dI are summed
 // over the 16 lanes of a column group, then over the 4 waves in LDS.
+constexpr int DVM_P = 72;   // elements per staged 64-wide 16-bit row (36 mod 64 dwords)
 constexpr int DVM_SP = 68;  // floats per row of the staged Sbar^T
 
 template <typename TQ, typename TG, int NRT>
@@ -824,11 +829,9 @@ __global__ __launch_bounds__(256) void bw_dv_mfma_kernel(const TQ* __restrict__ 
                                                           float qk_scale) {
   constexpr int L = 64;
   constexpr int DQK = 64 * NRT;
-  constexpr int XP = DQK + 8;  // elements per staged K row (16-byte rows, 4 mod 64 dwords apart)
-  constexpr int EPV = 16 / sizeof(TQ);
-  constexpr int PRX = DQK / EPV;
   static_assert(sizeof(TQ) == 2, "16-bit operands");
-  __shared__ __attribute__((aligned(16))) TQ sK[L * XP];
+  __shared__ __attribute__((aligned(16))) TQ sK[L * DVM_P];
+  __shared__ __attribute__((aligned(16))) TQ sQ[L * DVM_P];
   __shared__ float sS[L * DVM_SP];
   __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L];
   __shared__ float s_part[4][L];
@@ -837,13 +840,29 @@ __global__ __launch_bounds__(256) void bw_dv_mfma_kernel(const TQ* __restrict__ 
   const int bh = blockIdx.x / per_bh, rem = blockIdx.x - bh * per_bh;
   const int kc = rem / nvt, vt = rem - kc * nvt, v0 = vt * 64;
   const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
-  const float* dCk = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // gradient of the state after chunk kc
-  // stage K of the chunk
-  for (int p = tid; p < L * PRX; p += 256) {
-    const int t = p / PRX, c = (p % PRX) * EPV;
-    *reinterpret_cast<u32x4*>(sK + t * XP + c) = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + c);
-  }
-  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);  // its barrier also covers the K tile
+  // this lane's column of dC_k (the gradient of the state after chunk kc)
+  const float* dcol = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV + v0 + 16 * w + r;
+  // K, Q blocks of 64 x 64: 512 pieces of 16 bytes, 2 per thread; dC values d = db + 4 ks + g
+  u32x4 pk[2], pq[2];
+  float pc[16];
+  auto fetch = [&](int db) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      pk[u] = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + db + c);
+      pq[u] = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + db + c);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) pc[ks] = dcol[(size_t)(db + 4 * ks + g) * DV];
+  };
+  // the intra term's dH operands, j = 4 ks + g
+  float ph[16];
+  auto fetch_h = [&]() {
+    const TQ* hcol = dh + row0 * DV + v0 + 16 * w + r;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) ph[ks] = to_f32(hcol[(size_t)(4 * ks + g) * DV]);
+  };
+  chunk_gate_scan<TG, L>(ig, fg, row0, sb, si);
   if (tid < L) {
     const float mn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
     smc[tid] = vm[row0 + tid];
@@ -856,20 +875,33 @@ __global__ __launch_bounds__(256) void bw_dv_mfma_kernel(const TQ* __restrict__ 
     accS[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     accV[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const TQ* qrow = q + (row0 + 16 * w + r) * DQK;
-  const float* dcol = dCk + v0 + 16 * w + r;
-#pragma unroll 8
-  for (int d0 = 0; d0 < DQK; d0 += 4) {
-    const float bq = to_f32(qrow[d0 + g]);
-    const float bc = dcol[(size_t)(d0 + g) * DV];
+  fetch(0);
+  for (int db = 0; db < DQK; db += 64) {
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const float a = to_f32(sK[(16 * tt + r) * XP + d0 + g]);
-      accS[tt] = mfma4(a, bq, accS[tt]);
-      accV[tt] = mfma4(a, bc, accV[tt]);
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      *reinterpret_cast<u32x4*>(sK + t * DVM_P + c) = pk[u];
+      *reinterpret_cast<u32x4*>(sQ + t * DVM_P + c) = pq[u];
     }
+    float cc[16];
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) cc[ks] = pc[ks];
+    __syncthreads();
+    if (db + 64 < DQK) fetch(db + 64);
+    else fetch_h();
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const int dd = 4 * ks + g;
+      const float bq = to_f32(sQ[(16 * w + r) * DVM_P + dd]);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float a = to_f32(sK[(16 * tt + r) * DVM_P + dd]);
+        accS[tt] = mfma4(a, bq, accS[tt]);
+        accV[tt] = mfma4(a, cc[ks], accV[tt]);
+      }
+    }
+    __syncthreads();  // the blocks are read; the next staging may overwrite them
   }
-  __syncthreads();  // gate rows (smc, sab) visible
   // Sbar^T[t][j] = S[j][t] Dbar[j][t] on t <= j; inter rows scaled by Abar_t
   const int j = 16 * w + r;
 #pragma unroll
@@ -882,12 +914,12 @@ __global__ __launch_bounds__(256) void bw_dv_mfma_kernel(const TQ* __restrict__ 
     }
   __syncthreads();
   // intra: dV[t][v] += sum_j Sbar^T[t][j] dH[j][v] / (N_j + eps)
-  const TQ* hcol = dh + row0 * DV + v0 + 16 * w + r;
-#pragma unroll 4
-  for (int j0 = 0; j0 < L; j0 += 4) {
-    const float b = to_f32(hcol[(size_t)(j0 + g) * DV]) * sinv[j0 + g];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) accV[tt] = mfma4(sS[(16 * tt + r) * DVM_SP + j0 + g], b, accV[tt]);
+  for (int ks = 0; ks < 16; ++ks) {
+    const int j0 = 4 * ks + g;
+    const float b = ph[ks] * sinv[j0];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) accV[tt] = mfma4(sS[(16 * tt + r) * DVM_SP + j0], b, accV[tt]);
   }
   // store dV; v . dV partials of dI (bw.py:338)
 #pragma unroll
@@ -1066,19 +1098,18 @@ int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, c
                 const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst, float* sfin,
                 float* nfin, float* mfin, float* s_init, int BNH, int NC, int DV, float qk_scale, hipStream_t st) {
   const int nvt = DV / SC_V;
-  auto go = [&](auto kern, size_t smem) {
+  // 128 state rows per workgroup (64 for DQK 64): two workgroups share a DQK 256 state, so
+  // the chunk-sequential scan keeps two waves on every SIMD
+  auto go = [&](auto kern, size_t smem, int nrs) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess)
       return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_bwd: LDS attribute failed: %s", hipGetErrorString(e));
-    hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvt)), dim3(256), smem, st, X, Y, ig, fg, s0, n0, m0, vm, vn, Sst,
-                       nst, mst, sfin, nfin, mfin, s_init, NC, DV, nvt, qk_scale);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvt * nrs)), dim3(256), smem, st, X, Y, ig, fg, s0, n0, m0, vm, vn,
+                       Sst, nst, mst, sfin, nfin, mfin, s_init, NC, DQK, DV, nvt, qk_scale);
     return check_launch(REV ? "xl_mlstm_chunkwise_bwd(dC scan)" : "xl_mlstm_chunkwise_bwd(states scan)");
   };
-  switch (DQK) {
-    case 64: return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1));
-    case 128: return go(bw_scan_kernel<TQ, TG, L, 2, REV>, scan_smem<TQ, L>(2));
-    default: return go(bw_scan_kernel<TQ, TG, L, 4, REV>, scan_smem<TQ, L>(4));
-  }
+  if (DQK == 64) return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1), 1);
+  return go(bw_scan_kernel<TQ, TG, L, 2, REV>, scan_smem<TQ, L>(2), DQK / 128);
 }
 
 template <typename TQ, typename TG, int L>
