@@ -104,12 +104,14 @@ def test_stack_logits_fused_vs_linear(gpu_case):
     model = xLSTMStack.random(cfg, dev(), seed=3)
     g = torch.Generator(device=dev()).manual_seed(4)
     xb = torch.randn(1, 1, cfg.d_model, generator=g, device=dev()).to(cfg.dtype)
-    fused = model.logits(xb)
-    model.fused_lm_head = False
-    plain = model.logits(xb)
-    xn = model.out_norm(xb)
-    _check(fused.view(1, -1), xn.view(1, -1).cpu(), model.lm_head.weight.cpu(), cfg.logit_soft_cap, "fused")
-    _check(plain.view(1, -1), xn.view(1, -1).cpu(), model.lm_head.weight.cpu(), cfg.logit_soft_cap, "Linear")
+    with torch.no_grad():
+        fused = model.logits(xb)
+        model.fused_lm_head = False
+        plain = model.logits(xb)
+        xn = model.out_norm(xb).view(1, -1).cpu()
+    w = model.lm_head.weight.detach().cpu()
+    _check(fused.view(1, -1), xn, w, cfg.logit_soft_cap, "fused")
+    _check(plain.view(1, -1), xn, w, cfg.logit_soft_cap, "Linear")
 
 
 def test_rejects(gpu_case):

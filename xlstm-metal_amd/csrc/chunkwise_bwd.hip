@@ -29,6 +29,8 @@
 // [BNH][S][ceil(DV/64)].
 #include "chunkwise.h"
 
+#include <type_traits>
+
 namespace xl {
 namespace {
 
@@ -96,6 +98,21 @@ __device__ __forceinline__ void chunk_gate_scan(const TG* __restrict__ ig, const
     if (tid < L) {
       sb[tid] = b;
       si[tid] = to_f32(ig[g0 + tid]);
+    }
+  }
+  __syncthreads();
+}
+
+// chunk_gate_scan with token t's f and i already loaded by thread t (t < L), so that the
+// kernel's first global loads all go out together
+template <int L>
+__device__ __forceinline__ void chunk_gate_scan_v(float f, float i, float* sb, float* si) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    const float b = wave_incl_sum(tid < L ? logsigmoid(f) : 0.f, tid);
+    if (tid < L) {
+      sb[tid] = b;
+      si[tid] = i;
     }
   }
   __syncthreads();
@@ -793,6 +810,272 @@ constexpr size_t scan_smem(int NRT) {
   return (size_t)L * (64 * NRT + 16) * sizeof(TQ) + (size_t)L * SC_YP * sizeof(float);
 }
 
+// ------------------------------------------------ bf16 MFMA building blocks
+// v_mfma_f32_16x16x32_bf16: A[i][k] in lane i + 16 (k / 8), element k % 8; B[k][j] in lane
+// j + 16 (k / 8); D as for 16x16x4f32 (D[i][j] in lane j + 16 (i / 4), element i % 4).
+// Operands exact in bf16 (q, k, v, dH) enter once; a float32 operand x enters as the pair
+// hi = bf16(x), lo = bf16(x - hi) (two products, 16 significant bits of x), accumulated in
+// float32.
+typedef __bf16 bfx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bfx2 __attribute__((ext_vector_type(2)));
+typedef short sx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) sx4 lds_sx4;
+
+__device__ __forceinline__ f32x4 mfma_bf(bfx8 a, bfx8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// {bf16(x0), bf16(x1)} (round to nearest even), x0 in the low half
+__device__ __forceinline__ uint32_t pk_bf(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x0, x1}), bfx2));
+}
+__device__ __forceinline__ float bf_l(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_h(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// hi / lo pair of 8 floats (x - hi is exact in float32)
+__device__ __forceinline__ void split_bf(const float (&x)[8], u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = pk_bf(x[2 * e], x[2 * e + 1]);
+    lo[e] = pk_bf(x[2 * e] - bf_l(hi[e]), x[2 * e + 1] - bf_h(hi[e]));
+  }
+}
+// Two ds_read_b64_tr_b16 -> one 8 x bf16 operand.  Within each 16 lanes, lane s passes the
+// address of 4 consecutive 16-bit columns at 4 (s % 4) of row s / 4 (of a 4-row block) and
+// receives column s of the 4 rows: with p0 / p1 the addresses in two 4-row blocks, lane s ends
+// with column c0 + s of rows R0 .. R0 + 3 (elements 0..3) and R1 .. R1 + 3 (elements 4..7).
+__device__ __forceinline__ bfx8 tr_pair(const void* p0, const void* p1) {
+  const sx4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sx4*)p0);
+  const sx4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sx4*)p1);
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return __builtin_bit_cast(bfx8, (u32x4{ua[0], ua[1], ub[0], ub[1]}));
+}
+__device__ __forceinline__ bfx8 ld_bf8(const void* p) { return __builtin_bit_cast(bfx8, *(const u32x4*)p); }
+// Workgroup b of a grid of G runs on XCD b % 8 (round-robin dispatch over the 8 XCDs, each with
+// its own L2).  The logical index returned gives every XCD one contiguous range, so logical
+// neighbours (the column tiles of one head and chunk, which read the same q / k / v / dH rows)
+// share an L2.  A bijection on [0, G).
+__device__ __forceinline__ int xcd_contiguous(int b, int G) {
+  const int x = b & 7, i = b >> 3, per = G >> 3, rem = G & 7;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
+// ----------------------------------------------- bf16 MFMA chunk scans (1, 3)
+// bw_scan_kernel for bf16 X and Y on v_mfma_f32_16x16x32_bf16: the same workgroups,
+// gates, stores and state layout; per chunk X is staged in LDS as it is and coef_t Y[t] as
+// its bf16 hi and lo rows, then per 32-token step
+//   state[i][j] += sum_k X[T(k)][row i] (hi + lo)[T(k)][column j],
+// lane (g, r) holding k = 8 g .. 8 g + 7 at the tokens T = 4 g + 0..3 and 16 + 4 g + 0..3 of
+// the step (two transposed reads of each operand).  Rows of 2 DQK + 32 and 160 bytes put
+// the 8 consecutive token rows that half a wave reads in distinct banks.
+constexpr int SB_YP = SC_V + 16;  // bf16 per staged hi / lo row (160 bytes)
+
+template <typename TG, int L, int NRT, bool REV>
+__global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
+    const bf16_t* __restrict__ X, const bf16_t* __restrict__ Y, const TG* __restrict__ ig,
+    const TG* __restrict__ fg, const float* __restrict__ s0, const float* __restrict__ n0,
+    const float* __restrict__ m0, const float* __restrict__ vm, const float* __restrict__ vn,
+    float* __restrict__ Sst, float* __restrict__ nst, float* __restrict__ mst, float* __restrict__ sfin,
+    float* __restrict__ nfin, float* __restrict__ mfin, float* __restrict__ s_init, int NC, int DQKf, int DV,
+    int nvt, float qk_scale) {
+  static_assert(L % 32 == 0, "32-token MFMA steps");
+  constexpr int DQK = 64 * NRT;  // state rows of this workgroup
+  constexpr int XP = DQK + 16;   // bf16 per staged X row
+  constexpr int PRX = DQK / 8, NX = L * PRX, NXP = (NX + 255) / 256;
+  constexpr int PRY = SC_V / 8, NY = L * PRY, NYP = (NY + 255) / 256;
+  __shared__ __attribute__((aligned(16))) bf16_t sX[L * XP];
+  __shared__ __attribute__((aligned(16))) bf16_t sYh[L * SB_YP];
+  __shared__ __attribute__((aligned(16))) bf16_t sYl[L * SB_YP];
+  __shared__ float scoef[L];
+  __shared__ float s_mn, s_g;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int nrs = DQKf / DQK;
+  const int blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int bhv = blk / nrs, rs = blk - bhv * nrs;
+  const int bh = bhv / nvt, vt = bhv - bh * nvt, v0 = vt * SC_V;
+  const int d_off = rs * DQK;
+  const size_t S = (size_t)NC * L;
+  const int row0 = d_off + w * 16 * NRT;
+  const int nslots = REV ? NC + 1 : NC;
+
+  f32x4 acc[NRT][4];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[rt][ct][e] = s0 ? s0[((size_t)bh * DQKf + row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] : 0.f;
+  auto store_state = [&](float* dst) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(size_t)(row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] = acc[rt][ct][e];
+  };
+  // n (forward, the first column tile's workgroups): one more 16 x 16 accumulator tile per row
+  // tile, whose B operand is columns 64.. of the staged hi rows: coef_t hi in column 64, lo in
+  // column 65, zeros after; n = column 0 + column 1 (lanes r = 0, 1)
+  const bool owns_n = !REV && vt == 0;  // workgroup-uniform
+  f32x4 accN[NRT];
+#pragma unroll
+  for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      accN[rt][e] = (owns_n && n0 && r == 0) ? n0[(size_t)bh * DQKf + row0 + 16 * rt + 4 * g + e] : 0.f;
+  auto store_n = [&](float* dst) {  // dst: this head's DQKf values
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float nv = accN[rt][e] + __shfl_xor(accN[rt][e], 1, 64);
+        if (r == 0) dst[row0 + 16 * rt + 4 * g + e] = nv;
+      }
+  };
+  if (owns_n)
+    for (int p = tid; p < L * 16; p += 256) sYh[(p >> 4) * SB_YP + SC_V + (p & 15)] = bf16_t{0};
+  float m = (!REV && m0) ? m0[bh] : 0.f;
+
+  u32x4 px[NXP], py[NYP];
+  float pf = 0.f, pi = 0.f, pvm = 0.f, pvn = 1.f, pmp = 0.f;
+  auto fetch = [&](int kc) {
+    const size_t t0 = (size_t)bh * S + (size_t)kc * L;
+#pragma unroll
+    for (int u = 0; u < NXP; ++u) {
+      const int p = u * 256 + tid;
+      if (NX % 256 == 0 || p < NX)
+        px[u] = *reinterpret_cast<const u32x4*>(X + (t0 + p / PRX) * DQKf + d_off + (p % PRX) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < NYP; ++u) {
+      const int p = u * 256 + tid;
+      if (NY % 256 == 0 || p < NY) py[u] = *reinterpret_cast<const u32x4*>(Y + (t0 + p / PRY) * DV + v0 + (p % PRY) * 8);
+    }
+    if (tid < L) {
+      pf = to_f32(fg[t0 + tid]);
+      pi = to_f32(ig[t0 + tid]);
+      if (REV) {
+        pvm = vm[t0 + tid];
+        pvn = vn[t0 + tid];
+      }
+    }
+    if (REV) pmp = mst[(size_t)bh * NC + kc];
+  };
+  float mnext = REV ? mfin[bh] : 0.f;
+  fetch(REV ? NC - 1 : 0);
+  // this lane's transposed-read addresses: row r / 4 of a 4-row block, columns 4 (r % 4)
+  const int kk = r >> 2, ka = r & 3;
+  for (int it = 0; it < NC; ++it) {
+    const int kc = REV ? NC - 1 - it : it;
+    const size_t sidx = (size_t)bh * NC + kc;
+    const int slot = REV ? kc + 1 : kc;
+    const float cvm = pvm, cvn = pvn, cmp = pmp;
+    if (w == 0) {
+      const float b = wave_incl_sum(lane < L ? logsigmoid(pf) : 0.f, lane);
+      const float gl = __shfl(b, L - 1, 64);
+      if (!REV) {
+        const float a = lane < L ? gl - b + pi : -INFINITY;
+        const float mn = fmaxf(gl + m, wave_max(a));  // fw.py:115
+        if (lane < L) scoef[lane] = expf(a - mn);     // fw.py:121
+        if (lane == 0) {
+          s_mn = mn;
+          s_g = gl;
+        }
+      } else {
+        if (lane < L) scoef[lane] = expf(b + cmp - cvm) * qk_scale / cvn;  // bw.py:92-101
+        if (lane == 0) s_g = gl;
+      }
+    }
+    __syncthreads();
+    const float gch = s_g;
+    float decay;
+    const float m_in = m;
+    if (!REV) {
+      const float mn = s_mn;
+      decay = expf(gch + m - mn);  // fw.py:125
+      m = mn;
+    } else {
+      decay = expf(gch + cmp - mnext);  // bw.py:86-89
+      mnext = cmp;
+    }
+#pragma unroll
+    for (int u = 0; u < NXP; ++u) {
+      const int p = u * 256 + tid;
+      if (NX % 256 == 0 || p < NX) *reinterpret_cast<u32x4*>(sX + (p / PRX) * XP + (p % PRX) * 8) = px[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NYP; ++u) {
+      const int p = u * 256 + tid;
+      if (NY % 256 == 0 || p < NY) {
+        const int t = p / PRY, c = (p % PRY) * 8;
+        Piece16<bf16_t> pc;
+        pc.raw = py[u];
+        const float co = scoef[t];
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = co * to_f32(pc.v[e]);
+        u32x4 h, l;
+        split_bf(x, h, l);
+        *reinterpret_cast<u32x4*>(sYh + t * SB_YP + c) = h;
+        *reinterpret_cast<u32x4*>(sYl + t * SB_YP + c) = l;
+      }
+    }
+    if (owns_n && tid < L) {  // the n column pair
+      const float co = scoef[tid];
+      const uint32_t h = pk_bf(co, 0.f);
+      *reinterpret_cast<uint32_t*>(sYh + tid * SB_YP + SC_V) = (h & 0xffffu) | (pk_bf(co - bf_l(h), 0.f) << 16);
+    }
+    if (it + 1 < NC) fetch(REV ? kc - 1 : kc + 1);
+    __syncthreads();
+    store_state(Sst + ((size_t)bh * nslots + slot) * DQKf * DV);
+    if (owns_n) store_n(nst + sidx * DQKf);
+    if (!REV && vt == 0 && rs == 0 && tid == 0) mst[sidx] = m_in;
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) acc[rt][ct] *= decay;
+      accN[rt] *= decay;
+    }
+#pragma unroll
+    for (int ks = 0; ks < L / 32; ++ks) {
+      const int t1 = 32 * ks + 4 * g + kk, t2 = t1 + 16;
+      bfx8 a[NRT];
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        const int c = (row0 - d_off) + 16 * rt + 4 * ka;
+        a[rt] = tr_pair(sX + t1 * XP + c, sX + t2 * XP + c);
+      }
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int c = 16 * ct + 4 * ka;
+        const bfx8 bh8 = tr_pair(sYh + t1 * SB_YP + c, sYh + t2 * SB_YP + c);
+        const bfx8 bl8 = tr_pair(sYl + t1 * SB_YP + c, sYl + t2 * SB_YP + c);
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+          acc[rt][ct] = mfma_bf(a[rt], bh8, acc[rt][ct]);
+          acc[rt][ct] = mfma_bf(a[rt], bl8, acc[rt][ct]);
+        }
+      }
+      if (owns_n) {  // n' = decay n + sum_t coef_t k_t (fw.py:133)
+        const int c = SC_V + 4 * ka;
+        const bfx8 bn = tr_pair(sYh + t1 * SB_YP + c, sYh + t2 * SB_YP + c);
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) accN[rt] = mfma_bf(a[rt], bn, accN[rt]);
+      }
+    }
+    __syncthreads();
+  }
+  if (!REV) {
+    store_state(sfin + (size_t)bh * DQKf * DV);
+    if (owns_n) store_n(nfin + (size_t)bh * DQKf);
+    if (vt == 0 && rs == 0 && tid == 0) mfin[bh] = m;
+  } else {
+    store_state(Sst + (size_t)bh * nslots * DQKf * DV);
+    if (s_init) store_state(s_init + (size_t)bh * DQKf * DV);
+  }
+}
+
 // ---------------------------------------------------------------- launchers
 struct BwArgs {
   ChunkwiseArgs fw;
@@ -1093,6 +1376,416 @@ __global__ __launch_bounds__(256) void bw_dqk_mfma_kernel(const TQ* __restrict__
   if (tid < L) dfp[(row0 + tid) * ndt + dt] = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
 }
 
+// -------------------------------------------------- bf16 MFMA dV pass (4)
+// bw_dv_mfma_kernel for bf16 on v_mfma_f32_16x16x32_bf16: the same workgroups and outputs.
+// Wave w owns rows [16 w, 16 w + 16) of S[j][t] and columns [16 w, 16 w + 16) of the dV tile.
+//   Over DQK in blocks of 64 (K and Q rows and the dC_k block, as bf16 hi / lo rows, staged in
+//   LDS from 16-byte loads issued two blocks ahead, together with the gates, stats and the dH
+//   block at the start), 32 d per MFMA, lane (g, r) at d = 8 g .. 8 g + 7 of the step:
+//     S[j][t] += Q[j][d] K[t][d]            (A = Q rows, B = K rows: one product)
+//     dV[t][v] += K[t][d] dC_k[d][v]        (B = dC hi, lo by transposed reads)
+//   Sbar^T[t][j] = S[j][t] s Dbar[j][t] / (N_j + eps) on t <= j (fw.py:204-227, bw.py:156)
+//   into LDS as bf16 hi / lo rows; dV rows scaled by Abar_t (bw.py:179); then, with the dH
+//   block staged in place of K,
+//     dV[t][v] += Sbar^T[t][j] dH[j][v]     (A = Sbar^T hi, lo rows; B = dH by transposed reads).
+constexpr int BFP = 80;  // bf16 per staged 64-wide row (160 bytes)
+
+template <typename TG, int NRT>
+__global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                          const bf16_t* __restrict__ v, const bf16_t* __restrict__ dh,
+                                                          const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                          const float* __restrict__ mst,
+                                                          const float* __restrict__ mfin,
+                                                          const float* __restrict__ vm,
+                                                          const float* __restrict__ vn,
+                                                          const float* __restrict__ dCst, bf16_t* __restrict__ dv,
+                                                          float* __restrict__ dip, int NC, int DV, int nvt,
+                                                          float qk_scale) {
+  constexpr int L = 64;
+  constexpr int DQK = 64 * NRT;
+  __shared__ __attribute__((aligned(16))) bf16_t sK[L * BFP];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[L * BFP];
+  __shared__ __attribute__((aligned(16))) uint32_t sSh[L * BFP / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t sSl[L * BFP / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t sCh[L * BFP / 2];  // dC_k block [d][v], hi / lo
+  __shared__ __attribute__((aligned(16))) uint32_t sCl[L * BFP / 2];
+  __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L];
+  __shared__ float s_part[4][L];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int per_bh = NC * nvt;
+  const int blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int bh = blk / per_bh, rem = blk - bh * per_bh;
+  const int kc = rem / nvt, vt = rem - kc * nvt, v0 = vt * 64;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  // dC_k (the gradient of the state after chunk kc), columns v0 .. v0 + 63
+  const float* dcb = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV + v0;
+  // two register slots of a DQK block: K, Q rows (t = p / 8, 8 d at 8 (p % 8)) and the dC_k block
+  // (d = p / 16, 4 v at 4 (p % 16)); block b + 2 is loaded while block b is computed
+  u32x4 pk[2][2], pq[2][2];
+  f32x4 pc[2][4];
+  auto fetch = [&](auto slot, int db) {
+    constexpr int sl = decltype(slot)::value;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      pk[sl][u] = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + db + c);
+      pq[sl][u] = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + db + c);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = u * 256 + tid;
+      pc[sl][u] = *reinterpret_cast<const f32x4*>(dcb + (size_t)(db + (p >> 4)) * DV + (p & 15) * 4);
+    }
+  };
+  // the intra term's dH block [j][v], staged into sK after the last DQK block
+  u32x4 ph[2];
+  const int kk = r >> 2, ka = r & 3;  // transposed reads: row r / 4 of a 4-row block, columns 4 (r % 4)
+  // every load that does not depend on another goes out first: gates, stats, blocks 0 and 1, dH
+  float gf = 0.f, gi = 0.f, gvm = 0.f, gvn = 1.f, gmn = 0.f;
+  if (tid < L) {
+    gf = to_f32(fg[row0 + tid]);
+    gi = to_f32(ig[row0 + tid]);
+    gvm = vm[row0 + tid];
+    gvn = vn[row0 + tid];
+    gmn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+  }
+  const std::integral_constant<int, 0> S0{};
+  const std::integral_constant<int, 1> S1{};
+  fetch(S0, 0);
+  if (NRT > 1) fetch(S1, 64);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+    ph[u] = *reinterpret_cast<const u32x4*>(dh + (row0 + t) * DV + v0 + c);
+  }
+  chunk_gate_scan_v<L>(gf, gi, sb, si);
+  if (tid < L) {
+    smc[tid] = gvm;
+    sinv[tid] = 1.0f / gvn;
+    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - gmn);  // Abar (bw.py:168-176)
+  }
+  f32x4 accS[4], accV[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    accS[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accV[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto step = [&](auto slot, int bi) {
+    constexpr int sl = decltype(slot)::value;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      *reinterpret_cast<u32x4*>(sK + t * BFP + c) = pk[sl][u];
+      *reinterpret_cast<u32x4*>(sQ + t * BFP + c) = pq[sl][u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = u * 256 + tid, o = ((p >> 4) * BFP + (p & 15) * 4) >> 1;
+      const f32x4 x = pc[sl][u];
+      const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
+      *reinterpret_cast<u32x2*>(sCh + o) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(sCl + o) = u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
+    }
+    __syncthreads();
+    if (bi + 2 < NRT) fetch(slot, (bi + 2) * 64);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = 32 * ks + 8 * g;
+      // dC_k[d][16 w + r] at d = c + 0..7 (the k of the K operand)
+      const int o1 = ((c + kk) * BFP + 16 * w + 4 * ka) >> 1, o2 = o1 + 2 * BFP;
+      const bfx8 dch = tr_pair(sCh + o1, sCh + o2), dcl = tr_pair(sCl + o1, sCl + o2);
+      const bfx8 qa = ld_bf8(sQ + (16 * w + r) * BFP + c);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const bfx8 kb = ld_bf8(sK + (16 * tt + r) * BFP + c);
+        accS[tt] = mfma_bf(qa, kb, accS[tt]);
+        accV[tt] = mfma_bf(kb, dch, accV[tt]);
+        accV[tt] = mfma_bf(kb, dcl, accV[tt]);
+      }
+    }
+    __syncthreads();  // the blocks are read; the next staging may overwrite them
+  };
+#pragma unroll
+  for (int bi = 0; bi < NRT; bi += 2) {
+    step(S0, bi);
+    if (bi + 1 < NRT) step(S1, bi + 1);
+  }
+  // lane (g, r), element e of tile tt: S[j = 16 w + 4 g + e][t = 16 tt + r]
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = 16 * tt + r;
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 16 * w + 4 * g + e;
+      x[e] = (t <= j) ? accS[tt][e] * qk_scale * expf(sb[j] - sb[t] + si[t] - smc[j]) * sinv[j] : 0.f;
+    }
+    const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
+    const uint32_t l0 = pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), l1 = pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1));
+    const int o = (t * BFP + 16 * w + 4 * g) >> 1;
+    *reinterpret_cast<u32x2*>(sSh + o) = u32x2{h0, h1};
+    *reinterpret_cast<u32x2*>(sSl + o) = u32x2{l0, l1};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) accV[tt][e] *= sab[16 * tt + 4 * g + e];
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {  // dH block into sK (read by every wave before the last barrier)
+    const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+    *reinterpret_cast<u32x4*>(sK + t * BFP + c) = ph[u];
+  }
+  __syncthreads();
+  // intra: dV[t][v] += sum_j Sbar^T[t][j] dH[j][v]
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c = 32 * ks + 8 * g + kk;  // dH[j][16 w + r] at j = 32 ks + 8 g + 0..7
+    const bfx8 bh8 = tr_pair(sK + c * BFP + 16 * w + 4 * ka, sK + (c + 4) * BFP + 16 * w + 4 * ka);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int o = ((16 * tt + r) * BFP + 32 * ks + 8 * g) >> 1;
+      accV[tt] = mfma_bf(ld_bf8(sSh + o), bh8, accV[tt]);
+      accV[tt] = mfma_bf(ld_bf8(sSl + o), bh8, accV[tt]);
+    }
+  }
+  // store dV; v . dV partials of dI (bw.py:338)
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * g + e;
+      const size_t off = (row0 + t) * DV + v0 + 16 * w + r;
+      dv[off] = from_f32<bf16_t>(accV[tt][e]);
+      const float part = sum16(to_f32(v[off]) * accV[tt][e]);
+      if (r == 0) s_part[w][t] = part;
+    }
+  __syncthreads();
+  if (tid < L) dip[(row0 + tid) * nvt + vt] = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+}
+
+// ---------------------------------------------- bf16 MFMA dQ, dK pass (5)
+// bw_dqk_mfma_kernel for bf16 on v_mfma_f32_16x16x32_bf16: the same workgroups and outputs.
+// Wave w owns rows [16 w, 16 w + 16) of dS~[j][t] and columns [16 w, 16 w + 16) of the DQK tile.
+//  Phase 1, over DV in blocks of 64 (dH and V rows staged in LDS; the lane's C_{k-1} and dC_k
+//  row pieces in registers; loads issued two blocks ahead, the first two with the gates and
+//  stats at the start), 32 v per MFMA, lane (g, r) at v = 8 g .. 8 g + 7 of the step:
+//    dS~[j][t] += V[j][v] dH[t][v]     (A = V rows, B = dH rows: one product)
+//    Q~[t][d]  += dH[t][v] C[d][v]     (B = C hi, lo)
+//    K~[t][d]  += V[t][v] dC[d][v]     (B = dC hi, lo)
+//  dS[t][j] = dS~ / (N_t + eps) Dbar[t][j] s on j <= t (bw.py:158-159) into LDS as bf16 hi / lo
+//  rows, dQ = Q~ Bbar_t s / (N_t + eps) (bw.py:182), dK = K~ Abar_t (bw.py:181); phase 2, K and
+//  Q rows of the tile staged, 32 tokens per MFMA at j = 4 g + 0..3 and 16 + 4 g + 0..3 of the
+//  step (bw.py:161-162):
+//    dQ[t][d] += dS[t][j] K[j][d]      (A = dS rows hi, lo; B = K by transposed reads)
+//    dK[t][d] += dS[j][t] Q[j][d]      (A = dS columns hi, lo by transposed reads; B = Q likewise)
+template <typename TG, int NRT>
+__global__ __launch_bounds__(256, 2) void bw_dqk_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                           const bf16_t* __restrict__ v, const bf16_t* __restrict__ dh,
+                                                           const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                           const float* __restrict__ Cst,
+                                                           const float* __restrict__ mst,
+                                                           const float* __restrict__ mfin,
+                                                           const float* __restrict__ vm,
+                                                           const float* __restrict__ vn,
+                                                           const float* __restrict__ dCst, bf16_t* __restrict__ dq,
+                                                           bf16_t* __restrict__ dk, float* __restrict__ dfp, int NC,
+                                                           int DV, int ndt, float qk_scale) {
+  constexpr int L = 64;
+  constexpr int DQK = 64 * NRT;
+  // phase 1: sA = dH block, sB = V block; phase 2: sA = K tile, sB = Q tile
+  __shared__ __attribute__((aligned(16))) bf16_t sA[L * BFP];
+  __shared__ __attribute__((aligned(16))) bf16_t sB[L * BFP];
+  __shared__ __attribute__((aligned(16))) bf16_t sDh[L * BFP];
+  __shared__ __attribute__((aligned(16))) bf16_t sDl[L * BFP];
+  __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L], sbb[L];
+  __shared__ float s_part[4][L];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int per_bh = NC * ndt;
+  const int blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int bh = blk / per_bh, rem = blk - bh * per_bh;
+  const int kc = rem / ndt, dt = rem - kc * ndt, d0 = dt * 64;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  const float* crow = Cst + sidx * DQK * DV + (size_t)(d0 + 16 * w + r) * DV;                    // C_{k-1} row d
+  const float* dcrow = dCst + (((size_t)bh * (NC + 1) + kc + 1) * DQK + d0 + 16 * w + r) * DV;  // dC_k row d
+  // two register slots of a DV block: dH, V rows (t = p / 8, 8 v at 8 (p % 8)) and this lane's
+  // C, dC pieces (v = vb + 32 ks + 8 g + 0..7); block b + 2 is loaded while block b is computed,
+  // and phase 2's K and Q tiles go into the slot the last block frees
+  u32x4 pa[2][2], pb[2][2];
+  f32x4 pc[2][2][2], pd[2][2][2];
+  auto fetch = [&](auto slot, int vb) {
+    constexpr int sl = decltype(slot)::value;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      pa[sl][u] = *reinterpret_cast<const u32x4*>(dh + (row0 + t) * DV + vb + c);
+      pb[sl][u] = *reinterpret_cast<const u32x4*>(v + (row0 + t) * DV + vb + c);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        pc[sl][ks][h] = *reinterpret_cast<const f32x4*>(crow + vb + 32 * ks + 8 * g + 4 * h);
+        pd[sl][ks][h] = *reinterpret_cast<const f32x4*>(dcrow + vb + 32 * ks + 8 * g + 4 * h);
+      }
+  };
+  auto fetch_kq = [&](auto slot) {
+    constexpr int sl = decltype(slot)::value;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      pa[sl][u] = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + d0 + c);
+      pb[sl][u] = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + d0 + c);
+    }
+  };
+  auto store_tiles = [&](auto slot) {
+    constexpr int sl = decltype(slot)::value;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
+      *reinterpret_cast<u32x4*>(sA + t * BFP + c) = pa[sl][u];
+      *reinterpret_cast<u32x4*>(sB + t * BFP + c) = pb[sl][u];
+    }
+  };
+  const int nb = DV / 64;
+  // every load that does not depend on another goes out first: gates, stats, blocks 0 and 1
+  float gf = 0.f, gi = 0.f, gvm = 0.f, gvn = 1.f, gmp = 0.f, gmn = 0.f;
+  if (tid < L) {
+    gf = to_f32(fg[row0 + tid]);
+    gi = to_f32(ig[row0 + tid]);
+    gvm = vm[row0 + tid];
+    gvn = vn[row0 + tid];
+    gmp = mst[sidx];
+    gmn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
+  }
+  const std::integral_constant<int, 0> S0{};
+  const std::integral_constant<int, 1> S1{};
+  fetch(S0, 0);
+  if (nb > 1) fetch(S1, 64);
+  else fetch_kq(S1);
+  chunk_gate_scan_v<L>(gf, gi, sb, si);
+  if (tid < L) {
+    smc[tid] = gvm;
+    sinv[tid] = 1.0f / gvn;
+    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - gmn);  // Abar (bw.py:168-176)
+    sbb[tid] = expf(sb[tid] + gmp - gvm) * qk_scale;       // Bbar s (bw.py:175, 182)
+  }
+  f32x4 accS[4], accQ[4], accK[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    accS[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accQ[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accK[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto step = [&](auto slot, int bi) {
+    constexpr int sl = decltype(slot)::value;
+    store_tiles(slot);
+    bfx8 ch[2], cl[2], dch[2], dcl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float x[8], y[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = pc[sl][ks][0][e];
+        x[4 + e] = pc[sl][ks][1][e];
+        y[e] = pd[sl][ks][0][e];
+        y[4 + e] = pd[sl][ks][1][e];
+      }
+      u32x4 h, l;
+      split_bf(x, h, l);
+      ch[ks] = __builtin_bit_cast(bfx8, h);
+      cl[ks] = __builtin_bit_cast(bfx8, l);
+      split_bf(y, h, l);
+      dch[ks] = __builtin_bit_cast(bfx8, h);
+      dcl[ks] = __builtin_bit_cast(bfx8, l);
+    }
+    __syncthreads();
+    if (bi + 2 < nb) fetch(slot, (bi + 2) * 64);
+    else if (bi + 2 == nb) fetch_kq(slot);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = 32 * ks + 8 * g;
+      const bfx8 va = ld_bf8(sB + (16 * w + r) * BFP + c);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const bfx8 hb = ld_bf8(sA + (16 * tt + r) * BFP + c);
+        const bfx8 vb8 = ld_bf8(sB + (16 * tt + r) * BFP + c);
+        accS[tt] = mfma_bf(va, hb, accS[tt]);
+        accQ[tt] = mfma_bf(hb, ch[ks], accQ[tt]);
+        accQ[tt] = mfma_bf(hb, cl[ks], accQ[tt]);
+        accK[tt] = mfma_bf(vb8, dch[ks], accK[tt]);
+        accK[tt] = mfma_bf(vb8, dcl[ks], accK[tt]);
+      }
+    }
+    __syncthreads();  // the blocks are read; the next staging may overwrite them
+  };
+  for (int bi = 0; bi < nb; bi += 2) {
+    step(S0, bi);
+    if (bi + 1 < nb) step(S1, bi + 1);
+  }
+  // lane (g, r), element e of tile tt: dS~[j = 16 w + 4 g + e][t = 16 tt + r]
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = 16 * tt + r;
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 16 * w + 4 * g + e;
+      x[e] = (j <= t) ? accS[tt][e] * sinv[t] * expf(sb[t] - sb[j] + si[j] - smc[t]) * qk_scale : 0.f;
+    }
+    const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
+    const uint32_t l0 = pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), l1 = pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1));
+    const int o = t * BFP + 16 * w + 4 * g;
+    *reinterpret_cast<u32x2*>(sDh + o) = u32x2{h0, h1};
+    *reinterpret_cast<u32x2*>(sDl + o) = u32x2{l0, l1};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tq = 16 * tt + 4 * g + e;
+      accQ[tt][e] *= sbb[tq] * sinv[tq];
+      accK[tt][e] *= sab[tq];
+    }
+  }
+  if (nb & 1) store_tiles(S1);  // sA = K[t][d0 ..], sB = Q[t][d0 ..], in the slot block nb - 2 freed
+  else store_tiles(S0);
+  __syncthreads();
+  const int kk = r >> 2, ka = r & 3;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int j1 = 32 * ks + 4 * g + kk, j2 = j1 + 16;  // this lane's transposed-read rows
+    const int cd = 16 * w + 4 * ka;
+    const bfx8 bK = tr_pair(sA + j1 * BFP + cd, sA + j2 * BFP + cd);  // K[j][d0 + 16 w + r]
+    const bfx8 bQ = tr_pair(sB + j1 * BFP + cd, sB + j2 * BFP + cd);  // Q[j][d0 + 16 w + r]
+    const int jr = 32 * ks + 4 * g;  // the row pieces: j = jr + 0..3, jr + 16 + 0..3
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int rowo = (16 * tt + r) * BFP + jr;
+      const u32x2 h0 = *reinterpret_cast<const u32x2*>(sDh + rowo), h1 = *reinterpret_cast<const u32x2*>(sDh + rowo + 16);
+      const u32x2 l0 = *reinterpret_cast<const u32x2*>(sDl + rowo), l1 = *reinterpret_cast<const u32x2*>(sDl + rowo + 16);
+      const bfx8 ah = __builtin_bit_cast(bfx8, (u32x4{h0[0], h0[1], h1[0], h1[1]}));
+      const bfx8 al = __builtin_bit_cast(bfx8, (u32x4{l0[0], l0[1], l1[0], l1[1]}));
+      accQ[tt] = mfma_bf(ah, bK, accQ[tt]);  // dS[t][j] K[j][d]
+      accQ[tt] = mfma_bf(al, bK, accQ[tt]);
+      const int ct = 16 * tt + 4 * ka;
+      const bfx8 th = tr_pair(sDh + j1 * BFP + ct, sDh + j2 * BFP + ct);  // dS[j][16 tt + r]
+      const bfx8 tl = tr_pair(sDl + j1 * BFP + ct, sDl + j2 * BFP + ct);
+      accK[tt] = mfma_bf(th, bQ, accK[tt]);  // dS[j][t] Q[j][d]
+      accK[tt] = mfma_bf(tl, bQ, accK[tt]);
+    }
+  }
+  // store dQ, dK; q . dQ - k . dK partials of dF (bw.py:333)
+  const int dc = 16 * w + r;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * g + e;
+      const size_t off = (row0 + t) * DQK + d0 + dc;
+      dq[off] = from_f32<bf16_t>(accQ[tt][e]);
+      dk[off] = from_f32<bf16_t>(accK[tt][e]);
+      const float part = sum16(to_f32(sB[t * BFP + dc]) * accQ[tt][e] - to_f32(sA[t * BFP + dc]) * accK[tt][e]);
+      if (r == 0) s_part[w][t] = part;
+    }
+  __syncthreads();
+  if (tid < L) dfp[(row0 + tid) * ndt + dt] = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+}
+
 template <typename TQ, typename TG, int L, bool REV>
 int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* s0, const float* n0,
                 const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst, float* sfin,
@@ -1108,6 +1801,10 @@ int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, c
                        Sst, nst, mst, sfin, nfin, mfin, s_init, NC, DQK, DV, nvt, qk_scale);
     return check_launch(REV ? "xl_mlstm_chunkwise_bwd(dC scan)" : "xl_mlstm_chunkwise_bwd(states scan)");
   };
+  if constexpr (std::is_same<TQ, bf16_t>::value && L % 32 == 0) {  // bf16 operands, static LDS
+    if (DQK == 64) return go(bw_scan_bf16_kernel<TG, L, 1, REV>, 0, 1);
+    return go(bw_scan_bf16_kernel<TG, L, 2, REV>, 0, DQK / 128);
+  }
   if (DQK == 64) return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1), 1);
   return go(bw_scan_kernel<TQ, TG, L, 2, REV>, scan_smem<TQ, L>(2), DQK / 128);
 }
@@ -1147,7 +1844,15 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   bool tiles_mfma = false;
   if constexpr (sizeof(TQ) == 2 && L == 64) {
     tiles_mfma = scan_mfma;
-    if (tiles_mfma) {
+    if (tiles_mfma && std::is_same<TQ, bf16_t>::value) {
+      const dim3 grid((unsigned)(BNH * NC * nvt));
+      const bf16_t *qb = (const bf16_t*)q, *kb = (const bf16_t*)k, *vb = (const bf16_t*)v, *hb = (const bf16_t*)dh;
+      switch (F.DQK) {
+        case 64: hipLaunchKernelGGL((bw_dv_bf16_kernel<TG, 1>), grid, dim3(256), 0, s, qb, kb, vb, hb, ig, fg, mst, mfin, vm, vn, dC, (bf16_t*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
+        case 128: hipLaunchKernelGGL((bw_dv_bf16_kernel<TG, 2>), grid, dim3(256), 0, s, qb, kb, vb, hb, ig, fg, mst, mfin, vm, vn, dC, (bf16_t*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
+        default: hipLaunchKernelGGL((bw_dv_bf16_kernel<TG, 4>), grid, dim3(256), 0, s, qb, kb, vb, hb, ig, fg, mst, mfin, vm, vn, dC, (bf16_t*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
+      }
+    } else if (tiles_mfma) {
       const dim3 grid((unsigned)(BNH * NC * nvt));
       switch (F.DQK) {
         case 64: hipLaunchKernelGGL((bw_dv_mfma_kernel<TQ, TG, 1>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, mst, mfin, vm, vn, dC, (TQ*)A.dv, dip, NC, F.DV, nvt, F.qk_scale); break;
@@ -1162,7 +1867,14 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   }
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dV)"))) return rc;
   if (tiles_mfma) {
-    if constexpr (sizeof(TQ) == 2 && L == 64) {
+    if constexpr (std::is_same<TQ, bf16_t>::value && L == 64) {
+      const dim3 grid((unsigned)(BNH * NC * ndt));
+      switch (F.DQK) {
+        case 64: hipLaunchKernelGGL((bw_dqk_bf16_kernel<TG, 1>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
+        case 128: hipLaunchKernelGGL((bw_dqk_bf16_kernel<TG, 2>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
+        default: hipLaunchKernelGGL((bw_dqk_bf16_kernel<TG, 4>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
+      }
+    } else if constexpr (sizeof(TQ) == 2 && L == 64) {
       const dim3 grid((unsigned)(BNH * NC * ndt));
       switch (F.DQK) {
         case 64: hipLaunchKernelGGL((bw_dqk_mfma_kernel<TQ, TG, 1>), grid, dim3(256), 0, s, q, k, v, dh, ig, fg, Cst, mst, mfin, vm, vn, dC, (TQ*)A.dq, (TQ*)A.dk, dfp, NC, F.DV, ndt, F.qk_scale); break;
