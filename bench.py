@@ -566,9 +566,22 @@ def bwd_flops(B, NH, S, DQK, DV, L):
     return 2.0 * B * NH * NC * (5 * L * DQK * DV + 4 * L * L * DQK + 2 * L * L * DV)
 
 
+def bwd_bytes(B, NH, S, DQK, DV, L, esz=2):
+    """HBM bytes of the reference's custom backward with its per-chunk states materialised (bw.py:
+    matC_states recomputed, matDeltaC_states): q, k, v, dH, i, f read once; dq, dk, dv, di, df
+    written once; the NC entering states C written once and read once (dQ), the NC + 1 state
+    gradients dC written once and read twice (dV, dQ/dK), in float32."""
+    NC = S // L
+    io = B * NH * S * ((2 * DQK + 2 * DV) + (2 * DQK + DV) + 4) * esz  # q k v dH in, dq dk dv out, i f in, di df out
+    states = B * NH * (2 * NC + 3 * (NC + 1)) * DQK * DV * 4
+    return io + states
+
+
 def bench_chunkwise_bwd(args, dev):
     """The chunkwise backward (xl_mlstm_chunkwise_bwd, the reference's custom backward) on config 2's
-    shape: B4 NH8 S8192 DQK256 DV512 bf16, last-state gradient included; float32 arithmetic."""
+    shape: B4 NH8 S8192 DQK256 DV512 bf16, last-state gradient included.  Products on bf16 MFMA
+    (float32 operands as bf16 hi / lo pairs), float32 accumulation; bound by the float32 state
+    traffic, so the roofline is HBM bytes, with the bf16 MFMA fraction beside it."""
     from xlstm_hip.ops import mlstm_chunkwise_bwd_op
     from xlstm_hip.workloads import CFG2, chunkwise_inputs
     cfg = CFG2
@@ -582,12 +595,16 @@ def bench_chunkwise_bwd(args, dev):
 
     t = _timed(call, dev, max(3, args.steps // 4), warmup=2)
     fl = bwd_flops(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, 64)
+    by = bwd_bytes(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, 64)
     tf = fl / (t["ms"] * 1e-3) / 1e12
+    gbs = by / (t["ms"] * 1e-3) / 1e9
     return {"workload": f"cfg2 chunkwise backward B{cfg.B} NH{cfg.NH} S{cfg.S} DQK{cfg.DQK} DV{cfg.DV} bf16 in, "
-                        "float32 arithmetic", "ms_per_call": t["ms"], "ms_min": t["ms_min"], "mode": t["mode"],
-            "tokens_per_s": cfg.B * cfg.S / (t["ms"] * 1e-3), "flops_per_call": fl,
-            "roofline": {"bound": "fp32", "achieved": tf, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                         "frac": tf / PEAK_FP32_TFLOPS}}
+                        "bf16 MFMA (float32 operands as hi / lo pairs), float32 accumulation",
+            "ms_per_call": t["ms"], "ms_min": t["ms_min"], "mode": t["mode"],
+            "tokens_per_s": cfg.B * cfg.S / (t["ms"] * 1e-3), "flops_per_call": fl, "bytes_per_call": by,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS},
+            "mfma_bf16": {"achieved_tflops": tf, "peak": PEAK_BF16_TFLOPS, "frac": tf / PEAK_BF16_TFLOPS}}
 
 
 def bench_arbitrary_length(args, dev):

@@ -860,6 +860,98 @@ __device__ __forceinline__ int xcd_contiguous(int b, int G) {
   return x * per + (x < rem ? x : rem) + i;
 }
 
+// ------------------------------------------------------ bf16 MFMA stats (2)
+// bw_stats_kernel for bf16 q / k and 64-token chunks on v_mfma_f32_16x16x32_bf16: one
+// workgroup of 4 waves per (head, chunk); wave w owns query rows [16 w, 16 w + 16) and all
+// 64 key columns, so every row sum stays in the wave.  Per 32 d: A = Q rows (loaded from
+// global memory straight into the operand registers), B = K rows (the chunk's K staged once in
+// LDS) for S[i][j]; a fifth tile takes B = n_{k-1} as bf16 hi (column 0) and lo (column 1), so
+// q . n = D[i][0] + D[i][1].  Then M = S s exp(b_i - b_j + i_j - m_i) on j <= i, its row sums
+// over the tiles and the 16 lanes of a group, and the divisor (fw.py:219-245).
+template <typename TG, int NRT>
+__global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                             const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                             const float* __restrict__ nst,
+                                                             const float* __restrict__ mst, float* __restrict__ vm,
+                                                             float* __restrict__ vn, int NC, float qk_scale,
+                                                             float eps) {
+  constexpr int L = 64, DQK = 64 * NRT;
+  constexpr int KP = DQK + 16;               // bf16 per staged K row (2 DQK + 32 bytes)
+  constexpr int PR = DQK / 8, NP = L * PR / 256;  // 16-byte pieces per row, per thread
+  constexpr int NKS = DQK / 32;              // 32-d MFMA steps
+  __shared__ __attribute__((aligned(16))) bf16_t sK[L * KP];
+  __shared__ __attribute__((aligned(16))) float sn[DQK];
+  __shared__ float sb[L], si[L], smc[L], sqb[L];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int bh = blockIdx.x / NC, kc = blockIdx.x - bh * NC;
+  const size_t row0 = (size_t)bh * NC * L + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  // every load first: gates, m, the K chunk, n, this lane's Q operands
+  float gf = 0.f, gi = 0.f;
+  if (tid < L) {
+    gf = to_f32(fg[row0 + tid]);
+    gi = to_f32(ig[row0 + tid]);
+  }
+  const float mp = mst[sidx];
+  u32x4 pk[NP], pq[NKS];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int p = u * 256 + tid;
+    pk[u] = *reinterpret_cast<const u32x4*>(k + (row0 + p / PR) * DQK + (p % PR) * 8);
+  }
+  const float nv = tid < DQK ? nst[sidx * DQK + tid] : 0.f;
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+    pq[ks] = *reinterpret_cast<const u32x4*>(q + (row0 + 16 * w + r) * DQK + 32 * ks + 8 * g);
+  chunk_gate_scan_v<L>(gf, gi, sb, si);
+  if (tid < L) {
+    const float mc = m_combine<L>(sb, si, tid, mp);
+    smc[tid] = mc;
+    sqb[tid] = expf(sb[tid] + mp - mc) * qk_scale;  // fw.py:230-231
+  }
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int p = u * 256 + tid;
+    *reinterpret_cast<u32x4*>(sK + (p / PR) * KP + (p % PR) * 8) = pk[u];
+  }
+  if (tid < DQK) sn[tid] = nv;
+  __syncthreads();
+  f32x4 acc[4], accN = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) acc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    const int c = 32 * ks + 8 * g;
+    const bfx8 qa = __builtin_bit_cast(bfx8, pq[ks]);
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) acc[jt] = mfma_bf(qa, ld_bf8(sK + (16 * jt + r) * KP + c), acc[jt]);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = sn[c + e];
+    u32x4 h, l;
+    split_bf(x, h, l);
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    accN = mfma_bf(qa, __builtin_bit_cast(bfx8, r == 0 ? h : (r == 1 ? l : z)), accN);
+  }
+  // lane (g, r), element e: row i = 16 w + 4 g + e; S[i][16 jt + r], q . n in lanes r = 0, 1
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = 16 * w + 4 * g + e;
+    float rs = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const int j = 16 * jt + r;
+      rs += (j <= i) ? acc[jt][e] * qk_scale * expf(sb[i] - sb[j] + si[j] - smc[i]) : 0.f;
+    }
+    rs = sum16(rs);
+    const float qn = accN[e] + __shfl_xor(accN[e], 1, 64);
+    if (r == 0) {  // den = qbar (q . n) + sum_j M_ij; divisor max(|den|, exp(-m)) + eps (fw.py:237-245)
+      const float den = sqb[i] * qn + rs;
+      vm[row0 + i] = smc[i];
+      vn[row0 + i] = fmaxf(fabsf(den), expf(-smc[i])) + eps;
+    }
+  }
+}
+
 // ----------------------------------------------- bf16 MFMA chunk scans (1, 3)
 // bw_scan_kernel for bf16 X and Y on v_mfma_f32_16x16x32_bf16: the same workgroups,
 // gates, stores and state layout; per chunk X is staged in LDS as it is and coef_t Y[t] as
@@ -1391,7 +1483,7 @@ __global__ __launch_bounds__(256) void bw_dqk_mfma_kernel(const TQ* __restrict__
 constexpr int BFP = 80;  // bf16 per staged 64-wide row (160 bytes)
 
 template <typename TG, int NRT>
-__global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+__global__ __launch_bounds__(256, 3) void bw_dv_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                           const bf16_t* __restrict__ v, const bf16_t* __restrict__ dh,
                                                           const TG* __restrict__ ig, const TG* __restrict__ fg,
                                                           const float* __restrict__ mst,
@@ -1404,11 +1496,11 @@ __global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restric
   constexpr int L = 64;
   constexpr int DQK = 64 * NRT;
   __shared__ __attribute__((aligned(16))) bf16_t sK[L * BFP];
-  __shared__ __attribute__((aligned(16))) bf16_t sQ[L * BFP];
-  __shared__ __attribute__((aligned(16))) uint32_t sSh[L * BFP / 2];
-  __shared__ __attribute__((aligned(16))) uint32_t sSl[L * BFP / 2];
-  __shared__ __attribute__((aligned(16))) uint32_t sCh[L * BFP / 2];  // dC_k block [d][v], hi / lo
+  // the dC_k block [d][v] as bf16 hi / lo rows; after the DQK loop, Sbar^T [t][j] hi / lo
+  __shared__ __attribute__((aligned(16))) uint32_t sCh[L * BFP / 2];
   __shared__ __attribute__((aligned(16))) uint32_t sCl[L * BFP / 2];
+  uint32_t* const sSh = sCh;
+  uint32_t* const sSl = sCl;
   __shared__ float sb[L], si[L], smc[L], sinv[L], sab[L];
   __shared__ float s_part[4][L];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
@@ -1419,8 +1511,9 @@ __global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restric
   const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
   // dC_k (the gradient of the state after chunk kc), columns v0 .. v0 + 63
   const float* dcb = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV + v0;
-  // two register slots of a DQK block: K, Q rows (t = p / 8, 8 d at 8 (p % 8)) and the dC_k block
-  // (d = p / 16, 4 v at 4 (p % 16)); block b + 2 is loaded while block b is computed
+  // two register slots of a DQK block: K rows (t = p / 8, 8 d at 8 (p % 8)), this lane's Q
+  // operands (row 16 w + r, d = 32 ks + 8 g + 0..7: each wave reads only its own rows of Q) and
+  // the dC_k block (d = p / 16, 4 v at 4 (p % 16)); block b + 2 is loaded while block b is computed
   u32x4 pk[2][2], pq[2][2];
   f32x4 pc[2][4];
   auto fetch = [&](auto slot, int db) {
@@ -1429,7 +1522,7 @@ __global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restric
     for (int u = 0; u < 2; ++u) {
       const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
       pk[sl][u] = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + db + c);
-      pq[sl][u] = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + db + c);
+      pq[sl][u] = *reinterpret_cast<const u32x4*>(q + (row0 + 16 * w + r) * DQK + db + 32 * u + 8 * g);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -1476,7 +1569,6 @@ __global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restric
     for (int u = 0; u < 2; ++u) {
       const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
       *reinterpret_cast<u32x4*>(sK + t * BFP + c) = pk[sl][u];
-      *reinterpret_cast<u32x4*>(sQ + t * BFP + c) = pq[sl][u];
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -1486,6 +1578,7 @@ __global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restric
       *reinterpret_cast<u32x2*>(sCh + o) = u32x2{h0, h1};
       *reinterpret_cast<u32x2*>(sCl + o) = u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
     }
+    const u32x4 qv[2] = {pq[sl][0], pq[sl][1]};  // this block's Q operands, before the slot is reloaded
     __syncthreads();
     if (bi + 2 < NRT) fetch(slot, (bi + 2) * 64);
 #pragma unroll
@@ -1494,7 +1587,7 @@ __global__ __launch_bounds__(256) void bw_dv_bf16_kernel(const bf16_t* __restric
       // dC_k[d][16 w + r] at d = c + 0..7 (the k of the K operand)
       const int o1 = ((c + kk) * BFP + 16 * w + 4 * ka) >> 1, o2 = o1 + 2 * BFP;
       const bfx8 dch = tr_pair(sCh + o1, sCh + o2), dcl = tr_pair(sCl + o1, sCl + o2);
-      const bfx8 qa = ld_bf8(sQ + (16 * w + r) * BFP + c);
+      const bfx8 qa = __builtin_bit_cast(bfx8, qv[ks]);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const bfx8 kb = ld_bf8(sK + (16 * tt + r) * BFP + c);
@@ -1828,8 +1921,20 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
                                                      nst, mst, cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s)
                      : chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
   if (rc) return rc;
-  hipLaunchKernelGGL((bw_stats_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC)), dim3(BW_THREADS), 0, s, q, k, ig, fg,
-                     nst, mst, vm, vn, NC, F.DQK, F.qk_scale, F.eps);
+  bool stats_mfma = false;
+  if constexpr (std::is_same<TQ, bf16_t>::value && L == 64) {
+    stats_mfma = F.DQK == 64 || F.DQK == 128 || F.DQK == 256;
+    const dim3 grid((unsigned)(BNH * NC));
+    switch (stats_mfma ? F.DQK : 0) {
+      case 64: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 1>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, NC, F.qk_scale, F.eps); break;
+      case 128: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 2>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, NC, F.qk_scale, F.eps); break;
+      case 256: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 4>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, NC, F.qk_scale, F.eps); break;
+      default: break;
+    }
+  }
+  if (!stats_mfma)
+    hipLaunchKernelGGL((bw_stats_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC)), dim3(BW_THREADS), 0, s, q, k, ig, fg,
+                       nst, mst, vm, vn, NC, F.DQK, F.qk_scale, F.eps);
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(stats)"))) return rc;
   if (scan_mfma) {
     rc = launch_scan<TQ, TG, L, true>(F.DQK, q, dh, ig, fg, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr, mst,
