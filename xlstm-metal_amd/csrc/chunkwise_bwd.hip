@@ -557,43 +557,68 @@ __global__ __launch_bounds__(BW_THREADS) void bw_dqk_kernel(const TQ* __restrict
 }
 
 // --------------------------------------------------------------- 6. gates
-// One workgroup per head: dI_t = sum of its dV partials; dF_t = sigmoid(-f_t) times
-// the suffix sum over u >= t of the q . dQ - k . dK partials, 256 tokens per step
-// from the end of the sequence (a block-wide inclusive scan, then the carry).
+// One workgroup per (head, segment of GSEG tokens): dI_t = sum of its dV partials;
+// dF_t = sigmoid(-f_t) times the suffix sum over u >= t of the q . dQ - k . dK partials
+// (bw.py:332-338): the segment's own suffix scan (4 consecutive tokens per thread, then a
+// reverse scan over the lanes and the 4 waves) plus the total of every later segment, which
+// each workgroup sums itself (a plain reduction over contiguous partials).
+constexpr int GSEG = 1024;
+
 template <typename TG>
-__global__ __launch_bounds__(BW_THREADS) void bw_gates_kernel(const TG* __restrict__ fg,
-                                                               const float* __restrict__ dfp,
-                                                               const float* __restrict__ dip, TG* __restrict__ di,
-                                                               TG* __restrict__ df, int S, int ndt, int nvt) {
-  __shared__ float sx[BW_THREADS];
-  const int tid = threadIdx.x;
-  const size_t base = (size_t)blockIdx.x * S;
-  float carry = 0.f;
-  for (int end = S; end > 0; end -= BW_THREADS) {
-    // position tid counts back from the end of this block of tokens
-    const int t = end - 1 - tid;
-    float x = 0.f;
-    if (t >= 0) {
-      for (int j = 0; j < ndt; ++j) x += dfp[(base + t) * ndt + j];
-      float s = 0.f;
-      for (int j = 0; j < nvt; ++j) s += dip[(base + t) * nvt + j];
-      di[base + t] = from_f32<TG>(s);
+__global__ __launch_bounds__(256) void bw_gates_kernel(const TG* __restrict__ fg, const float* __restrict__ dfp,
+                                                       const float* __restrict__ dip, TG* __restrict__ di,
+                                                       TG* __restrict__ df, int S, int ndt, int nvt) {
+  __shared__ float s_wave[4], s_red[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nseg = (S + GSEG - 1) / GSEG;
+  const int bh = blockIdx.x / nseg, sg = blockIdx.x - bh * nseg;
+  const size_t base = (size_t)bh * S;
+  const int t0 = sg * GSEG, t1 = min(S, t0 + GSEG);
+  // total of the later segments' partials
+  float c = 0.f;
+  const float* later = dfp + (base + t1) * ndt;
+  const size_t nl = (size_t)(S - t1) * ndt;
+  for (size_t e = tid; e < nl; e += 256) c += later[e];
+  // this thread's tokens t0 + 4 tid + u
+  float x[4], fv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = t0 + 4 * tid + u;
+    float a = 0.f, sd = 0.f;
+    fv[u] = 0.f;
+    if (t < t1) {
+      for (int j = 0; j < ndt; ++j) a += dfp[(base + t) * ndt + j];
+      for (int j = 0; j < nvt; ++j) sd += dip[(base + t) * nvt + j];
+      di[base + t] = from_f32<TG>(sd);
+      fv[u] = to_f32(fg[base + t]);
     }
-    sx[tid] = x;
-    __syncthreads();
-    for (int o = 1; o < BW_THREADS; o <<= 1) {  // inclusive scan over the reversed positions
-      const float y = tid >= o ? sx[tid - o] : 0.f;
-      __syncthreads();
-      sx[tid] += y;
-      __syncthreads();
-    }
-    if (t >= 0) {
-      const float suffix = carry + sx[tid];
-      const float fv = to_f32(fg[base + t]);
-      df[base + t] = from_f32<TG>(suffix / (1.0f + expf(fv)));  // * sigmoid(-f)
-    }
-    carry += sx[BW_THREADS - 1];
-    __syncthreads();
+    x[u] = a;
+  }
+  float suf[4];
+  suf[3] = x[3];
+  suf[2] = x[2] + suf[3];
+  suf[1] = x[1] + suf[2];
+  suf[0] = x[0] + suf[1];
+  // inclusive suffix over the lanes of the wave, and the wave reductions
+  float v = suf[0];
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_down(v, o, 64);
+    if (lane + o < 64) v += y;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if (lane == 0) {
+    s_wave[w] = v;
+    s_red[w] = c;
+  }
+  __syncthreads();
+  float after = v - suf[0] + s_red[0] + s_red[1] + s_red[2] + s_red[3];  // everything past this thread's tokens
+  for (int w2 = w + 1; w2 < 4; ++w2) after += s_wave[w2];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = t0 + 4 * tid + u;
+    if (t < t1) df[base + t] = from_f32<TG>((suf[u] + after) / (1.0f + expf(fv[u])));  // * sigmoid(-f)
   }
 }
 
@@ -990,40 +1015,36 @@ __global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
   const int row0 = d_off + w * 16 * NRT;
   const int nslots = REV ? NC + 1 : NC;
 
+  // the state transposed in the accumulators: tile (rt, ct) holds D[column][row], lane (g, r)
+  // columns 16 ct + 4 g + 0..3 of row 16 rt + r, so a lane stores 16 contiguous bytes
   f32x4 acc[NRT][4];
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        acc[rt][ct][e] = s0 ? s0[((size_t)bh * DQKf + row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] : 0.f;
+      acc[rt][ct] = s0 ? *reinterpret_cast<const f32x4*>(s0 + ((size_t)bh * DQKf + row0 + 16 * rt + r) * DV + v0 +
+                                                          16 * ct + 4 * g)
+                       : f32x4{0.f, 0.f, 0.f, 0.f};
   auto store_state = [&](float* dst) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(size_t)(row0 + 16 * rt + 4 * g + e) * DV + v0 + 16 * ct + r] = acc[rt][ct][e];
+        *reinterpret_cast<f32x4*>(dst + (size_t)(row0 + 16 * rt + r) * DV + v0 + 16 * ct + 4 * g) = acc[rt][ct];
   };
-  // n (forward, the first column tile's workgroups): one more 16 x 16 accumulator tile per row
-  // tile, whose B operand is columns 64.. of the staged hi rows: coef_t hi in column 64, lo in
-  // column 65, zeros after; n = column 0 + column 1 (lanes r = 0, 1)
+  // n (forward, the first column tile's workgroups, which write whole n rows): one more 16 x 16
+  // accumulator tile per row tile, whose A operand is columns 64.. of the staged hi rows: coef_t
+  // hi in column 64, lo in column 65, zeros after; n[row 16 rt + r] = elements 0 + 1 of lane
+  // (0, r)
   const bool owns_n = !REV && vt == 0;  // workgroup-uniform
   f32x4 accN[NRT];
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      accN[rt][e] = (owns_n && n0 && r == 0) ? n0[(size_t)bh * DQKf + row0 + 16 * rt + 4 * g + e] : 0.f;
+    accN[rt] = f32x4{(owns_n && n0 && g == 0) ? n0[(size_t)bh * DQKf + row0 + 16 * rt + r] : 0.f, 0.f, 0.f, 0.f};
   auto store_n = [&](float* dst) {  // dst: this head's DQKf values
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float nv = accN[rt][e] + __shfl_xor(accN[rt][e], 1, 64);
-        if (r == 0) dst[row0 + 16 * rt + 4 * g + e] = nv;
-      }
+      if (g == 0) dst[row0 + 16 * rt + r] = accN[rt][0] + accN[rt][1];
   };
   if (owns_n)
     for (int p = tid; p < L * 16; p += 256) sYh[(p >> 4) * SB_YP + SC_V + (p & 15)] = bf16_t{0};
@@ -1144,16 +1165,16 @@ __global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
         const bfx8 bh8 = tr_pair(sYh + t1 * SB_YP + c, sYh + t2 * SB_YP + c);
         const bfx8 bl8 = tr_pair(sYl + t1 * SB_YP + c, sYl + t2 * SB_YP + c);
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-          acc[rt][ct] = mfma_bf(a[rt], bh8, acc[rt][ct]);
-          acc[rt][ct] = mfma_bf(a[rt], bl8, acc[rt][ct]);
+        for (int rt = 0; rt < NRT; ++rt) {  // D[column][row] += (hi + lo)[T][column] X[T][row]
+          acc[rt][ct] = mfma_bf(bh8, a[rt], acc[rt][ct]);
+          acc[rt][ct] = mfma_bf(bl8, a[rt], acc[rt][ct]);
         }
       }
       if (owns_n) {  // n' = decay n + sum_t coef_t k_t (fw.py:133)
         const int c = SC_V + 4 * ka;
         const bfx8 bn = tr_pair(sYh + t1 * SB_YP + c, sYh + t2 * SB_YP + c);
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) accN[rt] = mfma_bf(a[rt], bn, accN[rt]);
+        for (int rt = 0; rt < NRT; ++rt) accN[rt] = mfma_bf(bn, a[rt], accN[rt]);
       }
     }
     __syncthreads();
@@ -1993,8 +2014,8 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
                        F.qk_scale);
   }
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(dQ, dK)"))) return rc;
-  hipLaunchKernelGGL((bw_gates_kernel<TG>), dim3((unsigned)BNH), dim3(BW_THREADS), 0, s, fg, dfp, dip, (TG*)A.di,
-                     (TG*)A.df, F.S, ndt, nvt);
+  hipLaunchKernelGGL((bw_gates_kernel<TG>), dim3((unsigned)(BNH * ((F.S + GSEG - 1) / GSEG))), dim3(256), 0, s, fg,
+                     dfp, dip, (TG*)A.di, (TG*)A.df, F.S, ndt, nvt);
   return check_launch("xl_mlstm_chunkwise_bwd(gates)");
 }
 
