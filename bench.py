@@ -577,6 +577,33 @@ def bwd_bytes(B, NH, S, DQK, DV, L, esz=2):
     return io + states
 
 
+BWD_KERNELS = {  # kernel-name key -> short name, for the trace / counter summaries of the backward
+    "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, false>": "states scan",
+    "bw_stats_bf16_kernel": "stats",
+    "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, true>": "dC scan",
+    "bw_dv_bf16_kernel": "dV",
+    "bw_dqk_bf16_kernel": "dQ, dK",
+    "bw_gates_kernel": "gate gradients",
+}
+
+
+def bwd_kernel_bytes(B, NH, S, DQK, DV, L, esz=2):
+    """Algorithmic HBM bytes of each backward launch (bf16 q/k/v/dH/gates, float32 states): what it
+    must read and write once, with the states and partials in the float32 workspace."""
+    NC, BNH, ndt, nvt = S // L, B * NH, -(-DQK // 64), -(-DV // 64)
+    st = NC * DQK * DV * 4
+    g = 2 * S * esz  # i, f
+    return {
+        "states scan": BNH * (S * (DQK + DV) * esz + g + st + NC * (DQK + 1) * 4 + (DQK * DV + DQK + 1) * 4),
+        "stats": BNH * (2 * S * DQK * esz + g + NC * (DQK + 1) * 4 + 2 * S * 4),
+        "dC scan": BNH * (S * (DQK + DV) * esz + g + 2 * S * 4 + NC * 4 + DQK * DV * 4 + st + DQK * DV * 4),
+        "dV": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + st + g + 2 * S * 4 + S * DV * esz + S * nvt * 4),
+        "dQ, dK": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + 2 * st + g + 2 * S * 4 + 2 * S * DQK * esz
+                         + S * ndt * 4),
+        "gate gradients": BNH * (S * (ndt + nvt) * 4 + S * esz + 2 * S * esz),
+    }
+
+
 def bench_chunkwise_bwd(args, dev):
     """The chunkwise backward (xl_mlstm_chunkwise_bwd, the reference's custom backward) on config 2's
     shape: B4 NH8 S8192 DQK256 DV512 bf16, last-state gradient included.  Products on bf16 MFMA
@@ -792,7 +819,7 @@ def summarize_pmc(fetch_dir, write_dir):
                     name = row["Kernel_Name"]
                     key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel",
                                             SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL,
-                                            RMS_GATE_KERNEL, GATE_PROJ_KERNEL)
+                                            RMS_GATE_KERNEL, GATE_PROJ_KERNEL, *BWD_KERNELS)
                                 if k in name), None)
                     if key is None:
                         continue
@@ -819,6 +846,9 @@ def summarize_pmc(fetch_dir, write_dir):
             "gate_prep_kernel": ("cfg2 chunkwise gate prep",
                                  2 * CFG2.B * CFG2.NH * CFG2.S * 2 + CFG2.B * CFG2.NH * (CFG2.S // 64) * 258 * 4),
             **layer_stage_work()}
+    bwb = bwd_kernel_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV, 64)
+    for k, short in BWD_KERNELS.items():
+        work[k] = (f"cfg2 chunkwise backward: {short}", bwb[short])
     out = {"calibration": {"kernel": SOFT_CAP_KERNEL, "bytes_read": sc_bytes, "bytes_written": sc_bytes,
                            "fetch_scale": f_scale, "write_scale": w_scale},
            "kernels": {}}

@@ -267,7 +267,8 @@ int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias
  * Chunkwise mLSTM backward: the reference's custom backward mlstm_chunkwise_bw
  * (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/vendored/torch/native/
  * bw.py:198-352, wrapped by _mlstm_chunkwise_fwbw.backward, fwbw.py:102-173 and
- * mlstm_chunkwise__native_custbw, fwbw.py:232-281), float32 arithmetic.  The
+ * mlstm_chunkwise__native_custbw, fwbw.py:232-281), float32 accumulation (bf16
+ * inputs: bf16 matrix-core products, float32 operands as bf16 hi + lo pairs).  The
  * states are recomputed from the inputs (recompute_states_in_bw) and the
  * per-token denominator max(|q n|, exp(-m)) + eps is treated as a constant, as
  * there.  Inputs as for xl_mlstm_chunkwise_fwd plus dh [B,NH,S,DV] (dtype_qkv)

@@ -1,9 +1,11 @@
-// Chunkwise mLSTM backward (float32 arithmetic): the reference's custom backward
+// Chunkwise mLSTM backward (float32 accumulation): the reference's custom backward
 // mlstm_chunkwise_bw (kernel_development/xlstm/mlstm_block/mlstm_chunkwise/
 // vendored/torch/native/bw.py:198-352), which treats the per-token
 // denominator max(|q n|, exp(-m)) + eps as a constant (the mLSTM layer's
 // multi-head norm removes any per-row scale of h, so its gradient does not
-// reach the loss there).  Five launches after the states pass:
+// reach the loss there).  Five launches after the states pass (named here by
+// their FMA forms; the bf16 and float32-MFMA forms further down do the same
+// work per launch):
 //
 //   1. the states pass of the two-pass forward recomputes the state entering
 //      every chunk (bw.py:242-258, recompute_states_in_bw);
