@@ -1519,6 +1519,7 @@ __global__ __launch_bounds__(256, 3) void bw_dv_bf16_kernel(const bf16_t* __rest
   constexpr int L = 64;
   constexpr int DQK = 64 * NRT;
   __shared__ __attribute__((aligned(16))) bf16_t sK[L * BFP];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[L * BFP];  // the V tile, for the dI partials
   // the dC_k block [d][v] as bf16 hi / lo rows; after the DQK loop, Sbar^T [t][j] hi / lo
   __shared__ __attribute__((aligned(16))) uint32_t sCh[L * BFP / 2];
   __shared__ __attribute__((aligned(16))) uint32_t sCl[L * BFP / 2];
@@ -1553,8 +1554,8 @@ __global__ __launch_bounds__(256, 3) void bw_dv_bf16_kernel(const bf16_t* __rest
       pc[sl][u] = *reinterpret_cast<const f32x4*>(dcb + (size_t)(db + (p >> 4)) * DV + (p & 15) * 4);
     }
   };
-  // the intra term's dH block [j][v], staged into sK after the last DQK block
-  u32x4 ph[2];
+  // the intra term's dH block [j][v], staged into sK after the last DQK block, and the V tile
+  u32x4 ph[2], pv[2];
   const int kk = r >> 2, ka = r & 3;  // transposed reads: row r / 4 of a 4-row block, columns 4 (r % 4)
   // every load that does not depend on another goes out first: gates, stats, blocks 0 and 1, dH
   float gf = 0.f, gi = 0.f, gvm = 0.f, gvn = 1.f, gmn = 0.f;
@@ -1573,6 +1574,7 @@ __global__ __launch_bounds__(256, 3) void bw_dv_bf16_kernel(const bf16_t* __rest
   for (int u = 0; u < 2; ++u) {
     const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
     ph[u] = *reinterpret_cast<const u32x4*>(dh + (row0 + t) * DV + v0 + c);
+    pv[u] = *reinterpret_cast<const u32x4*>(v + (row0 + t) * DV + v0 + c);
   }
   chunk_gate_scan_v<L>(gf, gi, sb, si);
   if (tid < L) {
@@ -1648,6 +1650,7 @@ __global__ __launch_bounds__(256, 3) void bw_dv_bf16_kernel(const bf16_t* __rest
   for (int u = 0; u < 2; ++u) {  // dH block into sK (read by every wave before the last barrier)
     const int p = u * 256 + tid, t = p >> 3, c = (p & 7) * 8;
     *reinterpret_cast<u32x4*>(sK + t * BFP + c) = ph[u];
+    *reinterpret_cast<u32x4*>(sV + t * BFP + c) = pv[u];
   }
   __syncthreads();
   // intra: dV[t][v] += sum_j Sbar^T[t][j] dH[j][v]
@@ -1670,7 +1673,7 @@ __global__ __launch_bounds__(256, 3) void bw_dv_bf16_kernel(const bf16_t* __rest
       const int t = 16 * tt + 4 * g + e;
       const size_t off = (row0 + t) * DV + v0 + 16 * w + r;
       dv[off] = from_f32<bf16_t>(accV[tt][e]);
-      const float part = sum16(to_f32(v[off]) * accV[tt][e]);
+      const float part = sum16(to_f32(sV[t * BFP + 16 * w + r]) * accV[tt][e]);
       if (r == 0) s_part[w][t] = part;
     }
   __syncthreads();
