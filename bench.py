@@ -884,14 +884,15 @@ def _blas() -> str:
 
 def bench_cfg0(args, dev):
     """BASELINE config 0 on the GPU: one float32 mlstm_chunkwise call (B1 NH8 S256 DQK256 DV512, L 64,
-    last states returned), the two-pass float32 kernels, replayed from a HIP graph, HIP events."""
+    last states returned): the two-pass algorithm, states on float32 MFMA, outputs on bf16 MFMA in the
+    three-product form; replayed from a HIP graph, HIP events."""
     import xlstm_hip
     from xlstm_hip.workloads import CFG0, chunkwise_inputs
     x = chunkwise_inputs(CFG0, device=dev)
     t = _timed(lambda: xlstm_hip.mlstm_chunkwise(*x, return_last_states=True, chunk_size=CFG0.L), dev,
                max(20, args.steps))
     return {"workload": "cfg0 mlstm_chunkwise fp32 B1 NH8 S256 DQK256 DV512 L64", "us_per_call": 1e3 * t["ms"],
-            "us_min": 1e3 * t["ms_min"], "mode": t["mode"], "algo": "two_pass (float32)"}
+            "us_min": 1e3 * t["ms_min"], "mode": t["mode"], "algo": "two_pass (states: float32 MFMA; outputs: bf16 MFMA, three products)"}
 
 
 def cpu_baseline(args):

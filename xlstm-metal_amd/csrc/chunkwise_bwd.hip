@@ -30,11 +30,13 @@
 // 0 is dC_initial), the dF partials [BNH][S][ceil(DQK/64)] and the dI partials
 // [BNH][S][ceil(DV/64)].
 #include "chunkwise.h"
+#include "mfma_bf16.h"
 
 #include <type_traits>
 
 namespace xl {
 namespace {
+using namespace xl::mfma;  // bf16 MFMA building blocks (mfma_bf16.h)
 
 constexpr int BW_THREADS = 256;
 constexpr int BW_T = 64;   // DQK / DV tile
@@ -645,8 +647,6 @@ __global__ __launch_bounds__(256) void bw_gates_kernel(const TG* __restrict__ fg
 constexpr int SC_V = 64;          // DV columns per workgroup
 constexpr int SC_YP = SC_V + 16;  // floats per staged Y row (16 mod 64 dwords: 4 rows, distinct banks)
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -822,10 +822,10 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     }
     __syncthreads();  // the staged tiles are read; the next chunk may overwrite them
   }
-  if (!REV) {
-    store_state(sfin + (size_t)bh * DQKf * DV);
-    if (owns_n) nfin[(size_t)bh * DQKf + d_off + tid] = nn;
-    if (vt == 0 && rs == 0 && tid == 0) mfin[bh] = m;
+  if (!REV) {  // the final state (the forward's last states may not be asked for)
+    if (sfin) store_state(sfin + (size_t)bh * DQKf * DV);
+    if (owns_n && nfin) nfin[(size_t)bh * DQKf + d_off + tid] = nn;
+    if (vt == 0 && rs == 0 && tid == 0 && mfin) mfin[bh] = m;
   } else {
     store_state(Sst + (size_t)bh * nslots * DQKf * DV);
     if (s_init) store_state(s_init + (size_t)bh * DQKf * DV);
@@ -837,55 +837,6 @@ constexpr size_t scan_smem(int NRT) {
   return (size_t)L * (64 * NRT + 16) * sizeof(TQ) + (size_t)L * SC_YP * sizeof(float);
 }
 
-// ------------------------------------------------ bf16 MFMA building blocks
-// v_mfma_f32_16x16x32_bf16: A[i][k] in lane i + 16 (k / 8), element k % 8; B[k][j] in lane
-// j + 16 (k / 8); D as for 16x16x4f32 (D[i][j] in lane j + 16 (i / 4), element i % 4).
-// Operands exact in bf16 (q, k, v, dH) enter once; a float32 operand x enters as the pair
-// hi = bf16(x), lo = bf16(x - hi) (two products, 16 significant bits of x), accumulated in
-// float32.
-typedef __bf16 bfx8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bfx2 __attribute__((ext_vector_type(2)));
-typedef short sx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) sx4 lds_sx4;
-
-__device__ __forceinline__ f32x4 mfma_bf(bfx8 a, bfx8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-// {bf16(x0), bf16(x1)} (round to nearest even), x0 in the low half
-__device__ __forceinline__ uint32_t pk_bf(float x0, float x1) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x0, x1}), bfx2));
-}
-__device__ __forceinline__ float bf_l(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf_h(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-// hi / lo pair of 8 floats (x - hi is exact in float32)
-__device__ __forceinline__ void split_bf(const float (&x)[8], u32x4& hi, u32x4& lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    hi[e] = pk_bf(x[2 * e], x[2 * e + 1]);
-    lo[e] = pk_bf(x[2 * e] - bf_l(hi[e]), x[2 * e + 1] - bf_h(hi[e]));
-  }
-}
-// Two ds_read_b64_tr_b16 -> one 8 x bf16 operand.  Within each 16 lanes, lane s passes the
-// address of 4 consecutive 16-bit columns at 4 (s % 4) of row s / 4 (of a 4-row block) and
-// receives column s of the 4 rows: with p0 / p1 the addresses in two 4-row blocks, lane s ends
-// with column c0 + s of rows R0 .. R0 + 3 (elements 0..3) and R1 .. R1 + 3 (elements 4..7).
-__device__ __forceinline__ bfx8 tr_pair(const void* p0, const void* p1) {
-  const sx4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sx4*)p0);
-  const sx4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sx4*)p1);
-  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
-  return __builtin_bit_cast(bfx8, (u32x4{ua[0], ua[1], ub[0], ub[1]}));
-}
-__device__ __forceinline__ bfx8 ld_bf8(const void* p) { return __builtin_bit_cast(bfx8, *(const u32x4*)p); }
-// Workgroup b of a grid of G runs on XCD b % 8 (round-robin dispatch over the 8 XCDs, each with
-// its own L2).  The logical index returned gives every XCD one contiguous range, so logical
-// neighbours (the column tiles of one head and chunk, which read the same q / k / v / dH rows)
-// share an L2.  A bijection on [0, G).
-__device__ __forceinline__ int xcd_contiguous(int b, int G) {
-  const int x = b & 7, i = b >> 3, per = G >> 3, rem = G & 7;
-  return x * per + (x < rem ? x : rem) + i;
-}
 
 // ------------------------------------------------------ bf16 MFMA stats (2)
 // bw_stats_kernel for bf16 q / k and 64-token chunks on v_mfma_f32_16x16x32_bf16: one
@@ -2047,6 +1998,38 @@ bool bw_shape_ok(int B, int NH, int S, int DQK, int DV, int L) {
 }
 
 }  // namespace
+}  // namespace xl
+
+namespace xl {
+// The two-pass forward's states pass for float32 q/k/v on the matrix cores: bw_scan_kernel's
+// forward mode (float32 operands and accumulation), writing C, n, m entering every chunk and the
+// last states (each may be null).  Returns -1, launching nothing, where the tiles do not fit
+// (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}).
+int chunkwise_states_mfma(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst) {
+  if (A.dtype_qkv != XL_DTYPE_F32 || A.DV % SC_V != 0 || !(A.DQK == 64 || A.DQK == 128 || A.DQK == 256) ||
+      !(A.L == 16 || A.L == 32 || A.L == 64))
+    return -1;
+  auto go = [&](auto tg, auto lc) {
+    using TG = decltype(tg);
+    constexpr int L = decltype(lc)::value;
+    return launch_scan<float, TG, L, false>(A.DQK, (const float*)A.k, (const float*)A.v, (const TG*)A.i,
+                                            (const TG*)A.f, A.c0, A.n0, A.m0, nullptr, nullptr, Cst, nst, mst,
+                                            A.c_last, A.n_last, A.m_last, nullptr, A.B * A.NH, A.S / L, A.DV,
+                                            A.qk_scale, (hipStream_t)A.stream);
+  };
+  auto by_l = [&](auto tg) {
+    switch (A.L) {
+      case 16: return go(tg, std::integral_constant<int, 16>{});
+      case 32: return go(tg, std::integral_constant<int, 32>{});
+      default: return go(tg, std::integral_constant<int, 64>{});
+    }
+  };
+  switch (A.dtype_gates) {
+    case XL_DTYPE_F32: return by_l(float{});
+    case XL_DTYPE_BF16: return by_l(bf16_t{});
+    default: return by_l(f16_t{});
+  }
+}
 }  // namespace xl
 
 extern "C" size_t xl_mlstm_chunkwise_bwd_workspace_size(int B, int NH, int S, int DQK, int DV, int L) {

@@ -12,6 +12,9 @@
 // m_in [BNH][NC] — the reference's C_states/n_states/m_states without the
 // final entry (fw.py:337-339), which goes to c_last/n_last/m_last.
 #include "chunkwise.h"
+#include "mfma_bf16.h"
+
+#include <type_traits>
 
 namespace xl {
 
@@ -288,6 +291,194 @@ __global__ __launch_bounds__(CW_THREADS) void chunk_output_kernel(
   }
 }
 
+// ------------------------------- output pass, float32 on the bf16 matrix cores
+// chunk_output_kernel for float32 q/k/v, 64-token chunks and whole 64-wide tiles, on
+// v_mfma_f32_16x16x32_bf16 in the three-product form: every float32 operand x is split into
+// hi = bf16(x), lo = bf16(x - hi), and a product a b is taken as a_hi b_hi + a_hi b_lo + a_lo b_hi
+// (the a_lo b_lo term and the splits leave about 2^-16 of |a b|), accumulated in float32.  One
+// workgroup of 4 waves per (head, chunk, 64 columns of DV); wave w owns the tokens
+// i in [16 w, 16 w + 16).  Over DQK in blocks of 64, 32 d per MFMA, lane (g, r) at
+// d = 8 g .. 8 g + 7 of the step, holding its Q row 16 w + r split in registers:
+//   S^T[j][i] += K[j][d] Q[i][d]   (A = K rows hi / lo from LDS, B = Q)
+//   Hc[i][v]  += Q[i][d] C[d][v]   (A = Q, B = the C block hi / lo by transposed reads)
+//   q.n       += n[d] Q[i][d]      (A rows 0, 1 = n hi, lo, so D[0][i] + D[1][i] = q . n)
+// then M[i][j] = S s exp(b_i - b_j + i_j - m_i) on j <= i into LDS as hi / lo rows, the divisor
+// max(|qbar q.n + sum_j M_ij|, exp(-m_i)) + eps, and H = (qbar Hc + M V) / divisor (A = M rows,
+// B = V by transposed reads) (fw.py:193-245).
+constexpr int OX_P = 80;  // bf16 per staged 64-wide row (160 bytes)
+
+template <typename TG, int NRT>
+__global__ __launch_bounds__(256) void chunk_output_x3_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const TG* __restrict__ ig, const TG* __restrict__ fg, const float* __restrict__ Cst,
+    const float* __restrict__ nst, const float* __restrict__ mst, float* __restrict__ h, int NC, int DV, int nvt,
+    float qk_scale, float eps) {
+  using namespace xl::mfma;
+  constexpr int L = 64, DQK = 64 * NRT;
+  // K block [t][d], then M rows [i][j]; the C block [d][v], then V [j][v]; bf16 hi / lo each
+  __shared__ __attribute__((aligned(16))) uint32_t sAh[L * OX_P / 2], sAl[L * OX_P / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t sBh[L * OX_P / 2], sBl[L * OX_P / 2];
+  __shared__ float sn[64], sb[L], si[L], smc[L], sqb[L], sden[L];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+  const int kk = r >> 2, ka = r & 3;  // transposed reads: row r / 4 of a 4-row block, columns 4 (r % 4)
+  const int per_bh = NC * nvt;
+  const int blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int bh = blk / per_bh, rem = blk - bh * per_bh;
+  const int kc = rem / nvt, v0 = (rem - kc * nvt) * 64;
+  const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
+  const float* cblk = Cst + sidx * DQK * DV + v0;  // C entering the chunk, columns v0 ..
+  // one DQK block in registers: this lane's Q row pieces (d = 32 ks + 8 g + 4 h), K rows and C
+  // rows (row p / 16, 4 values at 4 (p % 16)), n; then the V chunk
+  f32x4 pq[4], pk[4], pc[4], pv[4];
+  float pn = 0.f;
+  auto fetch = [&](int db) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      pq[u] = *reinterpret_cast<const f32x4*>(q + (row0 + 16 * w + r) * DQK + db + 32 * (u >> 1) + 8 * g + 4 * (u & 1));
+      const int p = u * 256 + tid;
+      pk[u] = *reinterpret_cast<const f32x4*>(k + (row0 + (p >> 4)) * DQK + db + (p & 15) * 4);
+      pc[u] = *reinterpret_cast<const f32x4*>(cblk + (size_t)(db + (p >> 4)) * DV + (p & 15) * 4);
+    }
+    if (tid < 64) pn = nst[sidx * DQK + db + tid];
+  };
+  auto fetch_v = [&]() {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = u * 256 + tid;
+      pv[u] = *reinterpret_cast<const f32x4*>(v + (row0 + (p >> 4)) * DV + v0 + (p & 15) * 4);
+    }
+  };
+  // 4 floats of row p / 16, columns 4 (p % 16), as bf16 hi / lo into a pair of staged tiles
+  auto stage4 = [&](uint32_t* dh, uint32_t* dl, int p, f32x4 x) {
+    const int o = ((p >> 4) * OX_P + (p & 15) * 4) >> 1;
+    const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
+    *reinterpret_cast<u32x2*>(dh + o) = u32x2{h0, h1};
+    *reinterpret_cast<u32x2*>(dl + o) = u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
+  };
+  fetch(0);
+  chunk_gate_prefix<TG, L>(ig, fg, row0, sb, si);
+  if (tid < L) {  // fw.py:204-217, 230
+    const float mprev = mst[sidx];
+    float mi = -INFINITY;
+    for (int j = 0; j <= tid; ++j) mi = fmaxf(mi, sb[tid] - sb[j] + si[j]);
+    const float mb = sb[tid] + mprev;
+    const float mc = fmaxf(mb, mi);
+    smc[tid] = mc;
+    sqb[tid] = expf(mb - mc) * qk_scale;
+  }
+  f32x4 accS[4], accH[4], accN = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    accS[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accH[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const u32x4 z4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int db = 0; db < DQK; db += 64) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      stage4(sAh, sAl, u * 256 + tid, pk[u]);
+      stage4(sBh, sBl, u * 256 + tid, pc[u]);
+    }
+    if (tid < 64) sn[tid] = pn;
+    bfx8 qh[2], ql[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float x[8] = {pq[2 * ks][0], pq[2 * ks][1], pq[2 * ks][2], pq[2 * ks][3],
+                          pq[2 * ks + 1][0], pq[2 * ks + 1][1], pq[2 * ks + 1][2], pq[2 * ks + 1][3]};
+      u32x4 hh, ll;
+      split_bf(x, hh, ll);
+      qh[ks] = __builtin_bit_cast(bfx8, hh);
+      ql[ks] = __builtin_bit_cast(bfx8, ll);
+    }
+    __syncthreads();
+    if (db + 64 < DQK) fetch(db + 64);
+    else fetch_v();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = 32 * ks + 8 * g;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const int o = ((16 * jt + r) * OX_P + c) >> 1;
+        const bfx8 kh = ld_bf8(sAh + o), kl = ld_bf8(sAl + o);
+        accS[jt] = mfma_bf(kh, qh[ks], accS[jt]);
+        accS[jt] = mfma_bf(kh, ql[ks], accS[jt]);
+        accS[jt] = mfma_bf(kl, qh[ks], accS[jt]);
+      }
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int o1 = ((c + kk) * OX_P + 16 * ct + 4 * ka) >> 1, o2 = o1 + 2 * OX_P;
+        const bfx8 ch = tr_pair(sBh + o1, sBh + o2), cl = tr_pair(sBl + o1, sBl + o2);
+        accH[ct] = mfma_bf(qh[ks], ch, accH[ct]);
+        accH[ct] = mfma_bf(qh[ks], cl, accH[ct]);
+        accH[ct] = mfma_bf(ql[ks], ch, accH[ct]);
+      }
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = sn[c + e];
+      u32x4 nh, nl;
+      split_bf(x, nh, nl);
+      const bfx8 an = __builtin_bit_cast(bfx8, r == 0 ? nh : (r == 1 ? nl : z4));
+      accN = mfma_bf(an, qh[ks], accN);
+      accN = mfma_bf(an, ql[ks], accN);
+    }
+    __syncthreads();  // the blocks are read; the next staging may overwrite them
+  }
+  // lane (g, r), element e of tile jt: S[i = 16 w + r][j = 16 jt + 4 g + e]
+  const int i = 16 * w + r;
+  float rs = 0.f;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    float mm[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 16 * jt + 4 * g + e;
+      mm[e] = (j <= i) ? accS[jt][e] * qk_scale * expf(sb[i] - sb[j] + si[j] - smc[i]) : 0.f;  // fw.py:219-227
+      rs += mm[e];
+    }
+    const uint32_t h0 = pk_bf(mm[0], mm[1]), h1 = pk_bf(mm[2], mm[3]);
+    const int o = (i * OX_P + 16 * jt + 4 * g) >> 1;
+    *reinterpret_cast<u32x2*>(sAh + o) = u32x2{h0, h1};
+    *reinterpret_cast<u32x2*>(sAl + o) =
+        u32x2{pk_bf(mm[0] - bf_l(h0), mm[1] - bf_h(h0)), pk_bf(mm[2] - bf_l(h1), mm[3] - bf_h(h1))};
+  }
+  rs += __shfl_xor(rs, 16, 64);
+  rs += __shfl_xor(rs, 32, 64);
+  if (g == 0) {  // den = qbar (q . n) + sum_j M_ij; divisor max(|den|, exp(-m)) + eps (fw.py:237-245)
+    const float den = sqb[i] * (accN[0] + accN[1]) + rs;
+    sden[i] = fmaxf(fabsf(den), expf(-smc[i])) + eps;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) stage4(sBh, sBl, u * 256 + tid, pv[u]);
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) accH[ct][e] *= sqb[16 * w + 4 * g + e];
+  __syncthreads();
+  // H += M V (fw.py:233-235)
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c = 32 * ks + 8 * g;
+    const int om = (i * OX_P + c) >> 1;
+    const bfx8 mh = ld_bf8(sAh + om), ml = ld_bf8(sAl + om);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int o1 = ((c + kk) * OX_P + 16 * ct + 4 * ka) >> 1, o2 = o1 + 2 * OX_P;
+      const bfx8 vh = tr_pair(sBh + o1, sBh + o2), vl = tr_pair(sBl + o1, sBl + o2);
+      accH[ct] = mfma_bf(mh, vh, accH[ct]);
+      accH[ct] = mfma_bf(mh, vl, accH[ct]);
+      accH[ct] = mfma_bf(ml, vh, accH[ct]);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int it = 16 * w + 4 * g + e;
+      h[(row0 + it) * DV + v0 + 16 * ct + r] = accH[ct][e] / sden[it];
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 template <typename TQ, typename TG, int L>
 static int two_pass_t(const ChunkwiseArgs& A) {
@@ -301,6 +492,22 @@ static int two_pass_t(const ChunkwiseArgs& A) {
   float* mst = nst + (size_t)BNH * NC * A.DQK;
   hipStream_t s = (hipStream_t)A.stream;
 
+  // float32 q/k/v, 64-token chunks, whole 64-wide tiles: both passes on the matrix cores
+  if constexpr (std::is_same<TQ, float>::value && L == 64) {
+    const int rc = chunkwise_states_mfma(A, Cst, nst, mst);
+    if (rc > 0) return rc;
+    if (rc == 0) {
+      const dim3 grid((unsigned)(BNH * NC * nvt));
+      const float *q = (const float*)A.q, *k = (const float*)A.k, *v = (const float*)A.v;
+      const TG *ig = (const TG*)A.i, *fg = (const TG*)A.f;
+      switch (A.DQK) {
+        case 64: hipLaunchKernelGGL((chunk_output_x3_kernel<TG, 1>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (float*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
+        case 128: hipLaunchKernelGGL((chunk_output_x3_kernel<TG, 2>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (float*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
+        default: hipLaunchKernelGGL((chunk_output_x3_kernel<TG, 4>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (float*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
+      }
+      return check_launch("xl_mlstm_chunkwise_fwd(output pass)");
+    }
+  }
   hipLaunchKernelGGL((chunk_states_kernel<TQ, TG, L>), dim3((unsigned)(BNH * ndt * nvt)), dim3(CW_THREADS), 0, s,
                      (const TQ*)A.k, (const TQ*)A.v, (const TG*)A.i, (const TG*)A.f, A.c0, A.n0, A.m0, Cst, nst, mst,
                      A.c_last, A.n_last, A.m_last, NC, A.DQK, A.DV, ndt, nvt);
