@@ -240,8 +240,8 @@ def test_backend_any_length_bf16(gpu_case, S):
 
 
 def test_auto_fallback_warns_once(gpu_case):
-    """algo="auto" with float16 q/k/v runs the float32 two-pass kernels and says so once (a
-    RuntimeWarning naming the reason), still within the parity bar."""
+    """algo="auto" with float16 q/k/v runs the two-pass kernels and says so once (a RuntimeWarning
+    naming the reason), still within the parity bar."""
     import warnings
 
     import xlstm_hip

@@ -51,9 +51,9 @@ int chunkwise_two_pass(const ChunkwiseArgs& a);
 // nst [BNH][NC][DQK], mst [BNH][NC], the state after the last chunk into c_fin, n_fin, m_fin.
 int chunkwise_states_pass(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst, float* c_fin, float* n_fin,
                           float* m_fin);
-// The states pass for float32 q/k/v on the matrix cores (float32 operands and accumulation), the
-// last states into a.c_last / n_last / m_last (each may be null); -1, launching nothing, where
-// its tiles do not fit (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}).
+// The states pass on the matrix cores (float32 / f16 q/k/v on float32 MFMA, bf16 on bf16 MFMA),
+// the last states into a.c_last / n_last / m_last (each may be null); -1, launching nothing,
+// where its tiles do not fit (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}).
 int chunkwise_states_mfma(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst);
 
 // Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a

@@ -1,5 +1,5 @@
 // C-ABI entry point of the chunkwise mLSTM forward: validation and the choice
-// between the fused bf16-MFMA kernel and the two-pass float32 kernels.
+// between the fused bf16-MFMA kernel and the two-pass kernels.
 #include "chunkwise.h"
 
 namespace xl {

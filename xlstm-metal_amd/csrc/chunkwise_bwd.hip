@@ -1132,10 +1132,10 @@ __global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
     }
     __syncthreads();
   }
-  if (!REV) {
-    store_state(sfin + (size_t)bh * DQKf * DV);
-    if (owns_n) store_n(nfin + (size_t)bh * DQKf);
-    if (vt == 0 && rs == 0 && tid == 0) mfin[bh] = m;
+  if (!REV) {  // the final state (the forward's last states may not be asked for)
+    if (sfin) store_state(sfin + (size_t)bh * DQKf * DV);
+    if (owns_n && nfin) store_n(nfin + (size_t)bh * DQKf);
+    if (vt == 0 && rs == 0 && tid == 0 && mfin) mfin[bh] = m;
   } else {
     store_state(Sst + (size_t)bh * nslots * DQKf * DV);
     if (s_init) store_state(s_init + (size_t)bh * DQKf * DV);
@@ -2001,33 +2001,41 @@ bool bw_shape_ok(int B, int NH, int S, int DQK, int DV, int L) {
 }  // namespace xl
 
 namespace xl {
-// The two-pass forward's states pass for float32 q/k/v on the matrix cores: bw_scan_kernel's
-// forward mode (float32 operands and accumulation), writing C, n, m entering every chunk and the
-// last states (each may be null).  Returns -1, launching nothing, where the tiles do not fit
-// (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}).
+// The two-pass forward's states pass on the matrix cores: the backward's states scan in forward
+// mode (float32 and f16 q/k/v on float32 MFMA; bf16 on bf16 MFMA with the coefficients as hi /
+// lo pairs), writing C, n, m entering every chunk and the last states (each may be null).
+// Returns -1, launching nothing, where the tiles do not fit (DV % 64, DQK not in {64, 128, 256},
+// L not in {16, 32, 64}).
 int chunkwise_states_mfma(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst) {
-  if (A.dtype_qkv != XL_DTYPE_F32 || A.DV % SC_V != 0 || !(A.DQK == 64 || A.DQK == 128 || A.DQK == 256) ||
-      !(A.L == 16 || A.L == 32 || A.L == 64))
+  if (A.DV % SC_V != 0 || !(A.DQK == 64 || A.DQK == 128 || A.DQK == 256) || !(A.L == 16 || A.L == 32 || A.L == 64))
     return -1;
-  auto go = [&](auto tg, auto lc) {
+  auto go = [&](auto tq, auto tg, auto lc) {
+    using TQ = decltype(tq);
     using TG = decltype(tg);
     constexpr int L = decltype(lc)::value;
-    return launch_scan<float, TG, L, false>(A.DQK, (const float*)A.k, (const float*)A.v, (const TG*)A.i,
-                                            (const TG*)A.f, A.c0, A.n0, A.m0, nullptr, nullptr, Cst, nst, mst,
-                                            A.c_last, A.n_last, A.m_last, nullptr, A.B * A.NH, A.S / L, A.DV,
-                                            A.qk_scale, (hipStream_t)A.stream);
+    return launch_scan<TQ, TG, L, false>(A.DQK, (const TQ*)A.k, (const TQ*)A.v, (const TG*)A.i, (const TG*)A.f,
+                                         A.c0, A.n0, A.m0, nullptr, nullptr, Cst, nst, mst, A.c_last, A.n_last,
+                                         A.m_last, nullptr, A.B * A.NH, A.S / L, A.DV, A.qk_scale,
+                                         (hipStream_t)A.stream);
   };
-  auto by_l = [&](auto tg) {
+  auto by_l = [&](auto tq, auto tg) {
     switch (A.L) {
-      case 16: return go(tg, std::integral_constant<int, 16>{});
-      case 32: return go(tg, std::integral_constant<int, 32>{});
-      default: return go(tg, std::integral_constant<int, 64>{});
+      case 16: return go(tq, tg, std::integral_constant<int, 16>{});
+      case 32: return go(tq, tg, std::integral_constant<int, 32>{});
+      default: return go(tq, tg, std::integral_constant<int, 64>{});
     }
   };
-  switch (A.dtype_gates) {
-    case XL_DTYPE_F32: return by_l(float{});
-    case XL_DTYPE_BF16: return by_l(bf16_t{});
-    default: return by_l(f16_t{});
+  auto by_g = [&](auto tq) {
+    switch (A.dtype_gates) {
+      case XL_DTYPE_F32: return by_l(tq, float{});
+      case XL_DTYPE_BF16: return by_l(tq, bf16_t{});
+      default: return by_l(tq, f16_t{});
+    }
+  };
+  switch (A.dtype_qkv) {
+    case XL_DTYPE_F32: return by_g(float{});
+    case XL_DTYPE_BF16: return by_g(bf16_t{});
+    default: return by_g(f16_t{});
   }
 }
 }  // namespace xl

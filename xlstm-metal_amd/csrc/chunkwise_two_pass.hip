@@ -292,8 +292,8 @@ __global__ __launch_bounds__(CW_THREADS) void chunk_output_kernel(
 }
 
 // ------------------------------- output pass, float32 on the bf16 matrix cores
-// chunk_output_kernel for float32 q/k/v, 64-token chunks and whole 64-wide tiles, on
-// v_mfma_f32_16x16x32_bf16 in the three-product form: every float32 operand x is split into
+// chunk_output_kernel for 64-token chunks and whole 64-wide tiles, on v_mfma_f32_16x16x32_bf16
+// in the three-product form (q/k/v of any dtype, read as float32): every operand x is split into
 // hi = bf16(x), lo = bf16(x - hi), and a product a b is taken as a_hi b_hi + a_hi b_lo + a_lo b_hi
 // (the a_lo b_lo term and the splits leave about 2^-16 of |a b|), accumulated in float32.  One
 // workgroup of 4 waves per (head, chunk, 64 columns of DV); wave w owns the tokens
@@ -307,11 +307,20 @@ __global__ __launch_bounds__(CW_THREADS) void chunk_output_kernel(
 // B = V by transposed reads) (fw.py:193-245).
 constexpr int OX_P = 80;  // bf16 per staged 64-wide row (160 bytes)
 
-template <typename TG, int NRT>
+// 4 consecutive values as float32
+__device__ __forceinline__ mfma::f32x4 ld4f(const float* p) { return *reinterpret_cast<const mfma::f32x4*>(p); }
+template <typename T>
+__device__ __forceinline__ mfma::f32x4 ld4f(const T* p) {
+  const mfma::u32x2 w = *reinterpret_cast<const mfma::u32x2*>(p);
+  const T* e = reinterpret_cast<const T*>(&w);
+  return mfma::f32x4{to_f32(e[0]), to_f32(e[1]), to_f32(e[2]), to_f32(e[3])};
+}
+
+template <typename TQ, typename TG, int NRT>
 __global__ __launch_bounds__(256) void chunk_output_x3_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const TQ* __restrict__ q, const TQ* __restrict__ k, const TQ* __restrict__ v,
     const TG* __restrict__ ig, const TG* __restrict__ fg, const float* __restrict__ Cst,
-    const float* __restrict__ nst, const float* __restrict__ mst, float* __restrict__ h, int NC, int DV, int nvt,
+    const float* __restrict__ nst, const float* __restrict__ mst, TQ* __restrict__ h, int NC, int DV, int nvt,
     float qk_scale, float eps) {
   using namespace xl::mfma;
   constexpr int L = 64, DQK = 64 * NRT;
@@ -334,9 +343,9 @@ __global__ __launch_bounds__(256) void chunk_output_x3_kernel(
   auto fetch = [&](int db) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      pq[u] = *reinterpret_cast<const f32x4*>(q + (row0 + 16 * w + r) * DQK + db + 32 * (u >> 1) + 8 * g + 4 * (u & 1));
+      pq[u] = ld4f(q + (row0 + 16 * w + r) * DQK + db + 32 * (u >> 1) + 8 * g + 4 * (u & 1));
       const int p = u * 256 + tid;
-      pk[u] = *reinterpret_cast<const f32x4*>(k + (row0 + (p >> 4)) * DQK + db + (p & 15) * 4);
+      pk[u] = ld4f(k + (row0 + (p >> 4)) * DQK + db + (p & 15) * 4);
       pc[u] = *reinterpret_cast<const f32x4*>(cblk + (size_t)(db + (p >> 4)) * DV + (p & 15) * 4);
     }
     if (tid < 64) pn = nst[sidx * DQK + db + tid];
@@ -345,7 +354,7 @@ __global__ __launch_bounds__(256) void chunk_output_x3_kernel(
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int p = u * 256 + tid;
-      pv[u] = *reinterpret_cast<const f32x4*>(v + (row0 + (p >> 4)) * DV + v0 + (p & 15) * 4);
+      pv[u] = ld4f(v + (row0 + (p >> 4)) * DV + v0 + (p & 15) * 4);
     }
   };
   // 4 floats of row p / 16, columns 4 (p % 16), as bf16 hi / lo into a pair of staged tiles
@@ -475,7 +484,7 @@ __global__ __launch_bounds__(256) void chunk_output_x3_kernel(
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int it = 16 * w + 4 * g + e;
-      h[(row0 + it) * DV + v0 + 16 * ct + r] = accH[ct][e] / sden[it];
+      h[(row0 + it) * DV + v0 + 16 * ct + r] = from_f32<TQ>(accH[ct][e] / sden[it]);
     }
 }
 
@@ -492,18 +501,18 @@ static int two_pass_t(const ChunkwiseArgs& A) {
   float* mst = nst + (size_t)BNH * NC * A.DQK;
   hipStream_t s = (hipStream_t)A.stream;
 
-  // float32 q/k/v, 64-token chunks, whole 64-wide tiles: both passes on the matrix cores
-  if constexpr (std::is_same<TQ, float>::value && L == 64) {
+  // 64-token chunks, whole 64-wide tiles: both passes on the matrix cores
+  if constexpr (L == 64) {
     const int rc = chunkwise_states_mfma(A, Cst, nst, mst);
     if (rc > 0) return rc;
     if (rc == 0) {
       const dim3 grid((unsigned)(BNH * NC * nvt));
-      const float *q = (const float*)A.q, *k = (const float*)A.k, *v = (const float*)A.v;
+      const TQ *q = (const TQ*)A.q, *k = (const TQ*)A.k, *v = (const TQ*)A.v;
       const TG *ig = (const TG*)A.i, *fg = (const TG*)A.f;
       switch (A.DQK) {
-        case 64: hipLaunchKernelGGL((chunk_output_x3_kernel<TG, 1>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (float*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
-        case 128: hipLaunchKernelGGL((chunk_output_x3_kernel<TG, 2>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (float*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
-        default: hipLaunchKernelGGL((chunk_output_x3_kernel<TG, 4>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (float*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
+        case 64: hipLaunchKernelGGL((chunk_output_x3_kernel<TQ, TG, 1>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (TQ*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
+        case 128: hipLaunchKernelGGL((chunk_output_x3_kernel<TQ, TG, 2>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (TQ*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
+        default: hipLaunchKernelGGL((chunk_output_x3_kernel<TQ, TG, 4>), grid, dim3(256), 0, s, q, k, v, ig, fg, Cst, nst, mst, (TQ*)A.h, NC, A.DV, nvt, A.qk_scale, A.eps); break;
       }
       return check_launch("xl_mlstm_chunkwise_fwd(output pass)");
     }

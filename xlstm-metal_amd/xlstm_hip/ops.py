@@ -170,15 +170,15 @@ def chunkwise_algorithm(B, NH, S, DQK, DV, L, dtype, algo="auto") -> str:
 
 
 def _warn_slow_fallback(B, NH, S, DQK, DV, L, dtype) -> None:
-    """One warning per reason when algo="auto" leaves 16-bit inputs on the float32 two-pass kernels
-    (an order of magnitude slower than the fused kernel, with a workspace of every chunk's state)."""
+    """One warning per reason when algo="auto" leaves 16-bit inputs on the two-pass kernels (several
+    times slower than the fused kernel, and holding every chunk's state in a workspace)."""
     lib = _lib.load()
     if int(lib.xl_mlstm_chunkwise_algo(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype], 0)) != 1:
         return
     why = lib.xl_last_error().decode(errors="replace")
     if why not in _fallback_warned:
         _fallback_warned.add(why)
-        warnings.warn(f"xlstm_hip.mlstm_chunkwise: {dtype} inputs run the two-pass float32 kernels ({why}); "
+        warnings.warn(f"xlstm_hip.mlstm_chunkwise: {dtype} inputs run the two-pass kernels ({why}); "
                       "bf16 q/k/v with DQK 128 or 256 and DV a multiple of 64 take the fused kernel",
                       RuntimeWarning, stacklevel=3)
 
