@@ -23,10 +23,12 @@
 // resident) and written by tile 0 only.  In the sequence kernel C' lives in
 // registers for the whole sequence (every C byte crosses HBM once per launch),
 // the gates of 64 steps are formed together (lane = step), the next
-// step's q, k and v are loaded while the current step runs, and the LDS
-// buffers alternate with the step's parity, so a step costs two workgroup
-// barriers.
+// steps' q, k and v are loaded several steps ahead (a step is far shorter than
+// a memory latency), and the LDS buffers alternate with the step's parity, so a
+// step costs two workgroup barriers.
 #include "common.h"
+
+#include <type_traits>
 
 namespace xl {
 
@@ -36,6 +38,15 @@ constexpr int REC_MAX_DQK = 512;   // rows per thread RPT = DQK / 64 <= 8
 constexpr int STEP_THREADS = 1024;
 constexpr int STEP_RG = STEP_THREADS / 16;
 constexpr int STEP_COLS_WIDE = 256;  // decode step tile width when DV allows it
+
+// f(integral_constant<int, I>) for I = I0 .. N - 1, unrolled at compile time
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 
 template <typename TQ, typename TG, int RPT>
 __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
@@ -78,21 +89,25 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
   }
   float m = m_old ? m_old[bh] : 0.f;
 
-  // ---- operands of one step, raw (converted when used, one step after the load)
-  TQ qr[NPT], kr[NPT], vr[4];
-  auto fetch = [&](int t) {
+  // ---- operands of PF steps in flight, raw (converted when used): slot s holds the step t with
+  // t % PF == s, loaded PF steps before it runs (a step lasts well under one memory latency)
+  constexpr int PF = (RPT <= 2 || (RPT <= 4 && sizeof(TQ) == 2)) ? 8 : 4;  // within 128 VGPRs
+  TQ qr[PF][NPT], kr[PF][NPT], vr[PF][4];
+  auto fetch = [&](auto sc, int t) {
+    constexpr int sl = decltype(sc)::value;
+    if (t >= S) return;
     const size_t tok = (size_t)bh * S + t;
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
       const int d = tid + STEP_THREADS * j;
       const int dc = d < DQK ? d : 0;
-      qr[j] = q[tok * DQK + dc];
-      kr[j] = k[tok * DQK + dc];
+      qr[sl][j] = q[tok * DQK + dc];
+      kr[sl][j] = k[tok * DQK + dc];
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vr[j] = v[tok * DV + colc + j];
+    for (int j = 0; j < 4; ++j) vr[sl][j] = v[tok * DV + colc + j];
   };
-  fetch(0);
+  static_for<0, PF>([&](auto sc) { fetch(sc, decltype(sc)::value); });
 
   // ---- gates, 64 steps at a time with lane = step: logsig f and i per lane,
   // the stabiliser m' = max(logsig f + m, i) step by step exactly as the
@@ -101,7 +116,8 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
   // (q s)^T C' to bf16, and a 1-ulp change of m can flip those roundings),
   // then fa, ia and exp(-m') of every step, read back per step with v_readlane
   float gfa = 0.f, gia = 0.f, gem = 0.f;
-  for (int t = 0; t < S; ++t) {
+  auto step = [&](auto sc, int t) {
+    constexpr int sl = decltype(sc)::value;
     const int jg = t & 63;
     if (jg == 0) {  // uniform
       const int tg = t + lane;
@@ -127,12 +143,12 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
     float qv[NPT], kv_[NPT], vv[4];
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
-      qv[j] = to_f32(qr[j]);
-      kv_[j] = to_f32(kr[j]);
+      qv[j] = to_f32(qr[sl][j]);
+      kv_[j] = to_f32(kr[sl][j]);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vv[j] = to_f32(vr[j]);
-    fetch(t + 1 < S ? t + 1 : t);  // the next step's operands, in flight during this step
+    for (int j = 0; j < 4; ++j) vv[j] = to_f32(vr[sl][j]);
+    fetch(sc, t + PF);  // the operands PF steps ahead, into the slot just read
     const float fa = lane_of(gfa, jg), ia = lane_of(gia, jg), emn = lane_of(gem, jg);
 
     // ---- n', q s and k to LDS, and the partial of (q s) . n'
@@ -201,7 +217,12 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_recurrent_kernel(
         h[tok * DV + tile * REC_COLS + c] = from_f32<TQ>(hs / den);
       }
     }
-  }
+  };
+  for (int t0 = 0; t0 < S; t0 += PF)
+    static_for<0, PF>([&](auto sc) {
+      const int t = t0 + decltype(sc)::value;
+      if (t < S) step(sc, t);  // uniform
+    });
 
   // ---- write the state
   if (c_new) {
