@@ -69,6 +69,25 @@ def test_fp32_chunk_sizes(gpu_case, L, with_state):
         assert relerr(got, want) <= FP32_REL, name
 
 
+@pytest.mark.parametrize("shape,with_state,last", [((2, 2, 256, 64, 128), True, True), ((1, 2, 320, 128, 64), True, True),
+                                              ((2, 1, 192, 256, 192), False, True), ((1, 2, 128, 128, 128), True, False)])
+def test_fp32_matrix_core_two_pass(gpu_case, shape, with_state, last):
+    """float32 q/k/v with 64-token chunks and whole 64-wide tiles: the states pass on float32 MFMA and
+    the output pass in the three-product bf16 form, at each DQK the output kernel instantiates, with
+    and without initial states and last states."""
+    import xlstm_hip
+    B, NH, S, DQK, DV = shape
+    x, st = _inputs(B, NH, S, DQK, DV, torch.float32, seed=S + DQK + DV, with_state=with_state)
+    out = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=last, chunk_size=64)
+    hr, (Cr, nr, mr) = _oracle(x, st, 64)
+    if not last:
+        assert relerr(out, hr) <= FP32_REL, "h"
+        return
+    h, (C, n, m) = out
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert relerr(got, want) <= FP32_REL, f"{shape} {name}"
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 64, 32, 16), (2, 2, 128, 80, 72), (1, 2, 192, 256, 512)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("algo", ["auto", "two_pass"])

@@ -87,10 +87,12 @@ def test_lowp_vs_oracle(gpu_case, dtype, B, NH, S, DQK, DV):
 
 
 @pytest.mark.parametrize("B,NH,S,DQK,DV,L", [(1, 2, 512, 256, 512, 64), (1, 1, 192, 128, 192, 64),
-                                             (1, 2, 128, 64, 128, 32), (2, 1, 96, 256, 64, 32)])
+                                             (1, 2, 128, 64, 128, 32), (2, 1, 96, 256, 64, 32),
+                                             (1, 2, 96, 128, 64, 16)])
 def test_bf16_block_counts(gpu_case, B, NH, S, DQK, DV, L):
     """bf16 at config 2's head shape (8 DV blocks in the dQ/dK loop, 4 DQK blocks in dV), an odd
-    number of DV blocks (3), and 32-token chunks (the bf16 chunk scans with one 32-token step)."""
+    number of DV blocks (3), 32-token chunks (the bf16 chunk scans with one 32-token step) and
+    16-token chunks (float32-MFMA scans, FMA tile passes)."""
     _run(B, NH, S, DQK, DV, L, torch.bfloat16, True, True, seed=11 + S + DV)
 
 
