@@ -52,8 +52,9 @@ int chunkwise_two_pass(const ChunkwiseArgs& a);
 int chunkwise_states_pass(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst, float* c_fin, float* n_fin,
                           float* m_fin);
 // The states pass on the matrix cores (float32 / f16 q/k/v on float32 MFMA, bf16 on bf16 MFMA),
-// the last states into a.c_last / n_last / m_last (each may be null); -1, launching nothing,
-// where its tiles do not fit (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}).
+// the last states into a.c_last / n_last / m_last (each may be null); 1, launching nothing,
+// where its tiles do not fit (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}),
+// otherwise XL_OK or a negative XL_ERR_* code.
 int chunkwise_states_mfma(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst);
 
 // Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a

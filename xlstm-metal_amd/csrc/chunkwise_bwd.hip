@@ -2004,11 +2004,11 @@ namespace xl {
 // The two-pass forward's states pass on the matrix cores: the backward's states scan in forward
 // mode (float32 and f16 q/k/v on float32 MFMA; bf16 on bf16 MFMA with the coefficients as hi /
 // lo pairs), writing C, n, m entering every chunk and the last states (each may be null).
-// Returns -1, launching nothing, where the tiles do not fit (DV % 64, DQK not in {64, 128, 256},
-// L not in {16, 32, 64}).
+// Returns 1, launching nothing, where the tiles do not fit (DV % 64, DQK not in {64, 128, 256},
+// L not in {16, 32, 64}); otherwise XL_OK or a negative XL_ERR_* code.
 int chunkwise_states_mfma(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst) {
   if (A.DV % SC_V != 0 || !(A.DQK == 64 || A.DQK == 128 || A.DQK == 256) || !(A.L == 16 || A.L == 32 || A.L == 64))
-    return -1;
+    return 1;
   auto go = [&](auto tq, auto tg, auto lc) {
     using TQ = decltype(tq);
     using TG = decltype(tg);

@@ -504,7 +504,7 @@ static int two_pass_t(const ChunkwiseArgs& A) {
   // 64-token chunks, whole 64-wide tiles: both passes on the matrix cores
   if constexpr (L == 64) {
     const int rc = chunkwise_states_mfma(A, Cst, nst, mst);
-    if (rc > 0) return rc;
+    if (rc < 0) return rc;  // a launch error (1: the tiles do not fit, the FMA kernels below)
     if (rc == 0) {
       const dim3 grid((unsigned)(BNH * NC * nvt));
       const TQ *q = (const TQ*)A.q, *k = (const TQ*)A.k, *v = (const TQ*)A.v;
