@@ -2,6 +2,8 @@
 #pragma once
 #include "common.h"
 
+#include <type_traits>
+
 namespace xl {
 namespace mfma {
 
@@ -54,6 +56,15 @@ __device__ __forceinline__ bfx8 ld_bf8(const void* p) { return __builtin_bit_cas
 __device__ __forceinline__ int xcd_contiguous(int b, int G) {
   const int x = b & 7, i = b >> 3, per = G >> 3, rem = G & 7;
   return x * per + (x < rem ? x : rem) + i;
+}
+
+// f(integral_constant<int, I>) for I = I0 .. N - 1, unrolled at compile time
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 }  // namespace mfma
