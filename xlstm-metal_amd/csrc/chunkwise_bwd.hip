@@ -1862,7 +1862,7 @@ __global__ __launch_bounds__(256, 2) void bw_dqk_bf16_kernel(const bf16_t* __res
 // 16 tiles of 16 x 16, wave w owning row tile R = w / 2 and column tiles 2 (w % 2) + {0, 1}.
 //  * Over the d-tiles dt (64 rows of the state) and, in each, the v-blocks vb (64 columns), the
 //    blocks C[dt, vb], dC[dt, vb] (bf16 hi / lo), dH[:, vb], V[:, vb] (and at vb = 0 Q[:, dt],
-//    K[:, dt]) staged in LDS, their loads issued two blocks ahead:
+//    K[:, dt]) staged in LDS, their loads issued two blocks ahead (C, dC) or one (the rest):
 //      Q~[t][d] += dH[t] . C[d],  K~[t][d] += V[t] . dC[d]      (32 v per MFMA)
 //      dV[t][v] += K[t] . dC[:, v]                               (32 d per MFMA, transposed reads)
 //      dS~^T[j][t] += V[j] . dH[t]                               (first d-tile only)
@@ -1921,8 +1921,9 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 
   // ---- register slots of a block (dt, vb): C, dC (row p / 16, 4 columns at 4 (p % 16)), dH, V
   // (row tid / 8, 8 columns at 8 (tid % 8)) and, for vb = 0, Q and K of the d-tile
+  // C / dC (HBM) two blocks ahead in two slots; dH, V, Q, K (L2 resident) one block ahead
   f32x4 pc[2][2], pd[2][2];
-  u32x4 ph[2], pv[2], pq[2], pk[2];
+  u32x4 ph, pv, pq, pk;
   auto fetch = [&](auto slot, int dt, int vb) {
     constexpr int sl = decltype(slot)::value;
     if (dt >= NDT) return;
@@ -1933,12 +1934,15 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
       pc[sl][u] = *reinterpret_cast<const f32x4*>(cbase + off);
       pd[sl][u] = *reinterpret_cast<const f32x4*>(dcbase + off);
     }
+  };
+  auto fetch_hv = [&](int dt, int vb) {
+    if (dt >= NDT) return;
     const int t = tid >> 3, c = (tid & 7) * 8;
-    ph[sl] = *reinterpret_cast<const u32x4*>(dh + (row0 + t) * DV + 64 * vb + c);
-    pv[sl] = *reinterpret_cast<const u32x4*>(v + (row0 + t) * DV + 64 * vb + c);
+    ph = *reinterpret_cast<const u32x4*>(dh + (row0 + t) * DV + 64 * vb + c);
+    pv = *reinterpret_cast<const u32x4*>(v + (row0 + t) * DV + 64 * vb + c);
     if (vb == 0) {
-      pq[sl] = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + 64 * dt + c);
-      pk[sl] = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + 64 * dt + c);
+      pq = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + 64 * dt + c);
+      pk = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + 64 * dt + c);
     }
   };
   auto stage4 = [&](uint32_t* th, uint32_t* tl, int p, f32x4 x) {
@@ -1961,6 +1965,7 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
     gmn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
   }
   fetch(S0, 0, 0);
+  fetch_hv(0, 0);
   fetch(S1, 0, 1);
   chunk_gate_scan_v<L>(gf, gi, sb, si);
   if (tid < L) {
@@ -1994,16 +1999,18 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
       }
       {
         const int t = tid >> 3, c = (tid & 7) * 8;
-        *reinterpret_cast<u32x4*>(sH + t * BFP + c) = ph[sl];
-        *reinterpret_cast<u32x4*>(sV + t * BFP + c) = pv[sl];
+        *reinterpret_cast<u32x4*>(sH + t * BFP + c) = ph;
+        *reinterpret_cast<u32x4*>(sV + t * BFP + c) = pv;
         if (vb == 0) {
-          *reinterpret_cast<u32x4*>(sQ + t * BFP + c) = pq[sl];
-          *reinterpret_cast<u32x4*>(sK + t * BFP + c) = pk[sl];
+          *reinterpret_cast<u32x4*>(sQ + t * BFP + c) = pq;
+          *reinterpret_cast<u32x4*>(sK + t * BFP + c) = pk;
         }
       }
       __syncthreads();  // the block's tiles
       if (vb + 2 < NVB) fetch(slot, dt, vb + 2);
       else fetch(slot, dt + 1, vb + 2 - NVB);
+      if (vb + 1 < NVB) fetch_hv(dt, vb + 1);
+      else fetch_hv(dt + 1, 0);
       if (vb == 0) {  // S^T[j][t] += Q[j] . K[t] over this d-tile (A = Q rows j, B = K rows t)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
