@@ -583,6 +583,7 @@ BWD_KERNELS = {  # kernel-name key -> short name, for the trace / counter summar
     "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, true>": "dC scan",
     "bw_dv_bf16_kernel": "dV",
     "bw_dqk_bf16_kernel": "dQ, dK",
+    "bw_dvqk_bf16_kernel": "dV, dQ, dK",
     "bw_gates_kernel": "gate gradients",
 }
 
@@ -600,6 +601,9 @@ def bwd_kernel_bytes(B, NH, S, DQK, DV, L, esz=2):
         "dV": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + st + g + 2 * S * 4 + S * DV * esz + S * nvt * 4),
         "dQ, dK": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + 2 * st + g + 2 * S * 4 + 2 * S * DQK * esz
                          + S * ndt * 4),
+        # the fused pass: C and dC once, q k v dH in, dq dk dv out, the dF and dI partials
+        "dV, dQ, dK": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + 2 * st + g + 2 * S * 4
+                             + (2 * S * DQK + S * DV) * esz + S * (ndt + nvt) * 4),
         "gate gradients": BNH * (S * (ndt + nvt) * 4 + S * esz + 2 * S * esz),
     }
 

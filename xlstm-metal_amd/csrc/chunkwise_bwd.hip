@@ -1860,23 +1860,27 @@ __global__ __launch_bounds__(256, 2) void bw_dqk_bf16_kernel(const bf16_t* __res
 // The dV and dQ/dK passes fused per (head, chunk), so C_{k-1} and dC_k stream from HBM once
 // (the separate passes read dC_k twice).  One workgroup of 8 waves; every 64 x 64 product is
 // 16 tiles of 16 x 16, wave w owning row tile R = w / 2 and column tiles 2 (w % 2) + {0, 1}.
-//  * Over the d-tiles dt (64 rows of the state) and, in each, the v-blocks vb (64 columns), the
-//    blocks C[dt, vb], dC[dt, vb] (bf16 hi / lo), dH[:, vb], V[:, vb] (and at vb = 0 Q[:, dt],
-//    K[:, dt]) staged in LDS, their loads issued two blocks ahead (C, dC) or one (the rest):
-//      Q~[t][d] += dH[t] . C[d],  K~[t][d] += V[t] . dC[d]      (32 v per MFMA)
-//      dV[t][v] += K[t] . dC[:, v]                               (32 d per MFMA, transposed reads)
-//      dS~^T[j][t] += V[j] . dH[t]                               (first d-tile only)
-//      S^T[j][t] += Q[j] . K[t]                                   (at vb = 0)
-//    S is complete at the last d-tile's first block: Sbar^T[t][j] = S s Dbar[j][t] / (N_j + eps)
-//    on t <= j (fw.py:204-227, bw.py:156) goes to LDS as bf16 hi / lo rows, and every v-block of
-//    dV is scaled by Abar_t (bw.py:179), gets Sbar^T/N dH
-//    (bw.py:156) and is stored with its v . dV partial of dI.  At the end of each d-tile
-//    (dS = dS~ Dbar s / (N_t + eps) after the first, bw.py:158-159):
+//  * Q and K of the chunk are staged in LDS once; S^T[j][t] = Q[j] . K[t] over DQK, then
+//    Sbar^T[t][j] = S s Dbar[j][t] / (N_j + eps) on t <= j (fw.py:204-227, bw.py:156) into LDS
+//    as bf16 hi / lo rows.
+//  * Over the v-blocks vb (64 columns), dH[:, vb] and V[:, vb] staged once, and in each over the
+//    d-tiles dt (64 rows of the state), the blocks C[dt, vb], dC[dt, vb] staged as bf16 hi / lo
+//    (their loads issued two blocks ahead, dH and V a v-block ahead):
+//      Q~[dt][t][d] += dH[t] . C[d],  K~[dt][t][d] += V[t] . dC[d]    (32 v per MFMA)
+//      dV[t][v] += K[t] . dC[:, v]                                   (32 d per MFMA, transposed reads)
+//    then dV of the v-block is scaled by Abar_t (bw.py:179), gets Sbar^T/N dH (bw.py:156) and is
+//    stored with its v . dV partial of dI, and dS~^T[j][t] += V[j] . dH[t].
+//  * At the end dS = dS~ Dbar s / (N_t + eps) (bw.py:158-159) and, per d-tile,
 //      dQ = Q~ Bbar_t s / (N_t + eps) + dS K,  dK = K~ Abar_t + dS^T Q   (bw.py:161-185)
 //    stored with their q . dQ - k . dK partial of dF.
 // float32 operands enter as bf16 hi / lo pairs, q, k, v, dH once; float32 accumulation.
 constexpr int FV_THREADS = 512;
 constexpr int FV_TILE = 64 * BFP * 2;  // bytes of one staged 64 x 64 bf16 tile
+
+template <int NDT>
+constexpr size_t dvqk_qk_bytes() { return (size_t)64 * (64 * NDT + 16) * 2; }  // one full Q or K tile
+template <int NDT>
+constexpr size_t dvqk_smem() { return 2 * dvqk_qk_bytes<NDT>() + (size_t)8 * FV_TILE + (size_t)(6 + 16) * 64 * sizeof(float); }
 
 template <typename TG, int NDT, int NVB>
 __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
@@ -1887,29 +1891,30 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
     bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, float* __restrict__ dfp,
     float* __restrict__ dip, int NC, float qk_scale) {
   constexpr int L = 64, DQK = 64 * NDT, DV = 64 * NVB;
+  constexpr int QP = DQK + 16;   // bf16 per staged Q / K row (2 DQK + 32 bytes)
   constexpr int NKQ = DQK / 32;  // 32-deep k-steps over DQK
+  constexpr int NQP = L * (DQK / 8) / FV_THREADS;  // 16-byte Q / K pieces per thread
   extern __shared__ __attribute__((aligned(16))) char fv_smem[];
-  // staged tiles, rows of 64 bf16 at pitch BFP
-  bf16_t* sQ = reinterpret_cast<bf16_t*>(fv_smem);                       // Q[:, dt]  [t][d]
-  bf16_t* sK = reinterpret_cast<bf16_t*>(fv_smem + FV_TILE);             // K[:, dt]  [t][d]
-  bf16_t* sH = reinterpret_cast<bf16_t*>(fv_smem + 2 * FV_TILE);         // dH[:, vb] [t][v]
-  bf16_t* sV = reinterpret_cast<bf16_t*>(fv_smem + 3 * FV_TILE);         // V[:, vb]  [t][v]
-  uint32_t* sCh = reinterpret_cast<uint32_t*>(fv_smem + 4 * FV_TILE);    // C[dt, vb] [d][v] hi / lo
-  uint32_t* sCl = reinterpret_cast<uint32_t*>(fv_smem + 5 * FV_TILE);
-  uint32_t* sDh = reinterpret_cast<uint32_t*>(fv_smem + 6 * FV_TILE);    // dC[dt, vb] [d][v] hi / lo
-  uint32_t* sDl = reinterpret_cast<uint32_t*>(fv_smem + 7 * FV_TILE);
-  uint32_t* sBh = reinterpret_cast<uint32_t*>(fv_smem + 8 * FV_TILE);    // Sbar^T / N [t][j] hi / lo
-  uint32_t* sBl = reinterpret_cast<uint32_t*>(fv_smem + 9 * FV_TILE);
-  uint32_t* sSh = reinterpret_cast<uint32_t*>(fv_smem + 10 * FV_TILE);   // dS [t][j] hi / lo
-  uint32_t* sSl = reinterpret_cast<uint32_t*>(fv_smem + 11 * FV_TILE);
-  float* sb = reinterpret_cast<float*>(fv_smem + 12 * FV_TILE);
+  bf16_t* sQ = reinterpret_cast<bf16_t*>(fv_smem);                                   // Q [t][d]
+  bf16_t* sK = reinterpret_cast<bf16_t*>(fv_smem + dvqk_qk_bytes<NDT>());            // K [t][d]
+  char* tiles = fv_smem + 2 * dvqk_qk_bytes<NDT>();
+  bf16_t* sH = reinterpret_cast<bf16_t*>(tiles);                  // dH[:, vb] [t][v]
+  bf16_t* sV = reinterpret_cast<bf16_t*>(tiles + FV_TILE);        // V[:, vb]  [t][v]
+  uint32_t* sCh = reinterpret_cast<uint32_t*>(tiles + 2 * FV_TILE);  // C[dt, vb] [d][v] hi / lo
+  uint32_t* sCl = reinterpret_cast<uint32_t*>(tiles + 3 * FV_TILE);
+  uint32_t* sDh = reinterpret_cast<uint32_t*>(tiles + 4 * FV_TILE);  // dC[dt, vb] [d][v] hi / lo
+  uint32_t* sDl = reinterpret_cast<uint32_t*>(tiles + 5 * FV_TILE);
+  uint32_t* sBh = reinterpret_cast<uint32_t*>(tiles + 6 * FV_TILE);  // Sbar^T / N [t][j] hi / lo
+  uint32_t* sBl = reinterpret_cast<uint32_t*>(tiles + 7 * FV_TILE);
+  uint32_t* sSh = sCh;  // dS [t][j] hi / lo, after the last C block
+  uint32_t* sSl = sCl;
+  float* sb = reinterpret_cast<float*>(tiles + 8 * FV_TILE);
   float* si = sb + L;
   float* smc = si + L;
   float* sinv = smc + L;
   float* sab = sinv + L;
   float* sbb = sab + L;
-  float* s_part = sbb + L;        // [8 waves][L]: dI partials
-  float* s_pf = s_part + 8 * L;   // [8 waves][L]: dF partials
+  float* s_part = sbb + L;  // [8 waves][L] dI partials; then [2][8 waves][L] dF partials, by d-tile parity
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
   const int kk = r >> 2, ka = r & 3;  // transposed reads: row r / 4 of a 4-row block, columns 4 (r % 4)
   const int R = w >> 1, C0 = 2 * (w & 1);
@@ -1919,14 +1924,14 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
   const float* cbase = Cst + sidx * DQK * DV;                                // C_{k-1}
   const float* dcbase = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // dC_k
 
-  // ---- register slots of a block (dt, vb): C, dC (row p / 16, 4 columns at 4 (p % 16)), dH, V
-  // (row tid / 8, 8 columns at 8 (tid % 8)) and, for vb = 0, Q and K of the d-tile
-  // C / dC (HBM) two blocks ahead in two slots; dH, V, Q, K (L2 resident) one block ahead
+  // C / dC block (dt, vb) in two register slots (row p / 16, 4 columns at 4 (p % 16)); dH, V of
+  // a v-block in one (row tid / 8, 8 columns at 8 (tid % 8))
   f32x4 pc[2][2], pd[2][2];
-  u32x4 ph, pv, pq, pk;
-  auto fetch = [&](auto slot, int dt, int vb) {
+  u32x4 ph, pv;
+  auto fetch = [&](auto slot, int st) {  // block st = vb NDT + dt
     constexpr int sl = decltype(slot)::value;
-    if (dt >= NDT) return;
+    if (st >= NDT * NVB) return;
+    const int vb = st / NDT, dt = st - vb * NDT;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int p = u * FV_THREADS + tid;
@@ -1935,15 +1940,11 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
       pd[sl][u] = *reinterpret_cast<const f32x4*>(dcbase + off);
     }
   };
-  auto fetch_hv = [&](int dt, int vb) {
-    if (dt >= NDT) return;
+  auto fetch_hv = [&](int vb) {
+    if (vb >= NVB) return;
     const int t = tid >> 3, c = (tid & 7) * 8;
     ph = *reinterpret_cast<const u32x4*>(dh + (row0 + t) * DV + 64 * vb + c);
     pv = *reinterpret_cast<const u32x4*>(v + (row0 + t) * DV + 64 * vb + c);
-    if (vb == 0) {
-      pq = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + 64 * dt + c);
-      pk = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + 64 * dt + c);
-    }
   };
   auto stage4 = [&](uint32_t* th, uint32_t* tl, int p, f32x4 x) {
     const int o = ((p >> 4) * BFP + (p & 15) * 4) >> 1;
@@ -1954,7 +1955,7 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
   const std::integral_constant<int, 0> S0{};
   const std::integral_constant<int, 1> S1{};
 
-  // ---- every independent load first: gates, stats, blocks (0, 0) and (0, 1)
+  // ---- every independent load first: gates, stats, Q and K of the chunk, blocks 0 and 1, dH / V of vb 0
   float gf = 0.f, gi = 0.f, gvm = 0.f, gvn = 1.f, gmp = 0.f, gmn = 0.f;
   if (tid < L) {
     gf = to_f32(fg[row0 + tid]);
@@ -1964,121 +1965,130 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
     gmp = mst[sidx];
     gmn = (kc + 1 < NC) ? mst[sidx + 1] : mfin[bh];
   }
-  fetch(S0, 0, 0);
-  fetch_hv(0, 0);
-  fetch(S1, 0, 1);
-  chunk_gate_scan_v<L>(gf, gi, sb, si);
-  if (tid < L) {
-    smc[tid] = gvm;
-    sinv[tid] = 1.0f / gvn;
-    sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - gmn);  // Abar (bw.py:168-176)
-    sbb[tid] = expf(sb[tid] + gmp - gvm) * qk_scale;       // Bbar s (bw.py:175, 182)
+  {
+    u32x4 pq[NQP], pk[NQP];
+#pragma unroll
+    for (int u = 0; u < NQP; ++u) {
+      const int p = u * FV_THREADS + tid, t = p / (DQK / 8), c = (p % (DQK / 8)) * 8;
+      pq[u] = *reinterpret_cast<const u32x4*>(q + (row0 + t) * DQK + c);
+      pk[u] = *reinterpret_cast<const u32x4*>(k + (row0 + t) * DQK + c);
+    }
+    fetch(S0, 0);
+    fetch(S1, 1);
+    fetch_hv(0);
+    chunk_gate_scan_v<L>(gf, gi, sb, si);
+    if (tid < L) {
+      smc[tid] = gvm;
+      sinv[tid] = 1.0f / gvn;
+      sab[tid] = expf(sb[L - 1] - sb[tid] + si[tid] - gmn);  // Abar (bw.py:168-176)
+      sbb[tid] = expf(sb[tid] + gmp - gvm) * qk_scale;       // Bbar s (bw.py:175, 182)
+    }
+#pragma unroll
+    for (int u = 0; u < NQP; ++u) {
+      const int p = u * FV_THREADS + tid, t = p / (DQK / 8), c = (p % (DQK / 8)) * 8;
+      *reinterpret_cast<u32x4*>(sQ + t * QP + c) = pq[u];
+      *reinterpret_cast<u32x4*>(sK + t * QP + c) = pk[u];
+    }
   }
-  // (the first block's staging barrier publishes the gate rows and stats)
+  __syncthreads();  // gate rows, stats, Q, K
+  {  // S^T[j][t] (A = Q rows j = 16 R + r, B = K rows t), then Sbar^T / N into LDS rows t
+    f32x4 Sa[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < NKQ; ++ks) {
+      const int c = 32 * ks + 8 * g;
+      const bfx8 aq = ld_bf8(sQ + (16 * R + r) * QP + c);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) Sa[i] = mfma_bf(aq, ld_bf8(sK + (16 * (C0 + i) + r) * QP + c), Sa[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int t = 16 * (C0 + i) + r;
+      float x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = 16 * R + 4 * g + e;
+        x[e] = (t <= j) ? Sa[i][e] * qk_scale * expf(sb[j] - sb[t] + si[t] - smc[j]) * sinv[j] : 0.f;
+      }
+      const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
+      const int o = (t * BFP + 16 * R + 4 * g) >> 1;
+      *reinterpret_cast<u32x2*>(sBh + o) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(sBl + o) =
+          u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
+    }
+  }
 
-  // ---- accumulators: dV[vb][i] (t = 16 R + 4 g + e, v = 64 vb + 16 (C0 + i) + r); Q~, K~ of the
-  // d-tile (t as dV, d = 64 dt + 16 (C0 + i) + r); dS~^T and S^T (j = 16 R + 4 g + e,
+  // ---- accumulators: Q~, K~ of every d-tile (t = 16 R + 4 g + e, d = 64 dt + 16 (C0 + i) + r);
+  // dV of the v-block (t as above, v = 64 vb + 16 (C0 + i) + r); dS~^T (j = 16 R + 4 g + e,
   // t = 16 (C0 + i) + r)
-  f32x4 dVa[NVB][2], Qa[2], Ka[2], dSa[2], Sa[2];
+  f32x4 Qa[NDT][2], Ka[NDT][2], dSa[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
-    for (int b = 0; b < NVB; ++b) dVa[b][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    Qa[i] = Ka[i] = dSa[i] = Sa[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < NDT; ++d) Qa[d][i] = Ka[d][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dSa[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  static_for<0, NDT>([&](auto dtc) {
-    constexpr int dt = decltype(dtc)::value;
-    static_for<0, NVB>([&](auto vbc) {
-      constexpr int vb = decltype(vbc)::value;
-      const auto slot = std::integral_constant<int, vb & 1>{};
-      constexpr int sl = vb & 1;
+  static_for<0, NVB>([&](auto vbc) {
+    constexpr int vb = decltype(vbc)::value;
+    {  // dH and V of this v-block (every wave is past its last read of them)
+      const int t = tid >> 3, c = (tid & 7) * 8;
+      *reinterpret_cast<u32x4*>(sH + t * BFP + c) = ph;
+      *reinterpret_cast<u32x4*>(sV + t * BFP + c) = pv;
+    }
+    fetch_hv(vb + 1);
+    f32x4 dVa[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    static_for<0, NDT>([&](auto dtc) {
+      constexpr int dt = decltype(dtc)::value;
+      constexpr int st = vb * NDT + dt, sl = st & 1;
+      const auto slot = std::integral_constant<int, sl>{};
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         stage4(sCh, sCl, u * FV_THREADS + tid, pc[sl][u]);
         stage4(sDh, sDl, u * FV_THREADS + tid, pd[sl][u]);
       }
-      {
-        const int t = tid >> 3, c = (tid & 7) * 8;
-        *reinterpret_cast<u32x4*>(sH + t * BFP + c) = ph;
-        *reinterpret_cast<u32x4*>(sV + t * BFP + c) = pv;
-        if (vb == 0) {
-          *reinterpret_cast<u32x4*>(sQ + t * BFP + c) = pq;
-          *reinterpret_cast<u32x4*>(sK + t * BFP + c) = pk;
-        }
-      }
-      __syncthreads();  // the block's tiles
-      if (vb + 2 < NVB) fetch(slot, dt, vb + 2);
-      else fetch(slot, dt + 1, vb + 2 - NVB);
-      if (vb + 1 < NVB) fetch_hv(dt, vb + 1);
-      else fetch_hv(dt + 1, 0);
-      if (vb == 0) {  // S^T[j][t] += Q[j] . K[t] over this d-tile (A = Q rows j, B = K rows t)
+      __syncthreads();  // the block's tiles (and, at dt 0, dH / V of the v-block)
+      fetch(slot, st + 2);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int c = 32 * ks + 8 * g;
-          const bfx8 aq = ld_bf8(sQ + (16 * R + r) * BFP + c);
-#pragma unroll
-          for (int i = 0; i < 2; ++i) Sa[i] = mfma_bf(aq, ld_bf8(sK + (16 * (C0 + i) + r) * BFP + c), Sa[i]);
-        }
-        if (dt == NDT - 1) {  // S complete: Sbar^T / N into LDS rows t
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const int t = 16 * (C0 + i) + r;
-            float x[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int j = 16 * R + 4 * g + e;
-              x[e] = (t <= j) ? Sa[i][e] * qk_scale * expf(sb[j] - sb[t] + si[t] - smc[j]) * sinv[j] : 0.f;
-            }
-            const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
-            const int o = (t * BFP + 16 * R + 4 * g) >> 1;
-            *reinterpret_cast<u32x2*>(sBh + o) = u32x2{h0, h1};
-            *reinterpret_cast<u32x2*>(sBl + o) =
-                u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
-          }
-          __syncthreads();  // Sbar^T for the intra terms below
-        }
-      }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {  // 32 v per step
+      for (int ks = 0; ks < 2; ++ks) {  // 32 v per step: Q~ += dH . C, K~ += V . dC
         const int c = 32 * ks + 8 * g;
-        const bfx8 ah = ld_bf8(sH + (16 * R + r) * BFP + c);  // dH rows t
-        const bfx8 av = ld_bf8(sV + (16 * R + r) * BFP + c);  // V rows t (and rows j of dS~^T)
+        const bfx8 ah = ld_bf8(sH + (16 * R + r) * BFP + c);
+        const bfx8 av = ld_bf8(sV + (16 * R + r) * BFP + c);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int o = ((16 * (C0 + i) + r) * BFP + c) >> 1;
-          Qa[i] = mfma_bf(ah, ld_bf8(sCh + o), Qa[i]);
-          Qa[i] = mfma_bf(ah, ld_bf8(sCl + o), Qa[i]);
-          Ka[i] = mfma_bf(av, ld_bf8(sDh + o), Ka[i]);
-          Ka[i] = mfma_bf(av, ld_bf8(sDl + o), Ka[i]);
-          if (dt == 0) dSa[i] = mfma_bf(av, ld_bf8(sH + (16 * (C0 + i) + r) * BFP + c), dSa[i]);
+          Qa[dt][i] = mfma_bf(ah, ld_bf8(sCh + o), Qa[dt][i]);
+          Qa[dt][i] = mfma_bf(ah, ld_bf8(sCl + o), Qa[dt][i]);
+          Ka[dt][i] = mfma_bf(av, ld_bf8(sDh + o), Ka[dt][i]);
+          Ka[dt][i] = mfma_bf(av, ld_bf8(sDl + o), Ka[dt][i]);
         }
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {  // 32 d per step: dV += K . dC
         const int c = 32 * ks + 8 * g;
-        const bfx8 ak = ld_bf8(sK + (16 * R + r) * BFP + c);
+        const bfx8 ak = ld_bf8(sK + (16 * R + r) * QP + 64 * dt + c);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int o1 = ((c + kk) * BFP + 16 * (C0 + i) + 4 * ka) >> 1, o2 = o1 + 2 * BFP;
-          dVa[vb][i] = mfma_bf(ak, tr_pair(sDh + o1, sDh + o2), dVa[vb][i]);
-          dVa[vb][i] = mfma_bf(ak, tr_pair(sDl + o1, sDl + o2), dVa[vb][i]);
+          dVa[i] = mfma_bf(ak, tr_pair(sDh + o1, sDh + o2), dVa[i]);
+          dVa[i] = mfma_bf(ak, tr_pair(sDl + o1, sDl + o2), dVa[i]);
         }
       }
-      if (dt == NDT - 1) {  // this v-block of dV is complete but for Abar and the intra term
+      if (dt == NDT - 1) {  // the v-block of dV: Abar, the intra term, store; dS~ += V . dH
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) dVa[vb][i][e] *= sab[16 * R + 4 * g + e];
+          for (int e = 0; e < 4; ++e) dVa[i][e] *= sab[16 * R + 4 * g + e];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {  // 32 j per step: dV += Sbar^T / N . dH
           const int c = 32 * ks + 8 * g;
           const int ob = ((16 * R + r) * BFP + c) >> 1;
           const bfx8 bh8 = ld_bf8(sBh + ob), bl8 = ld_bf8(sBl + ob);
+          const bfx8 av = ld_bf8(sV + (16 * R + r) * BFP + c);
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const bfx8 hj = tr_pair(sH + (c + kk) * BFP + 16 * (C0 + i) + 4 * ka, sH + (c + kk + 4) * BFP + 16 * (C0 + i) + 4 * ka);
-            dVa[vb][i] = mfma_bf(bh8, hj, dVa[vb][i]);
-            dVa[vb][i] = mfma_bf(bl8, hj, dVa[vb][i]);
+            dVa[i] = mfma_bf(bh8, hj, dVa[i]);
+            dVa[i] = mfma_bf(bl8, hj, dVa[i]);
+            dSa[i] = mfma_bf(av, ld_bf8(sH + (16 * (C0 + i) + r) * BFP + c), dSa[i]);
           }
         }
         // store dV; v . dV partial of dI over this v-block (bw.py:338)
@@ -2089,44 +2099,45 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const int vc = 16 * (C0 + i) + r;
-            dv[(row0 + t) * DV + 64 * vb + vc] = from_f32<bf16_t>(dVa[vb][i][e]);
-            part += to_f32(sV[t * BFP + vc]) * dVa[vb][i][e];
+            dv[(row0 + t) * DV + 64 * vb + vc] = from_f32<bf16_t>(dVa[i][e]);
+            part += to_f32(sV[t * BFP + vc]) * dVa[i][e];
           }
           part = sum16(part);
           if (r == 0) s_part[w * L + t] = part;
         }
       }
-      __syncthreads();  // the block's tiles are read (and the dI partials written)
-      if (dt == NDT - 1 && tid < L) dip[(row0 + tid) * NVB + vb] = s_part[(2 * (tid >> 4)) * L + tid] +
-                                                                  s_part[(2 * (tid >> 4) + 1) * L + tid];
+      __syncthreads();  // the block's tiles are read (and, at the last d-tile, dH / V and the dI partials)
+      if (dt == NDT - 1 && tid < L)
+        dip[(row0 + tid) * NVB + vb] = s_part[(2 * (tid >> 4)) * L + tid] + s_part[(2 * (tid >> 4) + 1) * L + tid];
     });
-    // ---- the end of d-tile dt
-    if (dt == 0) {  // dS = dS~ Dbar s / (N_t + eps) on j <= t into LDS rows t
+  });
+  // ---- dS = dS~ Dbar s / (N_t + eps) on j <= t into LDS rows t (over the C block buffers)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int t = 16 * (C0 + i) + r;
-        float x[4];
+  for (int i = 0; i < 2; ++i) {
+    const int t = 16 * (C0 + i) + r;
+    float x[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = 16 * R + 4 * g + e;
-          x[e] = (j <= t) ? dSa[i][e] * sinv[t] * expf(sb[t] - sb[j] + si[j] - smc[t]) * qk_scale : 0.f;
-        }
-        const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
-        const int o = (t * BFP + 16 * R + 4 * g) >> 1;
-        *reinterpret_cast<u32x2*>(sSh + o) = u32x2{h0, h1};
-        *reinterpret_cast<u32x2*>(sSl + o) =
-            u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
-      }
-      __syncthreads();
+    for (int e = 0; e < 4; ++e) {
+      const int j = 16 * R + 4 * g + e;
+      x[e] = (j <= t) ? dSa[i][e] * sinv[t] * expf(sb[t] - sb[j] + si[j] - smc[t]) * qk_scale : 0.f;
     }
-    // dQ = Q~ Bbar s / N + dS K, dK = K~ Abar + dS^T Q over this d-tile
+    const uint32_t h0 = pk_bf(x[0], x[1]), h1 = pk_bf(x[2], x[3]);
+    const int o = (t * BFP + 16 * R + 4 * g) >> 1;
+    *reinterpret_cast<u32x2*>(sSh + o) = u32x2{h0, h1};
+    *reinterpret_cast<u32x2*>(sSl + o) =
+        u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
+  }
+  __syncthreads();
+  // ---- per d-tile: dQ = Q~ Bbar s / N + dS K, dK = K~ Abar + dS^T Q; store with the dF partials
+  static_for<0, NDT>([&](auto dtc) {
+    constexpr int dt = decltype(dtc)::value;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = 16 * R + 4 * g + e;
-        Qa[i][e] *= sbb[t] * sinv[t];
-        Ka[i][e] *= sab[t];
+        Qa[dt][i][e] *= sbb[t] * sinv[t];
+        Ka[dt][i][e] *= sab[t];
       }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {  // 32 j per step
@@ -2137,39 +2148,37 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
       const bfx8 th8 = tr_pair(sSh + ot1, sSh + ot2), tl8 = tr_pair(sSl + ot1, sSl + ot2);  // dS[j][t]
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int cd = 16 * (C0 + i) + 4 * ka;
-        const bfx8 kj = tr_pair(sK + (c + kk) * BFP + cd, sK + (c + kk + 4) * BFP + cd);  // K[j][d]
-        const bfx8 qj = tr_pair(sQ + (c + kk) * BFP + cd, sQ + (c + kk + 4) * BFP + cd);  // Q[j][d]
-        Qa[i] = mfma_bf(sh8, kj, Qa[i]);
-        Qa[i] = mfma_bf(sl8, kj, Qa[i]);
-        Ka[i] = mfma_bf(th8, qj, Ka[i]);
-        Ka[i] = mfma_bf(tl8, qj, Ka[i]);
+        const int cd = 64 * dt + 16 * (C0 + i) + 4 * ka;
+        const bfx8 kj = tr_pair(sK + (c + kk) * QP + cd, sK + (c + kk + 4) * QP + cd);  // K[j][d]
+        const bfx8 qj = tr_pair(sQ + (c + kk) * QP + cd, sQ + (c + kk + 4) * QP + cd);  // Q[j][d]
+        Qa[dt][i] = mfma_bf(sh8, kj, Qa[dt][i]);
+        Qa[dt][i] = mfma_bf(sl8, kj, Qa[dt][i]);
+        Ka[dt][i] = mfma_bf(th8, qj, Ka[dt][i]);
+        Ka[dt][i] = mfma_bf(tl8, qj, Ka[dt][i]);
       }
     }
-    // store dQ, dK; q . dQ - k . dK partial of dF over this d-tile (bw.py:333)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * R + 4 * g + e;
       float part = 0.f;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int dc = 16 * (C0 + i) + r;
-        const size_t off = (row0 + t) * DQK + 64 * dt + dc;
-        dq[off] = from_f32<bf16_t>(Qa[i][e]);
-        dk[off] = from_f32<bf16_t>(Ka[i][e]);
-        part += to_f32(sQ[t * BFP + dc]) * Qa[i][e] - to_f32(sK[t * BFP + dc]) * Ka[i][e];
+        const int dc = 64 * dt + 16 * (C0 + i) + r;
+        const size_t off = (row0 + t) * DQK + dc;
+        dq[off] = from_f32<bf16_t>(Qa[dt][i][e]);
+        dk[off] = from_f32<bf16_t>(Ka[dt][i][e]);
+        part += to_f32(sQ[t * QP + dc]) * Qa[dt][i][e] - to_f32(sK[t * QP + dc]) * Ka[dt][i][e];
       }
       part = sum16(part);
-      if (r == 0) s_pf[w * L + t] = part;
+      if (r == 0) s_part[(dt & 1) * 8 * L + w * L + t] = part;
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) Qa[i] = Ka[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    __syncthreads();  // the d-tile's Q and K are read; the dF partials are written
-    if (tid < L) dfp[(row0 + tid) * NDT + dt] = s_pf[(2 * (tid >> 4)) * L + tid] + s_pf[(2 * (tid >> 4) + 1) * L + tid];
+    __syncthreads();  // the dF partials of this d-tile
+    if (tid < L)
+      dfp[(row0 + tid) * NDT + dt] =
+          s_part[(dt & 1) * 8 * L + (2 * (tid >> 4)) * L + tid] + s_part[(dt & 1) * 8 * L + (2 * (tid >> 4) + 1) * L + tid];
   });
 }
 
-constexpr size_t dvqk_smem() { return (size_t)12 * FV_TILE + (size_t)(6 + 16) * 64 * sizeof(float); }
 
 template <typename TQ, typename TG, int L, bool REV>
 int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* s0, const float* n0,
@@ -2240,21 +2249,20 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   // dV, dQ and dK in one pass for bf16 with DV 256 or 512 (C and dC streamed once)
   if constexpr (std::is_same<TQ, bf16_t>::value && L == 64) {
     if (scan_mfma && (F.DV == 256 || F.DV == 512)) {
-      auto go = [&](auto kern) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)dvqk_smem());
+      auto go = [&](auto kern, size_t smem) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess)
           return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_bwd: LDS attribute failed: %s", hipGetErrorString(e));
-        hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * NC)), dim3(FV_THREADS), dvqk_smem(), s, q, k, v, dh, ig, fg,
+        hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * NC)), dim3(FV_THREADS), smem, s, q, k, v, dh, ig, fg,
                            Cst, mst, mfin, vm, vn, dC, (bf16_t*)A.dq, (bf16_t*)A.dk, (bf16_t*)A.dv, dfp, dip, NC,
                            F.qk_scale);
         return check_launch("xl_mlstm_chunkwise_bwd(dV, dQ, dK)");
       };
       const bool wide = F.DV == 512;
       switch (F.DQK) {
-        case 64: rc = wide ? go(bw_dvqk_bf16_kernel<TG, 1, 8>) : go(bw_dvqk_bf16_kernel<TG, 1, 4>); break;
-        case 128: rc = wide ? go(bw_dvqk_bf16_kernel<TG, 2, 8>) : go(bw_dvqk_bf16_kernel<TG, 2, 4>); break;
-        default: rc = wide ? go(bw_dvqk_bf16_kernel<TG, 4, 8>) : go(bw_dvqk_bf16_kernel<TG, 4, 4>); break;
+        case 64: rc = wide ? go(bw_dvqk_bf16_kernel<TG, 1, 8>, dvqk_smem<1>()) : go(bw_dvqk_bf16_kernel<TG, 1, 4>, dvqk_smem<1>()); break;
+        case 128: rc = wide ? go(bw_dvqk_bf16_kernel<TG, 2, 8>, dvqk_smem<2>()) : go(bw_dvqk_bf16_kernel<TG, 2, 4>, dvqk_smem<2>()); break;
+        default: rc = wide ? go(bw_dvqk_bf16_kernel<TG, 4, 8>, dvqk_smem<4>()) : go(bw_dvqk_bf16_kernel<TG, 4, 4>, dvqk_smem<4>()); break;
       }
       if (rc) return rc;
       hipLaunchKernelGGL((bw_gates_kernel<TG>), dim3((unsigned)(BNH * ((F.S + GSEG - 1) / GSEG))), dim3(256), 0, s,
