@@ -96,6 +96,15 @@ def test_bf16_block_counts(gpu_case, B, NH, S, DQK, DV, L):
     _run(B, NH, S, DQK, DV, L, torch.bfloat16, True, True, seed=11 + S + DV)
 
 
+@pytest.mark.parametrize("B,NH,S,DQK,DV", [(1, 2, 256, 64, 256), (2, 1, 192, 128, 512), (1, 1, 128, 256, 256),
+                                          (1, 3, 64, 128, 256)])
+@pytest.mark.parametrize("states,last", [(True, True), (False, False)])
+def test_bf16_fused_pass_shapes(gpu_case, B, NH, S, DQK, DV, states, last):
+    """bf16 with DV 256 / 512 (dV, dQ and dK in one pass per (head, chunk)) at every DQK the pass
+    is built for (1, 2 and 4 d-tiles, 4 and 8 v-blocks), an odd chunk count and a single chunk."""
+    _run(B, NH, S, DQK, DV, 64, torch.bfloat16, states, last, seed=23 + S + DQK + DV + states)
+
+
 def test_larger_fp32(gpu_case):
     _run(2, 4, 512, 128, 256, 64, torch.float32, True, True, seed=77)
 
