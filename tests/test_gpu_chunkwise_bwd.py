@@ -105,6 +105,12 @@ def test_bf16_fused_pass_shapes(gpu_case, B, NH, S, DQK, DV, states, last):
     _run(B, NH, S, DQK, DV, 64, torch.bfloat16, states, last, seed=23 + S + DQK + DV + states)
 
 
+def test_bf16_config2_heads_full_length(gpu_case):
+    """Two heads of config 2 over its whole sequence (S 8192, 128 chunks of the state and dC
+    recurrences; DQK 256, DV 512, bf16), with initial and last states."""
+    _run(1, 2, 8192, 256, 512, 64, torch.bfloat16, True, True, seed=8192)
+
+
 def test_larger_fp32(gpu_case):
     _run(2, 4, 512, 128, 256, 64, torch.float32, True, True, seed=77)
 
