@@ -939,6 +939,7 @@ __global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __rest
 // the step (two transposed reads of each operand).  Rows of 2 DQK + 32 and 160 bytes put
 // the 8 consecutive token rows that half a wave reads in distinct banks.
 constexpr int SB_YP = SC_V + 16;  // bf16 per staged hi / lo row (160 bytes)
+constexpr int SST_P = SC_V + 4;  // floats per LDS row of a state store (conflict-free 16-byte writes and reads)
 
 template <typename TG, int L, int NRT, bool REV>
 __global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
@@ -957,6 +958,7 @@ __global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t sYh[L * SB_YP];
   __shared__ __attribute__((aligned(16))) bf16_t sYl[L * SB_YP];
   __shared__ float scoef[L];
+  __shared__ __attribute__((aligned(16))) float sSt[4][16 * NRT * SST_P];  // per wave: its state rows, for the stores
   __shared__ float s_mn, s_g;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
   const int nrs = DQKf / DQK;
@@ -978,12 +980,23 @@ __global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
       acc[rt][ct] = s0 ? *reinterpret_cast<const f32x4*>(s0 + ((size_t)bh * DQKf + row0 + 16 * rt + r) * DV + v0 +
                                                           16 * ct + 4 * g)
                        : f32x4{0.f, 0.f, 0.f, 0.f};
+  // A state store goes through the wave's LDS rows, so that each store instruction writes 4 whole
+  // 256-byte rows (16 lanes per row, 128-byte lines): straight from the accumulators every row
+  // piece would be 64 bytes, and the stores, sent to L2 as 64-byte requests, capped the scans'
+  // write rate at about 2.8 TB/s.  Only this wave touches its rows: no barrier.
+  float* const st_w = sSt[w];
   auto store_state = [&](float* dst) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
-        *reinterpret_cast<f32x4*>(dst + (size_t)(row0 + 16 * rt + r) * DV + v0 + 16 * ct + 4 * g) = acc[rt][ct];
+        *reinterpret_cast<f32x4*>(st_w + (16 * rt + r) * SST_P + 16 * ct + 4 * g) = acc[rt][ct];
+#pragma unroll
+    for (int k = 0; k < 4 * NRT; ++k) {
+      const int row = 4 * k + (lane >> 4), col = 4 * (lane & 15);
+      *reinterpret_cast<f32x4*>(dst + (size_t)(row0 + row) * DV + v0 + col) =
+          *reinterpret_cast<const f32x4*>(st_w + row * SST_P + col);
+    }
   };
   // n (forward, the first column tile's workgroups, which write whole n rows): one more 16 x 16
   // accumulator tile per row tile, whose A operand is columns 64.. of the staged hi rows: coef_t
