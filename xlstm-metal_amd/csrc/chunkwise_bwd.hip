@@ -941,8 +941,10 @@ __global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __rest
 constexpr int SB_YP = SC_V + 16;  // bf16 per staged hi / lo row (160 bytes)
 constexpr int SST_P = SC_V + 4;  // floats per LDS row of a state store (conflict-free 16-byte writes and reads)
 
+// two workgroups per CU (at most 256 registers per lane): the scans are bound by their state
+// stores, and two workgroups keep more of them in flight
 template <typename TG, int L, int NRT, bool REV>
-__global__ __launch_bounds__(256) void bw_scan_bf16_kernel(
+__global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     const bf16_t* __restrict__ X, const bf16_t* __restrict__ Y, const TG* __restrict__ ig,
     const TG* __restrict__ fg, const float* __restrict__ s0, const float* __restrict__ n0,
     const float* __restrict__ m0, const float* __restrict__ vm, const float* __restrict__ vn,
