@@ -2143,7 +2143,11 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
         u32x2{pk_bf(x[0] - bf_l(h0), x[1] - bf_h(h0)), pk_bf(x[2] - bf_l(h1), x[3] - bf_h(h1))};
   }
   __syncthreads();
-  // ---- per d-tile: dQ = Q~ Bbar s / N + dS K, dK = K~ Abar + dS^T Q; store with the dF partials
+  // ---- per d-tile: dQ = Q~ Bbar s / N + dS K, dK = K~ Abar + dS^T Q; store with the dF partials.
+  // Each wave passes its 16 x 32 pieces of dQ and dK through its own part of the (now free) dC
+  // tiles, so that they leave as 16-byte row pieces instead of 2-byte ones
+  bf16_t* const oq = reinterpret_cast<bf16_t*>(sDh);
+  bf16_t* const ok = reinterpret_cast<bf16_t*>(sDl);
   static_for<0, NDT>([&](auto dtc) {
     constexpr int dt = decltype(dtc)::value;
 #pragma unroll
@@ -2179,13 +2183,18 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int dc = 64 * dt + 16 * (C0 + i) + r;
-        const size_t off = (row0 + t) * DQK + dc;
-        dq[off] = from_f32<bf16_t>(Qa[dt][i][e]);
-        dk[off] = from_f32<bf16_t>(Ka[dt][i][e]);
+        oq[t * BFP + 16 * (C0 + i) + r] = from_f32<bf16_t>(Qa[dt][i][e]);
+        ok[t * BFP + 16 * (C0 + i) + r] = from_f32<bf16_t>(Ka[dt][i][e]);
         part += to_f32(sQ[t * QP + dc]) * Qa[dt][i][e] - to_f32(sK[t * QP + dc]) * Ka[dt][i][e];
       }
       part = sum16(part);
       if (r == 0) s_part[(dt & 1) * 8 * L + w * L + t] = part;
+    }
+    {  // the wave's own rows back out of LDS (no other wave touches them): 8 columns per lane
+      const int t = 16 * R + (lane >> 2), c = 16 * C0 + 8 * (lane & 3);
+      const size_t off = (row0 + t) * DQK + 64 * dt + c;
+      *reinterpret_cast<u32x4*>(dq + off) = *reinterpret_cast<const u32x4*>(oq + t * BFP + c);
+      *reinterpret_cast<u32x4*>(dk + off) = *reinterpret_cast<const u32x4*>(ok + t * BFP + c);
     }
     __syncthreads();  // the dF partials of this d-tile
     if (tid < L)
