@@ -1883,8 +1883,10 @@ __global__ __launch_bounds__(256, 2) void bw_dqk_bf16_kernel(const bf16_t* __res
 //    (their loads issued two blocks ahead, dH and V a v-block ahead):
 //      Q~[dt][t][d] += dH[t] . C[d],  K~[dt][t][d] += V[t] . dC[d]    (32 v per MFMA)
 //      dV[t][v] += K[t] . dC[:, v]                                   (32 d per MFMA, transposed reads)
-//    then dV of the v-block is scaled by Abar_t (bw.py:179), gets Sbar^T/N dH (bw.py:156) and is
-//    stored with its v . dV partial of dI, and dS~^T[j][t] += V[j] . dH[t].
+//    with, at the first d-tile, the intra term Sbar^T/N dH of the v-block (bw.py:156) in its own
+//    accumulator and dS~^T[j][t] += V[j] . dH[t]; after the last d-tile dV of the v-block is
+//    Abar_t (bw.py:179) times the inter term plus the intra term, stored with its v . dV partial
+//    of dI.
 //  * At the end dS = dS~ Dbar s / (N_t + eps) (bw.py:158-159) and, per d-tile,
 //      dQ = Q~ Bbar_t s / (N_t + eps) + dS K,  dK = K~ Abar_t + dS^T Q   (bw.py:161-185)
 //    stored with their q . dQ - k . dK partial of dF.
@@ -2051,6 +2053,7 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
     }
     fetch_hv(vb + 1);
     f32x4 dVa[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    f32x4 dVi[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // the intra term of dV
     static_for<0, NDT>([&](auto dtc) {
       constexpr int dt = decltype(dtc)::value;
       constexpr int st = vb * NDT + dt, sl = st & 1;
@@ -2062,6 +2065,23 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
       }
       __syncthreads();  // the block's tiles (and, at dt 0, dH / V of the v-block)
       fetch(slot, st + 2);
+      if (dt == 0) {  // needing only dH and V: dV intra = Sbar^T / N . dH, dS~ += V . dH (32 j per step),
+                      // early, so that the v-block's finish waits on no MFMA chain of its own
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int c = 32 * ks + 8 * g;
+          const int ob = ((16 * R + r) * BFP + c) >> 1;
+          const bfx8 bh8 = ld_bf8(sBh + ob), bl8 = ld_bf8(sBl + ob);
+          const bfx8 av = ld_bf8(sV + (16 * R + r) * BFP + c);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const bfx8 hj = tr_pair(sH + (c + kk) * BFP + 16 * (C0 + i) + 4 * ka, sH + (c + kk + 4) * BFP + 16 * (C0 + i) + 4 * ka);
+            dVi[i] = mfma_bf(bh8, hj, dVi[i]);
+            dVi[i] = mfma_bf(bl8, hj, dVi[i]);
+            dSa[i] = mfma_bf(av, ld_bf8(sH + (16 * (C0 + i) + r) * BFP + c), dSa[i]);
+          }
+        }
+      }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {  // 32 v per step: Q~ += dH . C, K~ += V . dC
         const int c = 32 * ks + 8 * g;
@@ -2087,25 +2107,11 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
           dVa[i] = mfma_bf(ak, tr_pair(sDl + o1, sDl + o2), dVa[i]);
         }
       }
-      if (dt == NDT - 1) {  // the v-block of dV: Abar, the intra term, store; dS~ += V . dH
+      if (dt == NDT - 1) {  // the v-block of dV: Abar times the inter term plus the intra term, store
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) dVa[i][e] *= sab[16 * R + 4 * g + e];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {  // 32 j per step: dV += Sbar^T / N . dH
-          const int c = 32 * ks + 8 * g;
-          const int ob = ((16 * R + r) * BFP + c) >> 1;
-          const bfx8 bh8 = ld_bf8(sBh + ob), bl8 = ld_bf8(sBl + ob);
-          const bfx8 av = ld_bf8(sV + (16 * R + r) * BFP + c);
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const bfx8 hj = tr_pair(sH + (c + kk) * BFP + 16 * (C0 + i) + 4 * ka, sH + (c + kk + 4) * BFP + 16 * (C0 + i) + 4 * ka);
-            dVa[i] = mfma_bf(bh8, hj, dVa[i]);
-            dVa[i] = mfma_bf(bl8, hj, dVa[i]);
-            dSa[i] = mfma_bf(av, ld_bf8(sH + (16 * (C0 + i) + r) * BFP + c), dSa[i]);
-          }
-        }
+          for (int e = 0; e < 4; ++e) dVa[i][e] = dVa[i][e] * sab[16 * R + 4 * g + e] + dVi[i][e];
         // store dV; v . dV partial of dI over this v-block (bw.py:338)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
