@@ -42,10 +42,29 @@ constexpr int BW_THREADS = 256;
 constexpr int BW_T = 64;   // DQK / DV tile
 constexpr int BW_KT = 32;  // contraction tile
 
-__device__ __forceinline__ float sum16(float v) {  // over the 16 lanes of a tx group
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 16);
+// DPP moves inside a row of 16 lanes (VALU only, no LDS traffic)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum16(float v) {  // over the 16 lanes of a tx group (a DPP row)
+  v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+  v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2 (every lane holds its quad's sum)
+  v += dpp_f<0x141>(v);  // row_half_mirror: the other quad of the half row
+  v += dpp_f<0x140>(v);  // row_mirror: the other half row
   return v;
+}
+// the value of lane r ^ M (M = 1, 2, 4, 8) of the same row of 16 lanes
+template <int M>
+__device__ __forceinline__ float xor_lane(float x, int lane) {
+  if constexpr (M == 1) {
+    return dpp_f<0xB1>(x);
+  } else if constexpr (M == 2) {
+    return dpp_f<0x4E>(x);
+  } else {
+    const float up = dpp_f<0x100 + M>(x), down = dpp_f<0x110 + M>(x);  // row_shl:M (lane + M), row_shr:M (lane - M)
+    return (lane & M) ? down : up;
+  }
 }
 
 struct BwLayout {
@@ -2108,24 +2127,43 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
         }
       }
       if (dt == NDT - 1) {  // the v-block of dV: Abar times the inter term plus the intra term, store
+        // x[i][e]: row 16 R + 4 g + e, column 16 (C0 + i) + r.  Three swaps of a lane bit with a
+        // register bit inside each 16 lanes (r bit 0 with e bit 0, r bit 1 with e bit 1, r bit 2
+        // with i) leave lane (g, r) with row 16 R + 4 g + (r & 3) and the 8 consecutive columns
+        // 16 (C0 + ((r >> 2) & 1)) + 8 (r >> 3) + 4 i + e: one 16-byte store, one 16-byte V read
+        float x[2][4];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) dVa[i][e] = dVa[i][e] * sab[16 * R + 4 * g + e] + dVi[i][e];
-        // store dV; v . dV partial of dI over this v-block (bw.py:338)
+          for (int e = 0; e < 4; ++e) x[i][e] = dVa[i][e] * sab[16 * R + 4 * g + e] + dVi[i][e];
+        // swap of lane bit M with a register bit: the lane with the bit clear keeps register bit 0
+        // and takes its partner's register bit 0 into bit 1; the partner the other way round
+        auto swap_bit = [&](auto mc, auto ref) {
+          constexpr int M = decltype(mc)::value;
+          const bool up = (lane & M) != 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = 16 * R + 4 * g + e;
-          float part = 0.f;
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const int vc = 16 * (C0 + i) + r;
-            dv[(row0 + t) * DV + 64 * vb + vc] = from_f32<bf16_t>(dVa[i][e]);
-            part += to_f32(sV[t * BFP + vc]) * dVa[i][e];
+          for (int k = 0; k < 4; ++k) {
+            float& a = ref(k, 0);
+            float& b = ref(k, 1);
+            const float y = xor_lane<M>(up ? a : b, lane);
+            if (up) a = y; else b = y;
           }
-          part = sum16(part);
-          if (r == 0) s_part[w * L + t] = part;
-        }
+        };
+        swap_bit(std::integral_constant<int, 1>{}, [&](int k, int b) -> float& { return x[k >> 1][2 * (k & 1) + b]; });
+        swap_bit(std::integral_constant<int, 2>{}, [&](int k, int b) -> float& { return x[k >> 1][(k & 1) + 2 * b]; });
+        swap_bit(std::integral_constant<int, 4>{}, [&](int k, int b) -> float& { return x[b][k]; });
+        const int t = 16 * R + 4 * g + (r & 3), vc = 16 * (C0 + ((r >> 2) & 1)) + 8 * (r >> 3);
+        *reinterpret_cast<u32x4*>(dv + (row0 + t) * DV + 64 * vb + vc) =
+            u32x4{pk_bf(x[0][0], x[0][1]), pk_bf(x[0][2], x[0][3]), pk_bf(x[1][0], x[1][1]), pk_bf(x[1][2], x[1][3])};
+        // v . dV partial of dI over this v-block (bw.py:338): 8 columns here, the row's other 24 in
+        // the lanes r ^ 4, r ^ 8, r ^ 12
+        const u32x4 vw = *reinterpret_cast<const u32x4*>(sV + t * BFP + vc);
+        float part = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) part += bf_l(vw[k]) * x[k >> 1][2 * (k & 1)] + bf_h(vw[k]) * x[k >> 1][2 * (k & 1) + 1];
+        part += xor_lane<4>(part, lane);
+        part += xor_lane<8>(part, lane);
+        if ((r >> 2) == 0) s_part[w * L + t] = part;
       }
       __syncthreads();  // the block's tiles are read (and, at the last d-tile, dH / V and the dI partials)
       if (dt == NDT - 1 && tid < L)
