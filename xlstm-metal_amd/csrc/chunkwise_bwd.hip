@@ -98,14 +98,18 @@ BwLayout bw_layout(int B, int NH, int S, int DQK, int DV, int L) {
   return o;
 }
 
-// inclusive sum over the 64 lanes of a wave (lane order)
-__device__ __forceinline__ float wave_incl_sum(float x, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
+// inclusive sum over the 64 lanes of a wave (lane order): the DPP row shifts and row broadcasts
+// of wave_sum_dpp leave every lane with its prefix
+__device__ __forceinline__ float wave_incl_sum(float x, int) { return wave_sum_dpp(x); }
+
+// maximum over the 64 lanes of a wave, in every lane: DPP inside each row of 16, then the four
+// row maxima read as scalars
+__device__ __forceinline__ float wave_max_rows(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));   // lane ^ 1
+  v = fmaxf(v, dpp_f<0x4E>(v));   // lane ^ 2
+  v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+  return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
 }
 
 // Per-chunk gate prefix of the backward kernels: sb[t] = sum_{u<=t} logsig f_u, si[t] = i_t
@@ -762,10 +766,10 @@ __global__ __launch_bounds__(256) void bw_scan_kernel(
     const float cvm = pvm, cvn = pvn, cmp = pmp;
     if (w == 0) {
       const float b = wave_incl_sum(lane < L ? logsigmoid(pf) : 0.f, lane);
-      const float gl = __shfl(b, L - 1, 64);
+      const float gl = lane_of(b, L - 1);
       if (!REV) {
         const float a = lane < L ? gl - b + pi : -INFINITY;
-        const float mn = fmaxf(gl + m, wave_max(a));  // fw.py:115
+        const float mn = fmaxf(gl + m, wave_max_rows(a));  // fw.py:115
         if (lane < L) scoef[lane] = expf(a - mn);     // fw.py:121
         if (lane == 0) {
           s_mn = mn;
@@ -940,7 +944,7 @@ __global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __rest
       rs += (j <= i) ? acc[jt][e] * qk_scale * expf(sb[i] - sb[j] + si[j] - smc[i]) : 0.f;
     }
     rs = sum16(rs);
-    const float qn = accN[e] + __shfl_xor(accN[e], 1, 64);
+    const float qn = accN[e] + xor_lane<1>(accN[e], lane);
     if (r == 0) {  // den = qbar (q . n) + sum_j M_ij; divisor max(|den|, exp(-m)) + eps (fw.py:237-245)
       const float den = sqb[i] * qn + rs;
       vm[row0 + i] = smc[i];
@@ -1073,10 +1077,10 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     const float cvm = pvm, cvn = pvn, cmp = pmp;
     if (w == 0) {
       const float b = wave_incl_sum(lane < L ? logsigmoid(pf) : 0.f, lane);
-      const float gl = __shfl(b, L - 1, 64);
+      const float gl = lane_of(b, L - 1);
       if (!REV) {
         const float a = lane < L ? gl - b + pi : -INFINITY;
-        const float mn = fmaxf(gl + m, wave_max(a));  // fw.py:115
+        const float mn = fmaxf(gl + m, wave_max_rows(a));  // fw.py:115
         if (lane < L) scoef[lane] = expf(a - mn);     // fw.py:121
         if (lane == 0) {
           s_mn = mn;
