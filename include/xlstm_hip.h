@@ -51,7 +51,9 @@ enum xl_status {
 enum xl_chunkwise_algo {
   XL_CHUNKWISE_AUTO = 0,     /* fused when supported, else two-pass */
   XL_CHUNKWISE_TWO_PASS = 1, /* states kernel + output kernel, float32 math */
-  XL_CHUNKWISE_FUSED = 2     /* single pass, bf16 MFMA, states in registers */
+  XL_CHUNKWISE_FUSED = 2,    /* single pass, bf16 MFMA, states in registers */
+  XL_CHUNKWISE_PIPELINED = 3 /* XL_CHUNKWISE_FUSED's math and shapes; each chunk's state update
+                                overlaps the previous outputs (two-phase schedule) */
 };
 
 /* ABI version of the loaded library (XL_ABI_VERSION at build time). */
@@ -98,8 +100,8 @@ int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i
  *   h [B,NH,S,DV] (dtype_qkv); c_last, n_last, m_last float32 (all NULL when
  *   the last states are not wanted).
  * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.  With algo =
- * XL_CHUNKWISE_FUSED (bf16 q/k/v, DQK 128 or 256, DV % 64 == 0) any S >= 1 is
- * accepted: the fused kernel runs 64-token chunks and a ragged last chunk
+ * XL_CHUNKWISE_FUSED or XL_CHUNKWISE_PIPELINED (bf16 q/k/v, DQK 128 or 256,
+ * DV % 64 == 0) any S >= 1 is accepted: the fused kernel runs 64-token chunks and a ragged last chunk
  * (the forward is chunk-size invariant, so L only names the reference's
  * chunking there).
  * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned
@@ -110,7 +112,7 @@ size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, 
                                          int dtype_qkv, int algo);
 /*
  * The algorithm xl_mlstm_chunkwise_fwd takes for these arguments:
- * XL_CHUNKWISE_TWO_PASS or XL_CHUNKWISE_FUSED, or a negative XL_ERR_* code for
+ * XL_CHUNKWISE_TWO_PASS, XL_CHUNKWISE_FUSED or XL_CHUNKWISE_PIPELINED, or a negative XL_ERR_* code for
  * arguments it rejects.  When algo = XL_CHUNKWISE_AUTO falls back to the
  * two-pass algorithm, xl_last_error() says why the fused one was not taken.
  * (The reference has no algorithm choice: its torch-native chunkwise is one

@@ -12,7 +12,10 @@
   is chunk-size invariant): chunk sizes 16, 32, 128 against the oracle at that
   chunk size;
 * algo="fused" with any S (ragged last chunk) and the any-S backend's one-call
-  bf16 path against the oracle's any-S driver.
+  bf16 path against the oracle's any-S driver;
+* every single-pass case runs on both single-pass kernels: "fused" and
+  "pipelined" (the two-phase state/output-wave schedule of the same chunk
+  algorithm), each against the oracle.
 """
 
 import pytest
@@ -40,6 +43,10 @@ def _inputs(B, NH, S, DQK, DV, dtype, seed, with_state=False):
 
 def _gpu(ts):
     return [None if t is None else t.to(dev()) for t in ts]
+
+
+SINGLE_PASS = ["fused", "pipelined"]
+_cfg2_oracle = {}
 
 
 def _oracle(x, st, L):
@@ -156,22 +163,24 @@ def test_cfg2_full_size_prefix_and_invariance(gpu_case, L):
                                    (1, 1, 64, 128, 64)])
 @pytest.mark.parametrize("with_state", [False, True])
 @pytest.mark.parametrize("gate_dtype", [torch.bfloat16, torch.float32])
-def test_fused_vs_oracle(gpu_case, shape, with_state, gate_dtype):
+@pytest.mark.parametrize("algo", SINGLE_PASS)
+def test_fused_vs_oracle(gpu_case, shape, with_state, gate_dtype, algo):
     import xlstm_hip
     B, NH, S, DQK, DV = shape
     x, st = _inputs(B, NH, S, DQK, DV, torch.bfloat16, seed=S + DV, with_state=with_state)
     x = x[:3] + tuple(t.to(gate_dtype) for t in x[3:])
     h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=64,
-                                             algo="fused")
+                                             algo=algo)
     hr, (Cr, nr, mr) = _oracle(x, st, 64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         e = lowp_excess(got, want)
-        print(f"fused {shape} state={with_state} {gate_dtype} {name}: max-abs {maxabs(got, want):.3e}, "
+        print(f"{algo} {shape} state={with_state} {gate_dtype} {name}: max-abs {maxabs(got, want):.3e}, "
               f"beyond output rounding {e:.3e}")
         assert e <= LOWP_ABS, name
 
 
-def test_fused_strong_forget_gates(gpu_case):
+@pytest.mark.parametrize("algo", SINGLE_PASS)
+def test_fused_strong_forget_gates(gpu_case, algo):
     """Strongly negative forget gates and large input gates: the stabiliser path."""
     import xlstm_hip
     B, NH, S, DQK, DV = 1, 2, 256, 256, 64
@@ -180,59 +189,64 @@ def test_fused_strong_forget_gates(gpu_case):
     i = (15 * torch.tanh(4 * torch.randn(B, NH, S, generator=g) / 15)).to(torch.bfloat16)
     f = (15 * torch.tanh(6 * torch.randn(B, NH, S, generator=g) / 15)).to(torch.bfloat16)
     x = x[:3] + (i, f)
-    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, algo="fused")
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, algo=algo)
     hr, (Cr, nr, mr) = _oracle(x, (None, None, None), 64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         e = lowp_excess(got, want)
-        print(f"fused strong gates {name}: max-abs {maxabs(got, want):.3e}, beyond output rounding {e:.3e}")
+        print(f"{algo} strong gates {name}: max-abs {maxabs(got, want):.3e}, beyond output rounding {e:.3e}")
         assert e <= LOWP_ABS, name
 
 
 @pytest.mark.parametrize("L", [64, 128])
-def test_cfg2_full_size_vs_oracle(gpu_case, L):
+@pytest.mark.parametrize("algo", SINGLE_PASS)
+def test_cfg2_full_size_vs_oracle(gpu_case, L, algo):
     """cfg2 at full size, fused path, against the oracle at the same chunk size on the whole batch
     (h and final states).  chunk_size=128 runs on the fused kernel's 64-token chunks: the forward is
     chunk-size invariant, so only rounding separates it from the oracle's 128-token chunks."""
     import xlstm_hip
     from xlstm_hip.workloads import CFG2, chunkwise_inputs
     x = chunkwise_inputs(CFG2)
-    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, chunk_size=L, algo="fused")
-    hr, (Cr, nr, mr) = _oracle(x, (None, None, None), L)
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, chunk_size=L, algo=algo)
+    if L not in _cfg2_oracle:
+        _cfg2_oracle[L] = _oracle(x, (None, None, None), L)
+    hr, (Cr, nr, mr) = _cfg2_oracle[L]
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         e = lowp_excess(got, want)
-        print(f"cfg2 full L={L} {name}: max-abs {maxabs(got, want):.3e}, beyond output rounding {e:.3e}, "
+        print(f"cfg2 full {algo} L={L} {name}: max-abs {maxabs(got, want):.3e}, beyond output rounding {e:.3e}, "
               f"rel {relerr(got, want):.3e}")
         assert e <= LOWP_ABS, name
 
 
 @pytest.mark.parametrize("L", [16, 32, 128])
 @pytest.mark.parametrize("with_state", [False, True])
-def test_fused_other_chunk_sizes(gpu_case, L, with_state):
+@pytest.mark.parametrize("algo", SINGLE_PASS)
+def test_fused_other_chunk_sizes(gpu_case, L, with_state, algo):
     """chunk_size 16, 32 and 128 on the fused kernel (S a multiple of 64) against the oracle at that chunk size."""
     import xlstm_hip
     B, NH, S, DQK, DV = 1, 2, 256, 256, 128
     x, st = _inputs(B, NH, S, DQK, DV, torch.bfloat16, seed=L + with_state, with_state=with_state)
     h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=L,
-                                             algo="fused")
+                                             algo=algo)
     hr, (Cr, nr, mr) = _oracle(x, st, L)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
-        assert_parity(got, want, torch.bfloat16, f"fused L={L} state={with_state} {name}")
+        assert_parity(got, want, torch.bfloat16, f"{algo} L={L} state={with_state} {name}")
 
 
 @pytest.mark.parametrize("S", [1, 5, 63, 65, 100, 200, 1000])
 @pytest.mark.parametrize("DQK,DV", [(256, 64), (128, 128)])
 @pytest.mark.parametrize("with_state", [False, True])
-def test_fused_ragged_length(gpu_case, S, DQK, DV, with_state):
+@pytest.mark.parametrize("algo", SINGLE_PASS)
+def test_fused_ragged_length(gpu_case, S, DQK, DV, with_state, algo):
     """algo="fused" takes any S (64-token chunks, ragged last chunk), against the oracle's any-S
     driver (chunkwise pieces of 64/32/16 tokens, then the recurrent tail) on the same inputs."""
     import xlstm_hip
     x, st = _inputs(1, 2, S, DQK, DV, torch.bfloat16, seed=S + DQK, with_state=with_state)
     h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=64,
-                                             algo="fused")
+                                             algo=algo)
     q, k, v, i, f = (t.float() for t in x)
     hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
-        assert_parity(got, want, torch.bfloat16, f"fused ragged S={S} DQK={DQK} DV={DV} state={with_state} {name}")
+        assert_parity(got, want, torch.bfloat16, f"{algo} ragged S={S} DQK={DQK} DV={DV} state={with_state} {name}")
     # auto and two_pass keep the reference's contract
     if S % 64:
         with pytest.raises(AssertionError, match="not divisible"):
@@ -282,18 +296,19 @@ def test_auto_fallback_warns_once(gpu_case):
     (1, 8, 2048, 256, 512, True),    # config 3's heads: 4 segments of 8 chunks
     (1, 1, 300, 256, 64, False),     # 5 chunks: too short to split
 ])
-def test_fused_sequence_split(gpu_case, B, NH, S, DQK, DV, with_state):
+@pytest.mark.parametrize("algo", SINGLE_PASS)
+def test_fused_sequence_split(gpu_case, B, NH, S, DQK, DV, with_state, algo):
     """Few heads: the fused kernel splits the sequence into segments (a states-only pass, the
     segment combine, then all segments at once from their start states).  h and the last C, n, m
     against the oracle's any-S driver, and the workspace grows by the per-segment states."""
     import xlstm_hip
     from xlstm_hip.ops import chunkwise_workspace_bytes
     x, st = _inputs(B, NH, S, DQK, DV, torch.bfloat16, seed=S + NH, with_state=with_state)
-    ws = chunkwise_workspace_bytes(B, NH, S, DQK, DV, 64, torch.bfloat16, algo="fused")
+    ws = chunkwise_workspace_bytes(B, NH, S, DQK, DV, 64, torch.bfloat16, algo=algo)
     prep = ((B * NH * ((S + 63) // 64) * 1280 + 255) // 256) * 256
     assert (ws > prep) == (B * NH * DV // 64 < 256 and (S + 63) // 64 >= 8)
-    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, algo="fused")
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, algo=algo)
     q, k, v, i, f = (t.float() for t in x)
     hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
-        assert_parity(got.cpu(), want, torch.bfloat16, f"split B{B} NH{NH} S{S} DQK{DQK} DV{DV} {name}")
+        assert_parity(got.cpu(), want, torch.bfloat16, f"{algo} split B{B} NH{NH} S{S} DQK{DQK} DV{DV} {name}")

@@ -38,6 +38,7 @@ CXXFLAGS = [
 # over six alternating runs on one box).  (It crashes the compiler on chunkwise_bwd.hip.)
 EXTRA_FLAGS = {
     "chunkwise_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "chunkwise_pipe.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 
 

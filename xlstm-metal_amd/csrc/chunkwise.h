@@ -17,6 +17,7 @@ struct ChunkwiseArgs {
   size_t workspace_bytes;
   void* stream;
   int max_segments;  // fused algorithm: at most this many sequence segments (1: no split)
+  int pipelined;     // fused algorithm: the pipelined schedule (chunkwise_pipe.hip)
 };
 
 // Per-chunk gate prefix: sb[t] = sum_{u<=t} logsig(f_u) in sequential order

@@ -5,6 +5,8 @@
 namespace xl {
 
 static bool valid_L(int L) { return L == 16 || L == 32 || L == 64 || L == 128; }
+// the single-pass algorithms (fused and pipelined schedules) take any S (ragged last chunk)
+static bool single_pass(int algo) { return algo == XL_CHUNKWISE_FUSED || algo == XL_CHUNKWISE_PIPELINED; }
 
 int chunkwise_check_args(const ChunkwiseArgs& a, int algo) {
   const char* who = "xl_mlstm_chunkwise_fwd";
@@ -14,10 +16,10 @@ int chunkwise_check_args(const ChunkwiseArgs& a, int algo) {
   if (!valid_L(a.L)) return set_error(XL_ERR_UNSUPPORTED, "%s: chunk_size=%d not in {16,32,64,128}", who, a.L);
   // the reference's contract; the fused algorithm, asked for explicitly, runs 64-token
   // chunks with a ragged last chunk and accepts any S
-  if (a.S % a.L != 0 && algo != XL_CHUNKWISE_FUSED)
+  if (a.S % a.L != 0 && !single_pass(algo))
     return set_error(XL_ERR_INVALID_ARG, "%s: Sequence length %d is not divisible by chunk size %d.", who, a.S, a.L);
   if (!dtype_ok(a.dtype_qkv) || !dtype_ok(a.dtype_gates)) return set_error(XL_ERR_INVALID_ARG, "%s: unknown dtype", who);
-  if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_FUSED)
+  if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_PIPELINED)
     return set_error(XL_ERR_INVALID_ARG, "%s: unknown algo %d", who, algo);
   if (!a.q || !a.k || !a.v || !a.i || !a.f || !a.h) return set_error(XL_ERR_INVALID_ARG, "%s: null pointer", who);
   if (!((a.c0 && a.n0 && a.m0) || (!a.c0 && !a.n0 && !a.m0)))
@@ -35,9 +37,11 @@ int chunkwise_check_args(const ChunkwiseArgs& a, int algo) {
 static int pick(const ChunkwiseArgs& a, int algo, int* chosen) {
   const char* why = nullptr;
   const bool fused_ok = chunkwise_fused_supported(a, &why);
-  if (algo == XL_CHUNKWISE_FUSED && !fused_ok)
-    return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_fwd: fused algorithm unsupported here: %s", why);
+  if (single_pass(algo) && !fused_ok)
+    return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_fwd: %s algorithm unsupported here: %s",
+                     algo == XL_CHUNKWISE_FUSED ? "fused" : "pipelined", why);
   *chosen = (algo == XL_CHUNKWISE_TWO_PASS) ? XL_CHUNKWISE_TWO_PASS
+            : single_pass(algo)             ? algo
             : fused_ok                      ? XL_CHUNKWISE_FUSED
                                             : XL_CHUNKWISE_TWO_PASS;
   return XL_OK;
@@ -49,13 +53,13 @@ extern "C" size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQ
                                                     int algo) {
   using namespace xl;
   if (B <= 0 || NH <= 0 || S <= 0 || DQK <= 0 || DV <= 0 || !valid_L(L)) return 0;
-  if (S % L && algo != XL_CHUNKWISE_FUSED) return 0;
+  if (S % L && !single_pass(algo)) return 0;
   ChunkwiseArgs a = {};
   a.B = B; a.NH = NH; a.S = S; a.DQK = DQK; a.DV = DV; a.L = L;
   a.dtype_qkv = dtype_qkv; a.dtype_gates = dtype_qkv;
   int chosen = XL_CHUNKWISE_TWO_PASS;
   if (pick(a, algo, &chosen) != XL_OK) return 0;
-  return chosen == XL_CHUNKWISE_FUSED ? chunkwise_fused_workspace(B, NH, S, DQK, DV, kChunkwiseMaxSegments)
+  return single_pass(chosen) ? chunkwise_fused_workspace(B, NH, S, DQK, DV, kChunkwiseMaxSegments)
                                      : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
 }
 
@@ -66,9 +70,9 @@ extern "C" int xl_mlstm_chunkwise_algo(int B, int NH, int S, int DQK, int DV, in
     return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: dimensions must be positive");
   if (!valid_L(L)) return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_algo: chunk_size=%d not in {16,32,64,128}", L);
   if (!dtype_ok(dtype_qkv)) return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: unknown dtype");
-  if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_FUSED)
+  if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_PIPELINED)
     return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: unknown algo %d", algo);
-  if (S % L && algo != XL_CHUNKWISE_FUSED)
+  if (S % L && !single_pass(algo))
     return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_algo: Sequence length %d is not divisible by chunk size %d.",
                      S, L);
   ChunkwiseArgs a = {};
@@ -98,7 +102,8 @@ extern "C" int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* 
   int chosen = XL_CHUNKWISE_TWO_PASS;
   rc = pick(a, algo, &chosen);
   if (rc) return rc;
-  const bool fused = chosen == XL_CHUNKWISE_FUSED;
+  const bool fused = single_pass(chosen);
+  a.pipelined = chosen == XL_CHUNKWISE_PIPELINED;
   const size_t need = fused ? chunkwise_fused_workspace(B, NH, S, DQK, DV, kChunkwiseMaxSegments)
                             : chunkwise_two_pass_workspace(B, NH, S, DQK, DV, L);
   if (!workspace || workspace_bytes < need)

@@ -49,132 +49,13 @@
 //
 // Grid mapping is XCD aware: the DV tiles of one head land on the same XCD so
 // the head's q/k chunks are fetched from HBM once and then hit that XCD's L2.
-#include "chunkwise.h"
+#include "fused_common.h"
 
 #include <type_traits>
 
 namespace xl {
 namespace fused {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-constexpr int L = 64;           // chunk size (= wavefront size: one lane per token)
-constexpr int NSW = 4;          // state waves
-constexpr int NOW = 4;          // output waves
-constexpr int NTHREADS = 64 * (NSW + NOW);
-constexpr int DVT = 64;         // DV columns per workgroup
-constexpr int NVT = DVT / 16;   // 16-wide column tiles of v
-constexpr int NVX = NVT + 1;    // ... plus the ones tile (row sums of M)
-constexpr int VN_PITCH = 160;   // bytes per row of natural V (8 consecutive rows -> distinct 32 B bank groups)
-constexpr int AV_PITCH = 304;   // bytes per row of natural alpha' V: hi (64 bf16) | lo (64 bf16) | pad
-constexpr int HP_PITCH = 68;    // floats per token row of the partial Q C tiles
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr float LN2 = 0.6931471805599453f;
-constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
-constexpr int PREP_STRIDE = 320;  // floats per chunk of gate prep: b, a, cummax(i - b), (i - b) log2e, [g, max a]
-constexpr int kMaxSegmentsDev = 16;  // most sequence segments of one call (few heads)
-constexpr int GROWS = 7;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G], alpha' bf16 hi | lo
-
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-// 32 x 32 x 16: lane l holds A row l % 32 / B column l % 32 at k = 8 (l / 32) .. +7;
-// D column l % 32, rows 8i + 4 (l / 32) + j in element 4i + j
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  f32x2 v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-}
-__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-// The low part x - hi of a pair packed as hi = {bf16(x0), bf16(x1)}, one
-// v_dot2c_f32_bf16 per element: x_e + hi . (-1 in element e) is exact, since
-// x - bf16(x) is representable.  The {-1, 0} operand (bf16 bits 0x0000bf80) is
-// kept in an SGPR: the inline-constant form the compiler picks for it reads
-// as {0, -1} on gfx950.
-struct LoOps {
-  bf16x2 m0, m1;
-};
-__device__ __forceinline__ LoOps lo_ops() {
-  uint32_t k0 = 0x0000bf80u;
-  asm volatile("" : "+s"(k0));
-  return LoOps{__builtin_bit_cast(bf16x2, k0), __builtin_bit_cast(bf16x2, 0xbf800000u)};
-}
-__device__ __forceinline__ uint32_t pack_lo(const LoOps& lo, uint32_t hi, float x0, float x1) {
-  const bf16x2 h = __builtin_bit_cast(bf16x2, hi);
-  return pack_bf16(__builtin_amdgcn_fdot2_f32_bf16(h, lo.m0, x0, false),
-                   __builtin_amdgcn_fdot2_f32_bf16(h, lo.m1, x1, false));
-}
-// bf16 hi + lo split of 8 floats: hi = bf16(x), lo = bf16(x - hi)
-__device__ __forceinline__ void split8(const LoOps& lk, f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
-  const u32x4 h = {pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
-  const u32x4 l = {pack_lo(lk, h[0], a[0], a[1]), pack_lo(lk, h[1], a[2], a[3]), pack_lo(lk, h[2], b[0], b[1]),
-                   pack_lo(lk, h[3], b[2], b[3])};
-  hi = __builtin_bit_cast(bf16x8, h);
-  lo = __builtin_bit_cast(bf16x8, l);
-}
-__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
-// Chunk-relative global access: a raw buffer resource per 64-token chunk
-// (wave-uniform base, num_records = the chunk's valid rows) and a per-thread
-// byte offset that stays the same for every chunk.  Rows past S (a ragged last
-// chunk) read as 0 and their stores are dropped by the buffer range check, so
-// no address needs clamping.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const bf16_t* base, int rows, int row_bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, rows * row_bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-__device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 x) {
-  typedef unsigned int b128 __attribute__((ext_vector_type(4)));
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(b128, x), r, off, 0, 0);
-}
-__device__ __forceinline__ float exp_(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
-// log(sigmoid(x)) = min(x, 0) - log(1 + exp(-|x|)) via the hardware exp2/log2 (abs. error < 1e-7)
-__device__ __forceinline__ float logsig_fast(float x) {
-  return fminf(x, 0.f) - LN2 * __builtin_amdgcn_logf(1.0f + exp2_(-fabsf(x) * LOG2E));
-}
-// two 64-bit transposed LDS reads -> one 8 x bf16 MFMA operand
-__device__ __forceinline__ bf16x8 tr8(const char* p0, const char* p1) {
-  const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
-  const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
-  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
-  const u32x4 r = {ua[0], ua[1], ub[0], ub[1]};
-  return __builtin_bit_cast(bf16x8, r);
-}
-
-// Inclusive wave64 scans with DPP (row shifts, then row broadcasts).
-template <bool MAX>
-__device__ __forceinline__ float wave_scan(float x) {
-  const int iid = __float_as_int(MAX ? -INFINITY : 0.f);
-#define XL_SCAN_STEP(CTRL, ROWMASK)                                                                                 \
-  {                                                                                                                 \
-    const float y = __int_as_float(__builtin_amdgcn_update_dpp(iid, __float_as_int(x), CTRL, ROWMASK, 0xf, false)); \
-    x = MAX ? fmaxf(x, y) : x + y;                                                                                  \
-  }
-  XL_SCAN_STEP(0x111, 0xf)  // row_shr:1
-  XL_SCAN_STEP(0x112, 0xf)  // row_shr:2
-  XL_SCAN_STEP(0x114, 0xf)  // row_shr:4
-  XL_SCAN_STEP(0x118, 0xf)  // row_shr:8
-  XL_SCAN_STEP(0x142, 0xa)  // row_bcast:15 into rows 1, 3
-  XL_SCAN_STEP(0x143, 0xc)  // row_bcast:31 into rows 2, 3
-#undef XL_SCAN_STEP
-  return x;
-}
-
-__device__ __forceinline__ float lane63(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
 
 // Chunk-local gate prep, one wave per (head, chunk), lane = token t
 // (fw.py:308-316 and :98, :204-213 before the running stabiliser enters):
@@ -211,41 +92,8 @@ __global__ __launch_bounds__(256) void gate_prep_kernel(const TG* __restrict__ i
   }
 }
 
-// Column of the 64-wide DV tile held by column n of 16-wide tile vq of the
-// output waves: runs of 4 consecutive columns, and the tile pair (2h, 2h+1)
-// covers columns 32h .. 32h+31 so that a lane of the transposed output holds 8
-// consecutive columns (one 16-byte store).
-__device__ __forceinline__ int vcol_of(int vq, int n) { return 32 * (vq >> 1) + 8 * (n >> 2) + 4 * (vq & 1) + (n & 3); }
 
-template <int DQK>
-struct Smem {
-  static constexpr int KPD = DQK / 32;                   // 32-deep k-steps over DQK
-  static constexpr int KN_PITCH = DQK * 2 + 32;          // bytes per K row (= 32 mod 64, see the header)
-  static constexpr int KN = 0;                           // [64 t][KN_PITCH]: K natural
-  static constexpr int VN = KN + 64 * KN_PITCH;          // [64 t][VN_PITCH]: V natural
-  static constexpr int AV = VN + 64 * VN_PITCH;          // [64 t][AV_PITCH]: alpha' V hi (64 bf16) | lo (64 bf16)
-  static constexpr int HP = AV + 64 * AV_PITCH;          // [4 state waves][64 t][HP_PITCH] float: partial Q C
-  static constexpr int NB = HP + NSW * 64 * HP_PITCH * 4;  // [2 chunks][4 parts][NB_PITCH] bf16: n (hi, lo of both halves)
-  static constexpr int NB_PITCH = DQK + 16;              // bf16 per n part row (= 32 mod 64 bytes)
-  static constexpr int GATES = NB + 2 * 4 * NB_PITCH * 2;     // [2 chunks][GROWS][64] float: gate rows + scalars
-  static constexpr int BYTES = GATES + 2 * GROWS * 64 * 4;
-  static_assert(BYTES <= 160 * 1024, "LDS budget");
-};
 
-// Sequence segments (for few heads: B * NH * DV / 64 workgroups leave CUs idle).
-// The grid covers nseg segments of kc_per_seg chunks per (head, column tile).
-// Segment 0 starts from (c0, n0, m0) (zeros and m = 0 when absent, the
-// reference's zero state); segment s >= 1 starts from the s-1'th entry of
-// (sc, sn, sm) or, when sc is null, from the empty state (C = n = 0, m = -inf,
-// so its end state is the segment's own contribution).  With ec set, every
-// segment writes its end state to entry s of (ec, en, em); otherwise the last
-// segment writes (c_last, n_last, m_last).  STATES_ONLY launches skip q C and
-// the outputs (h is not written).
-struct SegArgs {
-  int nseg, kc_per_seg;
-  const float *sc, *sn, *sm;
-  float *ec, *en, *em;
-};
 
 template <int DQK, bool STATES_ONLY>
 __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
@@ -267,7 +115,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
   const int w = tid >> 6, lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
   const int ws = w & 3;  // index within the state or output group
-  const LoOps lk = lo_ops();
 
   // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
   const int nwg = BNH * nvtile * sg.nseg;
@@ -388,7 +235,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int dt = 0; dt < NTO; ++dt) {
         const f32x4 x = nacc[dt];
         const u32x2 hi = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
-        const u32x2 lo = {pack_lo(lk, hi[0], x[0], x[1]), pack_lo(lk, hi[1], x[2], x[3])};
+        const u32x2 lo = {pack_lo(hi[0], x[0], x[1]), pack_lo(hi[1], x[2], x[3])};
         *reinterpret_cast<u32x2*>(nb + (2 * r16) * SM::NB_PITCH + 16 * dt) = hi;
         *reinterpret_cast<u32x2*>(nb + (2 * r16 + 1) * SM::NB_PITCH + 16 * dt) = lo;
       }
@@ -472,7 +319,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
         for (int c2 = 0; c2 < 4; ++c2) {
           const float x0 = al2[r] * bf_lo(Vst[r][c2]), x1 = al2[r] * bf_hi(Vst[r][c2]);
           hv[c2] = pack_bf16(x0, x1);
-          lv[c2] = pack_lo(lk, hv[c2], x0, x1);
+          lv[c2] = pack_lo(hv[c2], x0, x1);
         }
         *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 2 * vcol) = hv;
         *reinterpret_cast<u32x4*>(av + (vrow + 2 * r) * AV_PITCH + 128 + 2 * vcol) = lv;
@@ -497,7 +344,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           const int vt = qi / QKS, s = qi % QKS;
           const f32x16& a = acc[s >> 1][vt];
           const int e0 = 8 * (s & 1);
-          split8(lk, f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]}, f32x4{a[e0 + 4], a[e0 + 5], a[e0 + 6], a[e0 + 7]},
+          split8(f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]}, f32x4{a[e0 + 4], a[e0 + 5], a[e0 + 6], a[e0 + 7]},
                  o[0], o[1]);
         };
         auto store_p = [&](int vt) {
@@ -683,7 +530,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       for (int pj = 0; pj < 2; ++pj) {
         if (32 * pj > 16 * o + 15) continue;  // all of M is masked for these tokens (compile-time)
         bf16x8 mh, ml;
-        split8(lk, Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
+        split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
 #pragma unroll
         for (int vq = 0; vq < NVX; ++vq) {
           bf16x8 vb;
@@ -886,11 +733,26 @@ static int launch(const ChunkwiseArgs& A) {
   hipLaunchKernelGGL(gate_prep_kernel<TG>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, st, (const TG*)A.i,
                      (const TG*)A.f, prep, total, NC, A.S);
   const size_t smem = Smem<DQK>::BYTES;
-  for (auto kern : {chunkwise_fused_kernel<DQK, false>, chunkwise_fused_kernel<DQK, true>}) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (e != hipSuccess)
-      return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
+  if (!A.pipelined) {
+    for (auto kern : {chunkwise_fused_kernel<DQK, false>, chunkwise_fused_kernel<DQK, true>}) {
+      hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess)
+        return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
+    }
   }
+  // the main kernel: the pipelined schedule (chunkwise_pipe.hip) or the fused one
+  auto main = [&](bool states_only, unsigned nwg, const MainArgs& m) -> int {
+    if (A.pipelined) return pipe_launch(DQK, states_only, nwg, st, m);
+    if (states_only)
+      hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, true>), dim3(nwg), dim3(NTHREADS), smem, st, m.q, m.k, m.v,
+                         m.c0, m.n0, m.m0, m.h, m.c_last, m.n_last, m.m_last, m.prep, m.S, m.NC, m.DV, m.BNH,
+                         m.nvtile, m.qk_scale, m.eps, m.sg);
+    else
+      hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, false>), dim3(nwg), dim3(NTHREADS), smem, st, m.q, m.k, m.v,
+                         m.c0, m.n0, m.m0, m.h, m.c_last, m.n_last, m.m_last, m.prep, m.S, m.NC, m.DV, m.BNH,
+                         m.nvtile, m.qk_scale, m.eps, m.sg);
+    return XL_OK;
+  };
   const bf16_t *q = (const bf16_t*)A.q, *k = (const bf16_t*)A.k, *v = (const bf16_t*)A.v;
   SegArgs sg = {1, NC, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (lay.P > 1) {
@@ -905,18 +767,20 @@ static int launch(const ChunkwiseArgs& A) {
     float* sns = scs + (lay.P - 1) * cst;
     float* sms = sns + (lay.P - 1) * nst;
     SegArgs s1 = {lay.P - 1, lay.kc_per_seg, nullptr, nullptr, nullptr, ec, en, em};
-    hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, true>), dim3((unsigned)(BNH * nvtile * (lay.P - 1))),
-                       dim3(NTHREADS), smem, st, q, k, v, A.c0, A.n0, A.m0, (bf16_t*)nullptr, nullptr, nullptr,
-                       nullptr, prep, A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, s1);
+    const MainArgs m1 = {q, k, v, A.c0, A.n0, A.m0, nullptr, nullptr, nullptr, nullptr, prep,
+                         A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, s1};
+    const int rc = main(true, (unsigned)(BNH * nvtile * (lay.P - 1)), m1);
+    if (rc) return rc;
     const int per4 = (A.DQK * A.DV + A.DQK) / 4;
     hipLaunchKernelGGL(segment_combine_kernel, dim3((unsigned)((per4 + 255) / 256), (unsigned)BNH), dim3(256), 0,
                        st, prep, ec, en, em, scs, sns, sms, lay.P, lay.kc_per_seg, NC, BNH, A.DQK, A.DV);
     sg = SegArgs{lay.P, lay.kc_per_seg, scs, sns, sms, nullptr, nullptr, nullptr};
   }
-  hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, false>), dim3((unsigned)(BNH * nvtile * sg.nseg)), dim3(NTHREADS),
-                     smem, st, q, k, v, A.c0, A.n0, A.m0, (bf16_t*)A.h, A.c_last, A.n_last, A.m_last, prep, A.S, NC,
-                     A.DV, BNH, nvtile, A.qk_scale, A.eps, sg);
-  return check_launch("xl_mlstm_chunkwise_fwd(fused)");
+  const MainArgs m2 = {q, k, v, A.c0, A.n0, A.m0, (bf16_t*)A.h, A.c_last, A.n_last, A.m_last, prep,
+                       A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, sg};
+  const int rc = main(false, (unsigned)(BNH * nvtile * sg.nseg), m2);
+  if (rc) return rc;
+  return check_launch(A.pipelined ? "xl_mlstm_chunkwise_fwd(pipelined)" : "xl_mlstm_chunkwise_fwd(fused)");
 }
 
 template <typename TG>

@@ -1,0 +1,605 @@
+// Pipelined single-pass chunkwise mLSTM forward for bf16 q/k/v on gfx950.
+//
+// Same math, data layout in HBM and work split over the chip as the fused
+// kernel (chunkwise_fused.hip): one workgroup = one (b, h) pair x one 64-column
+// tile of DV, 4 state waves holding C (DQK x 64, float32) in MFMA accumulators,
+// 4 output waves owning 16 output rows each, the chunk math of
+// kernel_development/xlstm/mlstm_block/mlstm_chunkwise/vendored/torch/native/
+// fw.py:98-143 (inter-chunk recurrence) and :193-245 (outputs).  What differs is
+// the schedule of a chunk, which the fused kernel spends mostly in barrier waits
+// (its state waves ran q C, the partial stores and the update back to back
+// before the output waves could finish a single row).  Here each chunk is two
+// phases, one barrier each:
+//
+//   phase A (after the chunk's tiles are staged):
+//     state waves:  partial q C over their rows (bf16 hi + lo of the state,
+//                   two MFMAs) -> LDS; then read their K^T operands of the
+//                   update into registers (8 x 16 bytes per lane)
+//     output waves: S^T = K Q^T (with q.n from a fifth tile), gating, M [V | 1],
+//                   alpha' V as bf16 hi | lo -> LDS, the next chunk's gate rows
+//   phase B (after the partials are complete):
+//     state waves:  renormalise if the chunk asks for it, C += K^T (alpha' V)
+//                   from the captured K^T and the alpha' V tile, and the
+//                   normaliser n += K^T alpha' on the VALU (v_dot2 over the same
+//                   K^T registers, alpha' as bf16 hi + lo) -- the n rows a state
+//                   wave carries are its own C rows; n goes to LDS as bf16
+//                   hi | lo rows for the next chunk's q.n
+//     output waves: add the four partials, normalise and store h; write the
+//                   next chunk's K and V tiles (loaded from HBM a whole chunk
+//                   earlier) into LDS
+//
+// The update no longer sits between a chunk's partials and its outputs, so the
+// output waves' finish overlaps the state waves' update MFMAs, and every LDS
+// tile is single-buffered: K and V of the next chunk are written only in
+// phase B, after the last reads of the current ones (the state waves took
+// their K^T operands in phase A).  The deferred forget rescale (state stored
+// as C e^{-G}, renormalised when G < -30), the ragged last chunk, the
+// sequence segments and the XCD-aware grid are those of the fused kernel.
+#include "fused_common.h"
+
+#include <type_traits>
+
+namespace xl {
+namespace fused {
+namespace pipe {
+
+
+constexpr int NOT = 64 * NOW;  // output-wave threads
+
+// Row of the C tile held by row l32 of 32-row tile dt of state wave rows
+// [dw0, dw0 + DW): the order of the transposed K^T reads (within each 16 rows,
+// row 4a + c holds state row 8 (a & 1) + 4 (a >> 1) + c); the same row as
+// accumulator element e of lane half hh where l32 = 8 (e >> 2) + 4 hh + (e & 3).
+__device__ __forceinline__ int state_row(int dw0, int dt, int l32) {
+  const int x = l32 & 15;
+  return dw0 + 32 * dt + 16 * (l32 >> 4) + 8 * ((x >> 2) & 1) + 4 * (x >> 3) + (x & 3);
+}
+
+template <int DQK, bool STATES_ONLY>
+__global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a) {
+  using SM = Smem<DQK>;
+  constexpr int KPD = SM::KPD;
+  constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
+  constexpr int NKO = DQK / 32;   // K staging: 16-byte pieces per output thread (64 rows x DQK / 256 threads / 8)
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int ws = w & 3;  // index within the state or output group
+  const SegArgs& sg = a.sg;
+  const int S = a.S, NC = a.NC, DV = a.DV, BNH = a.BNH, nvtile = a.nvtile;
+
+  // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
+  const int nwg = BNH * nvtile * sg.nseg;
+  int lin = blockIdx.x;
+  if ((nwg & 7) == 0) lin = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  const int bhs = lin / nvtile;  // segment * BNH + head
+  const int v0 = (lin - bhs * nvtile) * DVT;
+  const int seg = bhs / BNH, bh = bhs - seg * BNH;
+  const int kc0 = seg * sg.kc_per_seg, kc1 = min(NC, kc0 + sg.kc_per_seg);  // this segment's chunks
+  const size_t cst = (size_t)BNH * DQK * DV, nst = (size_t)BNH * DQK;
+  const float* ci = seg == 0 ? a.c0 : (sg.sc ? sg.sc + (seg - 1) * cst : nullptr);
+  const float* ni = seg == 0 ? a.n0 : (sg.sn ? sg.sn + (seg - 1) * nst : nullptr);
+  const float m_init = seg == 0 ? (a.m0 ? a.m0[bh] : 0.f) : (sg.sm ? sg.sm[(seg - 1) * BNH + bh] : -INFINITY);
+  float* ce = sg.ec ? sg.ec + seg * cst : (seg == sg.nseg - 1 ? a.c_last : nullptr);
+  float* ne = sg.ec ? sg.en + seg * nst : a.n_last;
+  float* me = sg.ec ? sg.em + (size_t)seg * BNH : a.m_last;
+
+  char* kn = smem + SM::KN;
+  char* vn = smem + SM::VN;
+  char* av = smem + SM::AV;
+  float* hp = (float*)(smem + SM::HP);
+  bf16_t* nbuf = (bf16_t*)(smem + SM::NB);   // [2][4][NB_PITCH]: n parts entering chunk kc live in buffer kc & 1
+  float* gbuf = (float*)(smem + SM::GATES);  // [2][GROWS][64]: rows of chunk kc live in buffer kc & 1
+
+  const bf16_t* qh = a.q + (size_t)bh * S * DQK;
+  const bf16_t* kh = a.k + (size_t)bh * S * DQK;
+  const bf16_t* vh = a.v + (size_t)bh * S * DV;
+  bf16_t* hh = a.h + (size_t)bh * S * DV;
+  // valid rows of chunk kc (0 past the sequence: a chunk past the end gets a buffer resource
+  // with no records, so its prefetches return zeros without touching memory; they are issued
+  // unconditionally, which keeps the compiler's load counters exact)
+  auto rows_of = [&](int kc) { return __builtin_amdgcn_readfirstlane(max(0, min(L, S - kc * L))); };
+  auto q_rsrc = [&](int kc) { return chunk_rsrc(qh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2); };
+
+  if (w < NSW) {
+    // =====================================================================
+    // state waves: rows [dw0, dw0 + DW) of C and n, stored as C e^{-G}, n e^{-G}
+    // =====================================================================
+    // 32 x 32 accumulator tiles acc[dt][vt]: lane (hh, l32) holds column
+    // 32 vt + l32 and, in element e = 4i + j, state row
+    //   dw0 + 32 dt + 16 (i >> 1) + 8 hh + 4 (i & 1) + j,
+    // so the 8 elements 8s' .. 8s'+7 of a lane are the 8 consecutive rows
+    // 16 s' + 8 hh .. +7 of the tile: a q C k-step of 16 rows is one split of
+    // 8 accumulator values per lane and one 16-byte q load.
+    constexpr int NDT = DW / 32;   // 32-row tiles per state wave (1 or 2)
+    constexpr int QKS = DW / 16;   // 16-deep k-steps of q C over the wave's rows
+    const int dw0 = ws * DW;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int kk = r16 >> 2, ka = r16 & 3;
+    auto srow = [&](int dt, int e) {
+      const int i = e >> 2;
+      return dw0 + 32 * dt + 16 * (i >> 1) + 8 * hh + 4 * (i & 1) + (e & 3);
+    };
+    f32x16 acc[NDT][2];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          acc[dt][vt][e] = ci ? ci[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] : 0.f;
+    // n of state row state_row(dw0, dt, l32): lane halves hh = 0, 1 sum the
+    // tokens of their half of every 16-token k-step
+    float nacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) nacc[dt] = (ni && hh == 0) ? ni[(size_t)bh * DQK + state_row(dw0, dt, l32)] : 0.f;
+    // n entering chunk kc as two bf16 rows (hi, lo) of buffer kc & 1 (rows 2, 3 stay zero):
+    // the fifth A tile of the output waves' S product
+    auto store_nparts = [&](int buf) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const float x = nacc[dt] + __shfl_xor(nacc[dt], 32);
+        if (hh == 0) {
+          const uint32_t hi = pack_bf16(x, 0.f);
+          bf16_t* nb = nbuf + buf * 4 * SM::NB_PITCH + state_row(dw0, dt, l32);
+          reinterpret_cast<uint16_t*>(nb)[0] = (uint16_t)hi;
+          reinterpret_cast<uint16_t*>(nb)[SM::NB_PITCH] = (uint16_t)pack_bf16(x - bf_lo(hi), 0.f);
+        }
+      }
+    };
+    for (int e = tid; e < 2 * 2 * DQK; e += 64 * NSW) {
+      const int buf = e / (2 * DQK), part = 2 + (e / DQK) % 2, d = e % DQK;
+      reinterpret_cast<uint16_t*>(nbuf)[(buf * 4 + part) * SM::NB_PITCH + d] = 0;
+    }
+    store_nparts(kc0 & 1);
+
+    // q fragments (B operand of the transposed product C^T Q^T): token 32 tt + l32,
+    // rows dw0 + 16 s + 8 hh .. +7
+    u32x4 Qs[2][QKS];
+    const uint32_t qs_off = (uint32_t)((l32 * DQK + dw0 + 8 * hh) * 2);
+    auto load_qs = [&](int kc) {
+      const auto rq = q_rsrc(kc);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int s = 0; s < QKS; ++s)
+          Qs[tt][s] = ld16s(rq, qs_off, (uint32_t)((32 * tt * DQK + 16 * s) * 2));
+    };
+    if (!STATES_ONLY) load_qs(kc0);
+    __syncthreads();  // B0: tiles, gate rows and n parts of the first chunk
+
+    for (int kc = kc0; kc < kc1; ++kc) {
+      const float* gb = gbuf + (kc & 1) * GROWS * 64;
+      // ---------------- phase A: partial q C; the update's K^T and alpha' operands are
+      // requested first and consumed in phase B, so their LDS latency hides behind q C.
+      // K^T: A = K^T, row l32 of tile dt = state row state_row(dw0, dt, l32), 16-token
+      // k-steps, tokens 16 ks + 8 hh + jj (jj = 0..7 in element order).  Transposed
+      // reads: within 16 lanes, source lane 4kk + a reads token 16 ks + 8 hh + kk (+4
+      // for the second read) at 4 consecutive columns.
+      bf16x8 Kt[NDT][4];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const char* base = kn + (16 * ks + 8 * hh + kk) * SM::KN_PITCH +
+                             2 * (dw0 + 32 * dt + 16 * (g & 1) + 8 * (ka & 1) + 4 * (ka >> 1));
+          Kt[dt][ks] = tr8(base, base + 4 * SM::KN_PITCH);
+        }
+      // alpha' of tokens 16 ks + 8 hh .. +7 (the n update's operand)
+      f32x4 alf[4][2];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) alf[ks][j] = *reinterpret_cast<const f32x4*>(gb + 256 + 16 * ks + 8 * hh + 4 * j);
+      if (!STATES_ONLY) {
+        // Transposed product C^T Q^T per 32-column tile vt: lane (hh, l32) gets
+        // columns 32 vt + 8i + 4hh + j of token 32 tt + l32.  The split of k-step
+        // q+1 (VALU) is interleaved with the four MFMAs of k-step q, and the
+        // partials of column tile 0 are stored one k-step into tile 1.
+        constexpr int NQ = 2 * QKS;
+        bf16x8 bsp[2][2];
+        f32x16 P[2][2];
+        auto split_q = [&](int qi, bf16x8 (&o)[2]) {
+          const int vt = qi / QKS, s = qi % QKS;
+          const f32x16& x = acc[s >> 1][vt];
+          const int e0 = 8 * (s & 1);
+          split8(f32x4{x[e0], x[e0 + 1], x[e0 + 2], x[e0 + 3]}, f32x4{x[e0 + 4], x[e0 + 5], x[e0 + 6], x[e0 + 7]},
+                 o[0], o[1]);
+        };
+        auto store_p = [&](int vt) {
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              *reinterpret_cast<f32x4*>(hp + (ws * 64 + 32 * tt + l32) * HP_PITCH + 32 * vt + 8 * i + 4 * hh) =
+                  f32x4{P[vt][tt][4 * i], P[vt][tt][4 * i + 1], P[vt][tt][4 * i + 2], P[vt][tt][4 * i + 3]};
+        };
+        split_q(0, bsp[0]);
+#pragma unroll
+        for (int qi = 0; qi < NQ; ++qi) {
+          const int cur = qi & 1, vt = qi / QKS, s = qi % QKS;
+          if (qi + 1 < NQ) split_q(qi + 1, bsp[cur ^ 1]);
+          if (s == 0) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) P[vt][tt] = f32x16{};
+          }
+#pragma unroll
+          for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+              P[vt][tt] = mfma32(bsp[cur][hl], __builtin_bit_cast(bf16x8, Qs[tt][s]), P[vt][tt]);
+          if (vt == 1 && s == 1) {
+            store_p(0);
+            __builtin_amdgcn_sched_barrier(0);  // keep these stores here, behind the MFMAs of tile 1
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          }
+        }
+        store_p(1);
+        load_qs(kc + 1);
+      }
+      __syncthreads();  // B2: partials and alpha' V of the chunk are complete
+
+      // ---------------- phase B: the chunk update of C and n
+      bf16x8 avh[2][2], avl[2][2];
+      auto load_av = [&](int ks, int buf) {
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt) {
+          const char* base = av + (16 * ks + 8 * hh + kk) * AV_PITCH + 2 * (32 * vt + 16 * (g & 1) + 4 * ka);
+          avh[buf][vt] = tr8(base, base + 4 * AV_PITCH);
+          avl[buf][vt] = tr8(base + 128, base + 128 + 4 * AV_PITCH);
+        }
+      };
+      load_av(0, 0);
+      if (gb[323] != 0.f) {  // renormalise the stored state (wave-uniform)
+        const float sc = gb[320];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          nacc[dt] *= sc;
+#pragma unroll
+          for (int vt = 0; vt < 2; ++vt) acc[dt][vt] *= sc;
+        }
+      }
+      // C += K^T (alpha' V), B = alpha' V hi / lo (column 32 vt + l32, the same token
+      // order as K^T), one k-step of operands ahead; and n += K^T alpha' on the VALU in
+      // the MFMAs' shadow: element jj of Kt[dt][ks] is token 16 ks + 8 hh + jj, float32
+      // products and sums, four partial sums per row tile
+      float np[NDT][4];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) np[dt][p] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) load_av(ks + 1, (ks + 1) & 1);
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            acc[dt][vt] = mfma32(Kt[dt][ks], avh[ks & 1][vt], acc[dt][vt]);
+            acc[dt][vt] = mfma32(Kt[dt][ks], avl[ks & 1][vt], acc[dt][vt]);
+          }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const u32x4 kt = __builtin_bit_cast(u32x4, Kt[dt][ks]);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint32_t kp = kt[p];  // tokens 2p, 2p + 1 of the half k-step
+            const float a0 = alf[ks][p >> 1][2 * (p & 1)], a1 = alf[ks][p >> 1][2 * (p & 1) + 1];
+            np[dt][p] = __builtin_fmaf(bf_lo(kp), a0, np[dt][p]);
+            np[dt][p] = __builtin_fmaf(bf_hi(kp), a1, np[dt][p]);
+          }
+        }
+        // ask the scheduler for 1 MFMA : 4 VALU
+#pragma unroll
+        for (int u = 0; u < 4 * NDT; ++u) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) nacc[dt] += (np[dt][0] + np[dt][1]) + (np[dt][2] + np[dt][3]);
+      if (!STATES_ONLY && kc + 1 < kc1) store_nparts((kc + 1) & 1);
+      __syncthreads();  // B1: the next chunk's tiles, gate rows and n parts are staged
+    }
+    // ---- final states (undo the deferred rescale)
+    if (ce) {
+      const float* gl = gbuf + ((kc1 - 1) & 1) * GROWS * 64;
+      const float sc = exp_(gl[322]);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            ce[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] = acc[dt][vt][e] * sc;
+      if (v0 == 0) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const float x = nacc[dt] + __shfl_xor(nacc[dt], 32);
+          if (hh == 0) ne[(size_t)bh * DQK + state_row(dw0, dt, l32)] = x * sc;
+        }
+        if (tid == 0) me[bh] = gl[321];
+      }
+    }
+  } else {
+    // =====================================================================
+    // output waves: rows [16o, 16o + 16) of every chunk, the staging of K and V,
+    // alpha' V, and (wave 0 of the group) the gate rows one chunk ahead
+    // =====================================================================
+    __builtin_amdgcn_s_setprio(2);
+    const int t = tid - 64 * NSW;  // 0 .. NOT-1
+    // ---- gate rows (output wave 0, one chunk ahead): row terms of the
+    // intra-chunk exponent, column terms, output row scales, the combined
+    // stabiliser mc and alpha' = exp(a_t - m') e^{-G} of chunk c go to buffer
+    // c & 1 with the chunk's renormalisation factor of the stored state, m',
+    // the deferred log rescale G, the renormalise flag, and alpha' as bf16
+    // hi (64) | lo (64) in token order (the n update's operand).
+    const float* preph = a.prep + (size_t)bh * NC * PREP_STRIDE;
+    float gm = m_init, gG = 0.f;  // running m and G (gate wave only)
+    auto prep_load = [&](int c, float (&pv)[5]) {
+      const float* pc = preph + (size_t)c * PREP_STRIDE;
+      pv[0] = pc[lane];
+      pv[1] = pc[64 + lane];
+      pv[2] = pc[128 + lane];
+      pv[3] = pc[192 + lane];
+      pv[4] = pc[256 + (lane & 1)];
+    };
+    auto gate_rows = [&](int c, const float (&pv)[5]) {
+      float* gb = gbuf + (c & 1) * GROWS * 64;
+      const float pg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[4]), 0));
+      const float pamax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[4]), 1));
+      const float b = pv[0], av_ = pv[1], cmu = pv[2];
+      const float m_next = fmaxf(pg + gm, pamax);
+      const float lg = pg + gm - m_next;  // log of this chunk's rescale of the state (<= 0)
+      float Gn = gG + lg;
+      const bool renorm = Gn < RENORM;   // wave-uniform
+      if (renorm) Gn = 0.f;
+      const float mb = b + gm;
+      const float mc = fmaxf(mb, b + cmu);
+      gb[lane] = (b - mc) * LOG2E;                       // row term of the intra-chunk exponent
+      gb[64 + lane] = pv[3];                             // column term
+      gb[128 + lane] = exp_(mb - mc + gG) * a.qk_scale;  // output row scale (deferred state rescale folded in)
+      gb[192 + lane] = mc;
+      const float al = exp_(av_ - m_next - Gn);          // alpha' = exp(a_t - m') e^{-G}
+      gb[256 + lane] = al;
+      const uint32_t ahi = pack_bf16(al, 0.f);
+      uint16_t* ar = reinterpret_cast<uint16_t*>(gb + 384);
+      ar[lane] = (uint16_t)ahi;
+      ar[64 + lane] = (uint16_t)pack_bf16(al - bf_lo(ahi), 0.f);
+      if (lane == 0) {
+        gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
+        gb[321] = m_next;
+        gb[322] = Gn;
+        gb[323] = renorm ? 1.f : 0.f;
+      }
+      gm = m_next;
+      gG = Gn;
+    };
+    // ---- K and V staging of the next chunk: piece u of thread t
+    u32x4 Kst[NKO], Vst[2];
+    // piece u * NOT + t: K row (piece / (DQK / 8)), 16-byte column piece % (DQK / 8) (rows are
+    // contiguous, so piece u is u * NOT * 16 bytes past piece 0); V row piece >> 3, 8 columns
+    const uint32_t k_off = (uint32_t)((t / (DQK / 8)) * DQK * 2 + 16 * (t % (DQK / 8)));
+    const uint32_t v_off = (uint32_t)(((t >> 3) * DV + v0 + 8 * (t & 7)) * 2);
+    auto load_kv = [&](int kc) {
+      const auto r = chunk_rsrc(kh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2);
+#pragma unroll
+      for (int u = 0; u < NKO; ++u) Kst[u] = ld16s(r, k_off, (uint32_t)(u * NOT * 16));  // NOT pieces of 16 B per u
+      const auto rv = chunk_rsrc(vh + (size_t)kc * L * DV, rows_of(kc), DV * 2);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) Vst[u] = ld16s(rv, v_off, (uint32_t)(u * (NOT / 8) * DV * 2));  // NOT / 8 rows per u
+    };
+    auto store_kv = [&]() {
+#pragma unroll
+      for (int u = 0; u < NKO; ++u) {
+        const int piece = u * NOT + t;
+        *reinterpret_cast<u32x4*>(kn + (piece / (DQK / 8)) * SM::KN_PITCH + 16 * (piece % (DQK / 8))) = Kst[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int piece = u * NOT + t;
+        *reinterpret_cast<u32x4*>(vn + (piece >> 3) * VN_PITCH + 16 * (piece & 7)) = Vst[u];
+      }
+    };
+    // ---- alpha' V of the chunk as bf16 hi | lo rows (B operand of the update)
+    auto alpha_v = [&](const float* gb) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int piece = u * NOT + t, row = piece >> 3, cg = piece & 7;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(vn + row * VN_PITCH + 16 * cg);
+        const float al = gb[256 + row];
+        u32x4 hv, lv;
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) {
+          const float x0 = al * bf_lo(x[c2]), x1 = al * bf_hi(x[c2]);
+          hv[c2] = pack_bf16(x0, x1);
+          lv[c2] = pack_lo(hv[c2], x0, x1);
+        }
+        *reinterpret_cast<u32x4*>(av + row * AV_PITCH + 16 * cg) = hv;
+        *reinterpret_cast<u32x4*>(av + row * AV_PITCH + 128 + 16 * cg) = lv;
+      }
+    };
+
+    // one specialisation per output row tile O: the causal bounds of the S and
+    // M V products are compile-time constants
+    auto out_wave = [&](auto otag) {
+      constexpr int o = decltype(otag)::value;
+      u32x4 Qf[KPD];
+      const uint32_t qf_off = (uint32_t)(((16 * o + r16) * DQK + 8 * g) * 2);
+      float pv[5];  // gate prep of the next chunk (gate wave)
+      // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
+      // 16-byte load; the K operand below uses the same contiguous k order)
+      auto load_q = [&](int kc) {
+        const auto rq = q_rsrc(kc);
+#pragma unroll
+        for (int p = 0; p < KPD; ++p) Qf[p] = ld16s(rq, qf_off, (uint32_t)(64 * p));
+      };
+      // prologue: the first chunk's tiles and gate rows, the second chunk's loads in flight
+      load_kv(kc0);
+      if (!STATES_ONLY) load_q(kc0);
+      if (o == 0) {
+        prep_load(kc0, pv);
+        gate_rows(kc0, pv);
+      }
+      store_kv();
+      load_kv(kc0 + 1);
+      if (o == 0) prep_load(min(kc0 + 1, kc1 - 1), pv);
+      __syncthreads();  // B0
+
+      for (int kc = kc0; kc < kc1; ++kc) {
+        const float* gb = gbuf + (kc & 1) * GROWS * 64;
+        const bf16_t* nbk = nbuf + (kc & 1) * 4 * SM::NB_PITCH;
+        // ---------------- phase A: alpha' V (its VALU work first, so that it can overlap the
+        // S product's MFMAs), S, M [V | 1]
+        alpha_v(gb);
+        f32x4 Hmv[NVX];
+        float qn = 0.f;
+        if (!STATES_ONLY) {
+          // S^T tiles over the whole DQK: A = K rows 16jt + r16, B = q rows; only the
+          // causal j-tiles jt <= o (the rest are masked).  A fifth A tile holds n as
+          // bf16 hi / lo rows (rows 2, 3 zero), so the same MFMAs give q.n.
+          f32x4 Sacc[5];
+          constexpr int KD = 2;  // K operands one k-step ahead
+          u32x4 kf[KD][5];
+          auto load_kf = [&](int p, u32x4 (&dst)[5]) {
+#pragma unroll
+            for (int jt = 0; jt <= o; ++jt)
+              dst[jt] = *reinterpret_cast<const u32x4*>(kn + (16 * jt + r16) * SM::KN_PITCH + 16 * g + 64 * p);
+            dst[4] = *reinterpret_cast<const u32x4*>(nbk + (r16 & 3) * SM::NB_PITCH + 32 * p + 8 * g);
+          };
+#pragma unroll
+          for (int p = 0; p < KD - 1; ++p) load_kf(p, kf[p]);
+#pragma unroll
+          for (int jt = 0; jt < 5; ++jt) Sacc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int p = 0; p < KPD; ++p) {
+            if (p + KD - 1 < KPD) load_kf(p + KD - 1, kf[(p + KD - 1) % KD]);
+#pragma unroll
+            for (int jt = 0; jt < 5; ++jt)
+              if (jt == 4 || jt <= o)
+                Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
+          }
+          load_q(kc + 1);  // q fragments are dead: prefetch
+          qn = (Sacc[4][0] + Sacc[4][1]) + (Sacc[4][2] + Sacc[4][3]);  // q . n (stored state)
+          // gate the scores of row i = 16o + r16, then M [V | 1] with M split hi + lo
+          const int i = 16 * o + r16;
+          const float bli = gb[i];
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) {
+            const f32x4 ul = *reinterpret_cast<const f32x4*>(gb + 64 + 16 * jt + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = 16 * jt + 4 * g + e;
+              Sacc[jt][e] = (j <= i) ? Sacc[jt][e] * a.qk_scale * exp2_(bli + ul[e]) : 0.f;
+            }
+          }
+#pragma unroll
+          for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
+          // the V operands of both token halves first (their LDS latency then overlaps the splits)
+          constexpr int NPJ = (16 * o + 15) / 32 + 1;  // token halves with unmasked M (compile-time)
+          bf16x8 vbs[NPJ][NVT];
+#pragma unroll
+          for (int pj = 0; pj < NPJ; ++pj)
+#pragma unroll
+            for (int vq = 0; vq < NVT; ++vq) {
+              const char* base = vn + (32 * pj + 4 * g + (r16 >> 2)) * VN_PITCH + 2 * vcol_of(vq, 4 * (r16 & 3));
+              vbs[pj][vq] = tr8(base, base + 16 * VN_PITCH);
+            }
+          // [.. | 1]: rows 0, 4, 8, 12 of the fifth tile are all ones
+          const uint32_t one = ((r16 & 3) == 0) ? 0x3f803f80u : 0u;
+          const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{one, one, one, one});
+#pragma unroll
+          for (int pj = 0; pj < NPJ; ++pj) {
+            bf16x8 mh, ml;
+            split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
+#pragma unroll
+            for (int vq = 0; vq < NVX; ++vq) {
+              const bf16x8 vb = vq < NVT ? vbs[pj][vq] : ones;
+              // transposed product [V | 1]^T M^T: lane (g, r16) gets columns 4g+e of row r16
+              Hmv[vq] = mfma(vb, mh, Hmv[vq]);
+              Hmv[vq] = mfma(vb, ml, Hmv[vq]);
+            }
+          }
+        }
+        __syncthreads();  // B2: the state waves' partial Q C of this chunk are complete
+
+        // ---------------- phase B: finish h of the chunk, stage the next chunk's K, V and
+        // gate rows.  The partials are read first, the K / V tiles written while they arrive.
+        // Q C of row 16o + r16, columns vcol_of(vq, 4g + e): sum of the four state waves'
+        // partials (two 16-byte runs of 4 columns per tile pair)
+        f32x4 Hqc[NVT];
+        if (!STATES_ONLY) {
+          const float* pr = hp + (16 * o + r16) * HP_PITCH + 8 * g;
+#pragma unroll
+          for (int vq = 0; vq < NVT; ++vq) Hqc[vq] = *reinterpret_cast<const f32x4*>(pr + 32 * (vq >> 1) + 4 * (vq & 1));
+#pragma unroll
+          for (int sw = 1; sw < NSW; ++sw)
+#pragma unroll
+            for (int vq = 0; vq < NVT; ++vq)
+              Hqc[vq] += *reinterpret_cast<const f32x4*>(pr + sw * 64 * HP_PITCH + 32 * (vq >> 1) + 4 * (vq & 1));
+        }
+        if (kc + 1 < kc1) store_kv();
+        if (!STATES_ONLY) {
+          // this lane holds columns vcol_of(vq, 4g + e), i.e. the 8 consecutive
+          // columns 32h + 8g .. +7 of tiles (2h, 2h+1); the row sum of M is element 0
+          // of the fifth tile
+          const float qb = gb[128 + 16 * o + r16];
+          const float mcr = gb[192 + 16 * o + r16];
+          const float den = qb * qn + Hmv[NVT][0];
+          const float inv = __builtin_amdgcn_rcpf(fmaxf(fabsf(den), exp_(-mcr)) + a.eps);
+          // rows past S (ragged last chunk) are dropped by the range check
+          const auto rh = chunk_rsrc(hh + (size_t)kc * L * DV, rows_of(kc), DV * 2);
+          const uint32_t hoff = (uint32_t)(((16 * o + r16) * DV + v0 + 8 * g) * 2);
+#pragma unroll
+          for (int h2 = 0; h2 < NVT / 2; ++h2) {
+            u32x4 out;
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              const int vq = 2 * h2 + b;
+              out[2 * b] = pack_bf16((qb * Hqc[vq][0] + Hmv[vq][0]) * inv, (qb * Hqc[vq][1] + Hmv[vq][1]) * inv);
+              out[2 * b + 1] = pack_bf16((qb * Hqc[vq][2] + Hmv[vq][2]) * inv, (qb * Hqc[vq][3] + Hmv[vq][3]) * inv);
+            }
+            st16(rh, hoff + 64 * h2, out);
+          }
+        }
+        if (o == 0 && kc + 1 < kc1) gate_rows(kc + 1, pv);
+        load_kv(kc + 2);
+        if (o == 0) prep_load(min(kc + 2, kc1 - 1), pv);
+        __syncthreads();  // B1
+      }
+    };
+    switch (__builtin_amdgcn_readfirstlane(ws)) {
+      case 0: out_wave(std::integral_constant<int, 0>{}); break;
+      case 1: out_wave(std::integral_constant<int, 1>{}); break;
+      case 2: out_wave(std::integral_constant<int, 2>{}); break;
+      default: out_wave(std::integral_constant<int, 3>{}); break;
+    }
+  }
+}
+
+template <int DQK, bool STATES_ONLY>
+static int launch_one(unsigned nwg, hipStream_t st, const MainArgs& a) {
+  const size_t smem = Smem<DQK>::BYTES;
+  auto kern = chunkwise_pipe_kernel<DQK, STATES_ONLY>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess)
+    return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
+  hipLaunchKernelGGL(kern, dim3(nwg), dim3(NTHREADS), smem, st, a);
+  return XL_OK;
+}
+
+}  // namespace pipe
+
+int pipe_launch(int DQK, bool states_only, unsigned nwg, hipStream_t st, const MainArgs& a) {
+  if (DQK == 256) return states_only ? pipe::launch_one<256, true>(nwg, st, a) : pipe::launch_one<256, false>(nwg, st, a);
+  return states_only ? pipe::launch_one<128, true>(nwg, st, a) : pipe::launch_one<128, false>(nwg, st, a);
+}
+
+}  // namespace fused
+}  // namespace xl

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libx
 XL_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 XL_ERRORS = {-1: "invalid argument", -2: "unsupported", -3: "workspace", -4: "launch"}
 
-ALGO = {"auto": 0, "two_pass": 1, "fused": 2}
+ALGO = {"auto": 0, "two_pass": 1, "fused": 2, "pipelined": 3}
 
 _vp, _fp, _i, _f, _sz, _i64 = ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_int64
 

@@ -39,7 +39,7 @@ __all__ = ["mlstm_chunkwise", "mlstm_chunkwise__native_autograd", "mlstm_chunkwi
 def mlstm_chunkwise(matQ, matK, matV, vecI, vecF, matC_initial=None, vecN_initial=None, scaM_initial=None,
                     qk_scale=None, return_last_states=False, chunk_size=64, eps=1e-6, algo="auto"):
     """h (B, NH, S, DHV), or (h, (C (B,NH,DHQK,DHV), n (B,NH,DHQK), m (B,NH,1))) when
-    ``return_last_states``.  ``algo``: "auto" | "fused" | "two_pass"."""
+    ``return_last_states``.  ``algo``: "auto" | "fused" | "pipelined" | "two_pass"."""
     if qk_scale is None:
         qk_scale = matQ.shape[-1] ** -0.5
     h, C, n, m = mlstm_chunkwise_op(matQ, matK, matV, vecI, vecF, matC_initial, vecN_initial, scaM_initial,

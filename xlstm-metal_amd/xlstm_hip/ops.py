@@ -156,12 +156,12 @@ def _seq_shapes(q, k, v, i, f, c0, n0, m0, what):
     return B, NH, S, DQK, DV
 
 
-_ALGO_NAMES = {1: "two_pass", 2: "fused"}
+_ALGO_NAMES = {1: "two_pass", 2: "fused", 3: "pipelined"}
 _fallback_warned: set = set()
 
 
 def chunkwise_algorithm(B, NH, S, DQK, DV, L, dtype, algo="auto") -> str:
-    """The algorithm ("fused" or "two_pass") xl_mlstm_chunkwise_fwd takes for these arguments."""
+    """The algorithm ("fused", "pipelined" or "two_pass") xl_mlstm_chunkwise_fwd takes for these arguments."""
     lib = _lib.load()
     rc = int(lib.xl_mlstm_chunkwise_algo(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype], _lib.ALGO[algo]))
     if rc < 0:
@@ -203,7 +203,7 @@ def mlstm_chunkwise_op(q: Tensor, k: Tensor, v: Tensor, i: Tensor, f: Tensor, c0
     what = "mlstm_chunkwise"
     _lib.require_gpu(q, k, v, i, f, c0, n0, m0, what=what)
     B, NH, S, DQK, DV = _seq_shapes(q, k, v, i, f, c0, n0, m0, what)
-    if S % chunk_size != 0 and algo != _lib.ALGO["fused"]:  # the fused kernel also takes a ragged last chunk
+    if S % chunk_size != 0 and algo not in (_lib.ALGO["fused"], _lib.ALGO["pipelined"]):  # single pass: ragged last chunk OK
         raise AssertionError(f"Sequence length {S} is not divisible by chunk size {chunk_size}.")
     q, k, v, i, f = (_prep(t) for t in (q, k, v, i, f))
     c0, n0, m0 = _f32(c0), _f32(n0), _f32(m0)
