@@ -10,10 +10,13 @@ at BASELINE config 2 (bf16 q/k/v/gates, float32 states, B4 NH8 S8192 DQK256
 DV512, L=64, last states returned).  One step = one `mlstm_chunkwise` call
 over the whole batch (B*S = 32768 tokens) with inputs resident in HBM; L2 and
 the 256 MB Infinity Cache are flushed (512 MB write) before every timed call,
-and each call (its gate-prep and fused kernels, replayed from a HIP graph) is
+and each call (its gate-prep and single-pass kernels, replayed from a HIP graph) is
 timed with HIP events on the stream the kernels run on (the flush is queued
 without a host sync, so the events bracket the kernels and not the host-side
-launch latency).  `prefill_chunk_size_128` is the chunk_size=128 sweep.
+launch latency).  Before the timed calls the call runs back to back for
+--warmup-seconds (default 1 s) after the --warmup calls, so the clocks have
+settled.  `prefill_chunk_size_128` is the chunk_size=128 sweep and
+`prefill_fused` the same call on the fused schedule (algo="fused").
 The decode step (config 1, B16 NH8 DQK256 DV512) is reported beside it in
 `decode`: 1000 chained steps over 6 rotating state sets (>256 MB, so the
 state really streams from HBM), captured in a HIP graph.  `soft_cap` reports
@@ -72,7 +75,8 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-PREFILL_KERNEL = "chunkwise_fused_kernel"
+PREFILL_KERNEL = "chunkwise_pipe_kernel"
+PREFILL_KERNEL_FUSED = "chunkwise_fused_kernel"
 SOFT_CAP_KERNEL = "soft_cap_kernel"
 CONV_KERNEL = "causal_conv1d_kernel"
 GROUP_NORM_KERNEL = "group_norm_kernel"
@@ -100,6 +104,17 @@ def decode_bytes(B, NH, DQK, DV, esz=2, gsz=4):
     return 2 * C + 2 * n + 2 * m + 2 * B * NH * DQK * esz + 2 * B * NH * DV * esz + 2 * B * NH * gsz
 
 
+def warm_clocks(fn, dev, seconds):
+    """Runs fn back to back for `seconds` of wall time (after the step-count warm-up): the GPU's
+    clocks take ~0.1 s of sustained load to settle, and the first calls after idle run 5-10 %
+    slower than the steady state every later call sees."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize(dev)
+
+
 class Flusher:
     """Writes a 512 MB buffer to evict L2 and the Infinity Cache (MALL)."""
 
@@ -110,23 +125,24 @@ class Flusher:
         self.buf.fill_(1.0)
 
 
-def bench_prefill(args, dev, L=None, steps=None):
+def bench_prefill(args, dev, L=None, steps=None, algo=None):
     import xlstm_hip
     from xlstm_hip.workloads import CFG2, chunkwise_inputs
     cfg = CFG2
     L = L or args.chunk_size
     steps = steps or args.steps
+    algo = algo or args.algo
     x = chunkwise_inputs(cfg, device=dev)
     flush = Flusher(dev)
     stream = torch.cuda.current_stream(dev)
 
     def call():
-        return xlstm_hip.mlstm_chunkwise(*x, return_last_states=True, chunk_size=L, algo=args.algo)
+        return xlstm_hip.mlstm_chunkwise(*x, return_last_states=True, chunk_size=L, algo=algo)
 
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize(dev)
-    # One mlstm_chunkwise call is two kernel launches (gate prep + fused) behind a
+    # One mlstm_chunkwise call is two kernel launches (gate prep + single pass) behind a
     # torch.library dispatch; replaying it from a HIP graph keeps host-side dispatch
     # time out of the event-timed region (the kernels and their inputs are unchanged).
     mode = "hip_graph"
@@ -145,6 +161,7 @@ def bench_prefill(args, dev, L=None, steps=None):
         call = graph.replay  # noqa: F811
     except Exception as exc:  # measurement method only; the kernels are the same
         mode = f"eager ({type(exc).__name__})"
+    warm_clocks(call, dev, args.warmup_seconds)
     times = []
     t_wall = 0.0
     for _ in range(steps):
@@ -223,6 +240,7 @@ def bench_decode(args, dev):
     reps = max(1, args.decode_steps // per_graph)
     for _ in range(3):
         run()
+    warm_clocks(run, dev, args.warmup_seconds)
     torch.cuda.synchronize(dev)
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -234,22 +252,28 @@ def bench_decode(args, dev):
     steps = reps * per_graph
     us = 1e3 * e0.elapsed_time(e1) / steps
     by = decode_bytes(B, NH, DQK, DV)
-    # the practical ceiling for a step's bytes: a plain device copy of each set's C (67 MB read,
-    # 67 MB written), the same rotation over the 6 sets, replayed from a HIP graph
-    dsts = [torch.empty_like(c) for c in Cs]
+    # the ceiling of the step's own access pattern: xl_mlstm_step_copy_ceiling moves each set's
+    # C (67 MB read, 67 MB written, in place like the step) with the step's grid, thread map and
+    # 16-byte nontemporal loads and stores and nothing else; the same 6-set rotation, HIP graph
+    def copy_launch(s_, stream_):
+        _lib.check(lib.xl_mlstm_step_copy_ceiling(Cs[s_].data_ptr(), Cs[s_].data_ptr(), B, NH, DQK, DV, stream_),
+                   "decode copy ceiling")
+
     copy_graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
         for s in range(nsets):
-            dsts[s].copy_(Cs[s])
+            copy_launch(s, side.cuda_stream)
     torch.cuda.current_stream(dev).wait_stream(side)
     torch.cuda.synchronize(dev)
     with torch.cuda.graph(copy_graph):
+        st = torch.cuda.current_stream(dev).cuda_stream
         for s in range(nsets):
-            dsts[s].copy_(Cs[s])
+            copy_launch(s, st)
     for _ in range(3):
         copy_graph.replay()
+    warm_clocks(copy_graph.replay, dev, min(0.3, args.warmup_seconds))
     torch.cuda.synchronize(dev)
     creps = max(1, args.decode_steps // nsets)
     e0.record(stream)
@@ -773,7 +797,7 @@ def _progress(what):
 
 def summarize_trace(trace_dir, headline_calls):
     """Markdown table of a rocprofv3 --kernel-trace run of this script: calls, mean, min and max
-    duration per kernel, the fused chunkwise kernel's first `headline_calls` dispatches (the
+    duration per kernel, the pipelined chunkwise kernel's first `headline_calls` dispatches (the
     headline: warm-up, the graph warm replay and the timed steps) listed on their own line."""
     import csv
     import glob
@@ -789,7 +813,8 @@ def summarize_trace(trace_dir, headline_calls):
     rows.sort()
 
     def short(name):
-        name = name.replace("(anonymous namespace)::", "").replace("xl::fused::", "").replace("xl::", "")
+        name = name.replace("(anonymous namespace)::", "").replace("xl::fused::pipe::", "")
+        name = name.replace("xl::fused::", "").replace("xl::", "")
         name = re.sub(r"\(.*$", "", name)  # drop the parameter list
         return re.sub(r"^void ", "", name)
 
@@ -798,7 +823,7 @@ def summarize_trace(trace_dir, headline_calls):
         per.setdefault(short(name), []).append(us)
     print("| kernel | calls | mean us | min us | max us |\n|---|---|---|---|---|")
     for name, ts in sorted(per.items(), key=lambda kv: -sum(kv[1])):
-        if name.startswith("chunkwise_fused_kernel<256, false>"):
+        if name.startswith(PREFILL_KERNEL + "<256, false>"):
             head = ts[:headline_calls]
             print(f"| {name}, first {len(head)} dispatches (cfg2 headline) | {len(head)} | "
                   f"{statistics.mean(head):.1f} | {min(head):.1f} | {max(head):.1f} |")
@@ -821,7 +846,8 @@ def summarize_pmc(fetch_dir, write_dir):
                     if row["Counter_Name"] != counter:
                         continue
                     name = row["Kernel_Name"]
-                    key = next((k for k in (PREFILL_KERNEL, SOFT_CAP_KERNEL, "mlstm_step_kernel", "gate_prep_kernel",
+                    key = next((k for k in (PREFILL_KERNEL, PREFILL_KERNEL_FUSED, SOFT_CAP_KERNEL, "mlstm_step_kernel",
+                                            "gate_prep_kernel",
                                             SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL,
                                             RMS_GATE_KERNEL, GATE_PROJ_KERNEL, *BWD_KERNELS)
                                 if k in name), None)
@@ -844,6 +870,8 @@ def summarize_pmc(fetch_dir, write_dir):
     work = {SLSTM_KERNEL: (wl_slstm, slstm_bytes()), SEQ_KERNEL: (wl_seq, mlstm_sequence_bytes()),
             PREFILL_KERNEL: ("cfg2 mlstm_chunkwise prefill",
                              prefill_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV)),
+            PREFILL_KERNEL_FUSED: ("cfg2 mlstm_chunkwise prefill (fused schedule)",
+                                   prefill_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV)),
             SOFT_CAP_KERNEL: ("cfg3 logit soft_cap (cap 30) [1,2048,50304] bf16", 2 * sc_bytes),
             "mlstm_step_kernel": ("cfg1 mlstm decode step", decode_bytes(CFG1.B, CFG1.NH, CFG1.DQK, CFG1.DV)),
             # gate prep: reads i, f (bf16), writes 258 floats of per-chunk gate scans per 64 tokens
@@ -952,8 +980,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-seconds", type=float, default=1.0,
+                    help="after --warmup calls, keep calling (untimed) for this long so the clocks settle")
     ap.add_argument("--chunk-size", type=int, default=64)
-    ap.add_argument("--algo", default="auto", choices=["auto", "fused", "two_pass"])
+    ap.add_argument("--algo", default="auto", choices=["auto", "pipelined", "fused", "two_pass"])
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
@@ -997,7 +1027,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / PEAK_BF16_TFLOPS,
                      "traffic": load_traffic(PREFILL_KERNEL, "cfg2 mlstm_chunkwise prefill")
-                     if (pre["L"] == 64 and args.algo in ("auto", "fused")) else None,
+                     if (pre["L"] == 64 and args.algo in ("auto", "pipelined")) else None,
                      "flops_per_call": pre["flops"],
                      "timing": f"HIP events per call ({pre['mode']} replay), caches flushed"},
         "roofline_hbm": {"achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
@@ -1005,7 +1035,10 @@ def main():
         "prefill_ms_median": pre["ms_median"], "prefill_ms_min": pre["ms_min"], "prefill_wall_ms": pre["wall_ms"],
     }
     if pre["L"] == 64 and args.algo == "auto":
-        # cfg2's chunk_size 128 sweep: the same fused kernel (64-token chunks; the forward is
+        pf = bench_prefill(args, dev, steps=max(3, args.steps // 2), algo="fused")
+        out["prefill_fused"] = {"ms_per_call": pf["ms"], "tokens_per_s": pf["tokens"] / (pf["ms"] * 1e-3),
+                                "tflops": pf["flops"] / (pf["ms"] * 1e-3) / 1e12}
+        # cfg2's chunk_size 128 sweep: the same single-pass kernel (64-token chunks; the forward is
         # chunk-size invariant), so its TFLOP/s are counted with the 64-token algorithm it runs
         p128 = bench_prefill(args, dev, L=128, steps=max(3, args.steps // 4))
         fl64 = prefill_flops(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, 64)
@@ -1023,8 +1056,10 @@ def main():
                          "roofline": {"bound": "hbm", "achieved": dgbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                       "frac": dgbs / PEAK_HBM_GBS, "bytes_per_step": dec["bytes"],
                                       "traffic": load_traffic("mlstm_step_kernel", "cfg1 mlstm decode step")},
-                         "copy_ceiling": {"what": "device copy of each step's C (torch copy_, same 6-set "
-                                                  "rotation, HIP graph)", "bytes": dec["copy_bytes"],
+                         "copy_ceiling": {"what": "xl_mlstm_step_copy_ceiling: each step's C copied in place "
+                                                  "with the step's grid, thread map and 16-byte nontemporal "
+                                                  "loads/stores and nothing else (same 6-set rotation, HIP "
+                                                  "graph)", "bytes": dec["copy_bytes"],
                                           "us": dec["copy_us"],
                                           "step_fraction_of_copy": dec["copy_us"] / dec["us_per_step"]}}
     if not args.no_soft_cap:

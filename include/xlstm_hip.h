@@ -49,7 +49,7 @@ enum xl_status {
 
 /* Chunkwise algorithm selector for xl_mlstm_chunkwise_fwd. */
 enum xl_chunkwise_algo {
-  XL_CHUNKWISE_AUTO = 0,     /* fused when supported, else two-pass */
+  XL_CHUNKWISE_AUTO = 0,     /* pipelined when supported, else two-pass */
   XL_CHUNKWISE_TWO_PASS = 1, /* states kernel + output kernel, float32 math */
   XL_CHUNKWISE_FUSED = 2,    /* single pass, bf16 MFMA, states in registers */
   XL_CHUNKWISE_PIPELINED = 3 /* XL_CHUNKWISE_FUSED's math and shapes; each chunk's state update
@@ -88,6 +88,16 @@ int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, const void* i
                       void* h, float* c_new, float* n_new, float* m_new,
                       int B, int NH, int DQK, int DV, float qk_scale, float eps,
                       int dtype_qkv, int dtype_gates, void* stream);
+
+/*
+ * Measurement aid, no counterpart in the reference: the HBM ceiling of
+ * xl_mlstm_step_fwd's state stream.  Copies c_old [B,NH,DQK,DV] float32 to
+ * c_new (may be the same pointer; both 16-byte aligned) with the decode step's
+ * grid, block, thread-to-element map, 16-byte nontemporal loads and stores and
+ * its read-then-write order, and nothing else, so its time is what the step's
+ * access pattern alone costs.
+ */
+int xl_mlstm_step_copy_ceiling(const float* c_old, float* c_new, int B, int NH, int DQK, int DV, void* stream);
 
 /*
  * Chunkwise mLSTM forward.  Replaces mlstm_chunkwise / mlstm_chunkwise_fw

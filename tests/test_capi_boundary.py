@@ -79,6 +79,12 @@ def test_step_rejects_bad_args(lib):
     a, b = ctypes.c_void_p(512), ctypes.c_void_p(1024)
     assert f(p, p, p, p, p, a, b, p, p, a, b, ctypes.c_void_p(2048), 2, 8, 256, 512, 0.0625, 1e-6, 1, 0, None) == -1
     assert b"alias" in lib.xl_last_error()
+    # the step's copy ceiling (a measurement aid): the step's shape checks, null and alignment
+    g = lib.xl_mlstm_step_copy_ceiling
+    assert g(p, p, 0, 8, 256, 512, None) == -1
+    assert g(p, p, 2, 8, 256, 514, None) == -2
+    assert g(None, p, 2, 8, 256, 512, None) == -1 and b"null" in lib.xl_last_error()
+    assert g(ctypes.c_void_p(260), p, 2, 8, 256, 512, None) == -1 and b"aligned" in lib.xl_last_error()
 
 
 def test_chunkwise_rejects_bad_args(lib):
@@ -207,8 +213,8 @@ def test_fake_tensor_shapes():
 def test_chunkwise_algorithm_query(lib):
     """xl_mlstm_chunkwise_algo names the algorithm auto picks and why it left the fused one."""
     from xlstm_hip import chunkwise_algorithm
-    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 64, torch.bfloat16) == "fused"
-    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 128, torch.bfloat16) == "fused"
+    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 64, torch.bfloat16) == "pipelined"
+    assert chunkwise_algorithm(4, 8, 8192, 256, 512, 128, torch.bfloat16) == "pipelined"
     assert chunkwise_algorithm(1, 8, 256, 256, 512, 64, torch.float32) == "two_pass"
     assert chunkwise_algorithm(4, 8, 8192, 256, 512, 64, torch.bfloat16, algo="two_pass") == "two_pass"
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 2, 0) == 1  # float16 q/k/v

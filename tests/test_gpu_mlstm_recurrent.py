@@ -151,6 +151,24 @@ def test_step_alias_rejected(gpu_case):
     assert rc == -1 and b"alias" in lib.xl_last_error()
 
 
+@pytest.mark.parametrize("B,NH,DQK,DV", [(16, 8, 256, 512), (2, 3, 256, 192), (1, 2, 512, 516), (4, 8, 64, 256)])
+@pytest.mark.parametrize("in_place", [True, False])
+def test_step_copy_ceiling(gpu_case, B, NH, DQK, DV, in_place):
+    """xl_mlstm_step_copy_ceiling (the decode step's access pattern without its arithmetic) moves
+    every element of C unchanged, in place and out of place, on the wide tiles (config 1) and the
+    64-column tiles (ragged last tile, 8 rows per thread)."""
+    from xlstm_hip import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev()).manual_seed(DQK + DV)
+    C = torch.randn(B, NH, DQK, DV, generator=g, device=dev())
+    want = C.clone()
+    out = C if in_place else torch.full_like(C, float("nan"))
+    rc = lib.xl_mlstm_step_copy_ceiling(C.data_ptr(), out.data_ptr(), B, NH, DQK, DV, None)
+    _lib.check(rc, "copy ceiling")
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+
+
 @pytest.mark.parametrize("DQK,DV", [(64, 64), (128, 256), (512, 128)])
 @pytest.mark.parametrize("S", [63, 150])
 def test_sequence_kernel_heads_and_strong_gates(gpu_case, DQK, DV, S):

@@ -1,5 +1,6 @@
 // C-ABI entry point of the chunkwise mLSTM forward: validation and the choice
-// between the fused bf16-MFMA kernel and the two-pass kernels.
+// between the single-pass bf16-MFMA kernels (pipelined schedule by default, the
+// fused schedule on request) and the two-pass kernels.
 #include "chunkwise.h"
 
 namespace xl {
@@ -42,7 +43,7 @@ static int pick(const ChunkwiseArgs& a, int algo, int* chosen) {
                      algo == XL_CHUNKWISE_FUSED ? "fused" : "pipelined", why);
   *chosen = (algo == XL_CHUNKWISE_TWO_PASS) ? XL_CHUNKWISE_TWO_PASS
             : single_pass(algo)             ? algo
-            : fused_ok                      ? XL_CHUNKWISE_FUSED
+            : fused_ok                      ? XL_CHUNKWISE_PIPELINED
                                             : XL_CHUNKWISE_TWO_PASS;
   return XL_OK;
 }

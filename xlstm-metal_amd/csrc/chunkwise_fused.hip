@@ -352,7 +352,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              *reinterpret_cast<f32x4*>(hp + (ws * 64 + 32 * tt + l32) * HP_PITCH + 32 * vt + 8 * i + 4 * hh) =
+              *reinterpret_cast<f32x4*>(hp + (ws * 64 + 32 * tt + l32) * HP_PITCH + hp_col(8 * vt + 2 * i + hh)) =
                   f32x4{P[vt][tt][4 * i], P[vt][tt][4 * i + 1], P[vt][tt][4 * i + 2], P[vt][tt][4 * i + 3]};
         };
         split_q(0, bsp[0]);
@@ -575,14 +575,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_fused_kernel(
       // Q C of row 16o + r16, columns vcol_of(vq, 4g + e): sum of the four state
       // waves' partials (two 16-byte runs of 4 columns per tile pair)
       f32x4 Hqc[NVT];
-      const float* pr = hp + (16 * o + r16) * HP_PITCH + 8 * g;
+      const float* pr = hp + (16 * o + r16) * HP_PITCH;
 #pragma unroll
-      for (int vq = 0; vq < NVT; ++vq) Hqc[vq] = *reinterpret_cast<const f32x4*>(pr + 32 * (vq >> 1) + 4 * (vq & 1));
+      for (int vq = 0; vq < NVT; ++vq) Hqc[vq] = *reinterpret_cast<const f32x4*>(pr + hp_col(8 * (vq >> 1) + 2 * g + (vq & 1)));
 #pragma unroll
       for (int sw = 1; sw < NSW; ++sw)
 #pragma unroll
         for (int vq = 0; vq < NVT; ++vq)
-          Hqc[vq] += *reinterpret_cast<const f32x4*>(pr + sw * 64 * HP_PITCH + 32 * (vq >> 1) + 4 * (vq & 1));
+          Hqc[vq] += *reinterpret_cast<const f32x4*>(pr + sw * 64 * HP_PITCH + hp_col(8 * (vq >> 1) + 2 * g + (vq & 1)));
       // finish row 16o + r16: this lane holds columns vcol_of(vq, 4g + e), i.e. the
       // 8 consecutive columns 32h + 8g .. +7 of tiles (2h, 2h+1); the row sum of M
       // (ones in rows 0, 4, 8, 12 of the fifth tile) is element 0

@@ -20,10 +20,10 @@
 //   phase B (after the partials are complete):
 //     state waves:  renormalise if the chunk asks for it, C += K^T (alpha' V)
 //                   from the captured K^T and the alpha' V tile, and the
-//                   normaliser n += K^T alpha' on the VALU (v_dot2 over the same
-//                   K^T registers, alpha' as bf16 hi + lo) -- the n rows a state
-//                   wave carries are its own C rows; n goes to LDS as bf16
-//                   hi | lo rows for the next chunk's q.n
+//                   normaliser n += K^T alpha' on 4 x 4 x 4 MFMA blocks over the
+//                   same K^T registers (alpha' as bf16 hi + lo rows) -- the n
+//                   rows a state wave carries are its own C rows; n goes to LDS
+//                   as bf16 hi | lo rows for the next chunk's q.n
 //     output waves: add the four partials, normalise and store h; write the
 //                   next chunk's K and V tiles (loaded from HBM a whole chunk
 //                   earlier) into LDS
@@ -187,12 +187,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
                              2 * (dw0 + 32 * dt + 16 * (g & 1) + 8 * (ka & 1) + 4 * (ka >> 1));
           Kt[dt][ks] = tr8(base, base + 4 * SM::KN_PITCH);
         }
-      // alpha' of tokens 16 ks + 8 hh .. +7 (the n update's operand)
-      f32x4 alf[4][2];
+      // A operand of the n update (4 x 4 x 4 MFMA blocks of 4 lanes): lane 4b + m holds
+      // alpha' of tokens 16 ks + 8 hh + 4 j .. +3 as bf16 hi (m = 0), lo (m = 1) or zeros
+      // (m = 2, 3), the 4 lanes of a block sharing hh
+      s16x4 an[4][2];
+      {
+        const char* ab = reinterpret_cast<const char*>(gb + 384) + 128 * min(lane & 3, 2) + 16 * hh;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) alf[ks][j] = *reinterpret_cast<const f32x4*>(gb + 256 + 16 * ks + 8 * hh + 4 * j);
+          for (int j = 0; j < 2; ++j) an[ks][j] = *reinterpret_cast<const s16x4*>(ab + 32 * ks + 8 * j);
+      }
       if (!STATES_ONLY) {
         // Transposed product C^T Q^T per 32-column tile vt: lane (hh, l32) gets
         // columns 32 vt + 8i + 4hh + j of token 32 tt + l32.  The split of k-step
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              *reinterpret_cast<f32x4*>(hp + (ws * 64 + 32 * tt + l32) * HP_PITCH + 32 * vt + 8 * i + 4 * hh) =
+              *reinterpret_cast<f32x4*>(hp + (ws * 64 + 32 * tt + l32) * HP_PITCH + hp_col(8 * vt + 2 * i + hh)) =
                   f32x4{P[vt][tt][4 * i], P[vt][tt][4 * i + 1], P[vt][tt][4 * i + 2], P[vt][tt][4 * i + 3]};
         };
         split_q(0, bsp[0]);
@@ -266,14 +271,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         }
       }
       // C += K^T (alpha' V), B = alpha' V hi / lo (column 32 vt + l32, the same token
-      // order as K^T), one k-step of operands ahead; and n += K^T alpha' on the VALU in
-      // the MFMAs' shadow: element jj of Kt[dt][ks] is token 16 ks + 8 hh + jj, float32
-      // products and sums, four partial sums per row tile
-      float np[NDT][4];
+      // order as K^T), one k-step of operands ahead; and n += K^T alpha' on 4 x 4 x 4
+      // MFMA blocks: B = 4 tokens of the lane's own K^T row (column n of block b is lane
+      // 4b + n), A = alpha' hi / lo rows, so element m of the lane's result is
+      // sum_t alpha'_{hi,lo}(t) K(t, row): products exact in float32, float32 sums
+      f32x4 nd[NDT];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int p = 0; p < 4; ++p) np[dt][p] = 0.f;
+      for (int dt = 0; dt < NDT; ++dt) nd[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         if (ks + 1 < 4) load_av(ks + 1, (ks + 1) & 1);
@@ -288,22 +292,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         for (int dt = 0; dt < NDT; ++dt) {
           const u32x4 kt = __builtin_bit_cast(u32x4, Kt[dt][ks]);
 #pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            const uint32_t kp = kt[p];  // tokens 2p, 2p + 1 of the half k-step
-            const float a0 = alf[ks][p >> 1][2 * (p & 1)], a1 = alf[ks][p >> 1][2 * (p & 1) + 1];
-            np[dt][p] = __builtin_fmaf(bf_lo(kp), a0, np[dt][p]);
-            np[dt][p] = __builtin_fmaf(bf_hi(kp), a1, np[dt][p]);
-          }
-        }
-        // ask the scheduler for 1 MFMA : 4 VALU
-#pragma unroll
-        for (int u = 0; u < 4 * NDT; ++u) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          for (int j = 0; j < 2; ++j)
+            nd[dt] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(an[ks][j], __builtin_bit_cast(s16x4, u32x2{kt[2 * j], kt[2 * j + 1]}),
+                                                            nd[dt], 0, 0, 0);
         }
       }
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) nacc[dt] += (np[dt][0] + np[dt][1]) + (np[dt][2] + np[dt][3]);
+      for (int dt = 0; dt < NDT; ++dt) nacc[dt] += nd[dt][0] + nd[dt][1];
       if (!STATES_ONLY && kc + 1 < kc1) store_nparts((kc + 1) & 1);
       __syncthreads();  // B1: the next chunk's tiles, gate rows and n parts are staged
     }
@@ -372,6 +367,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       uint16_t* ar = reinterpret_cast<uint16_t*>(gb + 384);
       ar[lane] = (uint16_t)ahi;
       ar[64 + lane] = (uint16_t)pack_bf16(al - bf_lo(ahi), 0.f);
+      ar[128 + lane] = 0;  // the zero rows of the n update's A operand
       if (lane == 0) {
         gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
         gb[321] = m_next;
@@ -535,14 +531,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         // partials (two 16-byte runs of 4 columns per tile pair)
         f32x4 Hqc[NVT];
         if (!STATES_ONLY) {
-          const float* pr = hp + (16 * o + r16) * HP_PITCH + 8 * g;
+          const float* pr = hp + (16 * o + r16) * HP_PITCH;
 #pragma unroll
-          for (int vq = 0; vq < NVT; ++vq) Hqc[vq] = *reinterpret_cast<const f32x4*>(pr + 32 * (vq >> 1) + 4 * (vq & 1));
+          for (int vq = 0; vq < NVT; ++vq) Hqc[vq] = *reinterpret_cast<const f32x4*>(pr + hp_col(8 * (vq >> 1) + 2 * g + (vq & 1)));
 #pragma unroll
           for (int sw = 1; sw < NSW; ++sw)
 #pragma unroll
             for (int vq = 0; vq < NVT; ++vq)
-              Hqc[vq] += *reinterpret_cast<const f32x4*>(pr + sw * 64 * HP_PITCH + 32 * (vq >> 1) + 4 * (vq & 1));
+              Hqc[vq] += *reinterpret_cast<const f32x4*>(pr + sw * 64 * HP_PITCH + hp_col(8 * (vq >> 1) + 2 * g + (vq & 1)));
         }
         if (kc + 1 < kc1) store_kv();
         if (!STATES_ONLY) {

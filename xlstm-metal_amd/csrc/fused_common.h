@@ -11,6 +11,7 @@ namespace fused {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -27,13 +28,18 @@ constexpr int NVT = DVT / 16;   // 16-wide column tiles of v
 constexpr int NVX = NVT + 1;    // ... plus the ones tile (row sums of M)
 constexpr int VN_PITCH = 160;   // bytes per row of natural V (8 consecutive rows -> distinct 32 B bank groups)
 constexpr int AV_PITCH = 304;   // bytes per row of natural alpha' V: hi (64 bf16) | lo (64 bf16) | pad
-constexpr int HP_PITCH = 68;    // floats per token row of the partial Q C tiles
+// Partial Q C tiles: 72 floats per token row (2 mod 16 slots of 16 bytes) with the row's
+// 4-column groups G stored in the order (G >> 1) + 8 (G & 1).  The output waves read groups
+// 2g + b of rows r16, which then fall on slots 2 r16 + g + const: a b128 read without bank
+// conflicts (the natural order at any padded pitch is served at half that rate).
+constexpr int HP_PITCH = 72;    // floats per token row of the partial Q C tiles
+__device__ __forceinline__ constexpr int hp_col(int G) { return 4 * ((G >> 1) + 8 * (G & 1)); }
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float RENORM = -30.f; // renormalise the stored state when the deferred log rescale drops below this
 constexpr int PREP_STRIDE = 320;  // floats per chunk of gate prep: b, a, cummax(i - b), (i - b) log2e, [g, max a]
 constexpr int kMaxSegmentsDev = 16;  // most sequence segments of one call (few heads)
-constexpr int GROWS = 7;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G], alpha' bf16 hi | lo
+constexpr int GROWS = 8;          // shared gate rows per chunk: bl, ul, qbar, mc, alpha', [renorm scale, m', G], alpha' bf16 hi | lo, bf16 zeros
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -402,6 +402,48 @@ __global__ __launch_bounds__(STEP_THREADS) void mlstm_step_kernel(
   }
 }
 
+// HBM ceiling of the decode step's state stream: mlstm_step_kernel's grid, block,
+// thread -> (row, 16-byte column group) map, nontemporal 16-byte loads, barrier,
+// whole-tile wait and stores, with its small operands, arithmetic and reductions
+// taken out.  c_new may be c_old (the step updates C in place).
+template <int RPT, int COLS>
+__global__ __launch_bounds__(STEP_THREADS) void step_copy_kernel(const float* c_old, float* c_new, int DQK, int DV,
+                                                                 int ntile) {
+  constexpr int CG = COLS / 4;
+  constexpr int RG = STEP_THREADS / CG;
+  const int bh = blockIdx.x / ntile;
+  const int tile = blockIdx.x - bh * ntile;
+  const int tid = threadIdx.x;
+  const int tx = tid % CG, ty = tid / CG;
+  const int col0 = tile * COLS + tx * 4;
+  const bool col_ok = col0 < DV;
+  const int colc = col_ok ? col0 : 0;
+  const size_t cbase = (size_t)bh * DQK * DV;
+  nt_f4 C[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int d = ty + RG * r;
+    const int dc = d < DQK ? d : 0;
+    C[r] = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(c_old + cbase + (size_t)dc * DV + colc));
+  }
+  __syncthreads();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int d = ty + RG * r;
+    if (col_ok && d < DQK)
+      __builtin_nontemporal_store(C[r], reinterpret_cast<nt_f4*>(c_new + cbase + (size_t)d * DV + col0));
+  }
+}
+
+// The decode step's tile choice: STEP_COLS_WIDE columns (a wave reads and writes whole
+// 1 KB row pieces of C) when DV is a multiple of it, that still gives >= 256 workgroups
+// and DQK fits 16 rows per thread; else REC_COLS columns.
+static bool step_wide(int BNH, int DQK, int DV) {
+  constexpr int RGW = STEP_THREADS / (STEP_COLS_WIDE / 4);
+  return DV % STEP_COLS_WIDE == 0 && (long long)BNH * (DV / STEP_COLS_WIDE) >= 256 && DQK <= 16 * RGW;
+}
+
 template <typename TQ, typename TG>
 static int launch_rec_t(const void* q, const void* k, const void* v, const void* i, const void* f,
                         const float* c0, const float* n0, const float* m0, void* h, float* c1, float* n1,
@@ -413,8 +455,7 @@ static int launch_rec_t(const void* q, const void* k, const void* v, const void*
     // tile width: STEP_COLS_WIDE columns (a wave reads and writes whole 1 KB row pieces of C)
     // when DV is a multiple of it, else 64
     constexpr int RGW = STEP_THREADS / (STEP_COLS_WIDE / 4);
-    const bool wide = DV % STEP_COLS_WIDE == 0 && (long long)BNH * (DV / STEP_COLS_WIDE) >= 256 && DQK <= 16 * RGW;
-    if (wide) {
+    if (step_wide(BNH, DQK, DV)) {
       const int rps = (DQK + RGW - 1) / RGW;
       const dim3 gw((unsigned)(BNH * (DV / STEP_COLS_WIDE)));
 #define XL_STEPW_LAUNCH(R)                                                                                     \
@@ -511,6 +552,37 @@ extern "C" int xl_mlstm_step_fwd(const void* q, const void* k, const void* v, co
     return set_error(XL_ERR_INVALID_ARG, "%s: n_new / m_new must not alias n_old / m_old", who);
   return launch_rec(dtype_qkv, dtype_gates, q, k, v, i, f, c_old, n_old, m_old, h, c_new, n_new, m_new, B * NH, 1,
                     DQK, DV, qk_scale, eps, (hipStream_t)stream, who);
+}
+
+extern "C" int xl_mlstm_step_copy_ceiling(const float* c_old, float* c_new, int B, int NH, int DQK, int DV,
+                                          void* stream) {
+  using namespace xl;
+  clear_error();
+  const char* who = "xl_mlstm_step_copy_ceiling";
+  int rc = check_rec_args(who, B, NH, 1, DQK, DV, XL_DTYPE_F32, XL_DTYPE_F32);
+  if (rc) return rc;
+  if (!c_old || !c_new) return set_error(XL_ERR_INVALID_ARG, "%s: null pointer", who);
+  if ((((uintptr_t)c_old) | ((uintptr_t)c_new)) & 15u)
+    return set_error(XL_ERR_INVALID_ARG, "%s: c_old / c_new must be 16-byte aligned", who);
+  const int BNH = B * NH;
+  const hipStream_t s = (hipStream_t)stream;
+  if (step_wide(BNH, DQK, DV)) {
+    constexpr int RGW = STEP_THREADS / (STEP_COLS_WIDE / 4);
+    const int rps = (DQK + RGW - 1) / RGW;
+    const dim3 gw((unsigned)(BNH * (DV / STEP_COLS_WIDE)));
+    if (rps <= 4) hipLaunchKernelGGL((step_copy_kernel<4, STEP_COLS_WIDE>), gw, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, DV / STEP_COLS_WIDE);
+    else if (rps <= 8) hipLaunchKernelGGL((step_copy_kernel<8, STEP_COLS_WIDE>), gw, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, DV / STEP_COLS_WIDE);
+    else hipLaunchKernelGGL((step_copy_kernel<16, STEP_COLS_WIDE>), gw, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, DV / STEP_COLS_WIDE);
+    return check_launch(who);
+  }
+  const int ntile = (DV + REC_COLS - 1) / REC_COLS;
+  const dim3 grid((unsigned)(BNH * ntile));
+  const int rps = (DQK + STEP_RG - 1) / STEP_RG;
+  if (rps <= 1) hipLaunchKernelGGL((step_copy_kernel<1, REC_COLS>), grid, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, ntile);
+  else if (rps <= 2) hipLaunchKernelGGL((step_copy_kernel<2, REC_COLS>), grid, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, ntile);
+  else if (rps <= 4) hipLaunchKernelGGL((step_copy_kernel<4, REC_COLS>), grid, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, ntile);
+  else hipLaunchKernelGGL((step_copy_kernel<8, REC_COLS>), grid, dim3(STEP_THREADS), 0, s, c_old, c_new, DQK, DV, ntile);
+  return check_launch(who);
 }
 
 extern "C" int xl_mlstm_sequence_fwd(const void* q, const void* k, const void* v, const void* i, const void* f,

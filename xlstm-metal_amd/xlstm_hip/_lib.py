@@ -28,6 +28,7 @@ SIGNATURES = {
     "xl_last_error": (ctypes.c_char_p, []),
     "xl_soft_cap_fwd": (_i, [_vp, _vp, _i64, _f, _i, _vp]),
     "xl_mlstm_step_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 4 + [_f, _f] + [_i, _i, _vp]),
+    "xl_mlstm_step_copy_ceiling": (_i, [_fp, _fp] + [_i] * 4 + [_vp]),
     "xl_mlstm_chunkwise_workspace_size": (_sz, [_i] * 8),
     "xl_mlstm_chunkwise_algo": (_i, [_i] * 8),
     "xl_mlstm_chunkwise_fwd": (_i, [_vp] * 5 + [_fp] * 3 + [_vp] + [_fp] * 3 + [_i] * 6 + [_f, _f] + [_i] * 3

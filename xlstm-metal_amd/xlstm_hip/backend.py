@@ -110,7 +110,7 @@ def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequ
         # chunk-size invariant), so it is called with the size its support was checked for
         h_out, (c_state, n_state, m_state) = mlstm_chunkwise_kernel(
             q=q, k=k, v=v, f=f, i=i, c_initial=c_state, n_initial=n_state, m_initial=m_state, chunk_size=64,
-            return_last_states=True, eps=eps, algo="fused")
+            return_last_states=True, eps=eps, algo="pipelined")
     elif S > 1:
         h_outs = []
         start = 0

@@ -171,7 +171,7 @@ def chunkwise_algorithm(B, NH, S, DQK, DV, L, dtype, algo="auto") -> str:
 
 def _warn_slow_fallback(B, NH, S, DQK, DV, L, dtype) -> None:
     """One warning per reason when algo="auto" leaves 16-bit inputs on the two-pass kernels (several
-    times slower than the fused kernel, and holding every chunk's state in a workspace)."""
+    times slower than the single-pass kernels, and holding every chunk's state in a workspace)."""
     lib = _lib.load()
     if int(lib.xl_mlstm_chunkwise_algo(B, NH, S, DQK, DV, L, _lib.XL_DTYPE[dtype], 0)) != 1:
         return
@@ -179,7 +179,7 @@ def _warn_slow_fallback(B, NH, S, DQK, DV, L, dtype) -> None:
     if why not in _fallback_warned:
         _fallback_warned.add(why)
         warnings.warn(f"xlstm_hip.mlstm_chunkwise: {dtype} inputs run the two-pass kernels ({why}); "
-                      "bf16 q/k/v with DQK 128 or 256 and DV a multiple of 64 take the fused kernel",
+                      "bf16 q/k/v with DQK 128 or 256 and DV a multiple of 64 take the single-pass kernels",
                       RuntimeWarning, stacklevel=3)
 
 
