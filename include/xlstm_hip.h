@@ -146,8 +146,11 @@ int xl_mlstm_chunkwise_fwd(const void* q, const void* k, const void* v, const vo
  * device array of XL_NOALLOC_SCRATCH_BYTES per GPU (1280 bytes per 64 tokens
  * of every head: B*NH*ceil(S/64) <= 13107), held until the process ends.
  * Larger requests return XL_ERR_UNSUPPORTED.  The stream's device must be the
- * current device.  Every call on a GPU shares that GPU's array: calls that
- * overlap on one GPU (concurrent streams or threads) race.
+ * current device.  Every call on a GPU shares that GPU's array; outside graph
+ * capture the calls are ordered (a call on another stream than the previous
+ * call's waits on an event recorded behind it; the first call on a device
+ * creates that event).  A stream under capture gets no such wait: a replay of
+ * a captured call that overlaps another call on the same GPU races.
  */
 #define XL_NOALLOC_SCRATCH_BYTES (16u * 1024u * 1024u)
 size_t xl_mlstm_chunkwise_noalloc_max_bytes(void);

@@ -42,6 +42,15 @@ def lowp_excess(got: torch.Tensor, want: torch.Tensor, roundings: int = 1) -> fl
     return float((d - roundings * half_ulp(want, got.dtype)).max())
 
 
+def print_margins(got, want, what=""):
+    """Prints the raw max-abs error and the excess beyond one, two and three 16-bit roundings of
+    the reference's output (the margin the bar at each choice would leave), and returns them."""
+    raw = float((got.detach().double().cpu() - want.detach().double().cpu()).abs().max())
+    ex = [lowp_excess(got, want, r) for r in (1, 2, 3)]
+    print(f"[margin] {what}: max-abs {raw:.3e}; beyond 1 / 2 / 3 roundings {ex[0]:.3e} / {ex[1]:.3e} / {ex[2]:.3e}")
+    return raw, ex
+
+
 def assert_parity(got, want, dtype, what="", roundings=1):
     """fp32: relerr <= FP32_REL; 16-bit inputs: max-abs <= LOWP_ABS beyond the output's own rounding
     (and, with roundings=2, one more 16-bit rounding the reference applies on the way to it)."""

@@ -13,7 +13,7 @@ import ctypes
 import pytest
 import torch
 
-from helpers import FP32_REL, assert_parity, dev, maxabs, relerr
+from helpers import FP32_REL, assert_parity, dev, maxabs, print_margins, relerr
 from oracle import mlstm as om
 
 pytestmark = pytest.mark.gpu
@@ -130,13 +130,19 @@ def test_sequence_kernel(gpu_case, S, dtype):
     # float32 exponentials differ by up to one ulp, which can flip the first two roundings:
     # tests/test_oracle_bf16_sensitivity.py shows the oracle alone, under seeded 1-ulp
     # changes of its gate exponentials, moving its own h beyond 2e-2 past one rounding (at
-    # this test's S = 130 inputs) and never beyond 2e-2 past three.  So h is held to 2e-2
-    # beyond the reference's three roundings of it, for every S.
-    rnd = 3
+    # this test's S = 130 inputs) and never beyond 2e-2 past three.  The kernel's measured
+    # excess (printed as "[margin]") stays within 2e-2 past two roundings at every S here
+    # (worst 1.6e-2 at S = 200), so h is held to 2e-2 beyond two of the reference's roundings.
+    rnd = 2
+    if dtype != torch.float32:
+        print_margins(h, hr, f"sequence h S={S}")
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got, want, dtype, f"S={S} {dtype} {name}", roundings=rnd if name == "h" else 1)
     h0 = xlstm_hip.mlstm_recurrent_sequence__native_fw(*_to((q, k, v, i, f)))
-    assert_parity(h0, om.mlstm_recurrent_sequence(q, k, v, i, f), dtype, "zero state", roundings=rnd)
+    h0r = om.mlstm_recurrent_sequence(q, k, v, i, f)
+    if dtype != torch.float32:
+        print_margins(h0, h0r, f"sequence h S={S} zero state")
+    assert_parity(h0, h0r, dtype, "zero state", roundings=rnd)
 
 
 def test_step_alias_rejected(gpu_case):

@@ -16,7 +16,7 @@ random-init stacks end to end (xlstm_hip.stack).
 import pytest
 import torch
 
-from helpers import assert_parity, dev
+from helpers import assert_parity, dev, print_margins
 from oracle import mlstm as om
 from oracle import slstm as osl
 
@@ -78,6 +78,7 @@ def test_cfg3_mlstm_layer_prefill_and_decode(gpu_case):
                                                   i1.float().cpu(), f1.float().cpu(), C.cpu(), n.cpu(), m.cpu())
     # h with a bf16 q: the reference's three bf16 roundings of it (q C', q n', the quotient), any of
     # which a 1-ulp difference of the gate exponentials can flip (tests/test_oracle_bf16_sensitivity.py)
+    print_margins(h.cpu(), hr, "cfg3 decode h")
     for got, want, nm in ((h, hr, "h"), (C2, C2r, "C"), (n2, n2r, "n"), (m2, m2r, "m")):
         assert_parity(got.cpu(), want, torch.bfloat16, f"cfg3 decode {nm}", roundings=3 if nm == "h" else 1)
 

@@ -7,7 +7,11 @@ device array (for callers that cannot allocate).
   holds the first call's larger contents) each equal xl_mlstm_chunkwise_fwd with the fused
   algorithm and a caller workspace, on h and on the last C, n, m: bit for bit where that call
   runs the same unsplit kernels, within the bf16 parity bar where it splits the sequence into
-  segments (few heads); and both also meet the bf16 parity bar against the CPU oracle.
+  segments (few heads); and both also meet the bf16 parity bar against the CPU oracle;
+* GPU: a long call on one stream and a short one right behind it on a second stream (no host
+  sync) both equal the workspace entry point bit for bit (the calls are ordered on the shared
+  array); and the call captured in a HIP graph, replayed on fresh inputs copied into its static
+  buffers, equals the eager call on every replay.
 """
 
 import ctypes
@@ -117,3 +121,88 @@ def test_noalloc_matches_workspace_entry_point(lib, gpu_case):
         assert_parity(got[1], Cr, torch.bfloat16, "noalloc C")
         assert_parity(got[2], nr, torch.bfloat16, "noalloc n")
         assert_parity(got[3], mr.reshape(B, NH), torch.bfloat16, "noalloc m")
+
+
+def _launch(lib, x, out, B, NH, S, DQK, DV, stream):
+    q, k, v, i, f, c0, n0, m0 = x
+    h, cl, nl, ml = out
+    rc = lib.xl_mlstm_chunkwise_fwd_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), i.data_ptr(), f.data_ptr(),
+                                            c0.data_ptr(), n0.data_ptr(), m0.data_ptr(), h.data_ptr(), cl.data_ptr(),
+                                            nl.data_ptr(), ml.data_ptr(), B, NH, S, DQK, DV, 64, DQK ** -0.5, 1e-6,
+                                            BF16, BF16, stream)
+    assert rc == 0, lib.xl_last_error()
+
+
+def _outs(B, NH, S, DQK, DV, dev):
+    return (torch.full((B, NH, S, DV), float("nan"), dtype=torch.bfloat16, device=dev),
+            torch.full((B, NH, DQK, DV), float("nan"), device=dev), torch.full((B, NH, DQK), float("nan"), device=dev),
+            torch.full((B, NH), float("nan"), device=dev))
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+def test_noalloc_two_streams_are_ordered(lib, gpu_case):
+    """A long call on one stream and, right behind it with no host sync, a shorter call on a second
+    stream: the second waits for the first (they share the static scratch), so both equal the
+    workspace entry point's results bit for bit (neither splits the sequence)."""
+    dev = torch.device("cuda:0")
+    shapes = ((4, 8, 2048, 256, 512, 21), (1, 8, 448, 128, 128, 22))
+    xs, wants = [], []
+    for (B, NH, S, DQK, DV, seed) in shapes:
+        x = _inputs(B, NH, S, DQK, DV, seed, dev)
+        ws = torch.empty(lib.xl_mlstm_chunkwise_workspace_size(B, NH, S, DQK, DV, 64, BF16, FUSED), dtype=torch.uint8,
+                         device=dev)
+        xs.append(x)
+        wants.append(_run(lib, lib.xl_mlstm_chunkwise_fwd, x, B, NH, S, DQK, DV, workspace=ws))
+    outs = [_outs(*sh[:5], dev) for sh in shapes]
+    sa, sb = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    for s in (sa, sb):
+        s.wait_stream(torch.cuda.current_stream(dev))
+    for rep in range(3):
+        print(f"[noalloc] two streams, rep {rep}", flush=True)
+        for o in outs:
+            for t in o:
+                t.fill_(float("nan"))
+        sa.wait_stream(torch.cuda.current_stream(dev))
+        sb.wait_stream(torch.cuda.current_stream(dev))
+        _launch(lib, xs[0], outs[0], *shapes[0][:5], sa.cuda_stream)
+        _launch(lib, xs[1], outs[1], *shapes[1][:5], sb.cuda_stream)
+        torch.cuda.synchronize(dev)
+        for got, want in zip(outs, wants):
+            for a, b, name in zip(got, want, ("h", "C", "n", "m")):
+                assert torch.equal(a, b), f"two streams rep {rep}: {name} differs from the workspace entry point"
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+def test_noalloc_graph_capture(lib, gpu_case):
+    """The entry point captured in a HIP graph (torch.cuda.graph) on static buffers: every replay, on
+    new inputs copied into those buffers with eager work and host syncs between replays, equals the
+    eager call on the same inputs bit for bit."""
+    dev = torch.device("cuda:0")
+    B, NH, S, DQK, DV = 1, 4, 512, 256, 128
+    static_x = _inputs(B, NH, S, DQK, DV, 30, dev)
+    static_out = _outs(B, NH, S, DQK, DV, dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm-up on a side stream, as torch.cuda.graph expects
+        _launch(lib, static_x, static_out, B, NH, S, DQK, DV, side.cuda_stream)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _launch(lib, static_x, static_out, B, NH, S, DQK, DV, torch.cuda.current_stream(dev).cuda_stream)
+    for rep in range(4):
+        print(f"[noalloc] graph replay {rep}", flush=True)
+        fresh = _inputs(B, NH, S, DQK, DV, 31 + rep, dev)
+        for dst, src in zip(static_x, fresh):
+            dst.copy_(src)
+        for t in static_out:
+            t.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        want = _outs(B, NH, S, DQK, DV, dev)
+        _launch(lib, fresh, want, B, NH, S, DQK, DV, torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize(dev)
+        for a, b, name in zip(static_out, want, ("h", "C", "n", "m")):
+            assert torch.equal(a, b), f"graph replay {rep}: {name} differs from the eager call"

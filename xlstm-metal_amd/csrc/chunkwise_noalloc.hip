@@ -7,11 +7,19 @@
 // holds its own copy for the life of the process.  Host code never passes the
 // array's name to a kernel (in host code it is a stand-in, not a device
 // address): the first call on a device, with that device current, resolves
-// the device address with hipGetSymbolAddress and keeps it per device.  The
-// gate-prep kernel writes every byte of the region a call uses before the
-// fused kernel reads it, so nothing has to be cleared between calls.  All
-// calls on one GPU share the array: calls that overlap on one GPU (two
-// streams, or two host threads enqueueing concurrently) race on it.
+// the device address with hipGetSymbolAddress and keeps it per device, and
+// creates one HIP event per device (no device memory).  The gate-prep kernel
+// writes every byte of the region a call uses before the fused kernel reads
+// it, so nothing has to be cleared between calls.
+//
+// All calls on one GPU share the array.  Outside graph capture the calls are
+// ordered: a call on a stream other than the previous call's waits on an
+// event recorded behind the previous call's kernels, so calls from several
+// streams (or host threads) run one after another on the array.  A stream
+// under capture gets no such wait (an event recorded outside a capture cannot
+// be waited on inside it): replays of a captured call are ordered with work on
+// the stream they are launched on only, and a replay that overlaps another
+// call on the same GPU races on the array.
 #include <mutex>
 
 #include "chunkwise.h"
@@ -22,11 +30,19 @@ namespace {
 static __device__ __align__(256) unsigned char scratch[XL_NOALLOC_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the stream's device, which must be current.
-int scratch_address(void* stream, void** out) {
+// Per-device set-up and the ordering of calls on the shared array.
+struct DeviceState {
+  void* scratch = nullptr;      // device address of `scratch`
+  hipEvent_t done = nullptr;    // recorded behind the last call's kernels (outside capture)
+  void* last_stream = nullptr;  // stream of that call
+  bool has_last = false;
+};
+std::mutex g_scratch_mu;  // held from the set-up through the launch and the event record
+DeviceState g_dev[kMaxDevices];
+
+// Device state of the stream's device, which must be current (g_scratch_mu held).
+int device_state(void* stream, DeviceState** out) {
   const char* who = "xl_mlstm_chunkwise_fwd_noalloc";
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -41,16 +57,24 @@ int scratch_address(void* stream, void** out) {
                        (int)sdev, dev);
   }
   if (dev < 0 || dev >= kMaxDevices) return set_error(XL_ERR_UNSUPPORTED, "%s: device ordinal %d", who, dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  DeviceState& d = g_dev[dev];
+  if (!d.scratch) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return set_error(XL_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
                        hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
+    d.scratch = p;
   }
-  *out = g_scratch_ptr[dev];
+  if (!d.done) {
+    e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      d.done = nullptr;
+      return set_error(XL_ERR_LAUNCH, "%s: hipEventCreateWithFlags failed on device %d: %s", who, dev,
+                       hipGetErrorString(e));
+    }
+  }
+  *out = &d;
   return XL_OK;
 }
 
@@ -81,10 +105,31 @@ extern "C" int xl_mlstm_chunkwise_fwd_noalloc(const void* q, const void* k, cons
                      "more than the static %zu (at most %zu chunks); use xl_mlstm_chunkwise_fwd with a workspace",
                      (long long)B * NH * ((S + 63) / 64), need, (size_t)XL_NOALLOC_SCRATCH_BYTES,
                      (size_t)XL_NOALLOC_SCRATCH_BYTES / chunkwise_fused_workspace(1, 1, 64, DQK, DV, 1));
-  void* ws = nullptr;
-  rc = scratch_address(stream, &ws);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  DeviceState* d = nullptr;
+  rc = device_state(stream, &d);
   if (rc) return rc;
-  a.workspace = ws;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing((hipStream_t)stream, &cap);
+  if (e != hipSuccess)
+    return set_error(XL_ERR_INVALID_ARG, "xl_mlstm_chunkwise_fwd_noalloc: hipStreamIsCapturing failed: %s",
+                     hipGetErrorString(e));
+  const bool eager = cap == hipStreamCaptureStatusNone;
+  if (eager && d->has_last && d->last_stream != stream) {
+    e = hipStreamWaitEvent((hipStream_t)stream, d->done, 0);
+    if (e != hipSuccess)
+      return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd_noalloc: hipStreamWaitEvent failed: %s",
+                       hipGetErrorString(e));
+  }
+  a.workspace = d->scratch;
   a.workspace_bytes = XL_NOALLOC_SCRATCH_BYTES;
-  return chunkwise_fused(a);
+  rc = chunkwise_fused(a);
+  if (rc == XL_OK && eager) {
+    e = hipEventRecord(d->done, (hipStream_t)stream);
+    if (e != hipSuccess)
+      return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd_noalloc: hipEventRecord failed: %s", hipGetErrorString(e));
+    d->last_stream = stream;
+    d->has_last = true;
+  }
+  return rc;
 }
