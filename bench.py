@@ -601,6 +601,13 @@ def bwd_bytes(B, NH, S, DQK, DV, L, esz=2):
     return io + states
 
 
+def bwd_io_bytes(B, NH, S, DQK, DV, esz=2):
+    """Compulsory HBM bytes of the chunkwise backward whatever its design: q, k, v, dH and the gates
+    read once, dq, dk, dv and the gate gradients written once, the last-state gradient dC_last read
+    once (float32)."""
+    return B * NH * S * ((2 * DQK + 2 * DV) + (2 * DQK + DV) + 4) * esz + B * NH * DQK * DV * 4
+
+
 BWD_KERNELS = {  # kernel-name key -> short name, for the trace / counter summaries of the backward
     "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, false>": "states scan",
     "bw_stats_bf16_kernel": "stats",
@@ -651,15 +658,22 @@ def bench_chunkwise_bwd(args, dev):
     t = _timed(call, dev, max(3, args.steps // 4), warmup=2)
     fl = bwd_flops(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, 64)
     by = bwd_bytes(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV, 64)
+    io = bwd_io_bytes(cfg.B, cfg.NH, cfg.S, cfg.DQK, cfg.DV)
     tf = fl / (t["ms"] * 1e-3) / 1e12
     gbs = by / (t["ms"] * 1e-3) / 1e9
+    gio = io / (t["ms"] * 1e-3) / 1e9
     return {"workload": f"cfg2 chunkwise backward B{cfg.B} NH{cfg.NH} S{cfg.S} DQK{cfg.DQK} DV{cfg.DV} bf16 in, "
                         "bf16 MFMA (float32 operands as hi / lo pairs), float32 accumulation",
             "ms_per_call": t["ms"], "ms_min": t["ms_min"], "mode": t["mode"],
-            "tokens_per_s": cfg.B * cfg.S / (t["ms"] * 1e-3), "flops_per_call": fl, "bytes_per_call": by,
-            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": gbs / PEAK_HBM_GBS},
-            "mfma_bf16": {"achieved_tflops": tf, "peak": PEAK_BF16_TFLOPS, "frac": tf / PEAK_BF16_TFLOPS}}
+            "tokens_per_s": cfg.B * cfg.S / (t["ms"] * 1e-3), "flops_per_call": fl,
+            # against what any backward must move (inputs, gradients) and the algorithmic flop
+            "roofline": {"bound": "hbm", "achieved": gio, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gio / PEAK_HBM_GBS, "bytes_per_call": io,
+                         "what": "compulsory I/O: q k v dH gates dC_last in, dq dk dv di df out"},
+            "mfma_bf16": {"achieved_tflops": tf, "peak": PEAK_BF16_TFLOPS, "frac": tf / PEAK_BF16_TFLOPS,
+                          "what": "algorithmic flop of the custom backward (bwd_flops)"},
+            # against this design's own traffic (the float32 per-chunk C and dC it materialises)
+            "design_traffic": {"bytes_per_call": by, "achieved": gbs, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}}
 
 
 def bench_arbitrary_length(args, dev):

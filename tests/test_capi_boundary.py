@@ -98,10 +98,29 @@ def test_chunkwise_rejects_bad_args(lib):
     assert f(*args(256, 64, algo=9)) == -1
     assert f(*args(256, 64, c0=p)) == -1
     assert b"together" in lib.xl_last_error()
+    mis = ctypes.c_void_p(264)  # 8-byte aligned only
+    assert f(mis, p, p, p, p, None, None, None, p, None, None, None, 1, 8, 256, 256, 512, 64, 0.0625, 1e-6, 1, 1, 0,
+             None, 0, None) == -1
+    assert b"16-byte aligned" in lib.xl_last_error()
     assert f(*args(256, 64, algo=1)) == -3  # two-pass without workspace
     assert b"workspace" in lib.xl_last_error()
     assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 256, 256, 512, 64, 0, 1) == (4 * 8 * (256 * 512 + 256 + 1) * 4 + 255) // 256 * 256
     assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 250, 256, 512, 64, 0, 1) == 0
+
+
+def test_chunkwise_bwd_rejects_bad_args(lib):
+    f = lib.xl_mlstm_chunkwise_bwd
+    p, mis = ctypes.c_void_p(256), ctypes.c_void_p(264)
+
+    def call(q=p, dq=p, L=64, S=256):
+        return f(q, p, p, p, p, None, None, None, p, None, dq, p, p, p, p, None, 1, 2, S, 64, 64, L, 0.125, 1e-6, 1,
+                 1, None, 0, None)
+
+    assert call(L=128) == -2 and b"chunk_size" in lib.xl_last_error()
+    assert call(S=100) == -1 and b"not divisible" in lib.xl_last_error()
+    assert call(q=mis) == -1 and b"16-byte aligned" in lib.xl_last_error()
+    assert call(dq=mis) == -1 and b"16-byte aligned" in lib.xl_last_error()
+    assert call() == -3 and b"workspace" in lib.xl_last_error()
 
 
 def test_slstm_rejects_bad_args(lib):

@@ -7,9 +7,10 @@ Bars, per gradient, relative to the largest magnitude of the expected tensor:
 * bf16 inputs (the gradients come back in bf16): |got - want| <= 2^-8 |want| + 2e-3 max|want|
   (the output's own rounding, one ulp, plus float32 accumulation over the chunk).
 
-Cases: with and without initial states, the last-state gradient, chunk sizes 16 / 32 / 64, DQK and
-DV that are not multiples of the 64-wide tiles, several heads and chunks, bf16 and f16 inputs, and
-the registry form mlstm_chunkwise__native_custbw.
+Cases: with and without initial states, the last-state gradient, chunk sizes 16 / 32 / 64 / 128
+(128 runs as 64-token chunks), DQK and DV that are not multiples of the 64-wide tiles, several heads
+and chunks, bf16 and f16 inputs, ragged sequences from the single-pass forward (padded to whole
+chunks with state-preserving tokens), and the registry form mlstm_chunkwise__native_custbw.
 """
 
 import pytest
@@ -37,9 +38,9 @@ def _inputs(B, NH, S, DQK, DV, seed, states):
     return (q, k, v, i, f), st, dh, dcl
 
 
-def _check(got, want, dtype, what):
+def _check(got, want, dtype, what, scale=None):
     got, want = got.detach().double().cpu(), want.detach().double().cpu()
-    scale = float(want.abs().max())
+    scale = float(want.abs().max()) if scale is None else scale
     if dtype == torch.float32:
         err = float((got - want).abs().max()) / scale
         assert err <= 1e-4, f"{what}: rel-err {err:.3e}"
@@ -134,11 +135,70 @@ def test_registry_form_and_gate_dtypes(gpu_case):
         _check(t.grad, w, dt if dt == torch.float32 else torch.bfloat16, nm)
 
 
-def test_ragged_sequence_backward_raises(gpu_case):
+@pytest.mark.parametrize("dtype,states,last", [(torch.bfloat16, True, True), (torch.float32, False, True),
+                                              (torch.bfloat16, False, False)])
+def test_chunk_size_128(gpu_case, dtype, states, last):
+    """Training with chunk_size=128: the backward runs at 64-token chunks (the custom backward's
+    gradients do not depend on the chunk size), against the oracle's backward at 128."""
+    _run(1, 2, 256, 128, 128, 128, dtype, states, last, seed=128 + 2 * states + last)
+
+
+@pytest.mark.parametrize("S", [1, 37, 100, 200, 1000])
+@pytest.mark.parametrize("states,last", [(True, True), (False, False)])
+@pytest.mark.parametrize("algo", ["pipelined", "fused"])
+def test_ragged_sequence_backward(gpu_case, S, states, last, algo):
+    """A sequence the single-pass forward ran with a ragged last chunk (bf16, S % 64 != 0) is
+    differentiable: the backward pads it to whole 64-token chunks with state-preserving tokens
+    (input gate -3e4, forget gate +30; tests/test_oracle_chunkwise_bw.py::test_state_preserving_padding
+    shows they change no gradient of the original tokens) and drops their gradients.  Against
+    the oracle's backward on the same padded sequence."""
     import xlstm_hip
-    x, _, _, _ = _inputs(1, 1, 100, 128, 64, 1, False)
+    from xlstm_hip.ops import _PAD_F, _PAD_I
+    B, NH, DQK, DV, dtype = 1, 2, 128, 128, torch.bfloat16
+    x, st, dh, dcl = _inputs(B, NH, S, DQK, DV, 300 + S, states)
+    xd = [t.to(dtype).to(dev()).requires_grad_(True) for t in x]
+    std = [t.to(dev()).requires_grad_(True) for t in st] if states else [None, None, None]
+    out = xlstm_hip.mlstm_chunkwise(*xd, *std, return_last_states=last, chunk_size=64, algo=algo)
+    h, (C, _, _) = out if last else (out, (None, None, None))
+    loss = (h.float() * dh.to(dev())).sum()
+    if last:
+        loss = loss + (C * dcl.to(dev())).sum()
+    loss.backward()
+    pad = (-S) % 64
+    padz = lambda t: torch.nn.functional.pad(t, (0, 0, 0, pad))
+    q, k, v, i, f = (t.to(dtype).double() for t in x)
+    xp = (padz(q), padz(k), padz(v), torch.nn.functional.pad(i, (0, pad), value=_PAD_I),
+          torch.nn.functional.pad(f, (0, pad), value=_PAD_F))
+    st64 = [t.double() for t in st] if states else [None, None, None]
+    want = om.mlstm_chunkwise_bw(*xp, padz(dh.to(dtype).double()), *st64,
+                                 matDeltaC_last=dcl.double() if last else None, chunk_size=64)
+    # the gate gradients against the larger of the two: with one token and no states df is a sum
+    # of terms that cancel exactly (the oracle's float64 leaves ~1e-12 of them)
+    gate_scale = max(float(want[3][:, :, :S].abs().max()), float(want[4][:, :, :S].abs().max()))
+    for nm, t, w in zip(["dq", "dk", "dv", "di", "df"], xd, want[:5]):
+        assert t.grad.shape == t.shape
+        _check(t.grad, w[:, :, :S], dtype, f"ragged {nm} S{S} {algo} states={states} last={last}",
+               scale=gate_scale if nm in ("di", "df") else None)
+    if states:
+        _check(std[0].grad, want[5], torch.float32, "ragged dc0")
+
+
+def test_native_autograd_name_warns_on_custom_gradients(gpu_case):
+    """Under the reference's __native_autograd name the gradients are the custom backward's: a
+    call that returns the last states with inputs that require grad says so (a RuntimeWarning,
+    once per process); one that returns h only does not."""
+    import warnings
+
+    import xlstm_hip
+    from xlstm_hip import chunkwise
+    x, _, _, _ = _inputs(1, 2, 64, 64, 64, 9, False)
     xd = [t.to(dev()).requires_grad_(True) for t in x]
-    h = xlstm_hip.mlstm_chunkwise(*(t.bfloat16() if j < 3 else t for j, t in enumerate(xd)), chunk_size=64,
-                                  algo="fused")
-    with pytest.raises(Exception, match="not divisible"):
-        h.float().sum().backward()
+    chunkwise._autograd_warned = False
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        xlstm_hip.mlstm_chunkwise__native_autograd(*xd)  # h only: no warning
+    with pytest.warns(RuntimeWarning, match="custom backward"):
+        xlstm_hip.mlstm_chunkwise__native_autograd(*xd, return_last_states=True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        xlstm_hip.mlstm_chunkwise__native_autograd(*xd, return_last_states=True)  # once only

@@ -148,3 +148,36 @@ def test_stack_end_to_end(gpu_case, which):
         torch.cuda.synchronize()
         _ = torch.ones(16, device=dev()).sum().item()
         assert torch.equal(toks[-1], runs[0][:, t]), f"{which}: graph decode token {t} differs from eager"
+
+
+@pytest.mark.parametrize("S", [200, 256])
+def test_stack_prefill_decode_handoff(gpu_case, S):
+    """prefill(tokens[:S]) followed by decode_step(tokens[S]) gives the logits of
+    prefill(tokens[:S + 1]), on a reduced stack of two mLSTM and two sLSTM blocks (cfg4's head
+    shapes): every state the prefill hands to decode -- each mLSTM block's C, n, m, each sLSTM
+    block's c, n, m and its conv window, the capped gates of the step -- is the one the longer
+    prefill carries through token S.  The two sides run different kernels (chunkwise and sLSTM
+    sequence kernels against the step kernels) in bf16, so they agree to bf16 roundings amplified
+    through four blocks (measured 2-4 % of the largest logit; bar 5 %), not bit for bit; dropping
+    the context moves the logits by more than the largest logit (checked, so the bar can tell)."""
+    from xlstm_hip.stack import StackConfig, xLSTMStack
+    cfg = StackConfig("handoff", d_model=2048, num_blocks=4, mlstm_heads=8, slstm_every=2, vocab=4096,
+                      init_std=0.05)
+    model = xLSTMStack.random(cfg, dev(), seed=17)
+    g = torch.Generator(device=dev()).manual_seed(18)
+    tokens = torch.randint(0, cfg.vocab, (2, S + 1), generator=g, device=dev())
+    want, _ = model.prefill(tokens)
+    _, states = model.prefill(tokens[:, :S])
+    got = model.decode_step(tokens[:, S], states)
+    diff = float((got.float() - want.float()).abs().max())
+    scale = float(want.float().abs().max())
+    # how far the logits move without the context (token S alone, every state from zero): what
+    # a hand-off that lost the states would give; the bar must sit well below it
+    alone, _ = model.prefill(tokens[:, S:S + 1])
+    ctx = float((alone.float() - want.float()).abs().max())
+    print(f"[handoff] S={S}: max |decode - prefill| {diff:.3e}, without the context {ctx:.3e} "
+          f"(max |logit| {scale:.3e})")
+    assert bool(torch.isfinite(got.float()).all())
+    bar = 0.05 * scale
+    assert ctx >= 4 * bar, f"the context moves the logits by only {ctx:.3e}: the check cannot tell"
+    assert diff <= bar, f"prefill -> decode hand-off: logits differ by {diff:.3e}"

@@ -101,3 +101,29 @@ def test_chunk_size_invariant():
     b = om.mlstm_chunkwise_bw(*x, dH, *st, matDeltaC_last=dCl, chunk_size=64)
     for nm, u, w in zip(["dq", "dk", "dv", "di", "df", "dc0"], a[:6], b[:6]):
         _close(u, w, nm, tol=1e-10)
+
+
+@pytest.mark.parametrize("S,pad", [(64, 64), (128, 32), (64, 48)])
+def test_state_preserving_padding(S, pad):
+    """Tokens with input gate -3e4 and forget gate +30 appended to a sequence change none of the
+    custom backward's gradients of the original tokens (nor dc0), with the last-state gradient
+    on: the padding the GPU backward uses for a ragged sequence (xlstm_hip.ops._PAD_I, _PAD_F)."""
+    from xlstm_hip.ops import _PAD_F, _PAD_I
+    B, NH, DQK, DV = 2, 1, 8, 8
+    x, st = _inputs(B, NH, S, DQK, DV, seed=31 + pad, states=True)
+    g = torch.Generator().manual_seed(3)
+    dH = torch.randn(B, NH, S, DV, generator=g, dtype=F64)
+    dCl = torch.randn(B, NH, DQK, DV, generator=g, dtype=F64)
+    want = om.mlstm_chunkwise_bw(*x, dH, *st, matDeltaC_last=dCl, chunk_size=64)
+    q, k, v, i, f = x
+    padz = lambda t: torch.nn.functional.pad(t, (0, 0, 0, pad))
+    xp = (padz(q), padz(k), padz(v), torch.nn.functional.pad(i, (0, pad), value=_PAD_I),
+          torch.nn.functional.pad(f, (0, pad), value=_PAD_F))
+    T = S + pad
+    Lp = 64 if T % 64 == 0 else (32 if T % 32 == 0 else (16 if T % 16 == 0 else 1))
+    if T % 16:
+        pytest.skip("padded length must be a whole number of 16-token chunks")
+    got = om.mlstm_chunkwise_bw(*xp, padz(dH), *st, matDeltaC_last=dCl, chunk_size=Lp)
+    for nm, u, w in zip(["dq", "dk", "dv", "di", "df"], got[:5], want[:5]):
+        _close(u[:, :, :S], w, nm, tol=1e-10)
+    _close(got[5], want[5], "dc0", tol=1e-10)

@@ -23,6 +23,10 @@ int chunkwise_check_args(const ChunkwiseArgs& a, int algo) {
   if (algo < XL_CHUNKWISE_AUTO || algo > XL_CHUNKWISE_PIPELINED)
     return set_error(XL_ERR_INVALID_ARG, "%s: unknown algo %d", who, algo);
   if (!a.q || !a.k || !a.v || !a.i || !a.f || !a.h) return set_error(XL_ERR_INVALID_ARG, "%s: null pointer", who);
+  // q, k, v, h and the float32 states move in 16-byte pieces
+  if ((((uintptr_t)a.q) | ((uintptr_t)a.k) | ((uintptr_t)a.v) | ((uintptr_t)a.h) | ((uintptr_t)a.c0) |
+       ((uintptr_t)a.n0) | ((uintptr_t)a.c_last) | ((uintptr_t)a.n_last)) & 15u)
+    return set_error(XL_ERR_INVALID_ARG, "%s: q, k, v, h, c0, n0, c_last and n_last must be 16-byte aligned", who);
   if (!((a.c0 && a.n0 && a.m0) || (!a.c0 && !a.n0 && !a.m0)))
     return set_error(XL_ERR_INVALID_ARG, "%s: initial states must be given together", who);
   if (!((a.c_last && a.n_last && a.m_last) || (!a.c_last && !a.n_last && !a.m_last)))

@@ -2486,6 +2486,11 @@ extern "C" int xl_mlstm_chunkwise_bwd(const void* q, const void* k, const void* 
   if (!((c0 && n0 && m0) || (!c0 && !n0 && !m0)))
     return set_error(XL_ERR_INVALID_ARG, "%s: initial states must be given together", who);
   if (dc0 && !c0) return set_error(XL_ERR_INVALID_ARG, "%s: dc0 asks for the gradient of an initial state not given", who);
+  // the tile kernels move q, k, v, dH, dq, dk, dv and the float32 states in 16-byte pieces
+  if ((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)dh) | ((uintptr_t)dq) | ((uintptr_t)dk) |
+       ((uintptr_t)dv) | ((uintptr_t)c0) | ((uintptr_t)n0) | ((uintptr_t)dc_last) | ((uintptr_t)dc0)) & 15u)
+    return set_error(XL_ERR_INVALID_ARG, "%s: q, k, v, dh, dq, dk, dv, c0, n0, dc_last and dc0 must be 16-byte aligned",
+                     who);
   const long long BNH = (long long)B * NH;
   if (BNH * (S / L) * ((DV + 63) / 64) > 0x7fffffffLL || BNH * (S / L) * ((DQK + 63) / 64) > 0x7fffffffLL)
     return set_error(XL_ERR_INVALID_ARG, "%s: too large", who);

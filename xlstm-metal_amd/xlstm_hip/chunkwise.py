@@ -28,6 +28,8 @@ results then differ from the reference's at that chunk size by rounding only.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from . import _lib
@@ -50,9 +52,44 @@ def mlstm_chunkwise(matQ, matK, matV, vecI, vecF, matC_initial=None, vecN_initia
     return h
 
 
+_autograd_warned = False
+
+
+def _warn_custom_gradients(c_initial, n_initial, m_initial, return_last_states, tensors) -> None:
+    """Once per process: under the __native_autograd name the gradients come from the reference's
+    custom backward, which differ from exact autograd where a loss sees the last states or the
+    initial n and m (see mlstm_chunkwise__native_autograd)."""
+    global _autograd_warned
+    if _autograd_warned or not torch.is_grad_enabled():
+        return
+    if not any(t is not None and t.requires_grad for t in tensors):
+        return
+    why = []
+    if return_last_states:
+        why.append("the last states are returned")
+    if any(t is not None and t.requires_grad for t in (n_initial, m_initial)):
+        why.append("n_initial / m_initial require grad")
+    if not why:
+        return
+    _autograd_warned = True
+    warnings.warn("mlstm_chunkwise__native_autograd: gradients come from the reference's custom backward "
+                  "(bw.py:198-352), not exact autograd: " + " and ".join(why) + ", and there the last-state "
+                  "path of df, and the gradients of n_initial and m_initial (zeros), differ from torch.autograd "
+                  "of the forward", RuntimeWarning, stacklevel=3)
+
+
 def mlstm_chunkwise__native_autograd(q, k, v, i, f, c_initial=None, n_initial=None, m_initial=None,
                                      return_last_states=False, eps=1e-6, chunk_size=64, **kwargs):
-    """Registry form (fwbw.py:192-229); extra kwargs such as ``autocast_kernel_dtype`` are accepted."""
+    """Registry form (fwbw.py:192-229); extra kwargs such as ``autocast_kernel_dtype`` are accepted.
+
+    The reference's function of this name differentiates its forward with torch.autograd; here the
+    gradients come from the reference's custom backward (the one mlstm_chunkwise__native_custbw
+    names), which treats each token's divisor and the stabilisers as constants, gives zero
+    gradients to n_initial and m_initial, and leaves a <dC_last, C_last> sigmoid(-f) term out of df
+    on the last-state path.  A loss that sees h only through the mLSTM layer's multi-head norm gets
+    identical gradients; otherwise a RuntimeWarning says so, once per process."""
+    _warn_custom_gradients(c_initial, n_initial, m_initial, return_last_states,
+                           (q, k, v, i, f, c_initial, n_initial, m_initial))
     return mlstm_chunkwise(q, k, v, i, f, c_initial, n_initial, m_initial, qk_scale=None,
                            return_last_states=return_last_states, chunk_size=chunk_size, eps=eps,
                            algo=kwargs.get("algo", "auto"))

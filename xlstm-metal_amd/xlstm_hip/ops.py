@@ -288,15 +288,40 @@ def _chunkwise_setup_context(ctx, inputs, output):
     ctx.params = (qk_scale, chunk_size, eps, return_last_states)
 
 
+# Tokens appended to a ragged sequence for its backward: an input gate this negative makes
+# exp(i - m) = 0 and leaves every stabiliser alone, and logsigmoid(30) = -9.4e-14 makes the
+# forget factor 1 to float32 precision, so (C, n, m) pass through them unchanged and so does the
+# gradient of the last state; their h gradient is zero and their own gradients are dropped.
+_PAD_I, _PAD_F = -3.0e4, 30.0
+
+
 def _chunkwise_backward(ctx, dh, dC, dn, dm):
     """Gradients of (h, C_last) through the reference's custom backward; those of n_last and m_last
-    are dropped and the initial n and m get zeros, as there (bw.py:340-342)."""
+    are dropped and the initial n and m get zeros, as there (bw.py:340-342).
+
+    The backward kernels take chunk sizes 16, 32 and 64.  The custom backward's gradients do not
+    depend on the chunk size (tests/test_oracle_chunkwise_bw.py::test_chunk_size_invariant), so
+    chunk_size 128 (S % 128 == 0, hence S % 64 == 0) runs at 64, and so does a sequence the
+    single-pass forward took with a ragged last chunk (S % chunk_size != 0), padded to whole
+    64-token chunks with state-preserving tokens (_PAD_I, _PAD_F) whose gradients are dropped."""
     q, k, v, i, f, c0, n0, m0 = ctx.saved_tensors
     qk_scale, chunk_size, eps, return_last_states = ctx.params
+    S = q.shape[2]
     if dh is None:
         dh = torch.zeros(q.shape[:3] + (v.shape[-1],), dtype=q.dtype, device=q.device)
     dcl = dC if (return_last_states and dC is not None) else None
-    dq, dk, dv, di, df, dc0 = mlstm_chunkwise_bwd_op(q, k, v, i, f, c0, n0, m0, dh, dcl, qk_scale, chunk_size, eps)
+    L = int(chunk_size)
+    if L not in (16, 32, 64) or S % L != 0:
+        L = 64
+    pad = (-S) % L
+    if pad:
+        q, k, v, dh = (torch.nn.functional.pad(t, (0, 0, 0, pad)) for t in (q, k, v, dh))
+        i = torch.nn.functional.pad(i, (0, pad), value=_PAD_I)
+        f = torch.nn.functional.pad(f, (0, pad), value=_PAD_F)
+    dq, dk, dv, di, df, dc0 = mlstm_chunkwise_bwd_op(q, k, v, i, f, c0, n0, m0, dh, dcl, qk_scale, L, eps)
+    if pad:
+        dq, dk, dv = (t[:, :, :S].contiguous() for t in (dq, dk, dv))
+        di, df = (t[:, :, :S].contiguous() for t in (di, df))
     g_c0 = dc0.to(c0.dtype) if c0 is not None else None
     g_n0 = torch.zeros_like(n0) if n0 is not None else None
     g_m0 = torch.zeros_like(m0) if m0 is not None else None
