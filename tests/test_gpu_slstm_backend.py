@@ -63,7 +63,7 @@ def test_slstm_cell_five_steps(gpu_case):
 @pytest.mark.parametrize("with_state", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(2, 7, 4, 8), (8, 256, 4, 512), (1, 33, 3, 100), (2, 1100, 2, 64),
-                                   (1, 4096, 2, 128), (1, 2000, 1, 200)])
+                                   (1, 4096, 2, 128), (1, 2000, 1, 200), (2, 1025, 2, 64), (1, 3000, 1, 64)])
 def test_slstm_sequence(gpu_case, dtype, shape, with_state):
     """With an initial state every element carries its own n; without one n is the same for
     every d of a head and the kernel forms h = c * og / (|n| + eps) with one scale per step."""
