@@ -15,8 +15,9 @@
 //     state waves:  partial q C over their rows (bf16 hi + lo of the state,
 //                   two MFMAs) -> LDS; then read their K^T operands of the
 //                   update into registers (8 x 16 bytes per lane)
-//     output waves: S^T = K Q^T (with q.n from a fifth tile), gating, M [V | 1],
-//                   alpha' V as bf16 hi | lo -> LDS, the next chunk's gate rows
+//     output waves: alpha' V of the chunk (formed in the previous phase B) ->
+//                   LDS, S^T = K Q^T (with q.n from a fifth tile), gating,
+//                   M [V | 1]
 //   phase B (after the partials are complete):
 //     state waves:  renormalise if the chunk asks for it, C += K^T (alpha' V)
 //                   from the captured K^T and the alpha' V tile, and the
@@ -26,7 +27,10 @@
 //                   as bf16 hi | lo rows for the next chunk's q.n
 //     output waves: add the four partials, normalise and store h; write the
 //                   next chunk's K and V tiles (loaded from HBM a whole chunk
-//                   earlier) into LDS
+//                   earlier) into LDS; step the gate recurrence (every output
+//                   wave; wave 0 writes the next chunk's gate rows) and form
+//                   the next chunk's alpha' V in registers from the V pieces
+//                   just staged
 //
 // The update no longer sits between a chunk's partials and its outputs, so the
 // output waves' finish overlaps the state waves' update MFMAs, and every LDS
@@ -325,18 +329,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
   } else {
     // =====================================================================
     // output waves: rows [16o, 16o + 16) of every chunk, the staging of K and V,
-    // alpha' V, and (wave 0 of the group) the gate rows one chunk ahead
+    // alpha' V one chunk ahead, and (wave 0 of the group) the gate rows
     // =====================================================================
     __builtin_amdgcn_s_setprio(2);
     const int t = tid - 64 * NSW;  // 0 .. NOT-1
     // ---- gate rows (output wave 0, one chunk ahead): row terms of the
-    // intra-chunk exponent, column terms, output row scales, the combined
+    // intra-chunk exponent (log2 of the score scale included), column terms,
+    // output row scales, the combined
     // stabiliser mc and alpha' = exp(a_t - m') e^{-G} of chunk c go to buffer
     // c & 1 with the chunk's renormalisation factor of the stored state, m',
     // the deferred log rescale G, the renormalise flag, and alpha' as bf16
     // hi (64) | lo (64) in token order (the n update's operand).
     const float* preph = a.prep + (size_t)bh * NC * PREP_STRIDE;
-    float gm = m_init, gG = 0.f;  // running m and G (gate wave only)
+    float gm = m_init, gG = 0.f;  // running m and G (every output wave runs the recurrence)
     auto prep_load = [&](int c, float (&pv)[5]) {
       const float* pc = preph + (size_t)c * PREP_STRIDE;
       pv[0] = pc[lane];
@@ -345,7 +350,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       pv[3] = pc[192 + lane];
       pv[4] = pc[256 + (lane & 1)];
     };
-    auto gate_rows = [&](int c, const float (&pv)[5]) {
+    // every output wave steps the recurrence and returns alpha' of its lane's token; only
+    // the writer (output wave 0) forms and stores the rows
+    auto gate_rows = [&](int c, const float (&pv)[5], bool writer) {
       float* gb = gbuf + (c & 1) * GROWS * 64;
       const float pg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[4]), 0));
       const float pamax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[4]), 1));
@@ -355,27 +362,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       float Gn = gG + lg;
       const bool renorm = Gn < RENORM;   // wave-uniform
       if (renorm) Gn = 0.f;
-      const float mb = b + gm;
-      const float mc = fmaxf(mb, b + cmu);
-      gb[lane] = (b - mc) * LOG2E;                       // row term of the intra-chunk exponent
-      gb[64 + lane] = pv[3];                             // column term
-      gb[128 + lane] = exp_(mb - mc + gG) * a.qk_scale;  // output row scale (deferred state rescale folded in)
-      gb[192 + lane] = mc;
-      const float al = exp_(av_ - m_next - Gn);          // alpha' = exp(a_t - m') e^{-G}
-      gb[256 + lane] = al;
-      const uint32_t ahi = pack_bf16(al, 0.f);
-      uint16_t* ar = reinterpret_cast<uint16_t*>(gb + 384);
-      ar[lane] = (uint16_t)ahi;
-      ar[64 + lane] = (uint16_t)pack_bf16(al - bf_lo(ahi), 0.f);
-      ar[128 + lane] = 0;  // the zero rows of the n update's A operand
-      if (lane == 0) {
-        gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
-        gb[321] = m_next;
-        gb[322] = Gn;
-        gb[323] = renorm ? 1.f : 0.f;
+      const float al = exp_(av_ - m_next - Gn);  // alpha' = exp(a_t - m') e^{-G}
+      if (writer) {
+        const float mb = b + gm;
+        const float mc = fmaxf(mb, b + cmu);
+        // row term of the intra-chunk exponent, with log2 of the score scale folded in
+        gb[lane] = (b - mc) * LOG2E + __builtin_amdgcn_logf(a.qk_scale);
+        gb[64 + lane] = pv[3];                             // column term
+        gb[128 + lane] = exp_(mb - mc + gG) * a.qk_scale;  // output row scale (deferred state rescale folded in)
+        gb[192 + lane] = mc;
+        const uint32_t ahi = pack_bf16(al, 0.f);
+        uint16_t* ar = reinterpret_cast<uint16_t*>(gb + 384);
+        ar[lane] = (uint16_t)ahi;
+        ar[64 + lane] = (uint16_t)pack_bf16(al - bf_lo(ahi), 0.f);
+        ar[128 + lane] = 0;  // the zero rows of the n update's A operand
+        if (lane == 0) {
+          gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
+          gb[321] = m_next;
+          gb[322] = Gn;
+          gb[323] = renorm ? 1.f : 0.f;
+        }
       }
       gm = m_next;
       gG = Gn;
+      return al;
     };
     // ---- K and V staging of the next chunk: piece u of thread t
     u32x4 Kst[NKO], Vst[2];
@@ -403,22 +413,29 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         *reinterpret_cast<u32x4*>(vn + (piece >> 3) * VN_PITCH + 16 * (piece & 7)) = Vst[u];
       }
     };
-    // ---- alpha' V of the chunk as bf16 hi | lo rows (B operand of the update)
-    auto alpha_v = [&](const float* gb) {
+    // ---- alpha' V of a chunk as bf16 hi | lo rows (B operand of the update), formed from
+    // the V pieces this thread stages (Vst, the same piece -> row map) while they are still
+    // in registers, one phase before they are written: alpha' of row r is lane r's value
+    u32x4 avh_r[2], avl_r[2];
+    auto alpha_v_regs = [&](float al) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int row = (u * NOT + t) >> 3;
+        const float ar = __shfl(al, row);
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) {
+          const float x0 = ar * bf_lo(Vst[u][c2]), x1 = ar * bf_hi(Vst[u][c2]);
+          avh_r[u][c2] = pack_bf16(x0, x1);
+          avl_r[u][c2] = pack_lo(avh_r[u][c2], x0, x1);
+        }
+      }
+    };
+    auto alpha_v_store = [&]() {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int piece = u * NOT + t, row = piece >> 3, cg = piece & 7;
-        const u32x4 x = *reinterpret_cast<const u32x4*>(vn + row * VN_PITCH + 16 * cg);
-        const float al = gb[256 + row];
-        u32x4 hv, lv;
-#pragma unroll
-        for (int c2 = 0; c2 < 4; ++c2) {
-          const float x0 = al * bf_lo(x[c2]), x1 = al * bf_hi(x[c2]);
-          hv[c2] = pack_bf16(x0, x1);
-          lv[c2] = pack_lo(hv[c2], x0, x1);
-        }
-        *reinterpret_cast<u32x4*>(av + row * AV_PITCH + 16 * cg) = hv;
-        *reinterpret_cast<u32x4*>(av + row * AV_PITCH + 128 + 16 * cg) = lv;
+        *reinterpret_cast<u32x4*>(av + row * AV_PITCH + 16 * cg) = avh_r[u];
+        *reinterpret_cast<u32x4*>(av + row * AV_PITCH + 128 + 16 * cg) = avl_r[u];
       }
     };
 
@@ -428,7 +445,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       constexpr int o = decltype(otag)::value;
       u32x4 Qf[KPD];
       const uint32_t qf_off = (uint32_t)(((16 * o + r16) * DQK + 8 * g) * 2);
-      float pv[5];  // gate prep of the next chunk (gate wave)
+      float pv[5];  // gate prep of the next chunk
       // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
       // 16-byte load; the K operand below uses the same contiguous k order)
       auto load_q = [&](int kc) {
@@ -439,21 +456,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       // prologue: the first chunk's tiles and gate rows, the second chunk's loads in flight
       load_kv(kc0);
       if (!STATES_ONLY) load_q(kc0);
-      if (o == 0) {
-        prep_load(kc0, pv);
-        gate_rows(kc0, pv);
-      }
+      prep_load(kc0, pv);
+      alpha_v_regs(gate_rows(kc0, pv, o == 0));
       store_kv();
       load_kv(kc0 + 1);
-      if (o == 0) prep_load(min(kc0 + 1, kc1 - 1), pv);
+      prep_load(min(kc0 + 1, kc1 - 1), pv);
       __syncthreads();  // B0
 
       for (int kc = kc0; kc < kc1; ++kc) {
         const float* gb = gbuf + (kc & 1) * GROWS * 64;
         const bf16_t* nbk = nbuf + (kc & 1) * 4 * SM::NB_PITCH;
-        // ---------------- phase A: alpha' V (its VALU work first, so that it can overlap the
-        // S product's MFMAs), S, M [V | 1]
-        alpha_v(gb);
+        // ---------------- phase A: alpha' V of the chunk (formed in the previous phase B) to
+        // LDS, S, M [V | 1]
+        alpha_v_store();
         f32x4 Hmv[NVX];
         float qn = 0.f;
         if (!STATES_ONLY) {
@@ -492,7 +507,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int j = 16 * jt + 4 * g + e;
-              Sacc[jt][e] = (j <= i) ? Sacc[jt][e] * a.qk_scale * exp2_(bli + ul[e]) : 0.f;
+              Sacc[jt][e] = (j <= i) ? Sacc[jt][e] * exp2_(bli + ul[e]) : 0.f;
             }
           }
 #pragma unroll
@@ -564,9 +579,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
             st16(rh, hoff + 64 * h2, out);
           }
         }
-        if (o == 0 && kc + 1 < kc1) gate_rows(kc + 1, pv);
+        if (kc + 1 < kc1) alpha_v_regs(gate_rows(kc + 1, pv, o == 0));  // before Vst is reloaded
         load_kv(kc + 2);
-        if (o == 0) prep_load(min(kc + 2, kc1 - 1), pv);
+        prep_load(min(kc + 2, kc1 - 1), pv);
         __syncthreads();  // B1
       }
     };
