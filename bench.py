@@ -590,15 +590,16 @@ def bwd_flops(B, NH, S, DQK, DV, L):
     return 2.0 * B * NH * NC * (5 * L * DQK * DV + 4 * L * L * DQK + 2 * L * L * DV)
 
 
+FUSED_PATH = ["states scan", "stats", "dC scan", "dV, dQ, dK", "gate gradients"]
+
+
 def bwd_bytes(B, NH, S, DQK, DV, L, esz=2):
-    """HBM bytes of the reference's custom backward with its per-chunk states materialised (bw.py:
-    matC_states recomputed, matDeltaC_states): q, k, v, dH, i, f read once; dq, dk, dv, di, df
-    written once; the NC entering states C written once and read once (dQ), the NC + 1 state
-    gradients dC written once and read twice (dV, dQ/dK), in float32."""
-    NC = S // L
-    io = B * NH * S * ((2 * DQK + 2 * DV) + (2 * DQK + DV) + 4) * esz  # q k v dH in, dq dk dv out, i f in, di df out
-    states = B * NH * (2 * NC + 3 * (NC + 1)) * DQK * DV * 4
-    return io + states
+    """HBM bytes of this design's backward on the path config 2 takes (bf16, 64-token chunks, DV 256
+    or 512): the algorithmic bytes of its five launches (bwd_kernel_bytes), with the per-chunk
+    states C and dC materialised once each (bw.py: matC_states recomputed, matDeltaC_states) in
+    the 24-bit packed form, written by the scans and read once by the fused dV / dQ / dK pass."""
+    kb = bwd_kernel_bytes(B, NH, S, DQK, DV, L, esz, st_esz=3)
+    return sum(kb[k] for k in FUSED_PATH)
 
 
 def bwd_io_bytes(B, NH, S, DQK, DV, esz=2):
@@ -619,16 +620,17 @@ BWD_KERNELS = {  # kernel-name key -> short name, for the trace / counter summar
 }
 
 
-def bwd_kernel_bytes(B, NH, S, DQK, DV, L, esz=2):
-    """Algorithmic HBM bytes of each backward launch (bf16 q/k/v/dH/gates, float32 states): what it
-    must read and write once, with the states and partials in the float32 workspace."""
+def bwd_kernel_bytes(B, NH, S, DQK, DV, L, esz=2, st_esz=4):
+    """Algorithmic HBM bytes of each backward launch (bf16 q/k/v/dH/gates): what it must read and
+    write once, with the per-chunk states at st_esz bytes per value (4: float32, the two-pass
+    launches; 3: the 24-bit packed states of the fused path) and the partials in float32."""
     NC, BNH, ndt, nvt = S // L, B * NH, -(-DQK // 64), -(-DV // 64)
-    st = NC * DQK * DV * 4
+    st = NC * DQK * DV * st_esz
     g = 2 * S * esz  # i, f
     return {
         "states scan": BNH * (S * (DQK + DV) * esz + g + st + NC * (DQK + 1) * 4 + (DQK * DV + DQK + 1) * 4),
         "stats": BNH * (2 * S * DQK * esz + g + NC * (DQK + 1) * 4 + 2 * S * 4),
-        "dC scan": BNH * (S * (DQK + DV) * esz + g + 2 * S * 4 + NC * 4 + DQK * DV * 4 + st + DQK * DV * 4),
+        "dC scan": BNH * (S * (DQK + DV) * esz + g + 2 * S * 4 + NC * 4 + DQK * DV * 4 + st + DQK * DV * st_esz),
         "dV": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + st + g + 2 * S * 4 + S * DV * esz + S * nvt * 4),
         "dQ, dK": BNH * (2 * S * DQK * esz + 2 * S * DV * esz + 2 * st + g + 2 * S * 4 + 2 * S * DQK * esz
                          + S * ndt * 4),
@@ -902,9 +904,11 @@ def summarize_pmc(fetch_dir, write_dir):
             "gate_prep_kernel": ("cfg2 chunkwise gate prep",
                                  2 * CFG2.B * CFG2.NH * CFG2.S * 2 + CFG2.B * CFG2.NH * (CFG2.S // 64) * 258 * 4),
             **layer_stage_work()}
+    # the fused path's launches keep C and dC packed (3 bytes a value), the two-pass ones float32
     bwb = bwd_kernel_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV, 64)
+    bwp = bwd_kernel_bytes(CFG2.B, CFG2.NH, CFG2.S, CFG2.DQK, CFG2.DV, 64, st_esz=3)
     for k, short in BWD_KERNELS.items():
-        work[k] = (f"cfg2 chunkwise backward: {short}", bwb[short])
+        work[k] = (f"cfg2 chunkwise backward: {short}", (bwp if short in FUSED_PATH else bwb)[short])
     out = {"calibration": {"kernel": SOFT_CAP_KERNEL, "bytes_read": sc_bytes, "bytes_written": sc_bytes,
                            "fetch_scale": f_scale, "write_scale": w_scale},
            "kernels": {}}

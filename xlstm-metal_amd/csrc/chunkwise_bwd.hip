@@ -28,7 +28,9 @@
 // [BNH][NC](...), the final state, m_comb and the divisor [BNH][S], dC
 // [BNH][NC + 1][DQK][DV] (index k: the gradient of the state after chunk k - 1;
 // 0 is dC_initial), the dF partials [BNH][S][ceil(DQK/64)] and the dI partials
-// [BNH][S][ceil(DV/64)].
+// [BNH][S][ceil(DV/64)].  On the path of the fused bf16 dV / dQ / dK pass the C and
+// dC states are kept as their upper 24 bits (pack24 below), in the first three
+// quarters of their regions.
 #include "chunkwise.h"
 #include "mfma_bf16.h"
 
@@ -41,6 +43,24 @@ using namespace xl::mfma;  // bf16 MFMA building blocks (mfma_bf16.h)
 constexpr int BW_THREADS = 256;
 constexpr int BW_T = 64;   // DQK / DV tile
 constexpr int BW_KT = 32;  // contraction tile
+
+// Per-chunk states C and dC on the fused bf16 path, 4 values in 12 bytes: the upper 24 bits of
+// each float32 (sign, exponent, 15 mantissa bits = 16 significant bits, what the bf16 hi + lo
+// pair that consumes them carries), rounded to nearest by adding half of the dropped byte.
+// A quarter less state traffic for the scans (which are bound by their state stores) and
+// the pass that reads them.
+typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
+__device__ __forceinline__ u32x3a pack24(f32x4 x) {
+  uint32_t b[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) b[e] = __float_as_uint(x[e]) + 0x80u;
+  return u32x3a{(b[0] >> 8) | ((b[1] >> 8) << 24), (b[1] >> 16) | ((b[2] >> 8) << 16),
+                (b[2] >> 24) | (b[3] & 0xffffff00u)};
+}
+__device__ __forceinline__ f32x4 unpack24(u32x3a w) {
+  return f32x4{__uint_as_float(w[0] << 8), __uint_as_float(((w[0] >> 24) << 8) | (w[1] << 16)),
+               __uint_as_float(((w[1] >> 16) << 8) | (w[2] << 24)), __uint_as_float(w[2] & 0xffffff00u)};
+}
 
 // DPP moves inside a row of 16 lanes (VALU only, no LDS traffic)
 template <int CTRL>
@@ -966,7 +986,7 @@ constexpr int SST_P = SC_V + 4;  // floats per LDS row of a state store (conflic
 
 // two workgroups per CU (at most 256 registers per lane): the scans are bound by their state
 // stores, and two workgroups keep more of them in flight
-template <typename TG, int L, int NRT, bool REV>
+template <typename TG, int L, int NRT, bool REV, bool PK>
 __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     const bf16_t* __restrict__ X, const bf16_t* __restrict__ Y, const TG* __restrict__ ig,
     const TG* __restrict__ fg, const float* __restrict__ s0, const float* __restrict__ n0,
@@ -1009,8 +1029,9 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
   // 256-byte rows (16 lanes per row, 128-byte lines): straight from the accumulators every row
   // piece would be 64 bytes, and the stores, sent to L2 as 64-byte requests, capped the scans'
   // write rate at about 2.8 TB/s.  Only this wave touches its rows: no barrier.
+  // With PK the per-chunk states (slots) go out as pack24 (12-byte pieces, 192-byte rows).
   float* const st_w = sSt[w];
-  auto store_state = [&](float* dst) {
+  auto store_state = [&](float* dst, bool packed) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
@@ -1019,9 +1040,18 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
 #pragma unroll
     for (int k = 0; k < 4 * NRT; ++k) {
       const int row = 4 * k + (lane >> 4), col = 4 * (lane & 15);
-      *reinterpret_cast<f32x4*>(dst + (size_t)(row0 + row) * DV + v0 + col) =
-          *reinterpret_cast<const f32x4*>(st_w + row * SST_P + col);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(st_w + row * SST_P + col);
+      const size_t e = (size_t)(row0 + row) * DV + v0 + col;
+      if (packed)
+        *reinterpret_cast<u32x3a*>(reinterpret_cast<char*>(dst) + 3 * e) = pack24(x);
+      else
+        *reinterpret_cast<f32x4*>(dst + e) = x;
     }
+  };
+  // slot j of this head: float32 [DQKf][DV], or its pack24 form in the first 3/4 of that room
+  auto slot_ptr = [&](int j) {
+    const size_t off = ((size_t)bh * nslots + j) * DQKf * DV;
+    return PK ? reinterpret_cast<float*>(reinterpret_cast<char*>(Sst) + 3 * off) : Sst + off;
   };
   // n (forward, the first column tile's workgroups, which write whole n rows): one more 16 x 16
   // accumulator tile per row tile, whose A operand is columns 64.. of the staged hi rows: coef_t
@@ -1132,7 +1162,7 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     }
     if (it + 1 < NC) fetch(REV ? kc - 1 : kc + 1);
     __syncthreads();
-    store_state(Sst + ((size_t)bh * nslots + slot) * DQKf * DV);
+    store_state(slot_ptr(slot), PK);
     if (owns_n) store_n(nst + sidx * DQKf);
     if (!REV && vt == 0 && rs == 0 && tid == 0) mst[sidx] = m_in;
 #pragma unroll
@@ -1171,12 +1201,12 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     __syncthreads();
   }
   if (!REV) {  // the final state (the forward's last states may not be asked for)
-    if (sfin) store_state(sfin + (size_t)bh * DQKf * DV);
+    if (sfin) store_state(sfin + (size_t)bh * DQKf * DV, false);
     if (owns_n && nfin) store_n(nfin + (size_t)bh * DQKf);
     if (vt == 0 && rs == 0 && tid == 0 && mfin) mfin[bh] = m;
   } else {
-    store_state(Sst + (size_t)bh * nslots * DQKf * DV);
-    if (s_init) store_state(s_init + (size_t)bh * DQKf * DV);
+    store_state(slot_ptr(0), PK);
+    if (s_init) store_state(s_init + (size_t)bh * DQKf * DV, false);
   }
 }
 
@@ -1961,12 +1991,13 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
   const int blk = xcd_contiguous(blockIdx.x, gridDim.x);
   const int bh = blk / NC, kc = blk - bh * NC;
   const size_t S = (size_t)NC * L, row0 = (size_t)bh * S + (size_t)kc * L, sidx = (size_t)bh * NC + kc;
-  const float* cbase = Cst + sidx * DQK * DV;                                // C_{k-1}
-  const float* dcbase = dCst + ((size_t)bh * (NC + 1) + kc + 1) * DQK * DV;  // dC_k
+  // C_{k-1} and dC_k as pack24 (3 bytes per value)
+  const char* cbase = reinterpret_cast<const char*>(Cst) + 3 * (sidx * DQK * DV);
+  const char* dcbase = reinterpret_cast<const char*>(dCst) + 3 * (((size_t)bh * (NC + 1) + kc + 1) * DQK * DV);
 
   // C / dC block (dt, vb) in two register slots (row p / 16, 4 columns at 4 (p % 16)); dH, V of
   // a v-block in one (row tid / 8, 8 columns at 8 (tid % 8))
-  f32x4 pc[2][2], pd[2][2];
+  u32x3a pc[2][2], pd[2][2];
   u32x4 ph, pv;
   auto fetch = [&](auto slot, int st) {  // block st = vb NDT + dt
     constexpr int sl = decltype(slot)::value;
@@ -1975,9 +2006,9 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int p = u * FV_THREADS + tid;
-      const size_t off = (size_t)(64 * dt + (p >> 4)) * DV + 64 * vb + (p & 15) * 4;
-      pc[sl][u] = *reinterpret_cast<const f32x4*>(cbase + off);
-      pd[sl][u] = *reinterpret_cast<const f32x4*>(dcbase + off);
+      const size_t off = 3 * ((size_t)(64 * dt + (p >> 4)) * DV + 64 * vb + (p & 15) * 4);
+      pc[sl][u] = *reinterpret_cast<const u32x3a*>(cbase + off);
+      pd[sl][u] = *reinterpret_cast<const u32x3a*>(dcbase + off);
     }
   };
   auto fetch_hv = [&](int vb) {
@@ -2083,8 +2114,8 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
       const auto slot = std::integral_constant<int, sl>{};
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        stage4(sCh, sCl, u * FV_THREADS + tid, pc[sl][u]);
-        stage4(sDh, sDl, u * FV_THREADS + tid, pd[sl][u]);
+        stage4(sCh, sCl, u * FV_THREADS + tid, unpack24(pc[sl][u]));
+        stage4(sDh, sDl, u * FV_THREADS + tid, unpack24(pd[sl][u]));
       }
       __syncthreads();  // the block's tiles (and, at dt 0, dH / V of the v-block)
       fetch(slot, st + 2);
@@ -2252,7 +2283,7 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 }
 
 
-template <typename TQ, typename TG, int L, bool REV>
+template <typename TQ, typename TG, int L, bool REV, bool PK = false>
 int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* s0, const float* n0,
                 const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst, float* sfin,
                 float* nfin, float* mfin, float* s_init, int BNH, int NC, int DV, float qk_scale, hipStream_t st) {
@@ -2268,11 +2299,13 @@ int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, c
     return check_launch(REV ? "xl_mlstm_chunkwise_bwd(dC scan)" : "xl_mlstm_chunkwise_bwd(states scan)");
   };
   if constexpr (std::is_same<TQ, bf16_t>::value && L % 32 == 0) {  // bf16 operands, static LDS
-    if (DQK == 64) return go(bw_scan_bf16_kernel<TG, L, 1, REV>, 0, 1);
-    return go(bw_scan_bf16_kernel<TG, L, 2, REV>, 0, DQK / 128);
+    if (DQK == 64) return go(bw_scan_bf16_kernel<TG, L, 1, REV, PK>, 0, 1);
+    return go(bw_scan_bf16_kernel<TG, L, 2, REV, PK>, 0, DQK / 128);
+  } else {
+    static_assert(!PK, "pack24 states come from the bf16 scans only");
+    if (DQK == 64) return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1), 1);
+    return go(bw_scan_kernel<TQ, TG, L, 2, REV>, scan_smem<TQ, L>(2), DQK / 128);
   }
-  if (DQK == 64) return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1), 1);
-  return go(bw_scan_kernel<TQ, TG, L, 2, REV>, scan_smem<TQ, L>(2), DQK / 128);
 }
 
 template <typename TQ, typename TG, int L>
@@ -2290,9 +2323,19 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   const TG *ig = (const TG*)F.i, *fg = (const TG*)F.f;
   // the chunk scans on the matrix cores when the state tiles fit their layout
   const bool scan_mfma = F.DV % SC_V == 0 && (F.DQK == 64 || F.DQK == 128 || F.DQK == 256);
-  int rc = scan_mfma ? launch_scan<TQ, TG, L, false>(F.DQK, k, v, ig, fg, F.c0, F.n0, F.m0, nullptr, nullptr, Cst,
-                                                     nst, mst, cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s)
-                     : chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
+  // the fused dV / dQ / dK pass (bf16, 64-token chunks, DV 256 or 512) reads C and dC as pack24
+  constexpr bool fused_types = std::is_same<TQ, bf16_t>::value && L == 64;
+  const bool fused_dvqk = fused_types && scan_mfma && (F.DV == 256 || F.DV == 512);
+  int rc = XL_OK;
+  if constexpr (fused_types) {
+    if (fused_dvqk)
+      rc = launch_scan<TQ, TG, L, false, true>(F.DQK, k, v, ig, fg, F.c0, F.n0, F.m0, nullptr, nullptr, Cst, nst, mst,
+                                               cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s);
+  }
+  if (!fused_dvqk)
+    rc = scan_mfma ? launch_scan<TQ, TG, L, false>(F.DQK, k, v, ig, fg, F.c0, F.n0, F.m0, nullptr, nullptr, Cst,
+                                                   nst, mst, cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s)
+                   : chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
   if (rc) return rc;
   bool stats_mfma = false;
   if constexpr (std::is_same<TQ, bf16_t>::value && L == 64) {
@@ -2309,7 +2352,13 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
     hipLaunchKernelGGL((bw_stats_kernel<TQ, TG, L>), dim3((unsigned)(BNH * NC)), dim3(BW_THREADS), 0, s, q, k, ig, fg,
                        nst, mst, vm, vn, NC, F.DQK, F.qk_scale, F.eps);
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(stats)"))) return rc;
-  if (scan_mfma) {
+  if constexpr (fused_types) {
+    if (fused_dvqk)
+      rc = launch_scan<TQ, TG, L, true, true>(F.DQK, q, dh, ig, fg, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr,
+                                              mst, nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
+  }
+  if (fused_dvqk) {
+  } else if (scan_mfma) {
     rc = launch_scan<TQ, TG, L, true>(F.DQK, q, dh, ig, fg, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr, mst,
                                       nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
   } else {
@@ -2319,8 +2368,8 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   }
   if (rc) return rc;
   // dV, dQ and dK in one pass for bf16 with DV 256 or 512 (C and dC streamed once)
-  if constexpr (std::is_same<TQ, bf16_t>::value && L == 64) {
-    if (scan_mfma && (F.DV == 256 || F.DV == 512)) {
+  if constexpr (fused_types) {
+    if (fused_dvqk) {
       auto go = [&](auto kern, size_t smem) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess)
