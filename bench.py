@@ -610,9 +610,9 @@ def bwd_io_bytes(B, NH, S, DQK, DV, esz=2):
 
 
 BWD_KERNELS = {  # kernel-name key -> short name, for the trace / counter summaries of the backward
-    "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, false>": "states scan",
+    "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, false, true>": "states scan",
     "bw_stats_bf16_kernel": "stats",
-    "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, true>": "dC scan",
+    "bw_scan_bf16_kernel<xl::bf16_t, 64, 2, true, true>": "dC scan",
     "bw_dv_bf16_kernel": "dV",
     "bw_dqk_bf16_kernel": "dQ, dK",
     "bw_dvqk_bf16_kernel": "dV, dQ, dK",

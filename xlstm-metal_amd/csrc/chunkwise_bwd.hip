@@ -48,7 +48,13 @@ constexpr int BW_KT = 32;  // contraction tile
 // each float32 (sign, exponent, 15 mantissa bits = 16 significant bits, what the bf16 hi + lo
 // pair that consumes them carries), rounded to nearest by adding half of the dropped byte.
 // A quarter less state traffic for the scans (which are bound by their state stores) and
-// the pass that reads them.
+// the pass that reads them.  Packed states are blocked by 64 columns: element (row, col) of a
+// [DQK][DV] state sits at byte ((col / 64) DQK + row) 192 + (col % 64) 3, so a 64 x 64 block is
+// 12 KB contiguous and every access covers whole 128-byte lines (row-major 192-byte rows would
+// split lines between neighbouring column blocks, read at different times).
+__host__ __device__ constexpr size_t pk24_offset(int row, int col, int DQK) {
+  return ((size_t)(col >> 6) * DQK + row) * 192 + (size_t)(col & 63) * 3;
+}
 typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
 __device__ __forceinline__ u32x3a pack24(f32x4 x) {
   uint32_t b[4];
@@ -1029,7 +1035,7 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
   // 256-byte rows (16 lanes per row, 128-byte lines): straight from the accumulators every row
   // piece would be 64 bytes, and the stores, sent to L2 as 64-byte requests, capped the scans'
   // write rate at about 2.8 TB/s.  Only this wave touches its rows: no barrier.
-  // With PK the per-chunk states (slots) go out as pack24 (12-byte pieces, 192-byte rows).
+  // With PK the per-chunk states (slots) go out as pack24 (12-byte pieces of 192-byte block rows).
   float* const st_w = sSt[w];
   auto store_state = [&](float* dst, bool packed) {
 #pragma unroll
@@ -1041,11 +1047,10 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     for (int k = 0; k < 4 * NRT; ++k) {
       const int row = 4 * k + (lane >> 4), col = 4 * (lane & 15);
       const f32x4 x = *reinterpret_cast<const f32x4*>(st_w + row * SST_P + col);
-      const size_t e = (size_t)(row0 + row) * DV + v0 + col;
       if (packed)
-        *reinterpret_cast<u32x3a*>(reinterpret_cast<char*>(dst) + 3 * e) = pack24(x);
+        *reinterpret_cast<u32x3a*>(reinterpret_cast<char*>(dst) + pk24_offset(row0 + row, v0 + col, DQKf)) = pack24(x);
       else
-        *reinterpret_cast<f32x4*>(dst + e) = x;
+        *reinterpret_cast<f32x4*>(dst + (size_t)(row0 + row) * DV + v0 + col) = x;
     }
   };
   // slot j of this head: float32 [DQKf][DV], or its pack24 form in the first 3/4 of that room
@@ -2006,7 +2011,7 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int p = u * FV_THREADS + tid;
-      const size_t off = 3 * ((size_t)(64 * dt + (p >> 4)) * DV + 64 * vb + (p & 15) * 4);
+      const size_t off = pk24_offset(64 * dt + (p >> 4), 64 * vb + (p & 15) * 4, DQK);
       pc[sl][u] = *reinterpret_cast<const u32x3a*>(cbase + off);
       pd[sl][u] = *reinterpret_cast<const u32x3a*>(dcbase + off);
     }
