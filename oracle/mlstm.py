@@ -367,7 +367,8 @@ def arbitrary_length(q, k, v, f, i, c_initial=None, n_initial=None, m_initial=No
 
 
 def mlstm_chunkwise_bw(matQ, matK, matV, vecI, vecF, matDeltaH, matC_initial=None, vecN_initial=None,
-                       scaM_initial=None, matDeltaC_last=None, qk_scale=None, chunk_size=64, eps=1e-6):
+                       scaM_initial=None, matDeltaC_last=None, qk_scale=None, chunk_size=64, eps=1e-6,
+                       state_round=None):
     """The reference's custom chunkwise backward, ``VTN/bw.py:198-352``.
 
     States are recomputed from the inputs (``:242-258``) and the forward's
@@ -381,7 +382,9 @@ def mlstm_chunkwise_bw(matQ, matK, matV, vecI, vecF, matDeltaH, matC_initial=Non
     ``Bbar = exp(b + m_c - m)``.  Gates (``:330-338``): ``dF = sigmoid(-f)`` times the
     suffix sum over the sequence of ``sum_d (q dq - k dk)``, ``dI = sum_d v dv``.
     Returns ``(dq, dk, dv, di, df, dc0 | None, dn0 | None, dm0 | None)``; dn0 and dm0
-    are zeros, as there (``:340-342``).
+    are zeros, as there (``:340-342``).  ``state_round`` (tests only), if given, is applied to
+    the per-chunk states C and dC where the per-chunk products consume them, to model a storage
+    format of the materialised states.
     """
     B, NH, S, DHQK = matQ.shape
     DHV = matV.shape[-1]
@@ -398,6 +401,8 @@ def mlstm_chunkwise_bw(matQ, matK, matV, vecI, vecF, matDeltaH, matC_initial=Non
                                     m_states[:, :, :-1], vecIr, vecB, qk_scale, chunk_size=L, num_chunks=NC,
                                     eps=eps)
     Cs = C_states.reshape(B, NH, NC + 1, DHQK, DHV)
+    if state_round is not None:
+        Cs = state_round(Cs)
     dH_t = matDeltaH / (n_out + eps)[..., None]  # dH~, (B, NH, S, DHV)
 
     def chunk(x, c):
@@ -409,7 +414,7 @@ def mlstm_chunkwise_bw(matQ, matK, matV, vecI, vecF, matDeltaH, matC_initial=Non
           else torch.zeros((B, NH, DHQK, DHV), dtype=matQ.dtype, device=matQ.device))
     dC_after = [None] * NC  # gradient of the state after chunk c
     for c in range(NC - 1, -1, -1):
-        dC_after[c] = dC
+        dC_after[c] = dC if state_round is None else state_round(dC)
         m_c, m_n = m_states[:, :, c], m_states[:, :, c + 1]
         gbar = torch.exp(g[:, :, c] + m_c - m_n)[:, :, None, None]
         bbar = torch.exp(vecB[:, :, c] + m_c[..., None] - chunk(m_out, c))[..., None]

@@ -127,3 +127,33 @@ def test_state_preserving_padding(S, pad):
     for nm, u, w in zip(["dq", "dk", "dv", "di", "df"], got[:5], want[:5]):
         _close(u[:, :, :S], w, nm, tol=1e-10)
     _close(got[5], want[5], "dc0", tol=1e-10)
+
+
+def _round24(x):
+    """The fused bf16 path's packed states (csrc/chunkwise_bwd.hip pack24): the upper 24 bits of
+    each float32, rounded to nearest by adding half of the dropped byte."""
+    a = x.to(torch.float32).contiguous().view(torch.int32)
+    return ((a + 0x80) & -256).view(torch.float32).to(x.dtype)
+
+
+def test_packed_state_rounding():
+    """The GPU backward's fused path keeps the per-chunk C and dC as their upper 24 bits.  In
+    float64 that moves every gradient by far less than the GPU tests' bar (2e-3 of the largest
+    value beyond one output rounding), while bf16 states (8 significant bits) move dF past it:
+    the packed format's precision is a measured choice, not a free one."""
+    B, NH, S, DQK, DV, L = 1, 1, 512, 128, 128, 64
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, NH, S, DQK, generator=g, dtype=F64)
+    k = torch.randn(B, NH, S, DQK, generator=g, dtype=F64)
+    v = torch.randn(B, NH, S, DV, generator=g, dtype=F64)
+    i = torch.randn(B, NH, S, generator=g, dtype=F64)
+    f = torch.randn(B, NH, S, generator=g, dtype=F64) + 3.0
+    dH = torch.randn(B, NH, S, DV, generator=g, dtype=F64)
+    want = om.mlstm_chunkwise_bw(q, k, v, i, f, dH, chunk_size=L)
+    p24 = om.mlstm_chunkwise_bw(q, k, v, i, f, dH, chunk_size=L, state_round=_round24)
+    bf16 = om.mlstm_chunkwise_bw(q, k, v, i, f, dH, chunk_size=L,
+                                 state_round=lambda t: t.to(torch.bfloat16).to(t.dtype))
+    rel = lambda a, b: float((a - b).abs().max() / b.abs().max())
+    for nm, u, w in zip(["dq", "dk", "dv", "di", "df"], p24[:5], want[:5]):
+        assert rel(u, w) <= 1e-4, f"{nm}: packed states move it by {rel(u, w):.2e} of its max"
+    assert max(rel(u, w) for u, w in zip(bf16[:5], want[:5])) > 2e-3
