@@ -23,7 +23,8 @@
  *    then available from xl_last_error() on the calling thread.
  *  - States (C, n, m) are always float32.  q/k/v/z and gates may be float32,
  *    bfloat16 or float16 (XL_DTYPE_*); arithmetic is float32, MFMA operands
- *    of the fused chunkwise kernel are bfloat16.
+ *    of the single-pass chunkwise kernels are q/k/v's 16-bit type (float32
+ *    operands as hi + lo pairs of it).
  */
 #ifndef XLSTM_HIP_H
 #define XLSTM_HIP_H
@@ -51,9 +52,10 @@ enum xl_status {
 enum xl_chunkwise_algo {
   XL_CHUNKWISE_AUTO = 0,     /* pipelined when supported, else two-pass */
   XL_CHUNKWISE_TWO_PASS = 1, /* states kernel + output kernel, float32 math */
-  XL_CHUNKWISE_FUSED = 2,    /* single pass, bf16 MFMA, states in registers */
-  XL_CHUNKWISE_PIPELINED = 3 /* XL_CHUNKWISE_FUSED's math and shapes; each chunk's state update
-                                overlaps the previous outputs (two-phase schedule) */
+  XL_CHUNKWISE_FUSED = 2,    /* single pass, bf16 MFMA, states in registers (bf16 q/k/v only) */
+  XL_CHUNKWISE_PIPELINED = 3 /* XL_CHUNKWISE_FUSED's math and shapes, bf16 or f16 q/k/v; each
+                                chunk's state update overlaps the previous outputs (two-phase
+                                schedule) */
 };
 
 /* ABI version of the loaded library (XL_ABI_VERSION at build time). */
@@ -110,8 +112,8 @@ int xl_mlstm_step_copy_ceiling(const float* c_old, float* c_new, int B, int NH, 
  *   h [B,NH,S,DV] (dtype_qkv); c_last, n_last, m_last float32 (all NULL when
  *   the last states are not wanted).
  * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.  With algo =
- * XL_CHUNKWISE_FUSED or XL_CHUNKWISE_PIPELINED (bf16 q/k/v, DQK 128 or 256,
- * DV % 64 == 0) any S >= 1 is accepted: the fused kernel runs 64-token chunks and a ragged last chunk
+ * XL_CHUNKWISE_FUSED (bf16 q/k/v) or XL_CHUNKWISE_PIPELINED (bf16 or f16 q/k/v),
+ * DQK 128 or 256 and DV % 64 == 0, any S >= 1 is accepted: the kernel runs 64-token chunks and a ragged last chunk
  * (the forward is chunk-size invariant, so L only names the reference's
  * chunking there).
  * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned

@@ -236,8 +236,11 @@ def test_chunkwise_algorithm_query(lib):
     assert chunkwise_algorithm(4, 8, 8192, 256, 512, 128, torch.bfloat16) == "pipelined"
     assert chunkwise_algorithm(1, 8, 256, 256, 512, 64, torch.float32) == "two_pass"
     assert chunkwise_algorithm(4, 8, 8192, 256, 512, 64, torch.bfloat16, algo="two_pass") == "two_pass"
-    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 2, 0) == 1  # float16 q/k/v
-    assert b"bfloat16" in lib.xl_last_error()
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 2, 0) == 3  # float16 q/k/v: pipelined
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 2, 2) == -2  # the fused schedule is bf16 only
+    assert b"bfloat16" in lib.xl_last_error() and b"pipelined" in lib.xl_last_error()
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 0, 0) == 1  # float32 q/k/v
+    assert b"bfloat16 or float16" in lib.xl_last_error()
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 96, 512, 64, 1, 0) == 1  # DQK 96
     assert b"DQK" in lib.xl_last_error()
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 100, 256, 512, 64, 1, 0) == -1  # S % L

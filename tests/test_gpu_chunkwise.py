@@ -15,7 +15,9 @@
   bf16 path against the oracle's any-S driver;
 * every single-pass case runs on both single-pass kernels: "fused" and
   "pipelined" (the two-phase state/output-wave schedule of the same chunk
-  algorithm), each against the oracle.
+  algorithm), each against the oracle;
+* float16 q/k/v on the pipelined kernel (f16 MFMA operands): any S, initial
+  states, the sequence split, and inputs where f16's range matters.
 """
 
 import pytest
@@ -312,3 +314,80 @@ def test_fused_sequence_split(gpu_case, B, NH, S, DQK, DV, with_state, algo):
     hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got.cpu(), want, torch.bfloat16, f"{algo} split B{B} NH{NH} S{S} DQK{DQK} DV{DV} {name}")
+
+
+@pytest.mark.parametrize("B,NH,S,DQK,DV,with_state", [
+    (1, 2, 256, 256, 128, False), (1, 2, 256, 256, 128, True), (2, 2, 320, 128, 64, True),
+    (1, 1, 100, 256, 64, True),     # ragged last chunk
+    (1, 2, 1000, 128, 128, False),
+    (1, 1, 5, 256, 64, True),
+    (1, 8, 2048, 256, 512, True),   # config 3's heads: the sequence split into 4 segments
+])
+def test_f16_pipelined(gpu_case, B, NH, S, DQK, DV, with_state):
+    """float16 q/k/v run the pipelined kernel (f16 MFMA operands, float32 operands as f16 hi + lo
+    pairs, the stored state renormalised at every chunk instead of the deferred rescale): h and
+    the last C, n, m against the oracle's any-S driver on the same f16 inputs, any S, with and
+    without initial states and with the sequence split."""
+    import xlstm_hip
+    x, st = _inputs(B, NH, S, DQK, DV, torch.float16, seed=S + DQK + 1, with_state=with_state)
+    if S % 64 == 0:
+        assert xlstm_hip.chunkwise_algorithm(B, NH, S, DQK, DV, 64, torch.float16) == "pipelined"
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=64,
+                                             algo="pipelined")
+    assert h.dtype == torch.float16
+    q, k, v, i, f = (t.float() for t in x)
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got.cpu(), want, torch.float16, f"f16 B{B} NH{NH} S{S} DQK{DQK} DV{DV} state={with_state} {name}")
+
+
+@pytest.mark.parametrize("case", ["wide_values", "strong_forget", "weak_forget"])
+def test_f16_pipelined_ranges(gpu_case, case):
+    """The f16 kernel where its range matters: q, k, v scaled up (|v| ~ 8, |k| ~ 2: the state and
+    alpha' V far from 1), forget gates near 0 (every chunk renormalises a large decay) and near
+    saturation (the state keeps its whole history)."""
+    import xlstm_hip
+    B, NH, S, DQK, DV = 1, 2, 640, 256, 128
+    g = torch.Generator().manual_seed(99)
+    q = torch.randn(B, NH, S, DQK, generator=g) / DQK ** 0.5
+    k = torch.randn(B, NH, S, DQK, generator=g)
+    v = torch.randn(B, NH, S, DV, generator=g)
+    i = torch.randn(B, NH, S, generator=g)
+    f = torch.randn(B, NH, S, generator=g) + 3
+    if case == "wide_values":
+        k, v = 2 * k, 8 * v
+    elif case == "strong_forget":
+        f = torch.randn(B, NH, S, generator=g) - 2
+    else:
+        f = torch.randn(B, NH, S, generator=g) + 8
+    x = [t.to(torch.float16) for t in (q, k, v, i, f)]
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), return_last_states=True, chunk_size=64, algo="pipelined")
+    assert bool(torch.isfinite(h).all()) and bool(torch.isfinite(C).all())
+    hr, (Cr, nr, mr) = _oracle(x, (None, None, None), 64)
+    scale = max(1.0, float(hr.abs().max()) / 16)  # wide values: the bar relative to |h| ~ 16
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        e = lowp_excess(got.cpu(), want) / (scale if name in ("h", "C") else 1.0)
+        assert e <= LOWP_ABS, f"f16 {case} {name}: {e:.3e}"
+
+
+def test_f16_fused_schedule_rejected(gpu_case):
+    """The fused schedule is bf16 only: algo="fused" with f16 inputs names the pipelined one."""
+    import xlstm_hip
+    x, _ = _inputs(1, 2, 128, 256, 64, torch.float16, seed=5)
+    with pytest.raises(Exception, match="pipelined"):
+        xlstm_hip.mlstm_chunkwise(*_gpu(x), algo="fused")
+
+
+@pytest.mark.parametrize("S", [37, 100, 1000])
+def test_backend_any_length_f16(gpu_case, S):
+    """mLSTMBackend inference on f16 inputs: one pipelined call for any S, against the oracle's
+    any-S driver on the same f16 inputs."""
+    import xlstm_hip
+    x, _ = _inputs(1, 2, S, 256, 128, torch.float16, seed=S + 7)
+    backend = xlstm_hip.mLSTMBackend(xlstm_hip.mLSTMBackendConfig(mode="inference", chunk_size=64))
+    h, (C, n, m) = backend(*_gpu(x))
+    assert h.dtype == torch.float16
+    q, k, v, i, f = (t.float() for t in x)
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, chunk_size=64)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got.cpu(), want, torch.float16, f"backend any-S f16 S={S} {name}")

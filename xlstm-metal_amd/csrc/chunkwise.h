@@ -58,9 +58,10 @@ int chunkwise_states_pass(const ChunkwiseArgs& a, float* Cst, float* nst, float*
 // otherwise XL_OK or a negative XL_ERR_* code.
 int chunkwise_states_mfma(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst);
 
-// Fused single-pass algorithm, bf16 MFMA.  fused_supported() says whether a
-// shape/dtype is covered (and why not, in `why`, when it is not).
-bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why);
+// The single-pass algorithms.  fused_supported() says whether a shape/dtype is covered by the
+// pipelined schedule (pipelined: bf16 or f16 q/k/v) or the fused one (bf16 only), and why not,
+// in `why`, when it is not.
+bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why, bool pipelined);
 // Workspace of the fused algorithm: the gate prep (1280 bytes per 64-token chunk of every
 // head) and, when the sequence is split into segments (few heads), two sets of per-segment
 // states.  max_segments 1 disables the split.

@@ -1,6 +1,6 @@
 // C-ABI entry point of the chunkwise mLSTM forward: validation and the choice
-// between the single-pass bf16-MFMA kernels (pipelined schedule by default, the
-// fused schedule on request) and the two-pass kernels.
+// between the single-pass MFMA kernels (the pipelined schedule by default, for bf16
+// or f16 q/k/v; the fused schedule, bf16 only, on request) and the two-pass kernels.
 #include "chunkwise.h"
 
 namespace xl {
@@ -41,13 +41,13 @@ int chunkwise_check_args(const ChunkwiseArgs& a, int algo) {
 
 static int pick(const ChunkwiseArgs& a, int algo, int* chosen) {
   const char* why = nullptr;
-  const bool fused_ok = chunkwise_fused_supported(a, &why);
-  if (single_pass(algo) && !fused_ok)
+  const bool pipe_ok = chunkwise_fused_supported(a, &why, algo != XL_CHUNKWISE_FUSED);
+  if (single_pass(algo) && !pipe_ok)
     return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_fwd: %s algorithm unsupported here: %s",
                      algo == XL_CHUNKWISE_FUSED ? "fused" : "pipelined", why);
   *chosen = (algo == XL_CHUNKWISE_TWO_PASS) ? XL_CHUNKWISE_TWO_PASS
             : single_pass(algo)             ? algo
-            : fused_ok                      ? XL_CHUNKWISE_PIPELINED
+            : pipe_ok                       ? XL_CHUNKWISE_PIPELINED
                                             : XL_CHUNKWISE_TWO_PASS;
   return XL_OK;
 }
@@ -87,7 +87,7 @@ extern "C" int xl_mlstm_chunkwise_algo(int B, int NH, int S, int DQK, int DV, in
   const int rc = pick(a, algo, &chosen);
   if (rc) return rc;
   const char* why = nullptr;
-  if (chosen == XL_CHUNKWISE_TWO_PASS && algo == XL_CHUNKWISE_AUTO && !chunkwise_fused_supported(a, &why))
+  if (chosen == XL_CHUNKWISE_TWO_PASS && algo == XL_CHUNKWISE_AUTO && !chunkwise_fused_supported(a, &why, true))
     set_error(XL_OK, "fused algorithm not taken: %s", why);  // informational: why auto fell back
   return chosen;
 }

@@ -742,7 +742,7 @@ static int launch(const ChunkwiseArgs& A) {
   }
   // the main kernel: the pipelined schedule (chunkwise_pipe.hip) or the fused one
   auto main = [&](bool states_only, unsigned nwg, const MainArgs& m) -> int {
-    if (A.pipelined) return pipe_launch(DQK, states_only, nwg, st, m);
+    if (A.pipelined) return pipe_launch(A.dtype_qkv == XL_DTYPE_F16, DQK, states_only, nwg, st, m);
     if (states_only)
       hipLaunchKernelGGL((chunkwise_fused_kernel<DQK, true>), dim3(nwg), dim3(NTHREADS), smem, st, m.q, m.k, m.v,
                          m.c0, m.n0, m.m0, m.h, m.c_last, m.n_last, m.m_last, m.prep, m.S, m.NC, m.DV, m.BNH,
@@ -798,9 +798,10 @@ int chunkwise_fused_segments(int B, int NH, int S, int DQK, int DV, int max_segm
   return fused::layout_for(B, NH, S, DQK, DV, max_segments).P;
 }
 
-bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why) {
+bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why, bool pipelined) {
   const char* r = nullptr;
-  if (a.dtype_qkv != XL_DTYPE_BF16) r = "q/k/v must be bfloat16";
+  if (pipelined && a.dtype_qkv != XL_DTYPE_BF16 && a.dtype_qkv != XL_DTYPE_F16) r = "q/k/v must be bfloat16 or float16";
+  else if (!pipelined && a.dtype_qkv != XL_DTYPE_BF16) r = "q/k/v must be bfloat16 (float16 runs the pipelined schedule)";
   else if (a.DQK != 128 && a.DQK != 256) r = "DQK must be 128 or 256";
   else if (a.DV % fused::DVT != 0) r = "DV must be a multiple of 64";
   if (why) *why = r;

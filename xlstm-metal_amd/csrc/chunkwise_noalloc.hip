@@ -96,7 +96,7 @@ extern "C" int xl_mlstm_chunkwise_fwd_noalloc(const void* q, const void* k, cons
   int rc = chunkwise_check_args(a, XL_CHUNKWISE_FUSED);
   if (rc) return rc;
   const char* why = nullptr;
-  if (!chunkwise_fused_supported(a, &why))
+  if (!chunkwise_fused_supported(a, &why, false))
     return set_error(XL_ERR_UNSUPPORTED, "xl_mlstm_chunkwise_fwd_noalloc: fused algorithm unsupported here: %s", why);
   const size_t need = chunkwise_fused_workspace(B, NH, S, DQK, DV, 1);
   if (need > (size_t)XL_NOALLOC_SCRATCH_BYTES)

@@ -50,6 +50,55 @@ namespace pipe {
 
 constexpr int NOT = 64 * NOW;  // output-wave threads
 
+// The 16-bit element type of q, k, v and h, and of every MFMA operand: bf16 (the reference's
+// usual dtype) or f16.  Float32 operands enter as hi + lo pairs of that type (16 or 22
+// significant bits).  f16 keeps no deferred forget rescale (RENORM 0: the stored state is
+// renormalised at every chunk whose decay is below 1), so that the state, alpha' <= 1 and
+// alpha' V stay within f16's range as they do in the reference's f16 arithmetic.
+template <typename T> struct Elt;
+template <> struct Elt<bf16_t> {
+  typedef bf16x8 V8;
+  static constexpr uint32_t ONE2 = 0x3f803f80u;  // {1, 1}
+  static constexpr float RENORM = fused::RENORM;
+  __device__ static f32x4 mma16(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+  __device__ static f32x16 mma32(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+  __device__ static f32x4 mma4(s16x4 a, s16x4 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0); }
+  __device__ static uint32_t pack(float lo, float hi) { return pack_bf16(lo, hi); }
+  __device__ static float lo(uint32_t w) { return bf_lo(w); }
+  __device__ static float hi(uint32_t w) { return bf_hi(w); }
+};
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <> struct Elt<f16_t> {
+  typedef f16x8 V8;
+  static constexpr uint32_t ONE2 = 0x3c003c00u;  // {1, 1}
+  static constexpr float RENORM = 0.f;
+  __device__ static f32x4 mma16(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+  __device__ static f32x16 mma32(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+  __device__ static f32x4 mma4(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  }
+  __device__ static float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w)[0]; }
+  __device__ static float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w)[1]; }
+};
+// hi + lo split of a pair: hi = T(x), lo = T(x - hi) (the subtraction exact in float32)
+template <typename E>
+__device__ __forceinline__ uint32_t pack_lo_t(uint32_t hi, float x0, float x1) {
+  return E::pack(x0 - E::lo(hi), x1 - E::hi(hi));
+}
+template <typename E>
+__device__ __forceinline__ void split8_t(f32x4 a, f32x4 b, typename E::V8& hi, typename E::V8& lo) {
+  const u32x4 h = {E::pack(a[0], a[1]), E::pack(a[2], a[3]), E::pack(b[0], b[1]), E::pack(b[2], b[3])};
+  const u32x4 l = {pack_lo_t<E>(h[0], a[0], a[1]), pack_lo_t<E>(h[1], a[2], a[3]), pack_lo_t<E>(h[2], b[0], b[1]),
+                   pack_lo_t<E>(h[3], b[2], b[3])};
+  hi = __builtin_bit_cast(typename E::V8, h);
+  lo = __builtin_bit_cast(typename E::V8, l);
+}
+
 // Row of the C tile held by row l32 of 32-row tile dt of state wave rows
 // [dw0, dw0 + DW): the order of the transposed K^T reads (within each 16 rows,
 // row 4a + c holds state row 8 (a & 1) + 4 (a >> 1) + c); the same row as
@@ -59,9 +108,11 @@ __device__ __forceinline__ int state_row(int dw0, int dt, int l32) {
   return dw0 + 32 * dt + 16 * (l32 >> 4) + 8 * ((x >> 2) & 1) + 4 * (x >> 3) + (x & 3);
 }
 
-template <int DQK, bool STATES_ONLY>
+template <typename T, int DQK, bool STATES_ONLY>
 __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a) {
   using SM = Smem<DQK>;
+  using E = Elt<T>;
+  typedef typename E::V8 V8;
   constexpr int KPD = SM::KPD;
   constexpr int DW = DQK / NSW;   // C rows per state wave (64 or 32)
   constexpr int NKO = DQK / 32;   // K staging: 16-byte pieces per output thread (64 rows x DQK / 256 threads / 8)
@@ -146,10 +197,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       for (int dt = 0; dt < NDT; ++dt) {
         const float x = nacc[dt] + __shfl_xor(nacc[dt], 32);
         if (hh == 0) {
-          const uint32_t hi = pack_bf16(x, 0.f);
+          const uint32_t hi = E::pack(x, 0.f);
           bf16_t* nb = nbuf + buf * 4 * SM::NB_PITCH + state_row(dw0, dt, l32);
           reinterpret_cast<uint16_t*>(nb)[0] = (uint16_t)hi;
-          reinterpret_cast<uint16_t*>(nb)[SM::NB_PITCH] = (uint16_t)pack_bf16(x - bf_lo(hi), 0.f);
+          reinterpret_cast<uint16_t*>(nb)[SM::NB_PITCH] = (uint16_t)E::pack(x - E::lo(hi), 0.f);
         }
       }
     };
@@ -182,14 +233,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       // k-steps, tokens 16 ks + 8 hh + jj (jj = 0..7 in element order).  Transposed
       // reads: within 16 lanes, source lane 4kk + a reads token 16 ks + 8 hh + kk (+4
       // for the second read) at 4 consecutive columns.
-      bf16x8 Kt[NDT][4];
+      V8 Kt[NDT][4];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const char* base = kn + (16 * ks + 8 * hh + kk) * SM::KN_PITCH +
                              2 * (dw0 + 32 * dt + 16 * (g & 1) + 8 * (ka & 1) + 4 * (ka >> 1));
-          Kt[dt][ks] = tr8(base, base + 4 * SM::KN_PITCH);
+          Kt[dt][ks] = __builtin_bit_cast(V8, tr8(base, base + 4 * SM::KN_PITCH));
         }
       // A operand of the n update (4 x 4 x 4 MFMA blocks of 4 lanes): lane 4b + m holds
       // alpha' of tokens 16 ks + 8 hh + 4 j .. +3 as bf16 hi (m = 0), lo (m = 1) or zeros
@@ -208,13 +259,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         // q+1 (VALU) is interleaved with the four MFMAs of k-step q, and the
         // partials of column tile 0 are stored one k-step into tile 1.
         constexpr int NQ = 2 * QKS;
-        bf16x8 bsp[2][2];
+        V8 bsp[2][2];
         f32x16 P[2][2];
-        auto split_q = [&](int qi, bf16x8 (&o)[2]) {
+        auto split_q = [&](int qi, V8 (&o)[2]) {
           const int vt = qi / QKS, s = qi % QKS;
           const f32x16& x = acc[s >> 1][vt];
           const int e0 = 8 * (s & 1);
-          split8(f32x4{x[e0], x[e0 + 1], x[e0 + 2], x[e0 + 3]}, f32x4{x[e0 + 4], x[e0 + 5], x[e0 + 6], x[e0 + 7]},
+          split8_t<E>(f32x4{x[e0], x[e0 + 1], x[e0 + 2], x[e0 + 3]}, f32x4{x[e0 + 4], x[e0 + 5], x[e0 + 6], x[e0 + 7]},
                  o[0], o[1]);
         };
         auto store_p = [&](int vt) {
@@ -238,7 +289,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
           for (int hl = 0; hl < 2; ++hl)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
-              P[vt][tt] = mfma32(bsp[cur][hl], __builtin_bit_cast(bf16x8, Qs[tt][s]), P[vt][tt]);
+              P[vt][tt] = E::mma32(bsp[cur][hl], __builtin_bit_cast(V8, Qs[tt][s]), P[vt][tt]);
           if (vt == 1 && s == 1) {
             store_p(0);
             __builtin_amdgcn_sched_barrier(0);  // keep these stores here, behind the MFMAs of tile 1
@@ -255,13 +306,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       __syncthreads();  // B2: partials and alpha' V of the chunk are complete
 
       // ---------------- phase B: the chunk update of C and n
-      bf16x8 avh[2][2], avl[2][2];
+      V8 avh[2][2], avl[2][2];
       auto load_av = [&](int ks, int buf) {
 #pragma unroll
         for (int vt = 0; vt < 2; ++vt) {
           const char* base = av + (16 * ks + 8 * hh + kk) * AV_PITCH + 2 * (32 * vt + 16 * (g & 1) + 4 * ka);
-          avh[buf][vt] = tr8(base, base + 4 * AV_PITCH);
-          avl[buf][vt] = tr8(base + 128, base + 128 + 4 * AV_PITCH);
+          avh[buf][vt] = __builtin_bit_cast(V8, tr8(base, base + 4 * AV_PITCH));
+          avl[buf][vt] = __builtin_bit_cast(V8, tr8(base + 128, base + 128 + 4 * AV_PITCH));
         }
       };
       load_av(0, 0);
@@ -289,16 +340,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
-            acc[dt][vt] = mfma32(Kt[dt][ks], avh[ks & 1][vt], acc[dt][vt]);
-            acc[dt][vt] = mfma32(Kt[dt][ks], avl[ks & 1][vt], acc[dt][vt]);
+            acc[dt][vt] = E::mma32(Kt[dt][ks], avh[ks & 1][vt], acc[dt][vt]);
+            acc[dt][vt] = E::mma32(Kt[dt][ks], avl[ks & 1][vt], acc[dt][vt]);
           }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const u32x4 kt = __builtin_bit_cast(u32x4, Kt[dt][ks]);
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            nd[dt] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(an[ks][j], __builtin_bit_cast(s16x4, u32x2{kt[2 * j], kt[2 * j + 1]}),
-                                                            nd[dt], 0, 0, 0);
+            nd[dt] = E::mma4(an[ks][j], __builtin_bit_cast(s16x4, u32x2{kt[2 * j], kt[2 * j + 1]}), nd[dt]);
         }
       }
 #pragma unroll
@@ -360,7 +410,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       const float m_next = fmaxf(pg + gm, pamax);
       const float lg = pg + gm - m_next;  // log of this chunk's rescale of the state (<= 0)
       float Gn = gG + lg;
-      const bool renorm = Gn < RENORM;   // wave-uniform
+      const bool renorm = Gn < E::RENORM;   // wave-uniform
       if (renorm) Gn = 0.f;
       const float al = exp_(av_ - m_next - Gn);  // alpha' = exp(a_t - m') e^{-G}
       if (writer) {
@@ -371,10 +421,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         gb[64 + lane] = pv[3];                             // column term
         gb[128 + lane] = exp_(mb - mc + gG) * a.qk_scale;  // output row scale (deferred state rescale folded in)
         gb[192 + lane] = mc;
-        const uint32_t ahi = pack_bf16(al, 0.f);
+        const uint32_t ahi = E::pack(al, 0.f);
         uint16_t* ar = reinterpret_cast<uint16_t*>(gb + 384);
         ar[lane] = (uint16_t)ahi;
-        ar[64 + lane] = (uint16_t)pack_bf16(al - bf_lo(ahi), 0.f);
+        ar[64 + lane] = (uint16_t)E::pack(al - E::lo(ahi), 0.f);
         ar[128 + lane] = 0;  // the zero rows of the n update's A operand
         if (lane == 0) {
           gb[320] = exp_(gG + lg);  // may underflow to 0: the old state is then negligible
@@ -424,9 +474,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         const float ar = __shfl(al, row);
 #pragma unroll
         for (int c2 = 0; c2 < 4; ++c2) {
-          const float x0 = ar * bf_lo(Vst[u][c2]), x1 = ar * bf_hi(Vst[u][c2]);
-          avh_r[u][c2] = pack_bf16(x0, x1);
-          avl_r[u][c2] = pack_lo(avh_r[u][c2], x0, x1);
+          const float x0 = ar * E::lo(Vst[u][c2]), x1 = ar * E::hi(Vst[u][c2]);
+          avh_r[u][c2] = E::pack(x0, x1);
+          avl_r[u][c2] = pack_lo_t<E>(avh_r[u][c2], x0, x1);
         }
       }
     };
@@ -494,7 +544,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
 #pragma unroll
             for (int jt = 0; jt < 5; ++jt)
               if (jt == 4 || jt <= o)
-                Sacc[jt] = mfma(__builtin_bit_cast(bf16x8, kf[p % KD][jt]), __builtin_bit_cast(bf16x8, Qf[p]), Sacc[jt]);
+                Sacc[jt] = E::mma16(__builtin_bit_cast(V8, kf[p % KD][jt]), __builtin_bit_cast(V8, Qf[p]), Sacc[jt]);
           }
           load_q(kc + 1);  // q fragments are dead: prefetch
           qn = (Sacc[4][0] + Sacc[4][1]) + (Sacc[4][2] + Sacc[4][3]);  // q . n (stored state)
@@ -514,27 +564,27 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
           for (int vq = 0; vq < NVX; ++vq) Hmv[vq] = f32x4{0.f, 0.f, 0.f, 0.f};
           // the V operands of both token halves first (their LDS latency then overlaps the splits)
           constexpr int NPJ = (16 * o + 15) / 32 + 1;  // token halves with unmasked M (compile-time)
-          bf16x8 vbs[NPJ][NVT];
+          V8 vbs[NPJ][NVT];
 #pragma unroll
           for (int pj = 0; pj < NPJ; ++pj)
 #pragma unroll
             for (int vq = 0; vq < NVT; ++vq) {
               const char* base = vn + (32 * pj + 4 * g + (r16 >> 2)) * VN_PITCH + 2 * vcol_of(vq, 4 * (r16 & 3));
-              vbs[pj][vq] = tr8(base, base + 16 * VN_PITCH);
+              vbs[pj][vq] = __builtin_bit_cast(V8, tr8(base, base + 16 * VN_PITCH));
             }
           // [.. | 1]: rows 0, 4, 8, 12 of the fifth tile are all ones
-          const uint32_t one = ((r16 & 3) == 0) ? 0x3f803f80u : 0u;
-          const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{one, one, one, one});
+          const uint32_t one = ((r16 & 3) == 0) ? E::ONE2 : 0u;
+          const V8 ones = __builtin_bit_cast(V8, u32x4{one, one, one, one});
 #pragma unroll
           for (int pj = 0; pj < NPJ; ++pj) {
-            bf16x8 mh, ml;
-            split8(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
+            V8 mh, ml;
+            split8_t<E>(Sacc[2 * pj], Sacc[2 * pj + 1], mh, ml);
 #pragma unroll
             for (int vq = 0; vq < NVX; ++vq) {
-              const bf16x8 vb = vq < NVT ? vbs[pj][vq] : ones;
+              const V8 vb = vq < NVT ? vbs[pj][vq] : ones;
               // transposed product [V | 1]^T M^T: lane (g, r16) gets columns 4g+e of row r16
-              Hmv[vq] = mfma(vb, mh, Hmv[vq]);
-              Hmv[vq] = mfma(vb, ml, Hmv[vq]);
+              Hmv[vq] = E::mma16(vb, mh, Hmv[vq]);
+              Hmv[vq] = E::mma16(vb, ml, Hmv[vq]);
             }
           }
         }
@@ -573,8 +623,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
               const int vq = 2 * h2 + b;
-              out[2 * b] = pack_bf16((qb * Hqc[vq][0] + Hmv[vq][0]) * inv, (qb * Hqc[vq][1] + Hmv[vq][1]) * inv);
-              out[2 * b + 1] = pack_bf16((qb * Hqc[vq][2] + Hmv[vq][2]) * inv, (qb * Hqc[vq][3] + Hmv[vq][3]) * inv);
+              out[2 * b] = E::pack((qb * Hqc[vq][0] + Hmv[vq][0]) * inv, (qb * Hqc[vq][1] + Hmv[vq][1]) * inv);
+              out[2 * b + 1] = E::pack((qb * Hqc[vq][2] + Hmv[vq][2]) * inv, (qb * Hqc[vq][3] + Hmv[vq][3]) * inv);
             }
             st16(rh, hoff + 64 * h2, out);
           }
@@ -594,10 +644,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
   }
 }
 
-template <int DQK, bool STATES_ONLY>
+template <typename T, int DQK, bool STATES_ONLY>
 static int launch_one(unsigned nwg, hipStream_t st, const MainArgs& a) {
   const size_t smem = Smem<DQK>::BYTES;
-  auto kern = chunkwise_pipe_kernel<DQK, STATES_ONLY>;
+  auto kern = chunkwise_pipe_kernel<T, DQK, STATES_ONLY>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess)
     return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_fwd: LDS attribute failed: %s", hipGetErrorString(e));
@@ -607,9 +657,15 @@ static int launch_one(unsigned nwg, hipStream_t st, const MainArgs& a) {
 
 }  // namespace pipe
 
-int pipe_launch(int DQK, bool states_only, unsigned nwg, hipStream_t st, const MainArgs& a) {
-  if (DQK == 256) return states_only ? pipe::launch_one<256, true>(nwg, st, a) : pipe::launch_one<256, false>(nwg, st, a);
-  return states_only ? pipe::launch_one<128, true>(nwg, st, a) : pipe::launch_one<128, false>(nwg, st, a);
+template <typename T>
+static int pipe_launch_t(int DQK, bool states_only, unsigned nwg, hipStream_t st, const MainArgs& a) {
+  if (DQK == 256)
+    return states_only ? pipe::launch_one<T, 256, true>(nwg, st, a) : pipe::launch_one<T, 256, false>(nwg, st, a);
+  return states_only ? pipe::launch_one<T, 128, true>(nwg, st, a) : pipe::launch_one<T, 128, false>(nwg, st, a);
+}
+
+int pipe_launch(bool f16, int DQK, bool states_only, unsigned nwg, hipStream_t st, const MainArgs& a) {
+  return f16 ? pipe_launch_t<f16_t>(DQK, states_only, nwg, st, a) : pipe_launch_t<bf16_t>(DQK, states_only, nwg, st, a);
 }
 
 }  // namespace fused

@@ -179,7 +179,7 @@ struct MainArgs {
 
 // The pipelined main kernel (chunkwise_pipe.hip): nwg workgroups of NTHREADS on stream st.
 // XL_OK or a negative XL_ERR_* code.
-int pipe_launch(int DQK, bool states_only, unsigned nwg, hipStream_t st, const MainArgs& a);
+int pipe_launch(bool f16, int DQK, bool states_only, unsigned nwg, hipStream_t st, const MainArgs& a);
 
 }  // namespace fused
 }  // namespace xl

@@ -74,12 +74,13 @@ def available_kernels() -> dict:
 
 
 def _fused_takes_any_length(q, k, v) -> bool:
-    """True when this library's fused chunkwise kernel runs the whole sequence in one call
-    (bf16 q/k/v and a head shape it supports; it runs 64-token chunks with a ragged last chunk)."""
-    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+    """True when this library's pipelined single-pass chunkwise kernel runs the whole sequence in
+    one call (bf16 or f16 q/k/v and a head shape it supports; it runs 64-token chunks with a
+    ragged last chunk)."""
+    if not (q.dtype == k.dtype == v.dtype and q.dtype in (torch.bfloat16, torch.float16)):
         return False
     B, NH, S, DQK = q.shape
-    return chunkwise_workspace_bytes(B, NH, S, DQK, v.shape[-1], 64, q.dtype, algo="fused") > 0
+    return chunkwise_workspace_bytes(B, NH, S, DQK, v.shape[-1], 64, q.dtype, algo="pipelined") > 0
 
 
 def wrap_chunkwise__arbitrary_sequence_length(mlstm_chunkwise_kernel, mlstm_sequence_kernel, mlstm_step_kernel, q,
