@@ -20,8 +20,8 @@ Differences from the reference, by design: the states are always float32
 (the reference keeps them in ``matK.dtype``, fw.py:65).
 
 ``chunk_size`` keeps the reference's contract (S must be a multiple of it,
-fw.py:303-305).  The forward is chunk-size invariant, so with bf16 q/k/v and
-S a multiple of 64 the fused kernel runs every chunk size on 64-token chunks;
+fw.py:303-305).  The forward is chunk-size invariant, so with bf16 or f16 q/k/v
+and S a multiple of 64 the single-pass kernel runs every chunk size on 64-token chunks;
 results then differ from the reference's at that chunk size by rounding only.
 ``algo="two_pass"`` runs the chunk size as given.
 """
