@@ -112,8 +112,8 @@ int xl_mlstm_step_copy_ceiling(const float* c_old, float* c_new, int B, int NH, 
  *   h [B,NH,S,DV] (dtype_qkv); c_last, n_last, m_last float32 (all NULL when
  *   the last states are not wanted).
  * S % L == 0 (fw.py:303-305).  L in {16, 32, 64, 128}.  With algo =
- * XL_CHUNKWISE_FUSED (bf16 q/k/v) or XL_CHUNKWISE_PIPELINED (bf16 or f16 q/k/v),
- * DQK 128 or 256 and DV % 64 == 0, any S >= 1 is accepted: the kernel runs 64-token chunks and a ragged last chunk
+ * XL_CHUNKWISE_FUSED (bf16 q/k/v, DQK 128 or 256) or XL_CHUNKWISE_PIPELINED (bf16 or f16 q/k/v,
+ * DQK 32, 64, 96, 128, 192 or 256), and DV % 64 == 0, any S >= 1 is accepted: the kernel runs 64-token chunks and a ragged last chunk
  * (the forward is chunk-size invariant, so L only names the reference's
  * chunking there).
  * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned

@@ -241,8 +241,10 @@ def test_chunkwise_algorithm_query(lib):
     assert b"bfloat16" in lib.xl_last_error() and b"pipelined" in lib.xl_last_error()
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 64, 0, 0) == 1  # float32 q/k/v
     assert b"bfloat16 or float16" in lib.xl_last_error()
-    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 96, 512, 64, 1, 0) == 1  # DQK 96
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 96, 512, 64, 1, 0) == 3  # DQK 96: pipelined, padded tile
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 80, 512, 64, 1, 0) == 1  # DQK 80
     assert b"DQK" in lib.xl_last_error()
+    assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 160, 512, 64, 1, 0) == 1  # DQK 160: not whole 64-row blocks
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 100, 256, 512, 64, 1, 0) == -1  # S % L
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 100, 256, 512, 64, 1, 2) == 2  # fused takes any S
     assert lib.xl_mlstm_chunkwise_algo(1, 2, 128, 256, 512, 48, 1, 0) == -2

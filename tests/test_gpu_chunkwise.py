@@ -275,14 +275,14 @@ def test_backend_any_length_bf16(gpu_case, S):
 
 
 def test_auto_fallback_warns_once(gpu_case):
-    """algo="auto" with float16 q/k/v runs the two-pass kernels and says so once (a RuntimeWarning
-    naming the reason), still within the parity bar."""
+    """algo="auto" with a head shape the single-pass kernels do not take (DV 48) runs the two-pass
+    kernels and says so once (a RuntimeWarning naming the reason), still within the parity bar."""
     import warnings
 
     import xlstm_hip
     from xlstm_hip import ops
     ops._fallback_warned.clear()
-    x, st = _inputs(1, 2, 128, 64, 64, torch.float16, seed=77)
+    x, st = _inputs(1, 2, 128, 64, 48, torch.float16, seed=77)
     with pytest.warns(RuntimeWarning, match="two-pass"):
         h = xlstm_hip.mlstm_chunkwise(*_gpu(x))
     with warnings.catch_warnings():
@@ -391,3 +391,26 @@ def test_backend_any_length_f16(gpu_case, S):
     hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, chunk_size=64)
     for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
         assert_parity(got.cpu(), want, torch.float16, f"backend any-S f16 S={S} {name}")
+
+
+@pytest.mark.parametrize("B,NH,S,DQK,DV,with_state", [
+    (1, 2, 256, 64, 128, True), (2, 2, 320, 32, 64, False), (1, 2, 1000, 96, 128, True),
+    (1, 1, 100, 192, 64, True), (1, 2, 37, 64, 64, False),
+    (1, 4, 2048, 96, 192, True),   # the sequence split (16 column tiles x 4 heads < 256)
+])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pipelined_narrow_heads(gpu_case, B, NH, S, DQK, DV, with_state, dtype):
+    """Head widths below the pipelined kernel's 128 / 256-row tile (32, 64, 96 in the 128 tile,
+    192 in the 256 tile): the tile's rows and columns past DQK stay zero, the state waves past it
+    idle.  h and the last states against the oracle's any-S driver, any S, initial states, the
+    sequence split, bf16 and f16."""
+    import xlstm_hip
+    x, st = _inputs(B, NH, S, DQK, DV, dtype, seed=S + DQK + 3, with_state=with_state)
+    if S % 64 == 0:
+        assert xlstm_hip.chunkwise_algorithm(B, NH, S, DQK, DV, 64, dtype) == "pipelined"
+    h, (C, n, m) = xlstm_hip.mlstm_chunkwise(*_gpu(x), *_gpu(st), return_last_states=True, chunk_size=64,
+                                             algo="pipelined")
+    q, k, v, i, f = (t.float() for t in x)
+    hr, (Cr, nr, mr) = om.arbitrary_length(q, k, v, f, i, *st, chunk_size=64)
+    for got, want, name in ((h, hr, "h"), (C, Cr, "C"), (n, nr, "n"), (m, mr, "m")):
+        assert_parity(got.cpu(), want, dtype, f"narrow B{B} NH{NH} S{S} DQK{DQK} DV{DV} {dtype} {name}")

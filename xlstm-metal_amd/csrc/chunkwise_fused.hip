@@ -768,7 +768,7 @@ static int launch(const ChunkwiseArgs& A) {
     float* sms = sns + (lay.P - 1) * nst;
     SegArgs s1 = {lay.P - 1, lay.kc_per_seg, nullptr, nullptr, nullptr, ec, en, em};
     const MainArgs m1 = {q, k, v, A.c0, A.n0, A.m0, nullptr, nullptr, nullptr, nullptr, prep,
-                         A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, s1};
+                         A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, s1, A.DQK};
     const int rc = main(true, (unsigned)(BNH * nvtile * (lay.P - 1)), m1);
     if (rc) return rc;
     const int per4 = (A.DQK * A.DV + A.DQK) / 4;
@@ -777,15 +777,15 @@ static int launch(const ChunkwiseArgs& A) {
     sg = SegArgs{lay.P, lay.kc_per_seg, scs, sns, sms, nullptr, nullptr, nullptr};
   }
   const MainArgs m2 = {q, k, v, A.c0, A.n0, A.m0, (bf16_t*)A.h, A.c_last, A.n_last, A.m_last, prep,
-                       A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, sg};
+                       A.S, NC, A.DV, BNH, nvtile, A.qk_scale, A.eps, sg, A.DQK};
   const int rc = main(false, (unsigned)(BNH * nvtile * sg.nseg), m2);
   if (rc) return rc;
   return check_launch(A.pipelined ? "xl_mlstm_chunkwise_fwd(pipelined)" : "xl_mlstm_chunkwise_fwd(fused)");
 }
 
 template <typename TG>
-static int launch_d(const ChunkwiseArgs& A) {
-  return A.DQK == 256 ? launch<TG, 256>(A) : launch<TG, 128>(A);
+static int launch_d(const ChunkwiseArgs& A) {  // the tile: 128 rows for DQK <= 128, else 256
+  return A.DQK > 128 ? launch<TG, 256>(A) : launch<TG, 128>(A);
 }
 
 }  // namespace fused
@@ -800,9 +800,13 @@ int chunkwise_fused_segments(int B, int NH, int S, int DQK, int DV, int max_segm
 
 bool chunkwise_fused_supported(const ChunkwiseArgs& a, const char** why, bool pipelined) {
   const char* r = nullptr;
+  // the pipelined kernel also takes a DQK below its 128 / 256 tile that is a whole number of
+  // state-wave row blocks (32 / 64 rows): the rows and columns past it stay zero
+  const bool dqk_pipe = a.DQK <= 128 ? (a.DQK >= 32 && a.DQK % 32 == 0) : (a.DQK <= 256 && a.DQK % 64 == 0);
   if (pipelined && a.dtype_qkv != XL_DTYPE_BF16 && a.dtype_qkv != XL_DTYPE_F16) r = "q/k/v must be bfloat16 or float16";
   else if (!pipelined && a.dtype_qkv != XL_DTYPE_BF16) r = "q/k/v must be bfloat16 (float16 runs the pipelined schedule)";
-  else if (a.DQK != 128 && a.DQK != 256) r = "DQK must be 128 or 256";
+  else if (pipelined && !dqk_pipe) r = "DQK must be 32, 64, 96, 128, 192 or 256";
+  else if (!pipelined && a.DQK != 128 && a.DQK != 256) r = "DQK must be 128 or 256 (32, 64, 96 and 192 run the pipelined schedule)";
   else if (a.DV % fused::DVT != 0) r = "DV must be a multiple of 64";
   if (why) *why = r;
   return r == nullptr;

@@ -124,6 +124,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
   const int ws = w & 3;  // index within the state or output group
   const SegArgs& sg = a.sg;
   const int S = a.S, NC = a.NC, DV = a.DV, BNH = a.BNH, nvtile = a.nvtile;
+  // the head's q / k width in memory: DQK, or less (a multiple of DW) with the tile's rows and
+  // columns past it zero (state waves past it idle, q and k read as zero there)
+  const int dq = a.dq;
 
   // ---- XCD-aware workgroup -> (head, column tile): consecutive tiles of a head share an XCD
   const int nwg = BNH * nvtile * sg.nseg;
@@ -133,7 +136,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
   const int v0 = (lin - bhs * nvtile) * DVT;
   const int seg = bhs / BNH, bh = bhs - seg * BNH;
   const int kc0 = seg * sg.kc_per_seg, kc1 = min(NC, kc0 + sg.kc_per_seg);  // this segment's chunks
-  const size_t cst = (size_t)BNH * DQK * DV, nst = (size_t)BNH * DQK;
+  const size_t cst = (size_t)BNH * dq * DV, nst = (size_t)BNH * dq;
   const float* ci = seg == 0 ? a.c0 : (sg.sc ? sg.sc + (seg - 1) * cst : nullptr);
   const float* ni = seg == 0 ? a.n0 : (sg.sn ? sg.sn + (seg - 1) * nst : nullptr);
   const float m_init = seg == 0 ? (a.m0 ? a.m0[bh] : 0.f) : (sg.sm ? sg.sm[(seg - 1) * BNH + bh] : -INFINITY);
@@ -148,15 +151,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
   bf16_t* nbuf = (bf16_t*)(smem + SM::NB);   // [2][4][NB_PITCH]: n parts entering chunk kc live in buffer kc & 1
   float* gbuf = (float*)(smem + SM::GATES);  // [2][GROWS][64]: rows of chunk kc live in buffer kc & 1
 
-  const bf16_t* qh = a.q + (size_t)bh * S * DQK;
-  const bf16_t* kh = a.k + (size_t)bh * S * DQK;
+  const bf16_t* qh = a.q + (size_t)bh * S * dq;
+  const bf16_t* kh = a.k + (size_t)bh * S * dq;
   const bf16_t* vh = a.v + (size_t)bh * S * DV;
   bf16_t* hh = a.h + (size_t)bh * S * DV;
   // valid rows of chunk kc (0 past the sequence: a chunk past the end gets a buffer resource
   // with no records, so its prefetches return zeros without touching memory; they are issued
   // unconditionally, which keeps the compiler's load counters exact)
   auto rows_of = [&](int kc) { return __builtin_amdgcn_readfirstlane(max(0, min(L, S - kc * L))); };
-  auto q_rsrc = [&](int kc) { return chunk_rsrc(qh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2); };
+  auto q_rsrc = [&](int kc) { return chunk_rsrc(qh + (size_t)kc * L * dq, rows_of(kc), dq * 2); };
 
   if (w < NSW) {
     // =====================================================================
@@ -184,12 +187,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
       for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          acc[dt][vt][e] = ci ? ci[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] : 0.f;
+          acc[dt][vt][e] = (ci && dw0 < dq) ? ci[((size_t)bh * dq + srow(dt, e)) * DV + v0 + 32 * vt + l32] : 0.f;
     // n of state row state_row(dw0, dt, l32): lane halves hh = 0, 1 sum the
     // tokens of their half of every 16-token k-step
     float nacc[NDT];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) nacc[dt] = (ni && hh == 0) ? ni[(size_t)bh * DQK + state_row(dw0, dt, l32)] : 0.f;
+    for (int dt = 0; dt < NDT; ++dt)
+      nacc[dt] = (ni && hh == 0 && dw0 < dq) ? ni[(size_t)bh * dq + state_row(dw0, dt, l32)] : 0.f;
     // n entering chunk kc as two bf16 rows (hi, lo) of buffer kc & 1 (rows 2, 3 stay zero):
     // the fifth A tile of the output waves' S product
     auto store_nparts = [&](int buf) {
@@ -204,23 +208,34 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         }
       }
     };
-    for (int e = tid; e < 2 * 2 * DQK; e += 64 * NSW) {
-      const int buf = e / (2 * DQK), part = 2 + (e / DQK) % 2, d = e % DQK;
-      reinterpret_cast<uint16_t*>(nbuf)[(buf * 4 + part) * SM::NB_PITCH + d] = 0;
+    for (int e = tid; e < 2 * 4 * DQK; e += 64 * NSW) {  // rows 2, 3, and rows 0, 1 past dq
+      const int buf = e / (4 * DQK), part = (e / DQK) % 4, d = e % DQK;
+      if (part >= 2 || d >= dq) reinterpret_cast<uint16_t*>(nbuf)[(buf * 4 + part) * SM::NB_PITCH + d] = 0;
+    }
+    if (dw0 >= dq) {
+      // state rows past the head's width: zero partials for the output waves' sums, then only
+      // the workgroup's barriers (B0, and B2, B1 of every chunk)
+      for (int e = lane; e < 64 * HP_PITCH; e += 64) hp[ws * 64 * HP_PITCH + e] = 0.f;
+      __syncthreads();  // B0
+      for (int kc = kc0; kc < kc1; ++kc) {
+        __syncthreads();  // B2
+        __syncthreads();  // B1
+      }
+      return;
     }
     store_nparts(kc0 & 1);
 
     // q fragments (B operand of the transposed product C^T Q^T): token 32 tt + l32,
     // rows dw0 + 16 s + 8 hh .. +7
     u32x4 Qs[2][QKS];
-    const uint32_t qs_off = (uint32_t)((l32 * DQK + dw0 + 8 * hh) * 2);
+    const uint32_t qs_off = (uint32_t)((l32 * dq + dw0 + 8 * hh) * 2);
     auto load_qs = [&](int kc) {
       const auto rq = q_rsrc(kc);
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int s = 0; s < QKS; ++s)
-          Qs[tt][s] = ld16s(rq, qs_off, (uint32_t)((32 * tt * DQK + 16 * s) * 2));
+          Qs[tt][s] = ld16s(rq, qs_off, (uint32_t)((32 * tt * dq + 16 * s) * 2));
     };
     if (!STATES_ONLY) load_qs(kc0);
     __syncthreads();  // B0: tiles, gate rows and n parts of the first chunk
@@ -366,12 +381,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
         for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
-            ce[((size_t)bh * DQK + srow(dt, e)) * DV + v0 + 32 * vt + l32] = acc[dt][vt][e] * sc;
+            ce[((size_t)bh * dq + srow(dt, e)) * DV + v0 + 32 * vt + l32] = acc[dt][vt][e] * sc;
       if (v0 == 0) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const float x = nacc[dt] + __shfl_xor(nacc[dt], 32);
-          if (hh == 0) ne[(size_t)bh * DQK + state_row(dw0, dt, l32)] = x * sc;
+          if (hh == 0) ne[(size_t)bh * dq + state_row(dw0, dt, l32)] = x * sc;
         }
         if (tid == 0) me[bh] = gl[321];
       }
@@ -439,14 +454,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
     };
     // ---- K and V staging of the next chunk: piece u of thread t
     u32x4 Kst[NKO], Vst[2];
-    // piece u * NOT + t: K row (piece / (DQK / 8)), 16-byte column piece % (DQK / 8) (rows are
-    // contiguous, so piece u is u * NOT * 16 bytes past piece 0); V row piece >> 3, 8 columns
-    const uint32_t k_off = (uint32_t)((t / (DQK / 8)) * DQK * 2 + 16 * (t % (DQK / 8)));
+    // piece u * NOT + t: K row (piece / (DQK / 8)), 16-byte column piece % (DQK / 8) of the
+    // tile (NOT / (DQK / 8) rows further per u); in memory rows of dq, so a column past dq
+    // gets an offset beyond the buffer's records and reads as zero; V row piece >> 3, 8 columns
+    const uint32_t k_off = (t % (DQK / 8)) < dq / 8 ? (uint32_t)((t / (DQK / 8)) * dq * 2 + 16 * (t % (DQK / 8)))
+                                                     : 0x80000000u;
     const uint32_t v_off = (uint32_t)(((t >> 3) * DV + v0 + 8 * (t & 7)) * 2);
     auto load_kv = [&](int kc) {
-      const auto r = chunk_rsrc(kh + (size_t)kc * L * DQK, rows_of(kc), DQK * 2);
+      const auto r = chunk_rsrc(kh + (size_t)kc * L * dq, rows_of(kc), dq * 2);
 #pragma unroll
-      for (int u = 0; u < NKO; ++u) Kst[u] = ld16s(r, k_off, (uint32_t)(u * NOT * 16));  // NOT pieces of 16 B per u
+      for (int u = 0; u < NKO; ++u) Kst[u] = ld16s(r, k_off, (uint32_t)(u * (NOT / (DQK / 8)) * dq * 2));
       const auto rv = chunk_rsrc(vh + (size_t)kc * L * DV, rows_of(kc), DV * 2);
 #pragma unroll
       for (int u = 0; u < 2; ++u) Vst[u] = ld16s(rv, v_off, (uint32_t)(u * (NOT / 8) * DV * 2));  // NOT / 8 rows per u
@@ -494,14 +511,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void chunkwise_pipe_kernel(MainArgs a)
     auto out_wave = [&](auto otag) {
       constexpr int o = decltype(otag)::value;
       u32x4 Qf[KPD];
-      const uint32_t qf_off = (uint32_t)(((16 * o + r16) * DQK + 8 * g) * 2);
+      const uint32_t qf_off = (uint32_t)(((16 * o + r16) * dq + 8 * g) * 2);
       float pv[5];  // gate prep of the next chunk
       // q fragments of rows 16o + r16 for S: k-slice 32p + 8g .. 32p + 8g + 7 (one
       // 16-byte load; the K operand below uses the same contiguous k order)
       auto load_q = [&](int kc) {
         const auto rq = q_rsrc(kc);
 #pragma unroll
-        for (int p = 0; p < KPD; ++p) Qf[p] = ld16s(rq, qf_off, (uint32_t)(64 * p));
+        for (int p = 0; p < KPD; ++p)  // k-steps past dq: an offset beyond the records reads zeros
+          Qf[p] = ld16s(rq, qf_off, 32 * p < dq ? (uint32_t)(64 * p) : 0x80000000u);
       };
       // prologue: the first chunk's tiles and gate rows, the second chunk's loads in flight
       load_kv(kc0);

@@ -175,6 +175,7 @@ struct MainArgs {
   int S, NC, DV, BNH, nvtile;
   float qk_scale, eps;
   SegArgs sg;
+  int dq;  // q / k width in memory (DQK of the launch, or less: a multiple of DQK / 4)
 };
 
 // The pipelined main kernel (chunkwise_pipe.hip): nwg workgroups of NTHREADS on stream st.

@@ -179,8 +179,8 @@ def _warn_slow_fallback(B, NH, S, DQK, DV, L, dtype) -> None:
     if why not in _fallback_warned:
         _fallback_warned.add(why)
         warnings.warn(f"xlstm_hip.mlstm_chunkwise: {dtype} inputs run the two-pass kernels ({why}); "
-                      "bf16 or f16 q/k/v with DQK 128 or 256 and DV a multiple of 64 take the single-pass "
-                      "kernels",
+                      "bf16 or f16 q/k/v with DQK 32, 64, 96, 128, 192 or 256 and DV a multiple of 64 take "
+                      "the single-pass kernels",
                       RuntimeWarning, stacklevel=3)
 
 
