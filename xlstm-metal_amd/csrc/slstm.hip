@@ -50,40 +50,35 @@ __global__ __launch_bounds__(256) void slstm_step_kernel(const TZ* __restrict__ 
 // The per-element recurrence is linear in (c, n) once the gates are known,
 // and the stabiliser m depends on the gates of its head only.  So the time
 // axis is split: one workgroup per (b, h, 64 consecutive d) with SEQ_WAVES
-// waves, wave w owning the time segment [w*SL, (w+1)*SL) (SL = ceil(S/16)).
-//  * Gates, 64 steps at a time with lane = step: m_t = max(m_{t-1} + logsig f_t, i_t)
-//    is the scan of the max-plus maps m -> max(m + a, b), a = logsig f_t,
-//    b = i_t, composed as (a, b) o (a', b') = (a + a', max(b + a', b')).  The
-//    map of a span carries the sums of logsig f over sub-spans only, so m has
-//    the rounding of the step-by-step recurrence (exact where i_t resets it).
-//  * Pass 0: each wave composes the map of its segment; the incoming m of
-//    segment w is m0 pushed through the maps of segments 0 .. w-1 (LDS).
-//  * Pass 1: each wave forms c at its segment's end from c = 0 (per lane) as
-//    a weighted sum of tanh z_t (one multiply-add per element and step), and
-//    the scans give the segment's F = prod fg and n from 0 (uniform), to LDS.
+// waves, and time runs in blocks of SEQ_WAVES * WS steps (WS = 64 steps per
+// wave, fewer when S is short), wave w owning steps [w WS, (w + 1) WS) of
+// every block.  Per block:
+//  * Gates, lane = step: m_t = max(m_{t-1} + logsig f_t, i_t) is the scan of
+//    the max-plus maps m -> max(m + a, b), a = logsig f_t, b = i_t, composed
+//    as (a, b) o (a', b') = (a + a', max(b + a', b')).  The map of a span
+//    carries the sums of logsig f over sub-spans only, so m has the rounding
+//    of the step-by-step recurrence (exact where i_t resets it).  The maps of
+//    the block's segments meet in LDS: each wave composes the ones before its
+//    own (its incoming m) and all of them (the next block's incoming m).
+//  * Pass 1: each wave evaluates tanh z_t over its segment once, keeps the
+//    WS values in registers, and forms c at the segment's end from c = 0 as
+//    the weighted sum sum_t w_t tanh z_t (one multiply-add per element and
+//    step; the weights ig_t prod_{s>t} fg_s come from the gate scans); the
+//    segment's F = prod fg and n from 0 go to LDS.
 //  * Pass 2: each wave composes its start state c = F c + c_seg over the
-//    earlier segments and reruns its segment from it, writing h; the wave of
-//    the last step writes the final states.  Without an initial n, n is the
-//    same for every d of a head and h = c * og / (|n| + eps) takes one
-//    multiply per element (the scale is formed per step in the gate phase).
-// z is read twice: for a 16-bit z pass 1 keeps the first 64 steps of every
-// segment in LDS (128 KB for 16 waves) and pass 2 reads them from there; the
-// rest of the second read often hits the Infinity Cache.  Every step of both
-// passes keeps z loads SEQ_PF steps ahead.
-constexpr int SEQ_WAVES = 16;
+//    earlier segments of the block (and every wave the block's end state, the
+//    next block's start) and reruns c = fg c + ig tanh z from the kept values,
+//    writing h.
+// So z crosses HBM once (nontemporal loads: nothing reads it again) and tanh
+// is evaluated once per element.  z is requested SEQ_PF steps ahead, into the
+// registers that will hold its tanh (the next block's first steps into those
+// pass 2 has consumed), and the gates one block ahead; a segment cut short by
+// the end of the sequence reads its z directly, twice.  Without an initial n,
+// n is the same for every d of a head and h = c * og / (|n| + eps) takes one
+// multiply per element (the scale is formed per step in the gate phase).
+constexpr int SEQ_WAVES = 12;  // 3 waves per SIMD: up to 168 registers, 64 of them the kept tanh z
+constexpr int SEQ_WS = 64;     // steps per wave and block (lane = step in the gate phase)
 constexpr int SEQ_PF = 16;
-// 16-bit z of the first 64 steps of every segment is kept in LDS by pass 1
-// and read from there by pass 2 (a quarter of the second z read at cfg4)
-constexpr int SEQ_ZC = 64;
-template <typename TZ> constexpr size_t seq_zc_bytes() { return sizeof(TZ) == 2 ? (size_t)SEQ_WAVES * SEQ_ZC * 64 * 2 : 0; }
-template <typename TZ> __device__ __forceinline__ TZ zc_get(uint16_t v) {
-  if constexpr (sizeof(TZ) == 2) return __builtin_bit_cast(TZ, v);
-  else return TZ{};
-}
-template <typename TZ> __device__ __forceinline__ uint16_t zc_put(TZ v) {
-  if constexpr (sizeof(TZ) == 2) return __builtin_bit_cast(uint16_t, v);
-  else return 0;
-}
 constexpr float SEQ_LOG2E = 1.4426950408889634f;
 
 // inclusive scan of the affine maps x -> F x + N (n from 0 and prod fg)
@@ -124,40 +119,13 @@ __device__ __forceinline__ float tanh_seq(float x) {
   return copysignf(fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f), x);
 }
 
-// Gates of the 64 steps c0 + lane (< t1) given m at step c0 - 1; returns the
-// per-lane fg, ig, og, the max-plus map of the chunk in lane 63 and m at its
-// last valid step.
-template <typename TG>
-__device__ __forceinline__ void seq_gates(const TG* __restrict__ ip, const TG* __restrict__ fp,
-                                          const TG* __restrict__ op, int64_t gbase, int gstride, int c0, int t1,
-                                          int lane, float mprev, float& fg, float& ig, float& og, float& ma,
-                                          float& mb, float& mlast) {
-  const int t = c0 + lane;
-  const bool ok = t < t1;
-  const int64_t gi = gbase + (int64_t)(ok ? t : c0) * gstride;
-  const float iv = to_f32(ip[gi]), fv = to_f32(fp[gi]), ov = to_f32(op[gi]);
-  const float lsf = ok ? logsig_f(fv) : 0.f;
-  float a = lsf, b = ok ? iv : -INFINITY;
-  maxplus_scan(a, b);
-  const float mt = fmaxf(mprev + a, b);                    // m_t
-  float mp = __shfl_up(mt, 1, 64);                         // m_{t-1}
-  if (lane == 0) mp = mprev;
-  fg = exp_f(mp + lsf - mt);
-  ig = exp_f(iv - mt);
-  og = __builtin_amdgcn_rcpf(1.0f + exp_f(-ov));
-  ma = a;
-  mb = b;
-  mlast = lane_of(mt, 63);  // invalid lanes repeat the last valid m
-}
-
 // Raw buffer access: wave-uniform resource and scalar byte offset, per-lane
 // byte offset (the step address costs no vector instruction).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
-// CP: cache policy bits of the access.  z keeps the default policy (the
-// second pass re-reads it, often from the Infinity Cache; nontemporal z loads
-// measured slower whenever z is cached), h is stored nontemporal (written once).
+// CP: cache policy bits of the access; z and h are streamed (each crosses HBM
+// once), so both use the nontemporal policy.
 constexpr int SEQ_NT = 2;
 template <typename T, int CP> __device__ __forceinline__ T buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
   if constexpr (sizeof(T) == 4) {
@@ -173,9 +141,18 @@ template <int CP, typename T> __device__ __forceinline__ void buf_st(T x, __amdg
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, x), r, voff, soff, CP);
   }
 }
+// raw z bits parked in a float register until converted (16-bit z zero-extended)
+template <typename TZ> __device__ __forceinline__ float z_park(TZ v) {
+  if constexpr (sizeof(TZ) == 4) return __builtin_bit_cast(float, v);
+  else return __builtin_bit_cast(float, (uint32_t)__builtin_bit_cast(uint16_t, v));
+}
+template <typename TZ> __device__ __forceinline__ TZ z_unpark(float v) {
+  if constexpr (sizeof(TZ) == 4) return __builtin_bit_cast(TZ, v);
+  else return __builtin_bit_cast(TZ, (uint16_t)__builtin_bit_cast(uint32_t, v));
+}
 
-// Per-wave gate rows of the current 64-step chunk in LDS, read with one
-// broadcast load per step (no v_readlane): {fg, ig, og or the h scale, w}.
+// Per-wave gate rows of the current segment in LDS, read with one broadcast
+// load per step (no v_readlane): {fg, ig, og or the h scale, w}.
 struct SeqGateRow {
   float fg, ig, hs, w;
 };
@@ -188,181 +165,208 @@ __global__ __launch_bounds__(64 * SEQ_WAVES) void slstm_seq_kernel(
     const TZ* __restrict__ z, const TG* __restrict__ ip, const TG* __restrict__ fp, const TG* __restrict__ op,
     const float* __restrict__ c0, const float* __restrict__ n0, const float* __restrict__ m0, TH* __restrict__ h,
     float* __restrict__ c_last, float* __restrict__ n_last, float* __restrict__ m_last, int S, int NH, int H,
-    int ndb, float eps) {
-  __shared__ float s_map[SEQ_WAVES][2];        // max-plus map of each segment
-  __shared__ float s_aff[SEQ_WAVES][2];        // F, n-from-0 of each segment
-  __shared__ float s_cseg[SEQ_WAVES][64];      // c from 0 at each segment's end, per lane
-  __shared__ SeqGateRow s_gate[SEQ_WAVES][64]; // gate rows of the wave's current chunk
-  extern __shared__ uint16_t s_zc[];            // [SEQ_WAVES][SEQ_ZC][64] raw 16-bit z (dynamic; 16-bit z only)
-  constexpr bool ZC = sizeof(TZ) == 2;
+    int ndb, int WS, float eps) {
+  // [block & 1]: a block's maps are published one block early, its segment states read while the
+  // faster waves write the next block's
+  __shared__ float s_map[2][SEQ_WAVES][2];     // max-plus map of each segment of the block
+  __shared__ float s_aff[2][SEQ_WAVES][2];     // F, n-from-0 of each segment
+  __shared__ float s_cseg[2][SEQ_WAVES][64];   // c from 0 at each segment's end, per lane
+  __shared__ SeqGateRow s_gate[SEQ_WAVES][64]; // gate rows of the wave's segment
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;  // w: wave-uniform
   const int bh = blockIdx.x / ndb, db = blockIdx.x - bh * ndb;
   const int b = bh / NH, hh = bh - b * NH;
   const int d = 64 * db + lane;
   const bool dok = d < H;
+  const bool dfull = 64 * (db + 1) <= H;  // uniform: every lane of the block is a real d
   // lane byte offsets within the d block (lanes past H read lane 0's element)
   const uint32_t zlb = (dok ? lane : 0) * (uint32_t)sizeof(TZ), hlb = lane * (uint32_t)sizeof(TH);
-  const int SL = (S + SEQ_WAVES - 1) / SEQ_WAVES;
-  const int t0 = min(S, w * SL), t1 = min(S, t0 + SL);
+  const int TB = SEQ_WAVES * WS;                   // steps per block
   const int64_t gbase = (int64_t)b * S * NH + hh;  // gates[b, t, hh] = gbase + t * NH
   const int64_t zrow = (int64_t)NH * H;            // z[b, t, hh, d] = z + zblk + t * zrow + lane
   const int64_t zblk = (int64_t)b * S * zrow + (int64_t)hh * H + 64 * db;  // wave-uniform
   const int zrowb = (int)zrow * (int)sizeof(TZ), hrowb = (int)zrow * (int)sizeof(TH);  // bytes per step
-  const float m_init = m0 ? m0[bh] : 0.f;
   SeqGateRow* gr = s_gate[w];
 
-  // ---- pass 0: the max-plus map of this segment
-  float sa = 0.f, sb = -INFINITY;
-  for (int c = t0; c < t1; c += 64) {
-    float fg, ig, og, ma, mb, ml;
-    seq_gates(ip, fp, op, gbase, NH, c, t1, lane, 0.f, fg, ig, og, ma, mb, ml);
-    const float ca = lane_of(ma, 63), cb = lane_of(mb, 63);
-    sb = fmaxf(sb + ca, cb);
-    sa += ca;
-  }
-  if (lane == 0) {
-    s_map[w][0] = sa;
-    s_map[w][1] = sb;
-  }
-  __syncthreads();
-  float m_in = m_init;  // m at step t0 - 1
-  for (int q = 0; q < w; ++q) m_in = fmaxf(m_in + s_map[q][0], s_map[q][1]);
+  // state entering the block (identical in every wave): c, n per lane (n uniform when UN), m
+  float c_blk = (c0 && dok) ? c0[(int64_t)bh * H + d] : 0.f;
+  float n_blk = (n0 && dok) ? n0[(int64_t)bh * H + d] : 0.f;
+  float m_blk = m0 ? m0[bh] : 0.f;
 
-  // One segment with the gates of its steps.  PASS 1: c at the segment end
-  // from c = 0, as the weighted sum sum_t w_t tanh z_t per chunk (w_t = ig_t
-  // prod_{s>t} fg_s, formed in the gate phase), and the segment's affine map of
-  // n.  PASS 2: the recurrence from the true start state, writing h.  Step
-  // indices are wave-uniform, so a step's z and h addresses are a scalar
-  // base plus the lane offset.
-  const bool dfull = 64 * (db + 1) <= H;  // uniform: every lane of the block is a real d
-  auto run = [&](auto pass_tag, float& c, float& n) {
-    constexpr int PASS = decltype(pass_tag)::value;
-    float mprev = m_in, Fs = 1.f, Ns = 0.f;
-    float nu = n;  // UN, pass 2: the uniform n
-    TZ zq[SEQ_PF];  // raw prefetched z (converted when used, so the load is not waited for early)
-    const int tlast = max(t1 - 1, 0);
-    // z of step t relative to the chunk starting at step cb (byte offsets < 2^31: checked at launch)
-    auto zat = [&](__amdgpu_buffer_rsrc_t r, int cb, int t) { return buf_ld<TZ, 0>(r, zlb, (t - cb) * zrowb); };
-    // the segment's first chunk is kept in LDS (pass 1 writes, pass 2 reads) when it is a whole chunk
-    const bool zc_seg = ZC && t0 + SEQ_ZC <= t1;
-    uint16_t* zcw = s_zc + (size_t)w * SEQ_ZC * 64 + lane;
-    {
-      const int tp = (PASS == 2 && zc_seg) ? t0 + SEQ_ZC : t0;  // pass 2 prefetches past the kept steps
-      const auto zr = seq_rsrc(z + zblk + (int64_t)tp * zrow);
+  // gates of a wave's segment starting at step ts (< te): lane = step, clamped loads
+  auto load_gates = [&](int ts, int te, float& iv, float& fv, float& ov) {
+    const int t = min(ts + lane, max(te - 1, 0));
+    const int64_t gi = gbase + (int64_t)t * NH;
+    iv = to_f32(ip[gi]);
+    fv = to_f32(fp[gi]);
+    ov = to_f32(op[gi]);
+  };
+  // tz: the raw z of a whole segment's next steps, then its tanh z (pass 1 converts in place,
+  // SEQ_PF steps requested ahead; pass 2 reads the values and requests the next segment's first
+  // SEQ_PF steps into the registers it has consumed)
+  float tz[SEQ_WS];
+  auto request_first = [&](int ts) {  // the first SEQ_PF steps of a whole segment starting at ts
+    const auto zr = seq_rsrc(z + zblk + (int64_t)ts * zrow);
 #pragma unroll
-      for (int j = 0; j < SEQ_PF; ++j) zq[j] = zat(zr, tp, min(tp + j, tlast));
+    for (int j = 0; j < SEQ_PF; ++j) tz[j] = z_park<TZ>(buf_ld<TZ, SEQ_NT>(zr, zlb, j * zrowb));
+  };
+  int t0 = min(S, w * WS), t1 = min(S, t0 + WS);
+  // gate scans of a segment (lane = step): the segment's logsig f, i, o, its prefix max-plus maps
+  // (a, bb), and its map published in s_map[par][w]
+  struct GScan {
+    float lsf, iv, ov, a, bb;
+  };
+  auto gate_scan = [&](int ts, int te, float iv_, float fv_, float ov_, int par) {
+    const bool okg = lane < te - ts;
+    GScan gsc;
+    gsc.lsf = okg ? logsig_f(fv_) : 0.f;
+    gsc.iv = iv_;
+    gsc.ov = ov_;
+    gsc.a = gsc.lsf;
+    gsc.bb = okg ? iv_ : -INFINITY;
+    maxplus_scan(gsc.a, gsc.bb);
+    if (lane == 63) {
+      s_map[par][w][0] = gsc.a;
+      s_map[par][w][1] = gsc.bb;
     }
-    for (int cst = t0; cst < t1; cst += 64) {
-      float fg, ig, og, ma, mb, ml;
-      seq_gates(ip, fp, op, gbase, NH, cst, t1, lane, mprev, fg, ig, og, ma, mb, ml);
-      mprev = ml;
-      const bool ok = cst + lane < t1;
-      const float fgv = ok ? fg : 1.f, igv = ok ? ig : 0.f;
-      float Fc = 1.f;  // PASS 1: prod fg over the chunk
-      if (PASS == 1) {
-        // suffix products prod_{s>=t} fg_s: inclusive scan of the lane-reversed fg
-        float y = __shfl(fgv, 63 - lane, 64), yn = 0.f;
-        affine_scan(y, yn);
-        Fc = lane_of(y, 63);
-        const float pin = __shfl(y, 63 - lane, 64);
-        float pex = __shfl_down(pin, 1, 64);
-        if (lane == 63) pex = 1.f;
-        gr[lane].w = igv * pex;
-        float F = fgv, N = igv;
-        affine_scan(F, N);
-        const float cF = lane_of(F, 63), cN = lane_of(N, 63);
-        Ns = fmaf(Ns, cF, cN);
-        Fs *= cF;
-      } else {
-        float hs = og;
-        if (UN) {
-          float F = fgv, N = igv;
-          affine_scan(F, N);
-          const float nt = fmaf(F, nu, N);  // n at step cst + lane
-          hs = og * __builtin_amdgcn_rcpf(fabsf(nt) + eps);
-          nu = lane_of(nt, 63);  // invalid lanes keep the last valid n
-        }
-        gr[lane] = SeqGateRow{fg, ig, hs, 0.f};
+    return gsc;
+  };
+  float iv, fv, ov;
+  load_gates(t0, t1, iv, fv, ov);
+  if (t1 - t0 == SEQ_WS) request_first(t0);
+  GScan gs = gate_scan(t0, t1, iv, fv, ov, 0);
+  {
+    const int t0n = min(S, t0 + TB), t1n = min(S, t0n + WS);
+    if (t0n < t1n) load_gates(t0n, t1n, iv, fv, ov);  // the next block's gates
+  }
+  __syncthreads();  // the first block's maps
+
+  for (int blk = 0, par = 0; blk < S; blk += TB, par ^= 1) {
+    const int nst = t1 - t0;  // steps of this wave's segment (0 .. WS)
+    const bool ok = lane < nst;
+    // the next block's segment of this wave
+    const int t0n = min(S, t0 + TB), t1n = min(S, t0n + WS);
+    const float lsf = gs.lsf, ivc = gs.iv, ovc = gs.ov, a = gs.a, bb = gs.bb;
+    float m_in = m_blk;  // m at step t0 - 1
+    for (int q = 0; q < w; ++q) m_in = fmaxf(m_in + s_map[par][q][0], s_map[par][q][1]);
+    {
+      float mb = m_blk;
+      for (int q = 0; q < SEQ_WAVES; ++q) mb = fmaxf(mb + s_map[par][q][0], s_map[par][q][1]);
+      m_blk = mb;  // m entering the next block
+    }
+    const float mt = fmaxf(m_in + a, bb);  // m_t (invalid lanes repeat the last valid m)
+    float mp = __shfl_up(mt, 1, 64);       // m_{t-1}
+    if (lane == 0) mp = m_in;
+    const float fgv = ok ? exp_f(mp + lsf - mt) : 1.f;
+    const float igv = ok ? exp_f(ivc - mt) : 0.f;
+    const float og = __builtin_amdgcn_rcpf(1.0f + exp_f(-ovc));
+    const float m_seg = lane_of(mt, 63);
+    // pass-1 weights w_t = ig_t prod_{s>t} fg_s: suffix products as a scan of the lane-reversed fg
+    float y = __shfl(fgv, 63 - lane, 64), yn = 0.f;
+    affine_scan(y, yn);
+    const float Fc = lane_of(y, 63);
+    const float pin = __shfl(y, 63 - lane, 64);
+    float pex = __shfl_down(pin, 1, 64);
+    if (lane == 63) pex = 1.f;
+    gr[lane].w = igv * pex;
+    float F = fgv, N = igv;  // the affine maps of n: prefix scan (n from 0 at every step)
+    affine_scan(F, N);
+    const float cN = lane_of(N, 63);
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- pass 1: tanh z of the segment into registers, c at its end from c = 0
+    float acc = 0.f;
+    if (nst == SEQ_WS) {
+      const auto zr = seq_rsrc(z + zblk + (int64_t)t0 * zrow);
+#pragma unroll
+      for (int j = 0; j < SEQ_WS; ++j) {
+        if (j % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // weights read from LDS at most 8 steps ahead
+        if (j + SEQ_PF < SEQ_WS) tz[j + SEQ_PF] = z_park<TZ>(buf_ld<TZ, SEQ_NT>(zr, zlb, (j + SEQ_PF) * zrowb));
+        tz[j] = tanh_seq(to_f32(z_unpark<TZ>(tz[j])));
+        acc = fmaf(gr[j].w, tz[j], acc);
       }
-      __builtin_amdgcn_wave_barrier();
-      const auto zr = seq_rsrc(z + zblk + (int64_t)cst * zrow);
-      const auto hr = seq_rsrc(h + zblk + (int64_t)cst * zrow);
-      float acc = 0.f;  // PASS 1: sum_t w_t tanh z_t over the chunk
-      auto step = [&](int j, float zt, auto store_tag) {
-        const float tz = tanh_seq(zt);
-        if (PASS == 1) {
-          acc = fmaf(gr[j].w, tz, acc);
-        } else {
-          const SeqGateRow gj = gr[j];
-          c = fmaf(gj.fg, c, gj.ig * tz);
-          float hv;
-          if (UN) {
-            hv = c * gj.hs;
-          } else {
-            n = fmaf(gj.fg, n, gj.ig);
-            hv = gj.hs * c * __builtin_amdgcn_rcpf(fabsf(n) + eps);
-          }
-          if (decltype(store_tag)::value || dok) buf_st<SEQ_NT>(from_f32_fast<TH>(hv), hr, hlb, j * hrowb);
+    } else if (nst > 0) {  // short or partial segment: no prefetch, z read again by pass 2
+      const auto zr = seq_rsrc(z + zblk + (int64_t)t0 * zrow);
+      for (int j = 0; j < nst; ++j) acc = fmaf(gr[j].w, tanh_seq(to_f32(buf_ld<TZ, 0>(zr, zlb, j * zrowb))), acc);
+      if (t1n - t0n == SEQ_WS) request_first(t0n);
+    }
+    s_cseg[par][w][lane] = acc;
+    if (lane == 0) {
+      s_aff[par][w][0] = Fc;
+      s_aff[par][w][1] = cN;
+    }
+    // the next block's gate scans and map (its gates arrived during this block), and the gates of
+    // the block after it
+    {
+      const int t0nn = min(S, t0n + TB), t1nn = min(S, t0nn + WS);
+      gs = gate_scan(t0n, t1n, iv, fv, ov, par ^ 1);
+      if (t0nn < t1nn) load_gates(t0nn, t1nn, iv, fv, ov);
+    }
+    __syncthreads();  // every segment's c, F and n from 0; the next block's maps
+    // ---- the segment's start state, and the block's end state (the next block's start)
+    float c = c_blk, n = n_blk;
+    for (int q = 0; q < w; ++q) {
+      const float Fq = s_aff[par][q][0];
+      c = fmaf(Fq, c, s_cseg[par][q][lane]);
+      n = fmaf(Fq, n, s_aff[par][q][1]);
+    }
+    {
+      float ce = c, ne = n;
+      for (int q = w; q < SEQ_WAVES; ++q) {
+        const float Fq = s_aff[par][q][0];
+        ce = fmaf(Fq, ce, s_cseg[par][q][lane]);
+        ne = fmaf(Fq, ne, s_aff[par][q][1]);
+      }
+      c_blk = ce;
+      n_blk = ne;
+    }
+    // ---- pass 2: the segment from its start state and the kept tanh z, h out
+    float hs = og;
+    if (UN) {
+      const float nt = fmaf(F, n, N);  // n at step t0 + lane (uniform over d)
+      hs = og * __builtin_amdgcn_rcpf(fabsf(nt) + eps);
+      n = lane_of(nt, 63);  // invalid lanes keep the last valid n
+    }
+    gr[lane] = SeqGateRow{fgv, igv, hs, 0.f};
+    __builtin_amdgcn_wave_barrier();
+    const auto hr = seq_rsrc(h + zblk + (int64_t)t0 * zrow);
+    auto step = [&](int j, float tzj, auto store_tag) {
+      const SeqGateRow gj = gr[j];
+      c = fmaf(gj.fg, c, gj.ig * tzj);
+      float hv;
+      if (UN) {
+        hv = c * gj.hs;
+      } else {
+        n = fmaf(gj.fg, n, gj.ig);
+        hv = gj.hs * c * __builtin_amdgcn_rcpf(fabsf(n) + eps);
+      }
+      if (decltype(store_tag)::value || dok) buf_st<SEQ_NT>(from_f32_fast<TH>(hv), hr, hlb, j * hrowb);
+    };
+    if (nst == SEQ_WS) {
+      // the next block's segment, when whole, has its first steps requested as registers free up
+      const bool nfull = t1n - t0n == SEQ_WS;
+      const auto zn = seq_rsrc(z + zblk + (int64_t)(nfull ? t0n : t0) * zrow);
+      auto seg = [&](auto store_tag) {
+#pragma unroll
+        for (int j = 0; j < SEQ_WS; ++j) {
+          if (j % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // LDS reads at most 8 steps ahead (registers)
+          step(j, tz[j], store_tag);
+          if (j < SEQ_PF && nfull) tz[j] = z_park<TZ>(buf_ld<TZ, SEQ_NT>(zn, zlb, j * zrowb));
         }
       };
-      if (PASS == 2 && zc_seg && cst == t0) {  // kept in LDS by pass 1 (the ring holds the next chunk)
-        auto chunk = [&](auto store_tag) {
-#pragma unroll
-          for (int j = 0; j < 64; ++j) {
-            if (j % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // LDS reads at most 8 steps ahead (registers)
-            step(j, to_f32(zc_get<TZ>(zcw[64 * j])), store_tag);
-          }
-        };
-        if (dfull) chunk(std::true_type{});
-        else chunk(std::false_type{});
-      } else if (cst + 64 <= t1) {
-        auto chunk = [&](auto store_tag, auto keep_tag) {
-#pragma unroll
-          for (int j = 0; j < 64; ++j) {
-            const TZ zraw = zq[j % SEQ_PF];
-            if (decltype(keep_tag)::value) zcw[64 * j] = zc_put(zraw);
-            zq[j % SEQ_PF] = zat(zr, cst, min(cst + j + SEQ_PF, tlast));
-            step(j, to_f32(zraw), store_tag);
-          }
-        };
-        if (PASS == 1 && zc_seg && cst == t0) chunk(std::true_type{}, std::true_type{});  // pass 1: no h stores
-        else if (dfull) chunk(std::true_type{}, std::false_type{});
-        else chunk(std::false_type{}, std::false_type{});
-      } else {  // partial chunk at the segment end: no prefetch
-        for (int j = 0; j < t1 - cst; ++j) step(j, to_f32(zat(zr, cst, cst + j)), std::false_type{});
-      }
-      if (PASS == 1) c = fmaf(Fc, c, acc);
-      __builtin_amdgcn_wave_barrier();
+      if (dfull) seg(std::true_type{});
+      else seg(std::false_type{});
+    } else {
+      const auto zr = seq_rsrc(z + zblk + (int64_t)t0 * zrow);
+      for (int j = 0; j < nst; ++j) step(j, tanh_seq(to_f32(buf_ld<TZ, 0>(zr, zlb, j * zrowb))), std::false_type{});
     }
-    if (PASS == 1) {
-      n = Ns;
-      if (lane == 0) {
-        s_aff[w][0] = Fs;
-        s_aff[w][1] = Ns;
-      }
+    if (c_last && nst > 0 && t1 == S && dok) {  // the wave of the last step
+      c_last[(int64_t)bh * H + d] = c;
+      n_last[(int64_t)bh * H + d] = n;
+      if (d == 0) m_last[bh] = m_seg;
     }
-    if (PASS == 2 && UN) n = nu;
-    return mprev;
-  };
-
-  // ---- pass 1: this segment from c = 0
-  float c = 0.f, n = 0.f;
-  run(std::integral_constant<int, 1>{}, c, n);
-  s_cseg[w][lane] = c;
-  __syncthreads();
-  // ---- start state of this segment, then pass 2
-  c = (c0 && dok) ? c0[(int64_t)bh * H + d] : 0.f;
-  n = (n0 && dok) ? n0[(int64_t)bh * H + d] : 0.f;
-  for (int q = 0; q < w; ++q) {
-    const float F = s_aff[q][0];
-    c = fmaf(F, c, s_cseg[q][lane]);
-    n = fmaf(F, n, s_aff[q][1]);
-  }
-  const float m_end = run(std::integral_constant<int, 2>{}, c, n);
-  if (c_last && t0 < t1 && t1 == S && dok) {  // the wave of the last step
-    c_last[(int64_t)bh * H + d] = c;
-    n_last[(int64_t)bh * H + d] = n;
-    if (d == 0) m_last[bh] = m_end;
+    __builtin_amdgcn_wave_barrier();
+    t0 = t0n;
+    t1 = t1n;
   }
 }
 
@@ -382,15 +386,11 @@ static int launch_seq3(const void* z, const void* i, const void* f, const void* 
                        int64_t total, float eps, hipStream_t s) {
   const int ndb = (H + 63) / 64;  // 64-element d blocks per head
   const int64_t blocks = total / H * ndb;
+  // steps per wave and block: the register-held maximum, fewer for a short sequence (one block)
+  const int WS = min(SEQ_WS, (S + SEQ_WAVES - 1) / SEQ_WAVES);
   auto kern = n ? slstm_seq_kernel<TZ, TG, TH, false> : slstm_seq_kernel<TZ, TG, TH, true>;
-  const size_t zc = seq_zc_bytes<TZ>();
-  if (zc) {
-    const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)zc);
-    if (e != hipSuccess)
-      return set_error(XL_ERR_LAUNCH, "xl_slstm_seq_fwd: LDS attribute failed: %s", hipGetErrorString(e));
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), zc, s, (const TZ*)z, (const TG*)i,
-                     (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H, ndb, eps);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * SEQ_WAVES), 0, s, (const TZ*)z, (const TG*)i,
+                     (const TG*)f, (const TG*)o, c, n, m, (TH*)h, c1, n1, m1, S, NH, H, ndb, WS, eps);
   return check_launch("xl_slstm_seq_fwd");
 }
 
