@@ -113,10 +113,11 @@ __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(
 __device__ __forceinline__ float logsig_f(float x) {
   return fminf(x, 0.f) - 0.6931471805599453f * __builtin_amdgcn_logf(1.0f + exp_f(-fabsf(x)));
 }
-// tanh(x) = sign(x) (1 - 2 / (1 + e^{2|x|})): absolute error ~1e-7, no branch
+// tanh(x) = 1 - 2 / (1 + e^{2x}) on either sign (e^{2x} -> 0 gives -1, -> inf gives 1): absolute
+// error below 2e-7 over every bf16 input, no branch, no sign fix-up
 __device__ __forceinline__ float tanh_seq(float x) {
-  const float e = __builtin_amdgcn_exp2f(fabsf(x) * (2.0f * SEQ_LOG2E));
-  return copysignf(fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f), x);
+  const float e = __builtin_amdgcn_exp2f(x * (2.0f * SEQ_LOG2E));
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
 }
 
 // Raw buffer access: wave-uniform resource and scalar byte offset, per-lane
