@@ -55,8 +55,11 @@ int chunkwise_states_pass(const ChunkwiseArgs& a, float* Cst, float* nst, float*
 // The states pass on the matrix cores (float32 / f16 q/k/v on float32 MFMA, bf16 on bf16 MFMA),
 // the last states into a.c_last / n_last / m_last (each may be null); 1, launching nothing,
 // where its tiles do not fit (DV % 64, DQK not in {64, 128, 256}, L not in {16, 32, 64}),
-// otherwise XL_OK or a negative XL_ERR_* code.
-int chunkwise_states_mfma(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst);
+// otherwise XL_OK or a negative XL_ERR_* code.  gprep: room for the bf16 scan's gate prefix,
+// kChunkGatePrefix floats per chunk of every head.
+int chunkwise_states_mfma(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst, float* gprep);
+// floats per chunk of the bf16 chunk scans' gate prefix: b[64], a[64], the chunk's log-decay, max a
+constexpr int kChunkGatePrefix = 132;
 
 // The single-pass algorithms.  fused_supported() says whether a shape/dtype is covered by the
 // pipelined schedule (pipelined: bf16 or f16 q/k/v) or the fused one (bf16 only), and why not,

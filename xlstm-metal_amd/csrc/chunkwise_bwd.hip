@@ -94,8 +94,10 @@ __device__ __forceinline__ float xor_lane(float x, int lane) {
 }
 
 struct BwLayout {
-  size_t Cst, nst, mst, cfin, nfin, mfin, vm, vn, dC, dfp, dip, total;
+  size_t Cst, nst, mst, cfin, nfin, mfin, vm, vn, dC, dfp, dip, gprep, total;
 };
+
+constexpr int GP_STRIDE = kChunkGatePrefix;  // floats per chunk of the scans' gate prefix
 
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -120,6 +122,7 @@ BwLayout bw_layout(int B, int NH, int S, int DQK, int DV, int L) {
   o.dC = take(BNH * (NC + 1) * DQK * DV);
   o.dfp = take(BNH * S * ndt);
   o.dip = take(BNH * S * nvt);
+  o.gprep = take(BNH * NC * GP_STRIDE);
   o.total = off;
   return o;
 }
@@ -979,6 +982,35 @@ __global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __rest
   }
 }
 
+// Gate prefix of every chunk for the bf16 chunk scans, all chunks at once (one wave per chunk,
+// lane = token): b = sum_{u<=t} logsig f_u, its last value gl, a = gl - b + i and max a
+// (fw.py:98, 115).  Every one of these is independent of the running stabiliser, so the scans
+// no longer form them chunk after chunk on one wave behind a barrier: per chunk each thread only
+// takes m' = max(gl + m, max a) and the exponentials of its own tokens.  The same operations in
+// the same order as the scans formed them, so the values are identical.
+template <typename TG, int L>
+__global__ __launch_bounds__(256) void bw_gate_prep_kernel(const TG* __restrict__ ig, const TG* __restrict__ fg,
+                                                           float* __restrict__ gp, int total_chunks) {
+  const int lane = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);  // bh * NC + chunk
+  if (c >= total_chunks) return;                      // no barrier follows
+  const size_t t0 = (size_t)c * L;                    // the chunk's first token (S = NC * L)
+  const float f = lane < L ? to_f32(fg[t0 + lane]) : 0.f, i = lane < L ? to_f32(ig[t0 + lane]) : 0.f;
+  const float b = wave_incl_sum(lane < L ? logsigmoid(f) : 0.f, lane);
+  const float gl = lane_of(b, L - 1);
+  const float a = lane < L ? gl - b + i : -INFINITY;
+  const float amax = wave_max_rows(a);
+  float* p = gp + (size_t)c * GP_STRIDE;
+  if (lane < L) {
+    p[lane] = b;
+    p[64 + lane] = a;
+  }
+  if (lane == 0) {
+    p[128] = gl;
+    p[129] = amax;
+  }
+}
+
 // ----------------------------------------------- bf16 MFMA chunk scans (1, 3)
 // bw_scan_kernel for bf16 X and Y on v_mfma_f32_16x16x32_bf16: the same workgroups,
 // gates, stores and state layout; per chunk X is staged in LDS as it is and coef_t Y[t] as
@@ -995,11 +1027,11 @@ constexpr int SST_P = SC_V + 4;  // floats per LDS row of a state store (conflic
 template <typename TG, int L, int NRT, bool REV, bool PK>
 __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     const bf16_t* __restrict__ X, const bf16_t* __restrict__ Y, const TG* __restrict__ ig,
-    const TG* __restrict__ fg, const float* __restrict__ s0, const float* __restrict__ n0,
-    const float* __restrict__ m0, const float* __restrict__ vm, const float* __restrict__ vn,
-    float* __restrict__ Sst, float* __restrict__ nst, float* __restrict__ mst, float* __restrict__ sfin,
-    float* __restrict__ nfin, float* __restrict__ mfin, float* __restrict__ s_init, int NC, int DQKf, int DV,
-    int nvt, float qk_scale) {
+    const TG* __restrict__ fg, const float* __restrict__ gp, const float* __restrict__ s0,
+    const float* __restrict__ n0, const float* __restrict__ m0, const float* __restrict__ vm,
+    const float* __restrict__ vn, float* __restrict__ Sst, float* __restrict__ nst, float* __restrict__ mst,
+    float* __restrict__ sfin, float* __restrict__ nfin, float* __restrict__ mfin, float* __restrict__ s_init, int NC,
+    int DQKf, int DV, int nvt, float qk_scale) {
   static_assert(L % 32 == 0, "32-token MFMA steps");
   constexpr int DQK = 64 * NRT;  // state rows of this workgroup
   constexpr int XP = DQK + 16;   // bf16 per staged X row
@@ -1008,9 +1040,7 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t sX[L * XP];
   __shared__ __attribute__((aligned(16))) bf16_t sYh[L * SB_YP];
   __shared__ __attribute__((aligned(16))) bf16_t sYl[L * SB_YP];
-  __shared__ float scoef[L];
   __shared__ __attribute__((aligned(16))) float sSt[4][16 * NRT * SST_P];  // per wave: its state rows, for the stores
-  __shared__ float s_mn, s_g;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
   const int nrs = DQKf / DQK;
   const int blk = xcd_contiguous(blockIdx.x, gridDim.x);
@@ -1077,7 +1107,10 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
   float m = (!REV && m0) ? m0[bh] : 0.f;
 
   u32x4 px[NXP], py[NYP];
-  float pf = 0.f, pi = 0.f, pvm = 0.f, pvn = 1.f, pmp = 0.f;
+  // the chunk's gate prefix (bw_gate_prep_kernel): for this thread's staged tokens a (forward) or
+  // b (reverse, with the token's stats), the chunk's gl and max a, and (forward, n column pair)
+  // a of token tid
+  float ga[NYP], gvm[NYP], gvn[NYP], gl = 0.f, gam = 0.f, gan = 0.f, pmp = 0.f;
   auto fetch = [&](int kc) {
     const size_t t0 = (size_t)bh * S + (size_t)kc * L;
 #pragma unroll
@@ -1091,13 +1124,22 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
       const int p = u * 256 + tid;
       if (NY % 256 == 0 || p < NY) py[u] = *reinterpret_cast<const u32x4*>(Y + (t0 + p / PRY) * DV + v0 + (p % PRY) * 8);
     }
-    if (tid < L) {
-      pf = to_f32(fg[t0 + tid]);
-      pi = to_f32(ig[t0 + tid]);
-      if (REV) {
-        pvm = vm[t0 + tid];
-        pvn = vn[t0 + tid];
+    const float* gb = gp + ((size_t)bh * NC + kc) * GP_STRIDE;
+#pragma unroll
+    for (int u = 0; u < NYP; ++u) {
+      const int t = (u * 256 + tid) / PRY;
+      if (NY % 256 == 0 || t < L) {
+        ga[u] = REV ? gb[t] : gb[64 + t];
+        if (REV) {
+          gvm[u] = vm[t0 + t];
+          gvn[u] = vn[t0 + t];
+        }
       }
+    }
+    gl = gb[128];
+    if (!REV) {
+      gam = gb[129];
+      if (owns_n && tid < L) gan = gb[64 + tid];
     }
     if (REV) pmp = mst[(size_t)bh * NC + kc];
   };
@@ -1109,34 +1151,23 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     const int kc = REV ? NC - 1 - it : it;
     const size_t sidx = (size_t)bh * NC + kc;
     const int slot = REV ? kc + 1 : kc;
-    const float cvm = pvm, cvn = pvn, cmp = pmp;
-    if (w == 0) {
-      const float b = wave_incl_sum(lane < L ? logsigmoid(pf) : 0.f, lane);
-      const float gl = lane_of(b, L - 1);
-      if (!REV) {
-        const float a = lane < L ? gl - b + pi : -INFINITY;
-        const float mn = fmaxf(gl + m, wave_max_rows(a));  // fw.py:115
-        if (lane < L) scoef[lane] = expf(a - mn);     // fw.py:121
-        if (lane == 0) {
-          s_mn = mn;
-          s_g = gl;
-        }
-      } else {
-        if (lane < L) scoef[lane] = expf(b + cmp - cvm) * qk_scale / cvn;  // bw.py:92-101
-        if (lane == 0) s_g = gl;
-      }
-    }
-    __syncthreads();
-    const float gch = s_g;
-    float decay;
+    // the chunk's decay and the coefficients of this thread's own tokens: every thread carries
+    // the running stabiliser, so no wave scans the gates and no barrier waits for it
+    float decay, co[NYP], con = 0.f;
     const float m_in = m;
     if (!REV) {
-      const float mn = s_mn;
-      decay = expf(gch + m - mn);  // fw.py:125
+      const float mn = fmaxf(gl + m, gam);  // fw.py:115
+      decay = expf(gl + m - mn);            // fw.py:125
       m = mn;
+#pragma unroll
+      for (int u = 0; u < NYP; ++u) co[u] = expf(ga[u] - mn);  // fw.py:121
+      if (owns_n && tid < L) con = expf(gan - mn);
     } else {
-      decay = expf(gch + cmp - mnext);  // bw.py:86-89
+      const float cmp = pmp;
+      decay = expf(gl + cmp - mnext);  // bw.py:86-89
       mnext = cmp;
+#pragma unroll
+      for (int u = 0; u < NYP; ++u) co[u] = expf(ga[u] + cmp - gvm[u]) * qk_scale / gvn[u];  // bw.py:92-101
     }
 #pragma unroll
     for (int u = 0; u < NXP; ++u) {
@@ -1150,10 +1181,9 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
         const int t = p / PRY, c = (p % PRY) * 8;
         Piece16<bf16_t> pc;
         pc.raw = py[u];
-        const float co = scoef[t];
         float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = co * to_f32(pc.v[e]);
+        for (int e = 0; e < 8; ++e) x[e] = co[u] * to_f32(pc.v[e]);
         u32x4 h, l;
         split_bf(x, h, l);
         *reinterpret_cast<u32x4*>(sYh + t * SB_YP + c) = h;
@@ -1161,9 +1191,8 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
       }
     }
     if (owns_n && tid < L) {  // the n column pair
-      const float co = scoef[tid];
-      const uint32_t h = pk_bf(co, 0.f);
-      *reinterpret_cast<uint32_t*>(sYh + tid * SB_YP + SC_V) = (h & 0xffffu) | (pk_bf(co - bf_l(h), 0.f) << 16);
+      const uint32_t h = pk_bf(con, 0.f);
+      *reinterpret_cast<uint32_t*>(sYh + tid * SB_YP + SC_V) = (h & 0xffffu) | (pk_bf(con - bf_l(h), 0.f) << 16);
     }
     if (it + 1 < NC) fetch(REV ? kc - 1 : kc + 1);
     __syncthreads();
@@ -2289,23 +2318,24 @@ __global__ __launch_bounds__(FV_THREADS) void bw_dvqk_bf16_kernel(
 
 
 template <typename TQ, typename TG, int L, bool REV, bool PK = false>
-int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* s0, const float* n0,
-                const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst, float* sfin,
-                float* nfin, float* mfin, float* s_init, int BNH, int NC, int DV, float qk_scale, hipStream_t st) {
+int launch_scan(int DQK, const TQ* X, const TQ* Y, const TG* ig, const TG* fg, const float* gp, const float* s0,
+                const float* n0, const float* m0, const float* vm, const float* vn, float* Sst, float* nst, float* mst,
+                float* sfin, float* nfin, float* mfin, float* s_init, int BNH, int NC, int DV, float qk_scale,
+                hipStream_t st) {
   const int nvt = DV / SC_V;
   // 128 state rows per workgroup (64 for DQK 64): two workgroups share a DQK 256 state, so
   // the chunk-sequential scan keeps two waves on every SIMD
-  auto go = [&](auto kern, size_t smem, int nrs) {
+  auto go = [&](auto kern, size_t smem, int nrs, auto... gprep) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess)
       return set_error(XL_ERR_LAUNCH, "xl_mlstm_chunkwise_bwd: LDS attribute failed: %s", hipGetErrorString(e));
-    hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvt * nrs)), dim3(256), smem, st, X, Y, ig, fg, s0, n0, m0, vm, vn,
-                       Sst, nst, mst, sfin, nfin, mfin, s_init, NC, DQK, DV, nvt, qk_scale);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(BNH * nvt * nrs)), dim3(256), smem, st, X, Y, ig, fg, gprep..., s0, n0, m0,
+                       vm, vn, Sst, nst, mst, sfin, nfin, mfin, s_init, NC, DQK, DV, nvt, qk_scale);
     return check_launch(REV ? "xl_mlstm_chunkwise_bwd(dC scan)" : "xl_mlstm_chunkwise_bwd(states scan)");
   };
-  if constexpr (std::is_same<TQ, bf16_t>::value && L % 32 == 0) {  // bf16 operands, static LDS
-    if (DQK == 64) return go(bw_scan_bf16_kernel<TG, L, 1, REV, PK>, 0, 1);
-    return go(bw_scan_bf16_kernel<TG, L, 2, REV, PK>, 0, DQK / 128);
+  if constexpr (std::is_same<TQ, bf16_t>::value && L % 32 == 0) {  // bf16 operands, static LDS, gate prefix in gp
+    if (DQK == 64) return go(bw_scan_bf16_kernel<TG, L, 1, REV, PK>, 0, 1, gp);
+    return go(bw_scan_bf16_kernel<TG, L, 2, REV, PK>, 0, DQK / 128, gp);
   } else {
     static_assert(!PK, "pack24 states come from the bf16 scans only");
     if (DQK == 64) return go(bw_scan_kernel<TQ, TG, L, 1, REV>, scan_smem<TQ, L>(1), 1);
@@ -2322,7 +2352,7 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   float *Cst = (float*)(ws + lay.Cst), *nst = (float*)(ws + lay.nst), *mst = (float*)(ws + lay.mst);
   float *cfin = (float*)(ws + lay.cfin), *nfin = (float*)(ws + lay.nfin), *mfin = (float*)(ws + lay.mfin);
   float *vm = (float*)(ws + lay.vm), *vn = (float*)(ws + lay.vn), *dC = (float*)(ws + lay.dC);
-  float *dfp = (float*)(ws + lay.dfp), *dip = (float*)(ws + lay.dip);
+  float *dfp = (float*)(ws + lay.dfp), *dip = (float*)(ws + lay.dip), *gpr = (float*)(ws + lay.gprep);
   hipStream_t s = (hipStream_t)F.stream;
   const TQ *q = (const TQ*)F.q, *k = (const TQ*)F.k, *v = (const TQ*)F.v, *dh = (const TQ*)A.dh;
   const TG *ig = (const TG*)F.i, *fg = (const TG*)F.f;
@@ -2332,13 +2362,21 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   constexpr bool fused_types = std::is_same<TQ, bf16_t>::value && L == 64;
   const bool fused_dvqk = fused_types && scan_mfma && (F.DV == 256 || F.DV == 512);
   int rc = XL_OK;
+  // the bf16 chunk scans take every chunk's gate prefix from gpr
+  if constexpr (std::is_same<TQ, bf16_t>::value && L % 32 == 0) {
+    if (scan_mfma) {
+      hipLaunchKernelGGL((bw_gate_prep_kernel<TG, L>), dim3((unsigned)((BNH * NC + 3) / 4)), dim3(256), 0, s, ig, fg,
+                         gpr, BNH * NC);
+      if ((rc = check_launch("xl_mlstm_chunkwise_bwd(gate prefix)"))) return rc;
+    }
+  }
   if constexpr (fused_types) {
     if (fused_dvqk)
-      rc = launch_scan<TQ, TG, L, false, true>(F.DQK, k, v, ig, fg, F.c0, F.n0, F.m0, nullptr, nullptr, Cst, nst, mst,
-                                               cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s);
+      rc = launch_scan<TQ, TG, L, false, true>(F.DQK, k, v, ig, fg, gpr, F.c0, F.n0, F.m0, nullptr, nullptr, Cst, nst,
+                                               mst, cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s);
   }
   if (!fused_dvqk)
-    rc = scan_mfma ? launch_scan<TQ, TG, L, false>(F.DQK, k, v, ig, fg, F.c0, F.n0, F.m0, nullptr, nullptr, Cst,
+    rc = scan_mfma ? launch_scan<TQ, TG, L, false>(F.DQK, k, v, ig, fg, gpr, F.c0, F.n0, F.m0, nullptr, nullptr, Cst,
                                                    nst, mst, cfin, nfin, mfin, nullptr, BNH, NC, F.DV, F.qk_scale, s)
                    : chunkwise_states_pass(F, Cst, nst, mst, cfin, nfin, mfin);
   if (rc) return rc;
@@ -2359,13 +2397,13 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
   if ((rc = check_launch("xl_mlstm_chunkwise_bwd(stats)"))) return rc;
   if constexpr (fused_types) {
     if (fused_dvqk)
-      rc = launch_scan<TQ, TG, L, true, true>(F.DQK, q, dh, ig, fg, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr,
-                                              mst, nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
+      rc = launch_scan<TQ, TG, L, true, true>(F.DQK, q, dh, ig, fg, gpr, A.dc_last, nullptr, nullptr, vm, vn, dC,
+                                              nullptr, mst, nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
   }
   if (fused_dvqk) {
   } else if (scan_mfma) {
-    rc = launch_scan<TQ, TG, L, true>(F.DQK, q, dh, ig, fg, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr, mst,
-                                      nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
+    rc = launch_scan<TQ, TG, L, true>(F.DQK, q, dh, ig, fg, gpr, A.dc_last, nullptr, nullptr, vm, vn, dC, nullptr,
+                                      mst, nullptr, nullptr, mfin, A.dc0, BNH, NC, F.DV, F.qk_scale, s);
   } else {
     hipLaunchKernelGGL((bw_dC_kernel<TQ, TG, L>), dim3((unsigned)(BNH * ndt * nvt)), dim3(BW_THREADS), 0, s, q, dh,
                        ig, fg, mst, mfin, vm, vn, A.dc_last, dC, A.dc0, NC, F.DQK, F.DV, ndt, nvt, F.qk_scale);
@@ -2480,16 +2518,22 @@ namespace xl {
 // lo pairs), writing C, n, m entering every chunk and the last states (each may be null).
 // Returns 1, launching nothing, where the tiles do not fit (DV % 64, DQK not in {64, 128, 256},
 // L not in {16, 32, 64}); otherwise XL_OK or a negative XL_ERR_* code.
-int chunkwise_states_mfma(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst) {
+int chunkwise_states_mfma(const ChunkwiseArgs& A, float* Cst, float* nst, float* mst, float* gprep) {
   if (A.DV % SC_V != 0 || !(A.DQK == 64 || A.DQK == 128 || A.DQK == 256) || !(A.L == 16 || A.L == 32 || A.L == 64))
     return 1;
   auto go = [&](auto tq, auto tg, auto lc) {
     using TQ = decltype(tq);
     using TG = decltype(tg);
     constexpr int L = decltype(lc)::value;
+    const int BNH = A.B * A.NH, NC = A.S / L;
+    if constexpr (std::is_same<TQ, bf16_t>::value && L % 32 == 0) {  // the bf16 scan reads the gate prefix
+      hipLaunchKernelGGL((bw_gate_prep_kernel<TG, L>), dim3((unsigned)((BNH * NC + 3) / 4)), dim3(256), 0,
+                         (hipStream_t)A.stream, (const TG*)A.i, (const TG*)A.f, gprep, BNH * NC);
+      if (const int rc = check_launch("xl_mlstm_chunkwise_fwd(gate prefix)")) return rc;
+    }
     return launch_scan<TQ, TG, L, false>(A.DQK, (const TQ*)A.k, (const TQ*)A.v, (const TG*)A.i, (const TG*)A.f,
-                                         A.c0, A.n0, A.m0, nullptr, nullptr, Cst, nst, mst, A.c_last, A.n_last,
-                                         A.m_last, nullptr, A.B * A.NH, A.S / L, A.DV, A.qk_scale,
+                                         gprep, A.c0, A.n0, A.m0, nullptr, nullptr, Cst, nst, mst, A.c_last,
+                                         A.n_last, A.m_last, nullptr, BNH, NC, A.DV, A.qk_scale,
                                          (hipStream_t)A.stream);
   };
   auto by_l = [&](auto tq, auto tg) {

@@ -503,7 +503,7 @@ static int two_pass_t(const ChunkwiseArgs& A) {
 
   // 64-token chunks, whole 64-wide tiles: both passes on the matrix cores
   if constexpr (L == 64) {
-    const int rc = chunkwise_states_mfma(A, Cst, nst, mst);
+    const int rc = chunkwise_states_mfma(A, Cst, nst, mst, mst + (size_t)BNH * NC);
     if (rc < 0) return rc;  // a launch error (1: the tiles do not fit, the FMA kernels below)
     if (rc == 0) {
       const dim3 grid((unsigned)(BNH * NC * nvt));
@@ -595,7 +595,7 @@ int chunkwise_states_pass(const ChunkwiseArgs& A, float* Cst, float* nst, float*
 size_t chunkwise_two_pass_workspace(int B, int NH, int S, int DQK, int DV, int L) {
   const size_t NC = (size_t)(S / L);
   const size_t BNH = (size_t)B * NH;
-  const size_t floats = BNH * NC * ((size_t)DQK * DV + DQK + 1);
+  const size_t floats = BNH * NC * ((size_t)DQK * DV + DQK + 1 + kChunkGatePrefix);
   return (floats * sizeof(float) + 255) & ~(size_t)255;
 }
 
