@@ -118,7 +118,8 @@ int xl_mlstm_step_copy_ceiling(const float* c_old, float* c_new, int B, int NH, 
  * chunking there).
  * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned
  * (fused algorithm: the per-chunk gate prep, 1280 bytes per 64 tokens of
- * every head; two-pass algorithm: the chunk-entry states).  q, k, v, h, c0,
+ * every head; two-pass algorithm: the chunk-entry states and the states
+ * pass's gate prefix, 528 bytes per chunk).  q, k, v, h, c0,
  * n0, c_last and n_last 16-byte aligned (XL_ERR_INVALID_ARG otherwise).
  */
 size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, int L,
@@ -297,7 +298,7 @@ int xl_gate_proj_softcap_fwd(const void* x, const void* weight, const void* bias
  * {16, 32, 64} (the Python autograd runs chunk_size 128 and ragged sequences
  * at 64: the custom backward does not depend on the chunk size).  Workspace:
  * xl_mlstm_chunkwise_bwd_workspace_size bytes, 256-byte aligned (every chunk's
- * state and its gradient in float32).  q, k, v, dh, dq, dk, dv, c0, n0,
+ * state and its gradient in float32, and every chunk's gate prefix).  q, k, v, dh, dq, dk, dv, c0, n0,
  * dc_last and dc0 16-byte aligned (XL_ERR_INVALID_ARG otherwise).
  */
 size_t xl_mlstm_chunkwise_bwd_workspace_size(int B, int NH, int S, int DQK, int DV, int L);
