@@ -119,7 +119,7 @@ int xl_mlstm_step_copy_ceiling(const float* c_old, float* c_new, int B, int NH, 
  * workspace: xl_mlstm_chunkwise_workspace_size(...) bytes, 256-byte aligned
  * (fused algorithm: the per-chunk gate prep, 1280 bytes per 64 tokens of
  * every head; two-pass algorithm: the chunk-entry states and the states
- * pass's gate prefix, 528 bytes per chunk).  q, k, v, h, c0,
+ * pass's gate prefix, 784 bytes per chunk).  q, k, v, h, c0,
  * n0, c_last and n_last 16-byte aligned (XL_ERR_INVALID_ARG otherwise).
  */
 size_t xl_mlstm_chunkwise_workspace_size(int B, int NH, int S, int DQK, int DV, int L,

@@ -104,8 +104,8 @@ def test_chunkwise_rejects_bad_args(lib):
     assert b"16-byte aligned" in lib.xl_last_error()
     assert f(*args(256, 64, algo=1)) == -3  # two-pass without workspace
     assert b"workspace" in lib.xl_last_error()
-    # two-pass: per chunk of every head the entering C, n, m and the states pass's 132-float gate prefix
-    assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 256, 256, 512, 64, 0, 1) == (4 * 8 * (256 * 512 + 256 + 1 + 132) * 4 + 255) // 256 * 256
+    # two-pass: per chunk of every head the entering C, n, m and the states pass's 196-float gate prefix
+    assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 256, 256, 512, 64, 0, 1) == (4 * 8 * (256 * 512 + 256 + 1 + 196) * 4 + 255) // 256 * 256
     assert lib.xl_mlstm_chunkwise_workspace_size(1, 8, 250, 256, 512, 64, 0, 1) == 0
 
 

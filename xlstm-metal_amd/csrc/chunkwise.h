@@ -58,8 +58,10 @@ int chunkwise_states_pass(const ChunkwiseArgs& a, float* Cst, float* nst, float*
 // otherwise XL_OK or a negative XL_ERR_* code.  gprep: room for the bf16 scan's gate prefix,
 // kChunkGatePrefix floats per chunk of every head.
 int chunkwise_states_mfma(const ChunkwiseArgs& a, float* Cst, float* nst, float* mst, float* gprep);
-// floats per chunk of the bf16 chunk scans' gate prefix: b[64], a[64], the chunk's log-decay, max a
-constexpr int kChunkGatePrefix = 132;
+// floats per chunk of the bf16 chunk scans' gate prefix: b[64], a[64], the chunk's log-decay, max a,
+// two spare, and (the backward's fused path, written by its stats pass over a) the dC scan's
+// per-token b - m_comb in place of a and qk_scale / divisor [64]
+constexpr int kChunkGatePrefix = 196;
 
 // The single-pass algorithms.  fused_supported() says whether a shape/dtype is covered by the
 // pipelined schedule (pipelined: bf16 or f16 q/k/v) or the fused one (bf16 only), and why not,

@@ -903,8 +903,8 @@ __global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __rest
                                                              const TG* __restrict__ ig, const TG* __restrict__ fg,
                                                              const float* __restrict__ nst,
                                                              const float* __restrict__ mst, float* __restrict__ vm,
-                                                             float* __restrict__ vn, int NC, float qk_scale,
-                                                             float eps) {
+                                                             float* __restrict__ vn, float* __restrict__ gp, int NC,
+                                                             float qk_scale, float eps) {
   constexpr int L = 64, DQK = 64 * NRT;
   constexpr int KP = DQK + 16;               // bf16 per staged K row (2 DQK + 32 bytes)
   constexpr int PR = DQK / 8, NP = L * PR / 256;  // 16-byte pieces per row, per thread
@@ -976,8 +976,14 @@ __global__ __launch_bounds__(256) void bw_stats_bf16_kernel(const bf16_t* __rest
     const float qn = accN[e] + xor_lane<1>(accN[e], lane);
     if (r == 0) {  // den = qbar (q . n) + sum_j M_ij; divisor max(|den|, exp(-m)) + eps (fw.py:237-245)
       const float den = sqb[i] * qn + rs;
+      const float dv = fmaxf(fabsf(den), expf(-smc[i])) + eps;
       vm[row0 + i] = smc[i];
-      vn[row0 + i] = fmaxf(fabsf(den), expf(-smc[i])) + eps;
+      vn[row0 + i] = dv;
+      if (gp) {  // the dC scan's per-token factors (bw.py:92-101): b - m_comb and qk_scale / divisor
+        float* g = gp + sidx * GP_STRIDE;
+        g[64 + i] = sb[i] - smc[i];
+        g[132 + i] = qk_scale / dv;
+      }
     }
   }
 }
@@ -1129,10 +1135,15 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
     for (int u = 0; u < NYP; ++u) {
       const int t = (u * 256 + tid) / PRY;
       if (NY % 256 == 0 || t < L) {
-        ga[u] = REV ? gb[t] : gb[64 + t];
-        if (REV) {
-          gvm[u] = vm[t0 + t];
-          gvn[u] = vn[t0 + t];
+        if (REV && PK) {  // b - m_comb and qk_scale / divisor, from the stats pass
+          ga[u] = gb[64 + t];
+          gvn[u] = gb[132 + t];
+        } else {
+          ga[u] = REV ? gb[t] : gb[64 + t];
+          if (REV) {
+            gvm[u] = vm[t0 + t];
+            gvn[u] = vn[t0 + t];
+          }
         }
       }
     }
@@ -1167,7 +1178,8 @@ __global__ __launch_bounds__(256, 2) void bw_scan_bf16_kernel(
       decay = expf(gl + cmp - mnext);  // bw.py:86-89
       mnext = cmp;
 #pragma unroll
-      for (int u = 0; u < NYP; ++u) co[u] = expf(ga[u] + cmp - gvm[u]) * qk_scale / gvn[u];  // bw.py:92-101
+      for (int u = 0; u < NYP; ++u)  // bw.py:92-101
+        co[u] = PK ? expf(ga[u] + cmp) * gvn[u] : expf(ga[u] + cmp - gvm[u]) * qk_scale / gvn[u];
     }
 #pragma unroll
     for (int u = 0; u < NXP; ++u) {
@@ -2385,9 +2397,9 @@ int bw_launch(const BwArgs& A, const BwLayout& lay) {
     stats_mfma = F.DQK == 64 || F.DQK == 128 || F.DQK == 256;
     const dim3 grid((unsigned)(BNH * NC));
     switch (stats_mfma ? F.DQK : 0) {
-      case 64: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 1>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, NC, F.qk_scale, F.eps); break;
-      case 128: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 2>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, NC, F.qk_scale, F.eps); break;
-      case 256: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 4>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, NC, F.qk_scale, F.eps); break;
+      case 64: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 1>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, fused_dvqk ? gpr : nullptr, NC, F.qk_scale, F.eps); break;
+      case 128: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 2>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, fused_dvqk ? gpr : nullptr, NC, F.qk_scale, F.eps); break;
+      case 256: hipLaunchKernelGGL((bw_stats_bf16_kernel<TG, 4>), grid, dim3(256), 0, s, q, k, ig, fg, nst, mst, vm, vn, fused_dvqk ? gpr : nullptr, NC, F.qk_scale, F.eps); break;
       default: break;
     }
   }
