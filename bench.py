@@ -834,9 +834,9 @@ def _progress(what):
 def summarize_trace(trace_dir, headline_calls):
     """Markdown table of a rocprofv3 --kernel-trace run of this script: calls, mean, min and max
     duration per kernel, and on its own line the headline: the pipelined chunkwise kernel's
-    dispatches that follow the 512 MB cache flush and the call's gate prep (the timed calls; the first
-    `headline_calls` of them are the cfg2 headline's, the untimed warm-up calls never follow a
-    flush)."""
+    dispatches that follow the 512 MB cache flush and the call's gate prep.  The headline entry's
+    first PATTERN_WARM_CALLS such dispatches are its untimed (flush, call) pairs, the next
+    `headline_calls` its timed calls (the back-to-back warm-up calls never follow a flush)."""
     import csv
     import glob
     import re
@@ -863,15 +863,18 @@ def summarize_trace(trace_dir, headline_calls):
         sn = short(name)
         per.setdefault(sn, []).append(us)
         # a timed call: flush fill, then the call's gate prep, then this kernel
-        if (sn.startswith(PREFILL_KERNEL + "<256, false>") and "gate_prep_kernel" in prev[1][0]
+        if (sn.startswith(PREFILL_KERNEL + "<bf16_t, 256, false>") and "gate_prep_kernel" in prev[1][0]
                 and "FillFunctor<float>" in prev[0][0] and prev[0][1] >= 40.0):
             head.append(us)
         prev = [prev[1], (name, us)]
-    head = head[:headline_calls]
+    warm, head = head[:PATTERN_WARM_CALLS], head[PATTERN_WARM_CALLS:PATTERN_WARM_CALLS + headline_calls]
     print("| kernel | calls | mean us | min us | max us |\n|---|---|---|---|---|")
     if head:
-        print(f"| {PREFILL_KERNEL}<256, false>, the {len(head)} timed cfg2 headline calls (after the cache flush) | "
-              f"{len(head)} | {statistics.mean(head):.1f} | {min(head):.1f} | {max(head):.1f} |")
+        print(f"| {PREFILL_KERNEL}<bf16_t, 256, false>, the {len(head)} timed cfg2 headline calls (after the cache "
+              f"flush) | {len(head)} | {statistics.mean(head):.1f} | {min(head):.1f} | {max(head):.1f} |")
+    if warm:
+        print(f"| {PREFILL_KERNEL}<bf16_t, 256, false>, the headline's {len(warm)} untimed (flush, call) pairs before "
+              f"them | {len(warm)} | {statistics.mean(warm):.1f} | {min(warm):.1f} | {max(warm):.1f} |")
     for name, ts in sorted(per.items(), key=lambda kv: -sum(kv[1])):
         print(f"| {name} | {len(ts)} | {statistics.mean(ts):.1f} | {min(ts):.1f} | {max(ts):.1f} |")
 
