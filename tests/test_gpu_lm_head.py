@@ -14,10 +14,10 @@ rounding boundary; sech^2 taken at the smaller end of that ulp), and the kernel'
 from the hardware exp2 and reciprocal, within 5e-7 absolute (so cap 5e-7 on y); the same bound
 against the exact form y64.
 
-Shapes: config 3's decode step (1 token, D 4096, vocab 50304), config 4's (8 tokens, D 2048),
+Shapes: config 3's decode step (1 token, D 4096, vocab 50304; 4 tokens), config 4's (8 tokens, D 2048),
 the most token rows the kernel stages (16 at D 4096: 131 KB of LDS), a vocabulary that is not a
 multiple of 16 or of a workgroup's 128 rows, D not a multiple of 32 (200) and below one k-step
-(8), f16, no cap (cap 0: the plain Linear), and weights scaled so that z reaches far into the
+(8), fewer vocabulary rows than the row form has waves (7), f16, no cap (cap 0: the plain Linear), and weights scaled so that z reaches far into the
 cap's saturation.  More than 16 rows take the Linear + soft_cap path, under the same bar.
 """
 
@@ -62,7 +62,8 @@ def _check(y, x, w, cap, what):
 
 @pytest.mark.parametrize("M,D,V,w_std", [(1, 4096, 50304, 0.02), (8, 2048, 50304, 0.02), (1, 4096, 50304, 0.6),
                                          (16, 4096, 50304, 0.3), (13, 512, 4099, 0.3), (3, 200, 1000, 1.0),
-                                         (16, 1024, 2048, 0.5), (5, 8, 37, 4.0)])
+                                         (16, 1024, 2048, 0.5), (5, 8, 37, 4.0), (2, 2048, 3001, 0.3),
+                                         (4, 4096, 50304, 0.02), (1, 1024, 7, 0.5)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_vs_float64(gpu_case, M, D, V, w_std, dtype):
     import xlstm_hip

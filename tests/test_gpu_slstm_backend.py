@@ -103,6 +103,41 @@ def test_slstm_sequence_strong_gates(gpu_case, shape, with_state):
         assert relerr(a, b) <= FP32_REL, f"{shape} state={with_state} {name}"
 
 
+@pytest.mark.parametrize("S", [768, 700])
+def test_slstm_sequence_tanh_every_bf16(gpu_case, S):
+    """tanh z of the sequence kernel over every bf16 value of z, against float64 tanh.
+
+    Gates that make each step its own (f = -inf: fg = 0; i = 0: ig = 1; o = +inf: og = 1;
+    eps = 0, fp32 h) give h_t = tanh z_t.  S = 768 runs the whole-segment pass (12 waves x 64
+    steps), S = 700 the short-segment one.  Every finite and infinite bf16 value appears in
+    steps 0 .. S-2; NaN in the last step, where it cannot reach another step.  Bound: the
+    kernel's tanh, 1 - 2 / (1 + e^{2z}), within 2e-7 absolute of tanh z, and +-1 exactly for
+    |z| >= 9.5 (where tanh z rounds to +-1 in fp32)."""
+    import xlstm_hip
+    H = 128
+    bits = torch.arange(65536, dtype=torch.int32)
+    nan = ((bits & 0x7F80) == 0x7F80) & ((bits & 0x7F) != 0)
+    finite = bits[~nan]
+    n_body = (S - 1) * H
+    body = finite.repeat((n_body + finite.numel() - 1) // finite.numel())[:n_body]
+    last = bits[nan][:H]
+    allb = torch.cat([body, last]).to(torch.int16)
+    z = allb.view(torch.bfloat16).view(1, S, 1, H)
+    i = torch.zeros(1, S, 1)
+    f = torch.full((1, S, 1), -float("inf"))
+    o = torch.full((1, S, 1), float("inf"))
+    h, _ = xlstm_hip.slstm_sequence(*_to((z, i, f, o)), eps=0.0)
+    assert h.dtype == torch.float32
+    h = h.cpu().double().view(S, H)
+    ref = torch.tanh(z.double().view(S, H))
+    err = (h[:-1] - ref[:-1]).abs()
+    print(f"S={S}: max |h - tanh z| {err.max().item():.3e} (bound 2e-7)")
+    assert err.max().item() < 2e-7
+    big = z.double().view(S, H)[:-1].abs() >= 9.5
+    assert torch.equal(h[:-1][big], torch.sign(ref[:-1][big]))
+    assert torch.isnan(h[-1]).all()
+
+
 @pytest.mark.parametrize("S", [1, 5, 16, 37, 100, 129, 200])
 def test_arbitrary_length_inference(gpu_case, S):
     import xlstm_hip
