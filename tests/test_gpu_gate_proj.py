@@ -2,7 +2,9 @@
 
 Shapes cover one to four 16-column output tiles (G 1 .. 64, ragged), D a multiple of 32 and not
 (40), M not a multiple of 16, config 4's sLSTM i/f gates (D 2048, G 8) and the 7B mLSTM cell's
-(D 4096, G 16).  Bar: 16-bit max-abs 2e-2 beyond two roundings of the output (its own and the
+(D 4096, G 16); the row-streaming form (D a multiple of 512, G x D / 512 x 4 registers of weight
+slices at most 128) takes D 2048 with G 8 and 4, D 512 with G 16 and D 1024 with G 2 (fewer rows
+than it has waves).  Bar: 16-bit max-abs 2e-2 beyond two roundings of the output (its own and the
 Linear's output rounding before the soft-cap, which the reference applies and a different
 summation order can move by one ulp); with the sLSTM cell's soft-cap in the dtype, beyond four
 (z / cap and tanh are rounded too).
@@ -28,7 +30,7 @@ def _inputs(M, D, G, dtype, seed, with_bias=True):
 
 
 @pytest.mark.parametrize("M,D,G", [(1000, 2048, 8), (300, 2048, 4), (77, 4096, 16), (5, 64, 3), (33, 40, 64),
-                                   (1, 8, 1), (129, 512, 17), (64, 1024, 48)])
+                                   (1, 8, 1), (129, 512, 17), (64, 1024, 48), (100, 512, 16), (3, 1024, 2)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("cap,in_dtype", [(15.0, False), (15.0, True), (0.0, False)])
 def test_vs_oracle(gpu_case, M, D, G, dtype, cap, in_dtype):

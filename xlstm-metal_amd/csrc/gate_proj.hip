@@ -4,7 +4,11 @@
 // the whole activation plus a separate soft-cap pass.
 //
 // A skinny GEMM (M = B * S rows, D up to a few thousand, G <= 64) is bound by
-// reading X once.  A workgroup per 16 rows, its 4 waves over 4 ranges of k,
+// reading X once.  Where D is a multiple of 512 and the G weight rows' slices
+// fit 128 registers (config 4's sLSTM gates: D 2048, G 8 or 4), the
+// row-streaming loop of rows_gemv.h reads each X row as 1 KB contiguous loads
+// with the weight rows held in registers (gate_rows_kernel).  Otherwise a
+// workgroup per 16 rows, its 4 waves over 4 ranges of k,
 // runs v_mfma_f32_16x16x32 (bf16 / f16) straight from the streamed rows (the
 // partial products summed through LDS): lane (g, r16) holds row r16's k-slice
 // 8g .. 8g + 7 of every 32-wide k-step (one 16-byte load, the next k-step
@@ -17,6 +21,7 @@
 // 16-bit tensors, as sLSTMProjectionCell.soft_cap evaluates it,
 // xlstm_metal/torch_native/blocks/slstm/slstm_layers/slstm_projection_cell.py:84-89).
 #include "common.h"
+#include "rows_gemv.h"
 
 #include <type_traits>
 
@@ -36,6 +41,21 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
   else
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                   0);
+}
+
+// The bias, the Linear's rounding and the soft-cap of one output (both forms).
+template <typename T>
+__device__ __forceinline__ float gate_epilogue(float acc, float bn, float cap, float inv_cap, int cap_rounding) {
+  float v = round_to<T>(acc + bn);  // the Linear's output in its dtype
+  if (cap > 0.0f) {
+    if (cap_rounding) {  // cap, x / cap, tanh and the product each in the dtype
+      const float capr = round_to<T>(cap);
+      v = capr * round_to<T>(tanh_f32(round_to<T>(v / capr)));
+    } else {
+      v = soft_cap16(v, cap, inv_cap);
+    }
+  }
+  return v;
 }
 
 constexpr int GP_WAVES = 4;  // waves per 16-row tile, each over a quarter of the k-steps
@@ -139,23 +159,42 @@ __global__ __launch_bounds__(GP_BLOCK) void gate_proj_kernel(const T* __restrict
     for (int e = 0; e < 4; ++e) {
       const int m = m0 + 4 * g + e;
       if (m >= M) continue;
-      float v = round_to<T>(acc[nt][e] + bn);  // the Linear's output in its dtype
-      if (cap > 0.0f) {
-        if (cap_rounding) {  // cap, x / cap, tanh and the product each in the dtype
-          const float capr = round_to<T>(cap);
-          v = capr * round_to<T>(tanh_f32(round_to<T>(v / capr)));
-        } else {
-          v = soft_cap16(v, cap, inv_cap);
-        }
-      }
-      y[(size_t)m * G + n] = from_f32<T>(v);
+      y[(size_t)m * G + n] = from_f32<T>(gate_epilogue<T>(acc[nt][e], bn, cap, inv_cap, cap_rounding));
     }
   }
+}
+
+// Row form: X streamed row by row, the G weight rows as the small rows; lane n < G of the wave
+// ends each row with output n, stored as one contiguous row of y.
+template <typename T, int MT, int NPC>
+__global__ __launch_bounds__(64 * rowgemv::WAVES) void gate_rows_kernel(const T* __restrict__ x,
+                                                                        const T* __restrict__ w,
+                                                                        const T* __restrict__ bias,
+                                                                        T* __restrict__ y, int M, int D, int G,
+                                                                        float cap, float inv_cap, int cap_rounding) {
+  const int lane = threadIdx.x & 63;
+  const float bn = (bias && lane < G) ? to_f32(bias[lane]) : 0.0f;
+  rowgemv::stream_rows<T, MT, NPC>(w, G, x, M, D, [&](int r, int ln, float dot) {
+    if (ln < G) y[(size_t)r * G + ln] = from_f32<T>(gate_epilogue<T>(dot, bn, cap, inv_cap, cap_rounding));
+  });
+}
+
+template <typename T>
+const void* gate_rows(int G, int D) {
+  const int mt = rowgemv::small_rows(G, D);
+  if (!mt) return nullptr;
+  XL_ROWGEMV_PICK(gate_rows_kernel, T, mt, D / 512);
 }
 
 template <typename T>
 int launch(const void* x, const void* w, const void* b, void* y, int M, int D, int G, float cap, int cap_rounding,
            hipStream_t st) {
+  if (const void* rk = gate_rows<T>(G, D)) {
+    const float inv = cap > 0.0f ? 1.0f / cap : 0.0f;
+    void* args[] = {(void*)&x, (void*)&w,   (void*)&b,   (void*)&y,   (void*)&M,
+                    (void*)&D, (void*)&G,   (void*)&cap, (void*)&inv, (void*)&cap_rounding};
+    return rowgemv::launch_streaming(rk, args, M, st, "xl_gate_proj_softcap_fwd");
+  }
   const int64_t blocks = ((int64_t)M + 15) / 16;
   if (blocks > 0x7fffffff) return set_error(XL_ERR_UNSUPPORTED, "xl_gate_proj_softcap_fwd: M=%d too large", M);
   const float inv_cap = cap > 0.0f ? 1.0f / cap : 0.0f;

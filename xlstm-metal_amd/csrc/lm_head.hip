@@ -11,18 +11,10 @@
 // weights cold in the caches):
 //
 // * D a multiple of 512 and the token rows' slices within 128 registers
-//   (lm_head_rows_kernel): each wave streams whole W rows, every load one
-//   contiguous 1 KB piece of a row (lane l holds elements 8l .. 8l + 7 of it),
-//   and keeps each token row's matching slices in registers.  The loads form
-//   the A operand as they stand: row i of the 16 x 32 operand is lane i, 16 + i,
-//   32 + i, 48 + i's pieces, and the token slices in the same lane layout form
-//   B, so D[i][j] pairs the W slices of lanes {16g + i} with the token slices of
-//   lanes {16g + j}: the diagonal D[i][i] is the dot product over lane i's
-//   quarter of the piece, and the trace, summed over the 16 lanes holding it,
-//   is the row's logit (one MFMA per token row and piece, 1/16 of it used: the
-//   GEMV is bound by the stream, not the matrix cores).  Reading W as 1 KB runs
-//   of one row streams it at 6.7 TB/s where the tile layout below (16 rows x
-//   64 bytes per load) reaches 4.5-5.2 TB/s; at the 7B shape 64 us against 83.
+//   (lm_head_rows_kernel): the row-streaming loop of rows_gemv.h with W as the
+//   streamed matrix and the token rows as the small ones (each W row as 1 KB
+//   contiguous loads, the logit as the trace of an MFMA diagonal); 64 us for
+//   412 MB at the 7B shape against 83 for the split form below.
 // * Otherwise the tile forms: 16 vocabulary rows as the A operand straight from
 //   nontemporal 16-byte loads (lane (g, r16) holds row r16's k-slice 8g .. 8g + 7
 //   of each 32-wide k-step), the token rows as B; lane (g, r16) ends with the
@@ -38,8 +30,8 @@
 //   blocks of 8 k-steps in flight; loading up to 16 distinct token rows
 //   alongside W slows the split form by a third at M = 16.
 #include "common.h"
+#include "rows_gemv.h"
 
-#include <algorithm>
 #include <type_traits>
 
 namespace xl {
@@ -60,8 +52,6 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                   0);
 }
 
-constexpr int LR_WAVES = 4;         // row form: waves per workgroup
-constexpr int LR_MAX_XREGS = 128;   // row form: registers of token slices per lane (MT * D / 512 * 4)
 constexpr int LS_WAVES = 4;  // split form: waves per vocabulary tile, each over a quarter of D
 constexpr int LS_KB = 8;     // split form: k-steps per load block
 constexpr int LS_MAX_ROWS = 4;
@@ -74,69 +64,19 @@ constexpr size_t LH_MAX_LDS = 160 * 1024;
 // LDS bytes of the staged token rows: M rows of D + 8 elements
 inline size_t lds_bytes(int M, int D) { return (size_t)M * (D + 8) * 2; }
 
-// Row form: wave gw of nw streams rows gw, gw + nw, ...; two rows' pieces in
-// flight (the next row requested before this one's MFMAs).  MT: token rows
-// rounded up to a power of two (rows past M are zero and not stored); NPC:
-// 1 KB pieces per row (D = 512 NPC).
+// Row form: the logits of W's rows against the token rows, soft-capped.
 template <typename T, int MT, int NPC>
-__global__ __launch_bounds__(64 * LR_WAVES) void lm_head_rows_kernel(const T* __restrict__ x, const T* __restrict__ w,
-                                                                     T* __restrict__ y, int M, int D, int V, float cap,
-                                                                     float inv_cap) {
-  const int lane = threadIdx.x & 63;
-  const int nw = gridDim.x * LR_WAVES;
-  const int gw = blockIdx.x * LR_WAVES + (threadIdx.x >> 6);
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  u32x4 xr[MT][NPC];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int p = 0; p < NPC; ++p)
-      xr[m][p] = m < M ? *reinterpret_cast<const u32x4*>(x + (size_t)m * D + 512 * p + 8 * lane) : zero;
-  // lane (g, r16) holds D[4g + e][r16], e = 0..3: the diagonal element D[i][i] sits in lane
-  // 16 (i >> 2) + i at e = i & 3
-  const bool on_diag = (lane >> 4) == ((lane & 15) >> 2);
-  const int de = lane & 3;
-  u32x4 wa[2][NPC];
-  auto load = [&](int r, auto buf_tag) {
-    constexpr int b = decltype(buf_tag)::value;
-    const T* wr = w + (size_t)r * D + 8 * lane;
-#pragma unroll
-    for (int p = 0; p < NPC; ++p) wa[b][p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 512 * p));
-  };
-  auto run = [&](int r, auto buf_tag) {
-    constexpr int b = decltype(buf_tag)::value;
-    f32x4 acc[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int p = 0; p < NPC; ++p)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) acc[m] = mfma16<T>(wa[b][p], xr[m][p], acc[m]);
-    float logit = 0.f;  // lane m < MT ends with token row m's logit
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float d = de == 0 ? acc[m][0] : de == 1 ? acc[m][1] : de == 2 ? acc[m][2] : acc[m][3];
-      const float tr = wave_sum_dpp(on_diag ? d : 0.f);  // the trace, in lane 63
-      const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tr), 63));
-      logit = lane == m ? s : logit;
-    }
+__global__ __launch_bounds__(64 * rowgemv::WAVES) void lm_head_rows_kernel(const T* __restrict__ x,
+                                                                           const T* __restrict__ w,
+                                                                           T* __restrict__ y, int M, int D, int V,
+                                                                           float cap, float inv_cap) {
+  rowgemv::stream_rows<T, MT, NPC>(x, M, w, V, D, [&](int r, int lane, float logit) {
     if (lane < M) {
       float z = round_to<T>(logit);  // the Linear's output in its dtype
       if (cap > 0.0f) z = soft_cap16(z, cap, inv_cap);
       y[(size_t)lane * V + r] = from_f32<T>(z);
     }
-  };
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
-  // two rows per trip keep the buffer indices compile-time constants
-  int r = gw;
-  if (r < V) load(r, B0{});
-  for (; r < V; r += 2 * nw) {
-    if (r + nw < V) load(r + nw, B1{});
-    run(r, B0{});
-    if (r + 2 * nw < V) load(r + 2 * nw, B0{});
-    if (r + nw < V) run(r + nw, B1{});
-  }
+  });
 }
 
 // Split form: one vocabulary tile per workgroup, wave wv over k-steps
@@ -266,23 +206,11 @@ __global__ __launch_bounds__(LH_BLOCK) void lm_head_staged_kernel(const T* __res
   }
 }
 
-// The row form's instance for M token rows and D, or null: D = 512 NPC with NPC in {1, 2, 4, 8}
-// and the token slices within LR_MAX_XREGS registers.
 template <typename T>
 const void* rows_kernel(int M, int D) {
-  if (D % 512 != 0 || M < 1) return nullptr;
-  const int npc = D / 512;
-  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
-  if (mt * npc * 4 > LR_MAX_XREGS) return nullptr;
-#define XL_LR(MT, NPC) \
-  if (mt == MT && npc == NPC) return (const void*)lm_head_rows_kernel<T, MT, NPC>;
-  XL_LR(1, 1) XL_LR(1, 2) XL_LR(1, 4) XL_LR(1, 8)
-  XL_LR(2, 1) XL_LR(2, 2) XL_LR(2, 4) XL_LR(2, 8)
-  XL_LR(4, 1) XL_LR(4, 2) XL_LR(4, 4) XL_LR(4, 8)
-  XL_LR(8, 1) XL_LR(8, 2) XL_LR(8, 4)
-  XL_LR(16, 1) XL_LR(16, 2)
-#undef XL_LR
-  return nullptr;
+  const int mt = rowgemv::small_rows(M, D);
+  if (!mt) return nullptr;
+  XL_ROWGEMV_PICK(lm_head_rows_kernel, T, mt, D / 512);
 }
 
 template <typename T>
@@ -290,19 +218,8 @@ int launch(const void* x, const void* w, void* y, int M, int D, int V, float cap
   const int64_t tiles = ((int64_t)V + 15) / 16;
   const float inv_cap = cap > 0.0f ? 1.0f / cap : 0.0f;
   if (const void* rk = rows_kernel<T>(M, D)) {
-    // one full set of resident workgroups, each wave striding over the rows
-    int dev = 0, cus = 0, per_cu = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rk, 64 * LR_WAVES, 0);
-    if (e != hipSuccess)
-      return set_error(XL_ERR_LAUNCH, "xl_lm_head_softcap_fwd: occupancy query failed: %s", hipGetErrorString(e));
-    const int64_t need = ((int64_t)V + LR_WAVES - 1) / LR_WAVES;  // no more waves than rows
-    const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * std::max(per_cu, 1), need));
     void* args[] = {(void*)&x, (void*)&w, (void*)&y, (void*)&M, (void*)&D, (void*)&V, (void*)&cap, (void*)&inv_cap};
-    e = hipLaunchKernel(rk, dim3(blocks), dim3(64 * LR_WAVES), args, 0, st);
-    if (e != hipSuccess) return set_error(XL_ERR_LAUNCH, "xl_lm_head_softcap_fwd: launch failed: %s", hipGetErrorString(e));
-    return check_launch("xl_lm_head_softcap_fwd");
+    return rowgemv::launch_streaming(rk, args, V, st, "xl_lm_head_softcap_fwd");
   }
   if (M <= LS_MAX_ROWS) {
     hipLaunchKernelGGL(lm_head_split_kernel<T>, dim3((unsigned)tiles), dim3(64 * LS_WAVES), 0, st, (const T*)x,
