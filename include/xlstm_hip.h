@@ -320,10 +320,10 @@ int xl_mlstm_chunkwise_bwd(const void* q, const void* k, const void* v, const vo
  * xlstm_metal/mlx_jit/generate.py:201).  The weights are streamed from HBM once
  * for all M rows.
  *   x [M, D], w [V, D] (nn.Linear's weight), y [M, V]; bf16 or f16 (float32:
- *   XL_ERR_UNSUPPORTED); M <= 16 and M * (D + 8) * 2 <= 160 KiB (the token
- *   rows are staged in LDS; logits of every position of a prompt are a GEMM:
- *   XL_ERR_UNSUPPORTED); D a multiple of 8; x and w 16-byte aligned; cap <= 0:
- *   no soft-cap.
+ *   XL_ERR_UNSUPPORTED); M <= 16 and M * (D + 8) * 2 <= 160 KiB (the limit of
+ *   the kernel form that stages the token rows in LDS, applied to every call;
+ *   logits of every position of a prompt are a GEMM: XL_ERR_UNSUPPORTED); D a
+ *   multiple of 8; x and w 16-byte aligned; cap <= 0: no soft-cap.
  */
 int xl_lm_head_softcap_fwd(const void* x, const void* weight, void* y, int M, int D, int V, float cap,
                            int dtype, void* stream);
