@@ -24,7 +24,9 @@
 
 #include "common.h"
 
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 namespace xl {
 namespace rowgemv {
@@ -115,16 +117,46 @@ inline int small_rows(int M, int D) {
   return mt * npc * 4 <= MAX_XREGS ? mt : 0;
 }
 
+// Resident workgroups of kern on the current device (CUs x workgroups per CU), queried once per
+// (device, kernel) and kept: the launch path then makes no runtime query.
+inline hipError_t resident_blocks(const void* kern, int* out) {
+  struct Entry {
+    int dev;
+    const void* kern;
+    int blocks;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& c : cache)
+      if (c.dev == dev && c.kern == kern) {
+        *out = c.blocks;
+        return hipSuccess;
+      }
+  }
+  int cus = 0, per_cu = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * WAVES, 0);
+  if (e != hipSuccess) return e;
+  const int blocks = cus * (per_cu > 0 ? per_cu : 1);
+  std::lock_guard<std::mutex> lock(mu);
+  cache.push_back(Entry{dev, kern, blocks});
+  *out = blocks;
+  return hipSuccess;
+}
+
 // One full set of resident workgroups of kern (each wave strides over the rows), at most one
 // wave per row; launches with args.
 inline int launch_streaming(const void* kern, void** args, int R, hipStream_t st, const char* who) {
-  int dev = 0, cus = 0, per_cu = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * WAVES, 0);
+  int resident = 0;
+  hipError_t e = resident_blocks(kern, &resident);
   if (e != hipSuccess) return set_error(XL_ERR_LAUNCH, "%s: occupancy query failed: %s", who, hipGetErrorString(e));
   const int64_t need = ((int64_t)R + WAVES - 1) / WAVES;
-  int64_t blocks = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
+  int64_t blocks = resident;
   if (blocks > need) blocks = need;
   if (blocks < 1) blocks = 1;
   e = hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(64 * WAVES), args, 0, st);
