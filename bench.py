@@ -84,6 +84,11 @@ CONV_KERNEL = "causal_conv1d_kernel"
 GROUP_NORM_KERNEL = "group_norm_kernel"
 RMS_GATE_KERNEL = "mh_rmsnorm_gate_kernel"
 GATE_PROJ_KERNEL = "gate_proj_kernel"
+GATE_ROWS_KERNEL = "gate_rows_kernel"  # the gate projection's row form (config 4's sLSTM gates)
+# the lm_head's row form at the decode rows of configs 3 (1 x 4096) and 4 (8 x 2048), vocab 50304
+LM_HEAD_VOCAB = 50304
+LM_HEAD_CFG3_KERNEL = "lm_head_rows_kernel<xl::bf16_t, 1, 8>"
+LM_HEAD_CFG4_KERNEL = "lm_head_rows_kernel<xl::bf16_t, 8, 4>"
 CFG4_D_MODEL = 2048  # config 4's d_model: the sLSTM projection conv runs over all of it
 CFG4_CONV_K = 4
 SOFT_CAP_SHAPE = (1, 2048, 50304)  # config 3 prefill logits
@@ -469,7 +474,8 @@ def _cfg4_layer_stage_inputs(dev):
 
 
 def layer_stage_work():
-    """(workload, algorithmic bytes) of the cfg4 conv + SiLU and GroupNorm launches."""
+    """(workload, algorithmic bytes) of the layer-stage and projection launches: cfg4's conv + SiLU,
+    GroupNorm and gate projection, cfg2's norm x sigmoid(o), the decode lm_heads of cfg3 / cfg4."""
     from xlstm_hip.workloads import CFG4_SLSTM as c
     D, NHH = CFG4_D_MODEL, c.NH * c.H
     conv = (f"cfg4 sLSTM conv1d K{CFG4_CONV_K} + SiLU [B{c.B}, S{c.S}, {D}] bf16",
@@ -481,7 +487,11 @@ def layer_stage_work():
            3 * nel * 2 + c2.NH * c2.DV * 2)
     gp = (f"cfg4 sLSTM i/f gate projection + soft-cap 15 [{c.B * c.S}, {D}] x [{2 * c.NH}, {D}] bf16",
           c.B * c.S * D * 2 + 2 * c.NH * D * 2 + c.B * c.S * 2 * c.NH * 2)
-    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn, RMS_GATE_KERNEL: rms, GATE_PROJ_KERNEL: gp}
+    def lm(M, Dm):  # weights, token rows, logits
+        return (f"lm_head + soft-cap 30: {M} row(s) x D {Dm} x vocab {LM_HEAD_VOCAB} bf16",
+                LM_HEAD_VOCAB * Dm * 2 + M * Dm * 2 + M * LM_HEAD_VOCAB * 2)
+    return {CONV_KERNEL: conv, GROUP_NORM_KERNEL: gn, RMS_GATE_KERNEL: rms, GATE_PROJ_KERNEL: gp, GATE_ROWS_KERNEL: gp,
+            LM_HEAD_CFG3_KERNEL: lm(1, 4096), LM_HEAD_CFG4_KERNEL: lm(8, CFG4_D_MODEL)}
 
 
 def bench_slstm_conv(args, dev):
@@ -898,7 +908,8 @@ def summarize_pmc(fetch_dir, write_dir):
                     key = next((k for k in (PREFILL_KERNEL, PREFILL_KERNEL_FUSED, SOFT_CAP_KERNEL, "mlstm_step_kernel",
                                             "gate_prep_kernel",
                                             SLSTM_KERNEL, SEQ_KERNEL, CONV_KERNEL, GROUP_NORM_KERNEL,
-                                            RMS_GATE_KERNEL, GATE_PROJ_KERNEL, *BWD_KERNELS)
+                                            RMS_GATE_KERNEL, GATE_PROJ_KERNEL, GATE_ROWS_KERNEL,
+                                            LM_HEAD_CFG3_KERNEL, LM_HEAD_CFG4_KERNEL, *BWD_KERNELS)
                                 if k in name), None)
                     if key is None:
                         continue
